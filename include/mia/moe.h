@@ -1,0 +1,100 @@
+#ifndef MIA_MOE_H
+#define MIA_MOE_H
+/*
+ * Public Q8_0 MoE FFN entry points on one GPU.
+ *
+ * The reference's layer is `static int moe(mia_model*, dims, int l)`
+ * (src/model/forward.c:167-197), called once per layer and token from
+ * mia_model_step (src/model/forward.c:210-213), with experts fetched through
+ * an LRU cache fed by the mia_expert_loader port. Here the layer is public,
+ * takes T tokens at once, and reads every expert of every layer from one
+ * HBM-resident table (48 x 128 Q8_0 experts of Qwen3-30B-A3B = 30.4 GiB).
+ *
+ * Conventions follow the reference engine: C99, functions return 0 or -1
+ * (with a message in mia_moe_error), rich error text at open time through
+ * (char *err, size_t errlen), not thread-safe (one host thread per handle).
+ */
+#include <stddef.h>
+#include <stdint.h>
+
+#include "mia/expert_cache.h"
+#include "mia/quant.h"
+#include "mia_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mia_moe mia_moe;
+
+/* Model shape: the MoE fields of the .mia header (include/mia/mia_file.h:
+ * 10-21 of the reference) plus the sizes of this handle. */
+typedef struct {
+    int dim;           /* header dim (2048) */
+    int n_layers;      /* header n_layers (48) */
+    int n_experts;     /* header n_experts (128) */
+    int n_active;      /* header n_active (8) */
+    int expert_hidden; /* header expert_hidden (768) */
+    int norm_topk;     /* header norm_topk (1 for Qwen3) */
+    float norm_eps;    /* header norm_eps (1e-6) */
+    int max_tokens;    /* largest T passed to one call */
+    int device;        /* HIP device ordinal */
+} mia_moe_config;
+
+int mia_moe_open(mia_moe **out, const mia_moe_config *cfg, char *err, size_t errlen);
+void mia_moe_close(mia_moe *m);
+const char *mia_moe_error(const mia_moe *m);
+
+/* Reference blob geometry for this shape (src/storage/mia_file.c:275-283,
+ * tools/internal/mia/format.go:160-163). */
+size_t mia_moe_blob_bytes(const mia_moe *m);
+size_t mia_moe_off_up(const mia_moe *m);
+size_t mia_moe_off_down(const mia_moe *m);
+
+/* Fill the whole table through the reference's storage port: one call of
+ * `load` per (layer, expert) into a host buffer, uploaded and regrouped in
+ * HBM. A failing load returns -1 naming the expert; the table keeps what was
+ * loaded before (the reference's cache likewise leaves no poisoned slot,
+ * src/storage/expert_cache.c:76-79). */
+int mia_moe_load_experts(mia_moe *m, mia_expert_loader load, void *ctx);
+/* One expert from a host blob in the .mia format. */
+int mia_moe_load_expert(mia_moe *m, int layer, int expert, const void *blob);
+/* Read one expert back in the .mia blob format (padding zeroed). */
+int mia_moe_read_expert(mia_moe *m, int layer, int expert, void *blob);
+/* Dense per-layer MoE weights: ffn_norm[dim] and router[E][dim] (fp32, the
+ * layout of mia_layer.ffn_norm/router, include/mia/mia_file.h:23-26). */
+int mia_moe_set_layer(mia_moe *m, int layer, const float *ffn_norm, const float *router);
+/* Seeded synthetic weights generated in HBM (include/mia/synth.h): experts
+ * and routers ~ N(0, 0.02), ffn_norm = 1. */
+int mia_moe_synth(mia_moe *m, uint64_t seed);
+
+/* One layer, moe() semantics, in place on host x[T][dim]. */
+int mia_moe_layer(mia_moe *m, int layer, float *x, int T);
+/* As mia_moe_layer with an optional logit bias[E] (added after the router,
+ * before the softmax) and optional outputs idx[T][K], w[T][K] and
+ * logits[T][E]. NULL skips any of them. */
+int mia_moe_layer_ex(mia_moe *m, int layer, float *x, int T, const float *bias, int *idx,
+                     float *w, float *logits);
+/* Layers [l0, l1) of RMSNorm -> MoE -> residual, in place on host x[T][dim]. */
+int mia_moe_stack(mia_moe *m, int l0, int l1, float *x, int T);
+
+/* Device-pointer forms: d_x[T][dim] (and d_bias[E]) live in HBM; the work is
+ * queued on the handle's stream and returns before it completes. */
+int mia_moe_layer_dev(mia_moe *m, int layer, float *d_x, int T, const float *d_bias);
+int mia_moe_stack_dev(mia_moe *m, int l0, int l1, float *d_x, int T);
+
+/* The handle's device context (memory, copies, stream marks of mia_hip.h)
+ * and the scratch of the last call (routing, dispatch, intermediates). */
+mhip_ctx *mia_moe_gpu(mia_moe *m);
+const mhip_scratch *mia_moe_scratch(const mia_moe *m);
+/* Flags forwarded to mhip_moe_layer (e.g. MHIP_FORCE_SEQ_RMS). */
+void mia_moe_set_flags(mia_moe *m, int flags);
+/* Device diagnostics: status[0] bit 0 = an expert index out of range;
+ * status[1] = tokens whose rmsnorm sum took the sequential path. Waits for
+ * the stream. */
+int mia_moe_status(mia_moe *m, int status[4]);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,138 @@
+#ifndef MIA_HIP_H
+#define MIA_HIP_H
+/*
+ * Thin C ABI over the gfx950 HIP kernels of the Q8_0 MoE FFN path.
+ *
+ * Plain pointers and sizes only. Every pointer named d_* is device memory
+ * (HBM) obtained from mhip_malloc; every launch is asynchronous on the
+ * context's stream. Functions return 0 on success or -1 with a message in
+ * mhip_error(). Not thread-safe: one host thread per context, as the
+ * reference engine is (include/mia/model.h:7 of the reference).
+ *
+ * The C host library (include/mia/moe.h, quant.h, matmul.h) is built on this
+ * layer; tests and benchmarks may also call it directly.
+ */
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mhip_ctx mhip_ctx;
+
+/* Shape of one MoE layer (Qwen3-30B-A3B: 2048, 128, 8, 768). */
+typedef struct {
+    int dim;           /* d, multiple of 32, <= 8192 */
+    int n_experts;     /* E, <= 256 */
+    int n_active;      /* K, <= 64 and <= E */
+    int expert_hidden; /* eh, multiple of 32, <= 8192 */
+    int norm_topk;     /* 1: renormalise the K gate weights to sum to 1 */
+    float norm_eps;    /* rmsnorm epsilon */
+} mhip_dims;
+
+/*
+ * HBM layout of one expert in the resident table (bytes; each section is
+ * 256-byte aligned). Codes are row-major int8, scales row-major fp32 with one
+ * scale per 32-value block; values and bytes-per-weight are those of the
+ * reference's 36-byte Q8_0 blocks, only regrouped (codes apart from scales)
+ * so that rows load as aligned 16-byte vectors.
+ */
+typedef struct {
+    size_t gate_q, up_q, down_q; /* [eh][d], [eh][d], [d][eh] int8 */
+    size_t gate_s, up_s, down_s; /* [eh][d/32], [eh][d/32], [d][eh/32] fp32 */
+    size_t expert_bytes;         /* stride between experts */
+} mhip_layout;
+
+int mhip_layout_of(const mhip_dims *s, mhip_layout *out);
+
+/* ---- context, memory, stream ---------------------------------------- */
+int mhip_device_count(void);
+int mhip_open(mhip_ctx **out, int device, char *err, size_t errlen);
+void mhip_close(mhip_ctx *c);
+const char *mhip_error(const mhip_ctx *c);
+void *mhip_malloc(mhip_ctx *c, size_t bytes);
+int mhip_free(mhip_ctx *c, void *d_ptr);
+int mhip_h2d(mhip_ctx *c, void *d_dst, const void *src, size_t bytes);
+int mhip_d2h(mhip_ctx *c, void *dst, const void *d_src, size_t bytes);
+int mhip_d2d(mhip_ctx *c, void *d_dst, const void *d_src, size_t bytes);
+int mhip_zero(mhip_ctx *c, void *d_ptr, size_t bytes); /* fill kernel, not memset */
+int mhip_sync(mhip_ctx *c);
+/* Milliseconds between two points of the context's stream (HIP events). */
+int mhip_mark(mhip_ctx *c, int slot); /* slot 0..15 */
+int mhip_elapsed(mhip_ctx *c, int slot0, int slot1, float *ms);
+
+/* ---- expert table ----------------------------------------------------- */
+/* Repack n reference-format blobs (d_blobs, blob_bytes apart; gate at 0, up
+ * at off_up, down at off_down) into table slots (layer, experts[i]). */
+int mhip_table_repack(mhip_ctx *c, const mhip_dims *s, void *d_table,
+                      int layer, const int *experts, int n,
+                      const void *d_blobs, size_t blob_bytes, size_t off_up,
+                      size_t off_down);
+/* Inverse: table slot -> reference-format blob (zero padded). */
+int mhip_table_unpack(mhip_ctx *c, const mhip_dims *s, const void *d_table,
+                      int layer, int expert, void *d_blob, size_t blob_bytes,
+                      size_t off_up, size_t off_down);
+/* Seeded synthetic experts for layers [l0, l1) generated in HBM, bit-equal
+ * to include/mia/synth.h quantized on the host. */
+int mhip_table_synth(mhip_ctx *c, const mhip_dims *s, void *d_table,
+                     uint64_t seed, int l0, int l1);
+/* Router of layer l, transposed: d_router_t[i*E + e] = W[e][i]. */
+int mhip_router_synth(mhip_ctx *c, const mhip_dims *s, float *d_router_t,
+                      uint64_t seed, int layer);
+int mhip_router_transpose(mhip_ctx *c, const mhip_dims *s, float *d_router_t,
+                          const float *d_router);
+int mhip_synth_f32(mhip_ctx *c, float *d_out, size_t n, uint64_t seed,
+                   uint64_t stream, double sigma);
+int mhip_fill_f32(mhip_ctx *c, float *d_out, size_t n, float value);
+
+/* ---- the MoE layer, one kernel per stage ------------------------------ */
+/* Scratch for one layer call over up to max_tokens tokens. */
+typedef struct {
+    float *xn;        /* [T][d]   rmsnorm output */
+    int8_t *xq;       /* [T][d]   Q8 codes of xn */
+    float *xs;        /* [T][d/32] Q8 scales of xn */
+    float *logits;    /* [T][E]   router logits (after bias) */
+    int *idx;         /* [T][K]   selected experts, descending probability */
+    float *w;         /* [T][K]   gate weights */
+    int *counts;      /* [E] */
+    int *offsets;     /* [E+1] */
+    int *perm;        /* [T*K]   assignment t*K+j in expert-bucketed order */
+    int *pos;         /* [T*K]   inverse of perm */
+    int *groups;      /* [1 + 3*E]: n_groups, then (expert, begin, end) */
+    float *h;         /* [T*K][eh] SwiGLU output, bucketed order */
+    float *tmp;       /* [T*K][d]  down output, bucketed order */
+    int *status;      /* [4] device-side error/diagnostic words */
+} mhip_scratch;
+
+size_t mhip_scratch_bytes(const mhip_dims *s, int max_tokens);
+int mhip_scratch_carve(const mhip_dims *s, int max_tokens, void *d_base,
+                       mhip_scratch *out);
+
+/* Flags for mhip_moe_layer. */
+#define MHIP_FORCE_SEQ_RMS 1 /* always take the sequential rmsnorm sum */
+
+/*
+ * One MoE layer (rmsnorm -> router/top-K -> dispatch -> gate/up+SwiGLU ->
+ * down -> combine) in place on d_x[T][d]. d_table/d_router_t/d_norm point to
+ * this layer's experts, transposed router and ffn_norm. d_bias (E floats) is
+ * added to the logits when non-NULL.
+ */
+int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
+                   const void *d_table_layer, const float *d_router_t,
+                   const float *d_norm, const float *d_bias, float *d_x, int T,
+                   const mhip_scratch *sc, int flags);
+
+/* ---- reference tensor ops on device pointers ---------------------------- */
+/* Q8_0 blocks in the reference's 36-byte format. */
+int mhip_quantize_q8(mhip_ctx *c, const float *d_x, void *d_blocks, int n);
+int mhip_dequantize_q8(mhip_ctx *c, const void *d_blocks, float *d_x, int n);
+/* out = W x (wtype 0: fp32 rows; 1: Q8_0 rows of 36-byte blocks, x is
+ * quantized into d_xq first). Bit-equal to the reference's scalar kernels. */
+int mhip_matvec(mhip_ctx *c, float *d_out, const void *d_w, int wtype,
+                const float *d_x, void *d_xq, int rows, int cols);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

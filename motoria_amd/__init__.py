@@ -1,0 +1,337 @@
+"""motoria_amd: MI355X-native Qwen3-30B-A3B Q8_0 MoE FFN path.
+
+The product is the C-ABI library motoria_amd/libmotoria.so (gfx950 HIP
+kernels + the C99 host library keeping motorIa's engine API). This module
+binds it with ctypes for tests and benchmarks. There is no Python or CPU
+implementation of the path: importing works without a GPU, but every call
+that computes goes to the library and fails loudly when it or the GPU is
+missing.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmotoria.so")
+_LIB = None
+
+_i = ctypes.c_int
+_f = ctypes.c_float
+_p = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_u64 = ctypes.c_uint64
+
+MHIP_FORCE_SEQ_RMS = 1
+
+
+class MoeConfig(ctypes.Structure):
+    _fields_ = [("dim", _i), ("n_layers", _i), ("n_experts", _i), ("n_active", _i),
+                ("expert_hidden", _i), ("norm_topk", _i), ("norm_eps", _f),
+                ("max_tokens", _i), ("device", _i)]
+
+
+class Dims(ctypes.Structure):
+    _fields_ = [("dim", _i), ("n_experts", _i), ("n_active", _i), ("expert_hidden", _i),
+                ("norm_topk", _i), ("norm_eps", _f)]
+
+
+class Layout(ctypes.Structure):
+    _fields_ = [("gate_q", _sz), ("up_q", _sz), ("down_q", _sz), ("gate_s", _sz),
+                ("up_s", _sz), ("down_s", _sz), ("expert_bytes", _sz)]
+
+
+class Scratch(ctypes.Structure):
+    _fields_ = [(n, _p) for n in ("xn", "xq", "xs", "logits", "idx", "w", "counts", "offsets",
+                                  "perm", "pos", "groups", "h", "tmp", "status")]
+
+
+# Every function the library exports, with its ctypes signature. tests check
+# this list against the declarations in include/.
+SIGNATURES = {
+    # include/mia_hip.h
+    "mhip_layout_of": (_i, [ctypes.POINTER(Dims), ctypes.POINTER(Layout)]),
+    "mhip_device_count": (_i, []),
+    "mhip_open": (_i, [ctypes.POINTER(_p), _i, ctypes.c_char_p, _sz]),
+    "mhip_close": (None, [_p]),
+    "mhip_error": (ctypes.c_char_p, [_p]),
+    "mhip_malloc": (_p, [_p, _sz]),
+    "mhip_free": (_i, [_p, _p]),
+    "mhip_h2d": (_i, [_p, _p, _p, _sz]),
+    "mhip_d2h": (_i, [_p, _p, _p, _sz]),
+    "mhip_d2d": (_i, [_p, _p, _p, _sz]),
+    "mhip_zero": (_i, [_p, _p, _sz]),
+    "mhip_sync": (_i, [_p]),
+    "mhip_mark": (_i, [_p, _i]),
+    "mhip_elapsed": (_i, [_p, _i, _i, ctypes.POINTER(_f)]),
+    "mhip_table_repack": (_i, [_p, ctypes.POINTER(Dims), _p, _i, ctypes.POINTER(_i), _i, _p,
+                               _sz, _sz, _sz]),
+    "mhip_table_unpack": (_i, [_p, ctypes.POINTER(Dims), _p, _i, _i, _p, _sz, _sz, _sz]),
+    "mhip_table_synth": (_i, [_p, ctypes.POINTER(Dims), _p, _u64, _i, _i]),
+    "mhip_router_synth": (_i, [_p, ctypes.POINTER(Dims), _p, _u64, _i]),
+    "mhip_router_transpose": (_i, [_p, ctypes.POINTER(Dims), _p, _p]),
+    "mhip_synth_f32": (_i, [_p, _p, _sz, _u64, _u64, ctypes.c_double]),
+    "mhip_fill_f32": (_i, [_p, _p, _sz, _f]),
+    "mhip_scratch_bytes": (_sz, [ctypes.POINTER(Dims), _i]),
+    "mhip_scratch_carve": (_i, [ctypes.POINTER(Dims), _i, _p, ctypes.POINTER(Scratch)]),
+    "mhip_moe_layer": (_i, [_p, ctypes.POINTER(Dims), ctypes.POINTER(Layout), _p, _p, _p, _p,
+                            _p, _i, ctypes.POINTER(Scratch), _i]),
+    "mhip_quantize_q8": (_i, [_p, _p, _p, _i]),
+    "mhip_dequantize_q8": (_i, [_p, _p, _p, _i]),
+    "mhip_matvec": (_i, [_p, _p, _p, _i, _p, _p, _i, _i]),
+    # include/mia/quant.h, include/mia/matmul.h
+    "mia_row_bytes": (_sz, [_i, _i]),
+    "mia_quantize_row_q8": (None, [_p, _p, _i]),
+    "mia_dequantize_row": (None, [_i, _p, _p, _i]),
+    "mia_matvec": (None, [_p, _p, _i, _p, _p, _i, _i]),
+    "mia_matvec_scalar": (None, [_p, _p, _i, _p, _p, _i, _i]),
+    # include/mia/moe.h
+    "mia_moe_open": (_i, [ctypes.POINTER(_p), ctypes.POINTER(MoeConfig), ctypes.c_char_p, _sz]),
+    "mia_moe_close": (None, [_p]),
+    "mia_moe_error": (ctypes.c_char_p, [_p]),
+    "mia_moe_blob_bytes": (_sz, [_p]),
+    "mia_moe_off_up": (_sz, [_p]),
+    "mia_moe_off_down": (_sz, [_p]),
+    "mia_moe_load_experts": (_i, [_p, _p, _p]),
+    "mia_moe_load_expert": (_i, [_p, _i, _i, _p]),
+    "mia_moe_read_expert": (_i, [_p, _i, _i, _p]),
+    "mia_moe_set_layer": (_i, [_p, _i, _p, _p]),
+    "mia_moe_synth": (_i, [_p, _u64]),
+    "mia_moe_layer": (_i, [_p, _i, _p, _i]),
+    "mia_moe_layer_ex": (_i, [_p, _i, _p, _i, _p, _p, _p, _p]),
+    "mia_moe_stack": (_i, [_p, _i, _i, _p, _i]),
+    "mia_moe_layer_dev": (_i, [_p, _i, _p, _i, _p]),
+    "mia_moe_stack_dev": (_i, [_p, _i, _i, _p, _i]),
+    "mia_moe_gpu": (_p, [_p]),
+    "mia_moe_scratch": (ctypes.POINTER(Scratch), [_p]),
+    "mia_moe_set_flags": (None, [_p, _i]),
+    "mia_moe_status": (_i, [_p, ctypes.POINTER(_i)]),
+}
+
+# The storage port type (include/mia/expert_cache.h).
+LOADER = ctypes.CFUNCTYPE(_i, _p, _i, _i, _p)
+
+
+def lib():
+    """Load libmotoria.so (raises if it is not built)."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError("motoria_amd/libmotoria.so is not built; run "
+                               "`python -c 'import __graft_entry__ as g; g.build()'`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def device_count():
+    return lib().mhip_device_count()
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+QWEN3_30B_A3B = dict(dim=2048, n_experts=128, n_active=8, expert_hidden=768, norm_topk=1,
+                     norm_eps=1e-6)
+
+
+class Moe:
+    """A mia_moe handle: resident expert table + scratch on one GPU."""
+
+    def __init__(self, n_layers, max_tokens, device=0, **shape):
+        shape = dict(QWEN3_30B_A3B, **shape)
+        self.shape = shape
+        self.n_layers = n_layers
+        self.max_tokens = max_tokens
+        cfg = MoeConfig(dim=shape["dim"], n_layers=n_layers, n_experts=shape["n_experts"],
+                        n_active=shape["n_active"], expert_hidden=shape["expert_hidden"],
+                        norm_topk=shape["norm_topk"], norm_eps=shape["norm_eps"],
+                        max_tokens=max_tokens, device=device)
+        h = _p()
+        err = ctypes.create_string_buffer(512)
+        if lib().mia_moe_open(ctypes.byref(h), ctypes.byref(cfg), err, 512) != 0:
+            raise RuntimeError("mia_moe_open: " + err.value.decode())
+        self.h = h
+        self.gpu = lib().mia_moe_gpu(h)
+        self.dims = Dims(shape["dim"], shape["n_experts"], shape["n_active"],
+                         shape["expert_hidden"], shape["norm_topk"], shape["norm_eps"])
+
+    def close(self):
+        if self.h:
+            lib().mia_moe_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc, what):
+        if rc != 0:
+            raise RuntimeError("%s: %s" % (what, lib().mia_moe_error(self.h).decode()))
+
+    # -- geometry / weights
+    @property
+    def blob_bytes(self):
+        return lib().mia_moe_blob_bytes(self.h)
+
+    @property
+    def off_up(self):
+        return lib().mia_moe_off_up(self.h)
+
+    @property
+    def off_down(self):
+        return lib().mia_moe_off_down(self.h)
+
+    def synth(self, seed):
+        self._check(lib().mia_moe_synth(self.h, seed), "mia_moe_synth")
+
+    def load_expert(self, layer, expert, blob):
+        blob = np.ascontiguousarray(blob, dtype=np.uint8)
+        self._check(lib().mia_moe_load_expert(self.h, layer, expert, _ptr(blob)),
+                    "mia_moe_load_expert")
+
+    def load_experts(self, loader_fn):
+        """loader_fn(layer, expert, dst_ptr) -> int, the storage port."""
+        cb = LOADER(lambda ctx, l, e, dst: loader_fn(l, e, dst))
+        self._check(lib().mia_moe_load_experts(self.h, cb, None), "mia_moe_load_experts")
+
+    def read_expert(self, layer, expert):
+        out = np.zeros(self.blob_bytes, dtype=np.uint8)
+        self._check(lib().mia_moe_read_expert(self.h, layer, expert, _ptr(out)),
+                    "mia_moe_read_expert")
+        return out
+
+    def set_layer(self, layer, ffn_norm, router):
+        ffn_norm = np.ascontiguousarray(ffn_norm, dtype=np.float32)
+        router = np.ascontiguousarray(router, dtype=np.float32)
+        self._check(lib().mia_moe_set_layer(self.h, layer, _ptr(ffn_norm), _ptr(router)),
+                    "mia_moe_set_layer")
+
+    def set_flags(self, flags):
+        lib().mia_moe_set_flags(self.h, flags)
+
+    def status(self):
+        st = (_i * 4)()
+        self._check(lib().mia_moe_status(self.h, st), "mia_moe_status")
+        return list(st)
+
+    # -- compute (host pointers)
+    def layer(self, layer, x, bias=None):
+        """Returns (x_out, idx, w, logits) for x[T][dim]."""
+        x = np.array(x, dtype=np.float32, order="C", ndmin=2)
+        T = x.shape[0]
+        K, E = self.shape["n_active"], self.shape["n_experts"]
+        idx = np.zeros((T, K), dtype=np.int32)
+        w = np.zeros((T, K), dtype=np.float32)
+        logits = np.zeros((T, E), dtype=np.float32)
+        bias = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        self._check(lib().mia_moe_layer_ex(self.h, layer, _ptr(x), T, _ptr(bias), _ptr(idx),
+                                           _ptr(w), _ptr(logits)), "mia_moe_layer_ex")
+        return x, idx, w, logits
+
+    def stack(self, l0, l1, x):
+        x = np.array(x, dtype=np.float32, order="C", ndmin=2)
+        self._check(lib().mia_moe_stack(self.h, l0, l1, _ptr(x), x.shape[0]), "mia_moe_stack")
+        return x
+
+    # -- compute (device pointers)
+    def layer_dev(self, layer, d_x, T, d_bias=None):
+        self._check(lib().mia_moe_layer_dev(self.h, layer, d_x, T, d_bias), "mia_moe_layer_dev")
+
+    def stack_dev(self, l0, l1, d_x, T):
+        self._check(lib().mia_moe_stack_dev(self.h, l0, l1, d_x, T), "mia_moe_stack_dev")
+
+    def scratch(self):
+        return lib().mia_moe_scratch(self.h).contents
+
+    # -- device memory through the handle's context
+    def malloc(self, nbytes):
+        p = lib().mhip_malloc(self.gpu, nbytes)
+        if not p:
+            raise RuntimeError("mhip_malloc: " + lib().mhip_error(self.gpu).decode())
+        return p
+
+    def free(self, p):
+        lib().mhip_free(self.gpu, p)
+
+    def h2d(self, d_dst, arr):
+        arr = np.ascontiguousarray(arr)
+        if lib().mhip_h2d(self.gpu, d_dst, _ptr(arr), arr.nbytes) != 0:
+            raise RuntimeError("mhip_h2d: " + lib().mhip_error(self.gpu).decode())
+
+    def d2h(self, d_src, shape, dtype):
+        out = np.zeros(shape, dtype=dtype)
+        if lib().mhip_d2h(self.gpu, _ptr(out), d_src, out.nbytes) != 0:
+            raise RuntimeError("mhip_d2h: " + lib().mhip_error(self.gpu).decode())
+        return out
+
+    def sync(self):
+        if lib().mhip_sync(self.gpu) != 0:
+            raise RuntimeError("mhip_sync: " + lib().mhip_error(self.gpu).decode())
+
+    def mark(self, slot):
+        if lib().mhip_mark(self.gpu, slot) != 0:
+            raise RuntimeError("mhip_mark: " + lib().mhip_error(self.gpu).decode())
+
+    def elapsed_ms(self, s0, s1):
+        ms = _f()
+        if lib().mhip_elapsed(self.gpu, s0, s1, ctypes.byref(ms)) != 0:
+            raise RuntimeError("mhip_elapsed: " + lib().mhip_error(self.gpu).decode())
+        return ms.value
+
+    def synth_f32(self, d_out, n, seed, stream, sigma):
+        if lib().mhip_synth_f32(self.gpu, d_out, n, seed, stream, sigma) != 0:
+            raise RuntimeError("mhip_synth_f32: " + lib().mhip_error(self.gpu).decode())
+
+
+class Gpu:
+    """A bare mhip context (for the tensor-op kernels on device pointers)."""
+
+    def __init__(self, device=0):
+        h = _p()
+        err = ctypes.create_string_buffer(512)
+        if lib().mhip_open(ctypes.byref(h), device, err, 512) != 0:
+            raise RuntimeError("mhip_open: " + err.value.decode())
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().mhip_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def check(self, rc, what):
+        if rc != 0:
+            raise RuntimeError("%s: %s" % (what, lib().mhip_error(self.h).decode()))
+
+    def malloc(self, nbytes):
+        p = lib().mhip_malloc(self.h, nbytes)
+        if not p:
+            raise RuntimeError("mhip_malloc: " + lib().mhip_error(self.h).decode())
+        return p
+
+    def free(self, p):
+        lib().mhip_free(self.h, p)
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        p = self.malloc(max(arr.nbytes, 1))
+        self.check(lib().mhip_h2d(self.h, p, _ptr(arr), arr.nbytes), "h2d")
+        return p
+
+    def download(self, p, shape, dtype):
+        out = np.zeros(shape, dtype=dtype)
+        self.check(lib().mhip_d2h(self.h, _ptr(out), p, out.nbytes), "d2h")
+        return out

@@ -1,0 +1,67 @@
+// Internal declarations shared by the HIP translation units of libmotoria.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+
+#include "mia_hip.h"
+
+struct mhip_ctx {
+    int device;
+    hipStream_t stream;
+    hipEvent_t marks[16];
+    char err[512];
+};
+
+namespace mhip {
+
+constexpr int QK = 32;
+
+int fail(mhip_ctx *c, const char *fmt, ...);
+// Checks a HIP status (and the launch status when `launch` is set).
+int check(mhip_ctx *c, hipError_t e, const char *what);
+int check_launch(mhip_ctx *c, const char *what);
+int use_device(mhip_ctx *c);
+
+// Validates shapes every kernel of the path assumes; returns 0 or fail().
+int check_dims(mhip_ctx *c, const mhip_dims *s);
+
+inline unsigned blocks_for(size_t n, unsigned per) {
+    return (unsigned)((n + per - 1) / per);
+}
+
+}  // namespace mhip
+
+// ---- device helpers --------------------------------------------------------
+
+#include "expf_glibc.h"
+
+namespace mhip_dev {
+
+__device__ __forceinline__ float expf_glibc(float x) { return mia_expf_glibc(x); }
+
+
+// Exact int32 dot of two 32-value int8 blocks held as 2 x int4.
+__device__ __forceinline__ int dot32_i8(const int4 a0, const int4 a1, const int4 b0,
+                                        const int4 b1) {
+    int acc = 0;
+    acc = __builtin_amdgcn_sdot4(a0.x, b0.x, acc, false);
+    acc = __builtin_amdgcn_sdot4(a0.y, b0.y, acc, false);
+    acc = __builtin_amdgcn_sdot4(a0.z, b0.z, acc, false);
+    acc = __builtin_amdgcn_sdot4(a0.w, b0.w, acc, false);
+    acc = __builtin_amdgcn_sdot4(a1.x, b1.x, acc, false);
+    acc = __builtin_amdgcn_sdot4(a1.y, b1.y, acc, false);
+    acc = __builtin_amdgcn_sdot4(a1.z, b1.z, acc, false);
+    acc = __builtin_amdgcn_sdot4(a1.w, b1.w, acc, false);
+    return acc;
+}
+
+// The reference's per-block term ((float)acc * d_w) * d_x, two roundings.
+__device__ __forceinline__ float block_term(int acc, float dw, float dx) {
+    return ((float)acc * dw) * dx;
+}
+
+}  // namespace mhip_dev

@@ -1,0 +1,576 @@
+// One Qwen3-MoE FFN layer over T tokens on the resident expert table:
+//
+//   k_rmsnorm_q8   rmsnorm + Q8_0 quantization of xn      forward.c:174, quant.c:11-27
+//   k_router       logits, softmax, top-K, gate weights  forward.c:175-181
+//   k_dispatch     stable bucketing of the T*K assignments by expert
+//   k_gateup       gate/up Q8 products + SwiGLU          forward.c:186-191
+//   k_down         Q8(h) + down Q8 product               forward.c:192-193
+//   k_combine      x += w_j * tmp_j, j in top-K order    forward.c:194
+//
+// Every fp32 value is produced in the reference's operation order, so the
+// results are bit-equal to the reference C path (src/model/forward.c:167-197
+// on x86): block dots are exact int32, the per-row sums over 32-value blocks
+// run in block order, and sums the reference takes in double are either
+// reproduced exactly or certified (see k_rmsnorm_q8).
+#include "mhip_internal.h"
+
+namespace {
+
+constexpr int QK = mhip::QK;
+constexpr int NT = 256;  // threads per workgroup of the GEMV stages
+constexpr int TB = 4;    // tokens per pass of the GEMV stages
+
+__host__ __device__ inline size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+// ---- rmsnorm + Q8 -------------------------------------------------------
+//
+// The reference sums x^2 in double, sequentially (forward.c:77-78), then
+// inv = (float)(1/sqrt(ss/n + eps)). Each x^2 is exact in double; only the
+// order of the additions is at stake. A tree sum S differs from the
+// sequential one by at most (n + log2 n) * 2^-53 * S (all terms are >= 0),
+// so with S -/+ m, m = (n + 64) * 2^-52 * S, the two inv candidates bracket
+// the reference's inv (every IEEE step is monotone). When they agree they are
+// the reference's value; otherwise (probability ~1e-5 per token) one thread
+// redoes the sequential sum. status[1] counts those fallbacks.
+__global__ __launch_bounds__(NT) void k_rmsnorm_q8(const float *__restrict__ x,
+                                                   const float *__restrict__ w,
+                                                   float *__restrict__ xn,
+                                                   int8_t *__restrict__ xq,
+                                                   float *__restrict__ xs, int d, float eps,
+                                                   int force_seq, int *status) {
+    __shared__ double part[NT / 64];
+    __shared__ float inv_sh;
+    const int t = blockIdx.x;
+    const float *xt = x + (size_t)t * d;
+    double s = 0.0;
+    for (int i = threadIdx.x; i < d; i += NT) {
+        const double v = (double)xt[i];
+        s = s + v * v;
+    }
+    for (int o = 32; o > 0; o >>= 1) s = s + __shfl_xor(s, o);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double S = part[0];
+        for (int i = 1; i < NT / 64; i++) S = S + part[i];
+        const double m = S * ((double)(d + 64) * 0x1p-52);
+        const float lo = (float)(1.0 / sqrt((S + m) / d + (double)eps));
+        const float hi = (float)(1.0 / sqrt((S - m) / d + (double)eps));
+        float inv = lo;
+        if (force_seq || lo != hi) {
+            double ss = 0.0;
+            for (int i = 0; i < d; i++) ss = ss + (double)xt[i] * (double)xt[i];
+            inv = (float)(1.0 / sqrt(ss / d + (double)eps));
+            atomicAdd(&status[1], 1);
+        }
+        inv_sh = inv;
+    }
+    __syncthreads();
+    const float inv = inv_sh;
+    const int nb = d / QK;
+    // 32 consecutive threads own one block; d is a multiple of 32, so a
+    // block is either wholly inside [0, d) or wholly outside.
+    for (int i0 = 0; i0 < d; i0 += NT) {
+        const int i = i0 + threadIdx.x;
+        const bool in = i < d;
+        const float v = in ? (xt[i] * inv) * w[i] : 0.0f;
+        float a = fabsf(v);
+        for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o));
+        const float dsc = a / 127.0f;
+        const float qi = dsc != 0.0f ? 1.0f / dsc : 0.0f;
+        if (in) {
+            xn[(size_t)t * d + i] = v;
+            xq[(size_t)t * d + i] = (int8_t)roundf(v * qi);
+            if ((i & 31) == 0) xs[(size_t)t * nb + i / QK] = dsc;
+        }
+    }
+}
+
+// ---- router ---------------------------------------------------------------
+//
+// Thread e computes logit e as the reference's sequential fp32 chain
+// (matmul.c:13-17) over xn staged in LDS, reading the transposed router so
+// a wavefront's loads are contiguous. Softmax (forward.c:95-101) uses the
+// restated glibc expf and a sequential sum; top-K (forward.c:104-114) takes
+// the largest untaken probability, lowest index on ties; the gate weights
+// are renormalised as forward.c:178-181.
+__global__ __launch_bounds__(256) void k_router(const float *__restrict__ xn,
+                                                const float *__restrict__ wt,
+                                                const float *__restrict__ bias,
+                                                float *__restrict__ logits,
+                                                int *__restrict__ idx_out,
+                                                float *__restrict__ w_out, int d, int E, int K,
+                                                int norm_topk) {
+    extern __shared__ float sh[];
+    float *xs = sh;       // [d]
+    float *p = sh + d;    // [E]
+    __shared__ float red[4];
+    __shared__ float sum_sh;
+    __shared__ int top[64];
+    const int t = blockIdx.x;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < d; i += blockDim.x) xs[i] = xn[(size_t)t * d + i];
+    __syncthreads();
+
+    float l = -__builtin_inff();
+    if (tid < E) {
+        const float *col = wt + tid;
+        float s = 0.0f;
+        int i = 0;
+        for (; i + 8 <= d; i += 8) {
+            float wv[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) wv[k] = col[(size_t)(i + k) * E];
+#pragma unroll
+            for (int k = 0; k < 8; k++) s = s + wv[k] * xs[i + k];
+        }
+        for (; i < d; i++) s = s + col[(size_t)i * E] * xs[i];
+        if (bias) s = s + bias[tid];
+        l = s;
+        logits[(size_t)t * E + tid] = s;
+    }
+    // max over E (order-free)
+    float mx = l;
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = red[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); i++) mx = fmaxf(mx, red[i]);
+    if (tid < E) p[tid] = mhip_dev::expf_glibc(l - mx);
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+        for (int i = 0; i < E; i++) sum = sum + p[i];
+        sum_sh = sum;
+    }
+    __syncthreads();
+    if (tid < E) p[tid] = p[tid] / sum_sh;
+    __syncthreads();
+
+    if (tid < 64) {
+        // Lane owns entries lane + 64c, c < 4 (E <= 256). Probabilities are
+        // >= +0, so their bit patterns order like the values; the low word
+        // ~index makes the lowest index win a tie.
+        float pv[4];
+        unsigned taken = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int e = tid + 64 * c;
+            pv[c] = e < E ? p[e] : 0.0f;
+        }
+        for (int j = 0; j < K; j++) {
+            unsigned long long best = 0;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int e = tid + 64 * c;
+                if (e < E && !(taken & (1u << c))) {
+                    unsigned long long key =
+                        ((unsigned long long)__float_as_uint(pv[c]) << 32) |
+                        (unsigned long long)(0xFFFFFFFFu - (unsigned)e);
+                    best = key > best ? key : best;
+                }
+            }
+            for (int o = 32; o > 0; o >>= 1) {
+                unsigned long long other = __shfl_xor(best, o);
+                best = other > best ? other : best;
+            }
+            const int win = (int)(0xFFFFFFFFu - (unsigned)(best & 0xFFFFFFFFu));
+            if ((win & 63) == tid) taken |= 1u << (win >> 6);
+            if (tid == 0) top[j] = win;
+        }
+        if (tid == 0) {
+            float sum = 0.0f;
+            for (int j = 0; j < K; j++) sum = sum + p[top[j]];
+            for (int j = 0; j < K; j++) {
+                const float wj = p[top[j]];
+                idx_out[(size_t)t * K + j] = top[j];
+                w_out[(size_t)t * K + j] = norm_topk ? wj / sum : wj;
+            }
+        }
+    }
+}
+
+// ---- dispatch -------------------------------------------------------------
+//
+// Stable counting sort of the A = T*K assignments a = t*K + j by expert
+// idx[a] in one workgroup: per-thread histograms of contiguous chunks, an
+// exclusive scan per expert over the threads, then each thread scatters its
+// chunk in order. Within an expert the order is by t (then j), the order in
+// which the reference visits tokens. Also emits the list of non-empty
+// experts as (expert, begin, end) groups. status[0] |= 1 on a bad index.
+__global__ __launch_bounds__(256) void k_dispatch(const int *__restrict__ idx, int A, int E,
+                                                  int *__restrict__ counts,
+                                                  int *__restrict__ offsets,
+                                                  int *__restrict__ perm,
+                                                  int *__restrict__ pos,
+                                                  int *__restrict__ groups, int *status) {
+    extern __shared__ unsigned char lds[];
+    const int nt = blockDim.x;
+    const int tid = threadIdx.x;
+    unsigned short *hist = (unsigned short *)lds;           // [nt][E]
+    int *off = (int *)(lds + align256((size_t)nt * E * 2));   // [E+1]
+    unsigned char *key = (unsigned char *)(off + E + 1);     // [A]
+    for (int i = tid; i < nt * E; i += nt) hist[i] = 0;
+    int bad = 0;
+    for (int a = tid; a < A; a += nt) {
+        int e = idx[a];
+        if (e < 0 || e >= E) {
+            bad = 1;
+            e = 0;
+        }
+        key[a] = (unsigned char)e;
+    }
+    if (bad) atomicOr(&status[0], 1);
+    __syncthreads();
+    const int chunk = (A + nt - 1) / nt;
+    const int a0 = tid * chunk < A ? tid * chunk : A;
+    const int a1 = a0 + chunk < A ? a0 + chunk : A;
+    for (int a = a0; a < a1; a++) hist[tid * E + key[a]]++;
+    __syncthreads();
+    for (int e = tid; e < E; e += nt) {
+        int run = 0;
+        for (int q = 0; q < nt; q++) {
+            const int cnt = hist[q * E + e];
+            hist[q * E + e] = (unsigned short)run;
+            run += cnt;
+        }
+        off[e] = run;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int acc = 0, g = 0;
+        for (int e = 0; e < E; e++) {
+            const int cnt = off[e];
+            counts[e] = cnt;
+            offsets[e] = acc;
+            off[e] = acc;
+            if (cnt > 0) {
+                groups[1 + 3 * g] = e;
+                groups[2 + 3 * g] = acc;
+                groups[3 + 3 * g] = acc + cnt;
+                g++;
+            }
+            acc += cnt;
+        }
+        off[E] = acc;
+        offsets[E] = acc;
+        groups[0] = g;
+    }
+    __syncthreads();
+    for (int a = a0; a < a1; a++) {
+        const int e = key[a];
+        const int p = off[e] + hist[tid * E + e]++;
+        perm[p] = a;
+        pos[a] = p;
+    }
+}
+
+// ---- gate/up + SwiGLU --------------------------------------------------------
+//
+// Workgroup = (group g of one expert, R consecutive rows of h). Its 2R weight
+// rows (R of gate, R of up) are split into (row, 32-block) pairs, one pair
+// per thread per step, codes held in registers across the expert's tokens.
+// For TB tokens at a time each pair's exact int32 dot is turned into the
+// reference's term ((float)acc*d_w)*d_x and parked in LDS; then one thread
+// per (token, row) adds its row's terms in block order, and SwiGLU
+// g/(1+expf(-g))*u (forward.c:190) produces h, written in bucketed order.
+template <int PK>
+__global__ __launch_bounds__(NT) void k_gateup(const uint8_t *__restrict__ table, mhip_layout lay,
+                                               const int8_t *__restrict__ xq,
+                                               const float *__restrict__ xs,
+                                               const int *__restrict__ groups,
+                                               const int *__restrict__ perm,
+                                               float *__restrict__ h, int d, int eh, int K,
+                                               int R) {
+    extern __shared__ float terms[];  // [TB][2R][nb+1], then gu[TB][2R]
+    const int nb = d / QK;
+    const int nrc = eh / R;
+    const int g = blockIdx.x / nrc;
+    const int rc = blockIdx.x % nrc;
+    if (g >= groups[0]) return;
+    const int e = groups[1 + 3 * g], b0 = groups[2 + 3 * g], b1 = groups[3 + 3 * g];
+    const uint8_t *ex = table + (size_t)e * lay.expert_bytes;
+    const int P = 2 * R * nb;
+    const int ld = nb + 1;
+    float *gu = terms + TB * 2 * R * ld;
+
+    int4 wc0[PK], wc1[PK];
+    float wd[PK];
+    int prow[PK], pblk[PK];
+#pragma unroll
+    for (int k = 0; k < PK; k++) {
+        const int p = threadIdx.x + NT * k;
+        prow[k] = p < P ? p / nb : -1;
+        pblk[k] = p < P ? p % nb : 0;
+        if (p < P) {
+            const int wr = prow[k];
+            const bool is_gate = wr < R;
+            const int row = rc * R + (is_gate ? wr : wr - R);
+            const int4 *src = (const int4 *)(ex + (is_gate ? lay.gate_q : lay.up_q) +
+                                             (size_t)row * d + (size_t)pblk[k] * QK);
+            wc0[k] = src[0];
+            wc1[k] = src[1];
+            wd[k] = ((const float *)(ex + (is_gate ? lay.gate_s : lay.up_s)))[(size_t)row * nb +
+                                                                             pblk[k]];
+        }
+    }
+    for (int base = b0; base < b1; base += TB) {
+        const int ntok = b1 - base < TB ? b1 - base : TB;
+#pragma unroll
+        for (int k = 0; k < PK; k++) {
+            if (prow[k] < 0) continue;
+            for (int tb = 0; tb < ntok; tb++) {
+                const int t = perm[base + tb] / K;
+                const int4 *xv = (const int4 *)(xq + (size_t)t * d + (size_t)pblk[k] * QK);
+                const int acc = mhip_dev::dot32_i8(wc0[k], wc1[k], xv[0], xv[1]);
+                terms[(tb * 2 * R + prow[k]) * ld + pblk[k]] =
+                    mhip_dev::block_term(acc, wd[k], xs[(size_t)t * nb + pblk[k]]);
+            }
+        }
+        __syncthreads();
+        for (int c = threadIdx.x; c < ntok * 2 * R; c += NT) {
+            const float *row = terms + c * ld;
+            float s = 0.0f;
+            for (int b = 0; b < nb; b++) s = s + row[b];
+            gu[c] = s;
+        }
+        __syncthreads();
+        for (int c = threadIdx.x; c < ntok * R; c += NT) {
+            const int tb = c / R, r = c % R;
+            const float gv = gu[tb * 2 * R + r];
+            const float uv = gu[tb * 2 * R + R + r];
+            h[(size_t)(base + tb) * eh + rc * R + r] =
+                (gv / (1.0f + mhip_dev::expf_glibc(-gv))) * uv;
+        }
+        __syncthreads();
+    }
+}
+
+// ---- down ----------------------------------------------------------------------
+//
+// Workgroup = (group g, R rows of down). For TB tokens at a time, h is
+// quantized (one thread per 32-block, quant.c:11-27) into LDS, the
+// (row, block) pairs produce the reference's terms, and one thread per
+// (token, row) sums them in block order into tmp (bucketed order).
+template <int PK>
+__global__ __launch_bounds__(NT) void k_down(const uint8_t *__restrict__ table, mhip_layout lay,
+                                             const float *__restrict__ h,
+                                             const int *__restrict__ groups,
+                                             float *__restrict__ tmp, int d, int eh, int R) {
+    extern __shared__ float terms[];  // [TB][R][nbh+1], hs[TB][nbh], hq[TB][eh] bytes
+    const int nbh = eh / QK;
+    const int nrc = d / R;
+    const int g = blockIdx.x / nrc;
+    const int rc = blockIdx.x % nrc;
+    if (g >= groups[0]) return;
+    const int e = groups[1 + 3 * g], b0 = groups[2 + 3 * g], b1 = groups[3 + 3 * g];
+    const uint8_t *ex = table + (size_t)e * lay.expert_bytes;
+    const int P = R * nbh;
+    const int ld = nbh + 1;
+    float *hs = terms + TB * R * ld;
+    int8_t *hq = (int8_t *)(hs + TB * nbh);
+
+    int4 wc0[PK], wc1[PK];
+    float wd[PK];
+    int prow[PK], pblk[PK];
+#pragma unroll
+    for (int k = 0; k < PK; k++) {
+        const int p = threadIdx.x + NT * k;
+        prow[k] = p < P ? p / nbh : -1;
+        pblk[k] = p < P ? p % nbh : 0;
+        if (p < P) {
+            const int row = rc * R + prow[k];
+            const int4 *src =
+                (const int4 *)(ex + lay.down_q + (size_t)row * eh + (size_t)pblk[k] * QK);
+            wc0[k] = src[0];
+            wc1[k] = src[1];
+            wd[k] = ((const float *)(ex + lay.down_s))[(size_t)row * nbh + pblk[k]];
+        }
+    }
+    for (int base = b0; base < b1; base += TB) {
+        const int ntok = b1 - base < TB ? b1 - base : TB;
+        for (int c = threadIdx.x; c < ntok * nbh; c += NT) {
+            const int tb = c / nbh, blk = c % nbh;
+            const float *v = h + (size_t)(base + tb) * eh + (size_t)blk * QK;
+            float vals[QK];
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < QK; i += 4) {
+                const float4 f = *(const float4 *)(v + i);
+                vals[i] = f.x;
+                vals[i + 1] = f.y;
+                vals[i + 2] = f.z;
+                vals[i + 3] = f.w;
+            }
+#pragma unroll
+            for (int i = 0; i < QK; i++) {
+                const float a = fabsf(vals[i]);
+                amax = a > amax ? a : amax;
+            }
+            const float dsc = amax / 127.0f;
+            const float qi = dsc != 0.0f ? 1.0f / dsc : 0.0f;
+            int8_t *dst = hq + (size_t)tb * eh + (size_t)blk * QK;
+#pragma unroll
+            for (int i = 0; i < QK; i++) dst[i] = (int8_t)roundf(vals[i] * qi);
+            hs[tb * nbh + blk] = dsc;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < PK; k++) {
+            if (prow[k] < 0) continue;
+            for (int tb = 0; tb < ntok; tb++) {
+                const int4 *xv = (const int4 *)(hq + (size_t)tb * eh + (size_t)pblk[k] * QK);
+                const int acc = mhip_dev::dot32_i8(wc0[k], wc1[k], xv[0], xv[1]);
+                terms[(tb * R + prow[k]) * ld + pblk[k]] =
+                    mhip_dev::block_term(acc, wd[k], hs[tb * nbh + pblk[k]]);
+            }
+        }
+        __syncthreads();
+        for (int c = threadIdx.x; c < ntok * R; c += NT) {
+            const int tb = c / R, r = c % R;
+            const float *row = terms + c * ld;
+            float s = 0.0f;
+            for (int b = 0; b < nbh; b++) s = s + row[b];
+            tmp[(size_t)(base + tb) * d + rc * R + r] = s;
+        }
+        __syncthreads();
+    }
+}
+
+// ---- combine -------------------------------------------------------------------
+// x_i = x_i + w_j * tmp_j,i for j = 0..K-1 in top-K order (forward.c:194).
+__global__ __launch_bounds__(256) void k_combine(float *__restrict__ x,
+                                                 const float *__restrict__ w,
+                                                 const int *__restrict__ pos,
+                                                 const float *__restrict__ tmp, int d, int K) {
+    const int t = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= d) return;
+    float v = x[(size_t)t * d + i];
+    for (int j = 0; j < K; j++) {
+        const int a = t * K + j;
+        v = v + w[a] * tmp[(size_t)pos[a] * d + i];
+    }
+    x[(size_t)t * d + i] = v;
+}
+
+// Rows per workgroup: the largest power of two <= 32 with 2R*nb <= PK*NT
+// pairs (gate/up), R*nbh <= PK*NT (down).
+constexpr int PK = 4;
+
+int rows_gateup(int nb) {
+    int r = 32;
+    while (r > 1 && 2 * r * nb > PK * NT) r >>= 1;
+    return r;
+}
+
+int rows_down(int nbh) {
+    int r = 32;
+    while (r > 1 && r * nbh > PK * NT) r >>= 1;
+    return r;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mhip_scratch_bytes(const mhip_dims *s, int T) {
+    const size_t d = s->dim, E = s->n_experts, K = s->n_active, eh = s->expert_hidden;
+    const size_t A = (size_t)T * K;
+    size_t n = 0;
+    n += align256(T * d * 4);          // xn
+    n += align256(T * d);              // xq
+    n += align256(T * (d / QK) * 4);   // xs
+    n += align256(T * E * 4);          // logits
+    n += align256(A * 4);              // idx
+    n += align256(A * 4);              // w
+    n += align256(E * 4);              // counts
+    n += align256((E + 1) * 4);        // offsets
+    n += align256(A * 4);              // perm
+    n += align256(A * 4);              // pos
+    n += align256((1 + 3 * E) * 4);    // groups
+    n += align256(A * eh * 4);         // h
+    n += align256(A * d * 4);          // tmp
+    n += align256(4 * 4);              // status
+    return n;
+}
+
+int mhip_scratch_carve(const mhip_dims *s, int T, void *d_base, mhip_scratch *o) {
+    const size_t d = s->dim, E = s->n_experts, K = s->n_active, eh = s->expert_hidden;
+    const size_t A = (size_t)T * K;
+    uint8_t *p = (uint8_t *)d_base;
+    auto take = [&](size_t bytes) {
+        void *r = p;
+        p += align256(bytes);
+        return r;
+    };
+    o->xn = (float *)take(T * d * 4);
+    o->xq = (int8_t *)take(T * d);
+    o->xs = (float *)take(T * (d / QK) * 4);
+    o->logits = (float *)take(T * E * 4);
+    o->idx = (int *)take(A * 4);
+    o->w = (float *)take(A * 4);
+    o->counts = (int *)take(E * 4);
+    o->offsets = (int *)take((E + 1) * 4);
+    o->perm = (int *)take(A * 4);
+    o->pos = (int *)take(A * 4);
+    o->groups = (int *)take((1 + 3 * E) * 4);
+    o->h = (float *)take(A * eh * 4);
+    o->tmp = (float *)take(A * d * 4);
+    o->status = (int *)take(4 * 4);
+    return 0;
+}
+
+int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
+                   const void *d_table_layer, const float *d_router_t, const float *d_norm,
+                   const float *d_bias, float *d_x, int T, const mhip_scratch *sc, int flags) {
+    if (mhip::check_dims(c, s) || mhip::use_device(c)) return -1;
+    if (T <= 0) return T == 0 ? 0 : mhip::fail(c, "T=%d", T);
+    const int d = s->dim, E = s->n_experts, K = s->n_active, eh = s->expert_hidden;
+    const int A = T * K;
+    if (A > 65535) return mhip::fail(c, "T*K=%d exceeds 65535 assignments", A);
+    const int nb = d / QK, nbh = eh / QK;
+    hipStream_t st = c->stream;
+
+    k_rmsnorm_q8<<<T, NT, 0, st>>>(d_x, d_norm, sc->xn, sc->xq, sc->xs, d, s->norm_eps,
+                                   (flags & MHIP_FORCE_SEQ_RMS) ? 1 : 0, sc->status);
+    if (mhip::check_launch(c, "rmsnorm_q8")) return -1;
+
+    const int rthreads = E <= 64 ? 64 : E <= 128 ? 128 : 256;
+    const size_t rsh = (size_t)(d + E) * sizeof(float);
+    k_router<<<T, rthreads, rsh, st>>>(sc->xn, d_router_t, d_bias, sc->logits, sc->idx, sc->w, d,
+                                       E, K, s->norm_topk);
+    if (mhip::check_launch(c, "router")) return -1;
+
+    const int dnt = E <= 128 ? 256 : 128;
+    const size_t dsh = align256((size_t)dnt * E * 2) + (size_t)(E + 1) * 4 + (size_t)A;
+    if (dsh > 65536 &&
+        mhip::check(c, hipFuncSetAttribute((const void *)k_dispatch,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)dsh),
+                    "dispatch LDS attribute"))
+        return -1;
+    k_dispatch<<<1, dnt, dsh, st>>>(sc->idx, A, E, sc->counts, sc->offsets, sc->perm, sc->pos,
+                                    sc->groups, sc->status);
+    if (mhip::check_launch(c, "dispatch")) return -1;
+
+    const int G = A < E ? A : E;  // at most this many non-empty experts
+    const int Rg = rows_gateup(nb);
+    const size_t gsh = ((size_t)TB * 2 * Rg * (nb + 1) + (size_t)TB * 2 * Rg) * sizeof(float);
+    k_gateup<PK><<<(unsigned)G * (eh / Rg), NT, gsh, st>>>(
+        (const uint8_t *)d_table_layer, *lay, sc->xq, sc->xs, sc->groups, sc->perm, sc->h, d, eh,
+        K, Rg);
+    if (mhip::check_launch(c, "gateup")) return -1;
+
+    const int Rd = rows_down(nbh);
+    const size_t dsh2 = ((size_t)TB * Rd * (nbh + 1) + (size_t)TB * nbh) * sizeof(float) +
+                        (size_t)TB * eh;
+    k_down<PK><<<(unsigned)G * (d / Rd), NT, dsh2, st>>>((const uint8_t *)d_table_layer, *lay,
+                                                         sc->h, sc->groups, sc->tmp, d, eh, Rd);
+    if (mhip::check_launch(c, "down")) return -1;
+
+    dim3 cg(mhip::blocks_for(d, 256), T);
+    k_combine<<<cg, 256, 0, st>>>(d_x, sc->w, sc->pos, sc->tmp, d, K);
+    return mhip::check_launch(c, "combine");
+}
+
+}  // extern "C"

@@ -1,0 +1,103 @@
+/*
+ * The reference's Q8_0 tensor ops (include/mia/quant.h, include/mia/matmul.h)
+ * with their host-pointer interface, executed by the HIP kernels of
+ * include/mia_hip.h on a lazily opened context of device 0 (or
+ * $MIA_DEVICE). The functions return void in the reference interface, so a
+ * GPU failure is reported on stderr and aborts.
+ */
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "mia/matmul.h"
+#include "mia/quant.h"
+#include "mia_hip.h"
+
+static mhip_ctx *g_ctx;
+static void *g_buf[4];
+static size_t g_cap[4];
+
+static void die(const char *what) {
+    fprintf(stderr, "motoria: %s: %s\n", what, g_ctx ? mhip_error(g_ctx) : "no GPU context");
+    abort();
+}
+
+static mhip_ctx *ctx(void) {
+    if (!g_ctx) {
+        char err[256];
+        const char *dev = getenv("MIA_DEVICE");
+        if (mhip_open(&g_ctx, dev ? atoi(dev) : 0, err, sizeof(err)) != 0) {
+            fprintf(stderr, "motoria: cannot open a GPU for the tensor ops: %s\n", err);
+            abort();
+        }
+    }
+    return g_ctx;
+}
+
+/* Grow-only device staging buffer number `i`. */
+static void *buf(int i, size_t bytes) {
+    if (bytes > g_cap[i]) {
+        if (g_buf[i] && mhip_free(ctx(), g_buf[i])) die("free");
+        g_buf[i] = mhip_malloc(ctx(), bytes);
+        if (!g_buf[i]) die("malloc");
+        g_cap[i] = bytes;
+    }
+    return g_buf[i];
+}
+
+size_t mia_row_bytes(mia_wtype t, int cols) {
+    if (t == MIA_Q8_0) return (size_t)(cols / MIA_QK) * sizeof(mia_block_q8);
+    return (size_t)cols * sizeof(float);
+}
+
+void mia_quantize_row_q8(const float *x, mia_block_q8 *y, int n) {
+    if (n < MIA_QK) return;
+    const int nb = n / MIA_QK;
+    const size_t xb = (size_t)nb * MIA_QK * sizeof(float), yb = (size_t)nb * sizeof(mia_block_q8);
+    mhip_ctx *c = ctx();
+    float *dx = buf(0, xb);
+    void *dy = buf(1, yb);
+    if (mhip_h2d(c, dx, x, xb) || mhip_quantize_q8(c, dx, dy, nb * MIA_QK) ||
+        mhip_d2h(c, y, dy, yb))
+        die("quantize_row_q8");
+}
+
+void mia_dequantize_row(mia_wtype t, const void *src, float *dst, int n) {
+    if (n <= 0) return;
+    if (t == MIA_F32) { /* a copy, as src/tensor/quant.c:30-33 */
+        memcpy(dst, src, sizeof(float) * (size_t)n);
+        return;
+    }
+    mhip_ctx *c = ctx();
+    const int nb = n / MIA_QK;
+    if (!nb) return;
+    const size_t sb = (size_t)nb * sizeof(mia_block_q8), db = (size_t)nb * MIA_QK * sizeof(float);
+    void *ds = buf(1, sb);
+    float *dd = buf(0, db);
+    if (mhip_h2d(c, ds, src, sb) || mhip_dequantize_q8(c, ds, dd, nb * MIA_QK) ||
+        mhip_d2h(c, dst, dd, db))
+        die("dequantize_row");
+}
+
+void mia_matvec(float *out, const void *w, mia_wtype t, const float *x, mia_block_q8 *xq,
+                int rows, int cols) {
+    if (rows <= 0) return;
+    mhip_ctx *c = ctx();
+    const size_t wb = (size_t)rows * mia_row_bytes(t, cols);
+    const size_t xb = (size_t)cols * sizeof(float);
+    const size_t qb = t == MIA_Q8_0 ? (size_t)(cols / MIA_QK) * sizeof(mia_block_q8) : 0;
+    void *dw = buf(0, wb);
+    float *dx = buf(1, xb ? xb : 4);
+    void *dq = buf(2, qb ? qb : 4);
+    float *dout = buf(3, (size_t)rows * sizeof(float));
+    if (mhip_h2d(c, dw, w, wb) || mhip_h2d(c, dx, x, xb) ||
+        mhip_matvec(c, dout, dw, (int)t, dx, dq, rows, cols) ||
+        mhip_d2h(c, out, dout, (size_t)rows * sizeof(float)) ||
+        (qb && xq && mhip_d2h(c, xq, dq, qb)))
+        die("matvec");
+}
+
+void mia_matvec_scalar(float *out, const void *w, mia_wtype t, const float *x,
+                       mia_block_q8 *xq, int rows, int cols) {
+    mia_matvec(out, w, t, x, xq, rows, cols);
+}

@@ -1,0 +1,97 @@
+#ifndef MIA_ORACLE_H
+#define MIA_ORACLE_H
+/*
+ * CPU restatement of motorIa's Q8_0 MoE FFN path.
+ *
+ * TEST INFRASTRUCTURE ONLY: this is the parity checker and the CPU baseline.
+ * Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg may
+ * load it. The product (motoria_amd/) never links, calls or falls back to it.
+ *
+ * Semantics follow the reference's Linux/x86 build (scalar dot products, no
+ * threading), compiled -std=c99 -O3 -ffp-contract=off so no product is fused
+ * into an add. Each function cites the reference lines it restates.
+ *
+ * Parity pinning (what checks each function besides retyping its formula):
+ *   orc_quantize_row_q8  known answers of tests/test_quant.c:24-41 and
+ *                        tools/internal/mia/format_test.go:35-55; bit-equal to
+ *                        the reference build (oracle/_ref) on random rows.
+ *   orc_matvec           closed form / tolerance of tests/test_matmul.c:6-60;
+ *                        bit-equal to oracle/_ref.
+ *   orc_rmsnorm          unit-RMS invariant (tools/internal/ref/ref_test.go:18-28);
+ *                        bit-equal to oracle/_ref inside the layer.
+ *   orc_softmax/top_k    known answers (ref_test.go:30-56), tie rule, brute force.
+ *   orc_moe_token        bit-equal to oracle/_ref (real moe()) on golden vectors.
+ *   orc_dispatch         brute-force stable sort; permutation invariants.
+ */
+#include <stddef.h>
+#include <stdint.h>
+
+#define ORC_QK 32
+enum { ORC_F32 = 0, ORC_Q8_0 = 1 };
+
+/* include/mia/quant.h:12-15: 36-byte block, value = d * q. */
+typedef struct {
+    float d;
+    int8_t q[ORC_QK];
+} orc_block_q8;
+
+typedef struct {
+    int dim;           /* d: hidden size (2048) */
+    int n_experts;     /* E (128) */
+    int n_active;      /* K (8) */
+    int expert_hidden; /* eh (768) */
+    int norm_topk;     /* renormalise the top-K gates (Qwen3: 1) */
+    float norm_eps;    /* rmsnorm epsilon (1e-6) */
+} orc_dims;
+
+size_t orc_row_bytes(int wtype, int cols);
+void orc_quantize_row_q8(const float *x, orc_block_q8 *y, int n);
+void orc_dequantize_row(int wtype, const void *src, float *dst, int n);
+void orc_matvec(float *out, const void *w, int wtype, const float *x,
+                orc_block_q8 *xq, int rows, int cols);
+void orc_rmsnorm(float *out, const float *x, const float *w, int n, float eps);
+void orc_softmax(float *x, int n);
+void orc_top_k(const float *p, int n, int k, int *idx);
+float orc_expf(float x);
+/* Softmax in place over logits[E], top-K idx[K], gate weights w[K]. */
+void orc_route(float *logits, int E, int K, int norm_topk, int *idx, float *w);
+
+/* Offsets of up/down inside a reference-format expert blob
+ * (src/storage/mia_file.c:98-101) and the blob size (format.go:160-163). */
+size_t orc_off_up(const orc_dims *s);
+size_t orc_off_down(const orc_dims *s);
+size_t orc_blob_bytes(const orc_dims *s);
+
+/*
+ * One MoE layer over T independent tokens, in place on x[T][dim]
+ * (src/model/forward.c:167-197 applied per token). blobs[e] points to expert
+ * e of this layer in the reference blob format, or NULL if unavailable (the
+ * call then fails like a cache miss whose load failed). bias may be NULL.
+ * Optional outputs (NULL to skip): idx[T][K], w[T][K], logits[T][E] (after
+ * the bias), xn[T][dim]. Returns 0, or -1 (K > 64 or a missing expert).
+ * nthreads > 1 spreads tokens over OpenMP threads (same bits).
+ */
+int orc_moe_layer(const orc_dims *s, int T, float *x, const float *ffn_norm,
+                  const float *router, const float *bias,
+                  const unsigned char *const *blobs, int *idx, float *w,
+                  float *logits, float *xn, int nthreads);
+
+/* MoE-only stack: layers l = 0..L-1 of RMSNorm -> MoE -> residual.
+ * blobs[l*E + e], ffn_norm[l*dim], router[l*E*dim]. */
+int orc_moe_stack(const orc_dims *s, int L, int T, float *x,
+                  const float *ffn_norm, const float *router,
+                  const unsigned char *const *blobs, int nthreads);
+
+/* Stable counting sort of the T*K assignments (t, j) by expert idx[t][j],
+ * t-major then j. counts[E], offsets[E+1], perm[T*K] = t*K + j in bucketed
+ * order, pos[t*K + j] = its position in perm. Returns 0 or -1 (bad index). */
+int orc_dispatch(const int *idx, int T, int K, int E, int *counts,
+                 int *offsets, int *perm, int *pos);
+
+/* Synthetic tensors (same generator as include/mia/synth.h). */
+void orc_synth_x(uint64_t seed, int T, int dim, float *x);
+void orc_synth_router(uint64_t seed, int layer, const orc_dims *s, float *w);
+void orc_synth_expert_blob(uint64_t seed, int layer, int expert,
+                           const orc_dims *s, unsigned char *blob);
+
+#endif

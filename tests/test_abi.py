@@ -1,0 +1,85 @@
+"""The C-ABI library loads and exports every function include/ declares
+(no compute calls: this runs without a GPU)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import motoria_amd as M
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADERS = ["include/mia_hip.h", "include/mia/quant.h", "include/mia/matmul.h",
+           "include/mia/moe.h"]
+
+
+def declared_functions():
+    names = set()
+    for h in HEADERS:
+        text = open(os.path.join(ROOT, h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        for m in re.finditer(r"\b([a-z_][a-z0-9_]*)\s*\(([^;{}]*)\)\s*;", text):
+            names.add(m.group(1))
+    return names
+
+
+def exported_symbols():
+    out = subprocess.run(["nm", "-D", "--defined-only", M.LIB_PATH], check=True,
+                         capture_output=True, text=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if " T " in line}
+
+
+def test_library_loads():
+    L = M.lib()
+    assert isinstance(L, ctypes.CDLL)
+
+
+def test_every_declared_function_is_exported_and_bound():
+    declared = declared_functions()
+    assert len(declared) > 40
+    exported = exported_symbols()
+    missing = sorted(declared - exported)
+    assert not missing, "declared in include/ but not exported: %s" % missing
+    unbound = sorted(declared - set(M.SIGNATURES))
+    assert not unbound, "not bound in motoria_amd.SIGNATURES: %s" % unbound
+    extra = sorted(set(M.SIGNATURES) - declared)
+    assert not extra, "bound but not declared: %s" % extra
+
+
+def test_row_bytes_by_type():
+    # tests/test_quant.c:4-8 of the reference (pure arithmetic, no GPU call)
+    L = M.lib()
+    assert L.mia_row_bytes(0, 64) == 256
+    assert L.mia_row_bytes(1, 64) == 72
+    assert L.mia_row_bytes(1, 2048) == 2304 and L.mia_row_bytes(1, 768) == 864
+
+
+def test_layout_matches_blob_size():
+    d = M.Dims(2048, 128, 8, 768, 1, 1e-6)
+    lay = M.Layout()
+    assert M.lib().mhip_layout_of(ctypes.byref(d), ctypes.byref(lay)) == 0
+    # Regrouping keeps 1.125 bytes per weight: the .mia blob size exactly.
+    assert lay.expert_bytes == 5308416
+    for off in (lay.gate_q, lay.up_q, lay.down_q, lay.gate_s, lay.up_s, lay.down_s):
+        assert off % 256 == 0
+
+
+def test_layout_rejects_unsupported_shapes():
+    lay = M.Layout()
+    for bad in [M.Dims(2047, 128, 8, 768, 1, 1e-6), M.Dims(2048, 300, 8, 768, 1, 1e-6),
+                M.Dims(2048, 128, 65, 768, 1, 1e-6), M.Dims(2048, 4, 8, 768, 1, 1e-6)]:
+        assert M.lib().mhip_layout_of(ctypes.byref(bad), ctypes.byref(lay)) == -1
+
+
+def test_no_oracle_in_product():
+    """The product library links nothing from oracle/ and exports no oracle
+    symbol; the package never imports the oracle."""
+    exported = exported_symbols()
+    assert not any(s.startswith("orc_") or s.startswith("ref_") for s in exported)
+    deps = subprocess.run(["ldd", M.LIB_PATH], capture_output=True, text=True).stdout
+    assert "oracle" not in deps
+    for dirpath, _, files in os.walk(os.path.join(ROOT, "motoria_amd")):
+        for f in files:
+            if f.endswith((".py", ".c", ".h", ".hip")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "import oracle" not in text and "mia_oracle" not in text, f
