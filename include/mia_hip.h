@@ -62,6 +62,21 @@ int mhip_sync(mhip_ctx *c);
 int mhip_mark(mhip_ctx *c, int slot); /* slot 0..15 */
 int mhip_elapsed(mhip_ctx *c, int slot0, int slot1, float *ms);
 
+/* Per-stage kernel timing. While a mask is set, every launch of a selected
+ * stage of mhip_moe_layer is bracketed by two HIP events on the context's
+ * stream (up to max_launches launches; later ones are not timed).
+ * mhip_stage_time waits for them and returns the summed milliseconds and the
+ * number of timed launches of one stage. mask 0 turns timing off. */
+#define MHIP_STAGE_RMSNORM 0
+#define MHIP_STAGE_ROUTER 1
+#define MHIP_STAGE_DISPATCH 2
+#define MHIP_STAGE_GATEUP 3
+#define MHIP_STAGE_DOWN 4
+#define MHIP_STAGE_COMBINE 5
+#define MHIP_N_STAGES 6
+int mhip_stage_timing(mhip_ctx *c, unsigned mask, int max_launches);
+int mhip_stage_time(mhip_ctx *c, int stage, double *ms, int *launches);
+
 /* ---- expert table ----------------------------------------------------- */
 /* Repack n reference-format blobs (d_blobs, blob_bytes apart; gate at 0, up
  * at off_up, down at off_down) into table slots (layer, experts[i]). */

@@ -23,6 +23,7 @@ _sz = ctypes.c_size_t
 _u64 = ctypes.c_uint64
 
 MHIP_FORCE_SEQ_RMS = 1
+STAGES = ["rmsnorm", "router", "dispatch", "gateup", "down", "combine"]
 
 
 class MoeConfig(ctypes.Structure):
@@ -64,6 +65,8 @@ SIGNATURES = {
     "mhip_sync": (_i, [_p]),
     "mhip_mark": (_i, [_p, _i]),
     "mhip_elapsed": (_i, [_p, _i, _i, ctypes.POINTER(_f)]),
+    "mhip_stage_timing": (_i, [_p, ctypes.c_uint, _i]),
+    "mhip_stage_time": (_i, [_p, _i, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i)]),
     "mhip_table_repack": (_i, [_p, ctypes.POINTER(Dims), _p, _i, ctypes.POINTER(_i), _i, _p,
                                _sz, _sz, _sz]),
     "mhip_table_unpack": (_i, [_p, ctypes.POINTER(Dims), _p, _i, _i, _p, _sz, _sz, _sz]),
@@ -285,6 +288,21 @@ class Moe:
         if lib().mhip_elapsed(self.gpu, s0, s1, ctypes.byref(ms)) != 0:
             raise RuntimeError("mhip_elapsed: " + lib().mhip_error(self.gpu).decode())
         return ms.value
+
+    def stage_timing(self, stages, max_launches):
+        mask = 0
+        for st in stages:
+            mask |= 1 << STAGES.index(st)
+        if lib().mhip_stage_timing(self.gpu, mask, max_launches) != 0:
+            raise RuntimeError("mhip_stage_timing: " + lib().mhip_error(self.gpu).decode())
+
+    def stage_time(self, stage):
+        ms = ctypes.c_double()
+        n = _i()
+        if lib().mhip_stage_time(self.gpu, STAGES.index(stage), ctypes.byref(ms),
+                                 ctypes.byref(n)) != 0:
+            raise RuntimeError("mhip_stage_time: " + lib().mhip_error(self.gpu).decode())
+        return ms.value, n.value
 
     def synth_f32(self, d_out, n, seed, stream, sigma):
         if lib().mhip_synth_f32(self.gpu, d_out, n, seed, stream, sigma) != 0:

@@ -43,9 +43,34 @@ int check_dims(mhip_ctx *c, const mhip_dims *s) {
     return 0;
 }
 
+int stage_begin(mhip_ctx *c, int stage) {
+    if (!(c->st_mask & (1u << stage)) || c->st_n >= c->st_cap) return -1;
+    const int slot = c->st_n++;
+    c->st_stage[slot] = stage;
+    (void)hipEventRecord(c->st_ev[2 * slot], c->stream);
+    return slot;
+}
+
+void stage_end(mhip_ctx *c, int slot) {
+    if (slot >= 0) (void)hipEventRecord(c->st_ev[2 * slot + 1], c->stream);
+}
+
 }  // namespace mhip
 
 namespace {
+
+void free_stage_events(mhip_ctx *c) {
+    if (c->st_ev) {
+        for (int i = 0; i < 2 * c->st_cap; i++)
+            if (c->st_ev[i]) (void)hipEventDestroy(c->st_ev[i]);
+    }
+    free(c->st_ev);
+    free(c->st_stage);
+    c->st_ev = nullptr;
+    c->st_stage = nullptr;
+    c->st_cap = c->st_n = 0;
+    c->st_mask = 0;
+}
 
 __global__ void k_fill_bytes(uint8_t *p, size_t n, uint8_t v) {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -107,8 +132,47 @@ void mhip_close(mhip_ctx *c) {
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     for (int i = 0; i < 16; i++)
         if (c->marks[i]) (void)hipEventDestroy(c->marks[i]);
+    free_stage_events(c);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     free(c);
+}
+
+int mhip_stage_timing(mhip_ctx *c, unsigned mask, int max_launches) {
+    if (mhip::use_device(c)) return -1;
+    if (mhip::check(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize")) return -1;
+    free_stage_events(c);
+    if (!mask || max_launches <= 0) return 0;
+    c->st_ev = (hipEvent_t *)calloc((size_t)2 * max_launches, sizeof(hipEvent_t));
+    c->st_stage = (int *)calloc((size_t)max_launches, sizeof(int));
+    if (!c->st_ev || !c->st_stage) {
+        free_stage_events(c);
+        return mhip::fail(c, "out of host memory");
+    }
+    c->st_cap = max_launches;
+    for (int i = 0; i < 2 * max_launches; i++)
+        if (mhip::check(c, hipEventCreate(&c->st_ev[i]), "hipEventCreate")) {
+            free_stage_events(c);
+            return -1;
+        }
+    c->st_mask = mask;
+    return 0;
+}
+
+int mhip_stage_time(mhip_ctx *c, int stage, double *ms, int *launches) {
+    *ms = 0.0;
+    *launches = 0;
+    if (mhip::use_device(c)) return -1;
+    if (mhip::check(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize")) return -1;
+    for (int i = 0; i < c->st_n; i++) {
+        if (c->st_stage[i] != stage) continue;
+        float t = 0.0f;
+        if (mhip::check(c, hipEventElapsedTime(&t, c->st_ev[2 * i], c->st_ev[2 * i + 1]),
+                        "hipEventElapsedTime"))
+            return -1;
+        *ms += t;
+        (*launches)++;
+    }
+    return 0;
 }
 
 const char *mhip_error(const mhip_ctx *c) { return c ? c->err : "null context"; }

@@ -13,6 +13,11 @@ struct mhip_ctx {
     int device;
     hipStream_t stream;
     hipEvent_t marks[16];
+    // stage timing (mhip_stage_timing)
+    unsigned st_mask;
+    int st_cap, st_n;
+    hipEvent_t *st_ev;  // [2 * st_cap]
+    int *st_stage;      // [st_cap]
     char err[512];
 };
 
@@ -28,6 +33,11 @@ int use_device(mhip_ctx *c);
 
 // Validates shapes every kernel of the path assumes; returns 0 or fail().
 int check_dims(mhip_ctx *c, const mhip_dims *s);
+
+// Brackets one launch of `stage` with events when stage timing selects it.
+// stage_begin returns the record slot or -1; stage_end closes that slot.
+int stage_begin(mhip_ctx *c, int stage);
+void stage_end(mhip_ctx *c, int slot);
 
 inline unsigned blocks_for(size_t n, unsigned per) {
     return (unsigned)((n + per - 1) / per);

@@ -532,14 +532,18 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     const int nb = d / QK, nbh = eh / QK;
     hipStream_t st = c->stream;
 
+    int slot = mhip::stage_begin(c, MHIP_STAGE_RMSNORM);
     k_rmsnorm_q8<<<T, NT, 0, st>>>(d_x, d_norm, sc->xn, sc->xq, sc->xs, d, s->norm_eps,
                                    (flags & MHIP_FORCE_SEQ_RMS) ? 1 : 0, sc->status);
+    mhip::stage_end(c, slot);
     if (mhip::check_launch(c, "rmsnorm_q8")) return -1;
 
     const int rthreads = E <= 64 ? 64 : E <= 128 ? 128 : 256;
     const size_t rsh = (size_t)(d + E) * sizeof(float);
+    slot = mhip::stage_begin(c, MHIP_STAGE_ROUTER);
     k_router<<<T, rthreads, rsh, st>>>(sc->xn, d_router_t, d_bias, sc->logits, sc->idx, sc->w, d,
                                        E, K, s->norm_topk);
+    mhip::stage_end(c, slot);
     if (mhip::check_launch(c, "router")) return -1;
 
     const int dnt = E <= 128 ? 256 : 128;
@@ -549,27 +553,35 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)dsh),
                     "dispatch LDS attribute"))
         return -1;
+    slot = mhip::stage_begin(c, MHIP_STAGE_DISPATCH);
     k_dispatch<<<1, dnt, dsh, st>>>(sc->idx, A, E, sc->counts, sc->offsets, sc->perm, sc->pos,
                                     sc->groups, sc->status);
+    mhip::stage_end(c, slot);
     if (mhip::check_launch(c, "dispatch")) return -1;
 
     const int G = A < E ? A : E;  // at most this many non-empty experts
     const int Rg = rows_gateup(nb);
     const size_t gsh = ((size_t)TB * 2 * Rg * (nb + 1) + (size_t)TB * 2 * Rg) * sizeof(float);
+    slot = mhip::stage_begin(c, MHIP_STAGE_GATEUP);
     k_gateup<PK><<<(unsigned)G * (eh / Rg), NT, gsh, st>>>(
         (const uint8_t *)d_table_layer, *lay, sc->xq, sc->xs, sc->groups, sc->perm, sc->h, d, eh,
         K, Rg);
+    mhip::stage_end(c, slot);
     if (mhip::check_launch(c, "gateup")) return -1;
 
     const int Rd = rows_down(nbh);
     const size_t dsh2 = ((size_t)TB * Rd * (nbh + 1) + (size_t)TB * nbh) * sizeof(float) +
                         (size_t)TB * eh;
+    slot = mhip::stage_begin(c, MHIP_STAGE_DOWN);
     k_down<PK><<<(unsigned)G * (d / Rd), NT, dsh2, st>>>((const uint8_t *)d_table_layer, *lay,
                                                          sc->h, sc->groups, sc->tmp, d, eh, Rd);
+    mhip::stage_end(c, slot);
     if (mhip::check_launch(c, "down")) return -1;
 
     dim3 cg(mhip::blocks_for(d, 256), T);
+    slot = mhip::stage_begin(c, MHIP_STAGE_COMBINE);
     k_combine<<<cg, 256, 0, st>>>(d_x, sc->w, sc->pos, sc->tmp, d, K);
+    mhip::stage_end(c, slot);
     return mhip::check_launch(c, "combine");
 }
 
