@@ -106,6 +106,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-layers", type=int, default=4)
     ap.add_argument("--cpu-tokens", type=int, default=256)
+    ap.add_argument("--multi-kernel", action="store_true",
+                    help="batch-1 workloads: one launch per stage instead of the "
+                         "persistent decode kernel")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -138,9 +141,13 @@ def main():
         moe.h2d(d_bias, W.zipf_bias(shape["n_experts"]))
     moe.synth_f32(d_x0, T * d, W.X_SEED, 1 << 40, 1.0)
 
+    persistent = T == 1 and not args.multi_kernel
+
     def step():
         M.lib().mhip_d2d(moe.gpu, d_x, d_x0, nbytes)
-        if d_bias is None:
+        if persistent:
+            moe.decode_dev(0, L, d_x, d_bias)
+        elif d_bias is None:
             moe.stack_dev(0, L, d_x, T)
         else:
             for l in range(L):
@@ -155,8 +162,10 @@ def main():
     moe.sync()
 
     # Timed region: host clock between two stream synchronisations, HIP events
-    # on the library stream, and events around every gate/up launch.
-    moe.stage_timing(["gateup"], max_launches=L * args.steps + 16)
+    # on the library stream, and events around every launch of the dominant
+    # kernel (the persistent decode kernel, or k_gateup per layer).
+    dom = "decode" if persistent else "gateup"
+    moe.stage_timing([dom], max_launches=(1 if persistent else L) * args.steps + 16)
     moe.sync()
     t0 = time.perf_counter()
     moe.mark(0)
@@ -166,7 +175,8 @@ def main():
     moe.sync()
     t1 = time.perf_counter()
     ev_ms = moe.elapsed_ms(0, 1)
-    stage = {"gateup": moe.stage_time("gateup")}
+    stage = {dom: moe.stage_time(dom)}
+    dstat = moe.decode_status() if persistent else None
     # Untimed diagnostic pass: every stage bracketed by events.
     diag_steps = min(args.steps, 5)
     moe.stage_timing(M.STAGES, max_launches=len(M.STAGES) * L * diag_steps + 16)
@@ -179,14 +189,26 @@ def main():
     ms_step = (t1 - t0) * 1e3 / args.steps
     tokens_per_s = T / (ms_step / 1e3)
     hbm_gbs = step_bytes / (ms_step / 1e3) / 1e9
-    gu_ms, gu_n = stage["gateup"]
-    gu_avg_s = gu_ms / max(gu_n, 1) / 1e3
-    gu_bytes = sum(gateup_bytes(n, T, shape) for n in touched) / len(touched)
-    achieved = gu_bytes / gu_avg_s / 1e9
+    dom_ms, dom_n = stage[dom]
+    dom_avg_s = dom_ms / max(dom_n, 1) / 1e3
+    if persistent:
+        dom_bytes = step_bytes
+        dom_name = ("k_decode_stack (persistent: %d layers of rmsnorm, router/top-8, "
+                    "gate/up+SwiGLU, down, combine in one launch)" % L)
+    else:
+        dom_bytes = sum(gateup_bytes(n, T, shape) for n in touched) / len(touched)
+        dom_name = "k_gateup (gate/up Q8_0 grouped GEMV + SwiGLU)"
+    achieved = dom_bytes / dom_avg_s / 1e9
     for s in M.STAGES:
         ms, n = diag[s]
-        log("  stage %-8s %4d launches, avg %8.2f us, %5.1f %% of step (diagnostic pass)"
-            % (s, n, ms / max(n, 1) * 1e3, 100.0 * ms / (ms_step * diag_steps)))
+        if n:
+            log("  stage %-8s %4d launches, avg %8.2f us, %5.1f %% of step (diagnostic pass)"
+                % (s, n, ms / max(n, 1) * 1e3, 100.0 * ms / (ms_step * diag_steps)))
+    if dstat is not None:
+        log("decode status %s (abort bits, rmsnorm fallbacks, exact-router layers)" % dstat)
+        if dstat[0]:
+            print("bench.py: the decode kernel aborted (%s)" % dstat, file=sys.stderr)
+            sys.exit(1)
     log("step %.3f ms (events %.3f ms), %.1f tokens/s, %.1f GB/s algorithmic"
         % (ms_step, ev_ms / args.steps, tokens_per_s, hbm_gbs))
 
@@ -221,16 +243,17 @@ def main():
         "hbm": {"bytes_per_step": step_bytes, "achieved_gbs": hbm_gbs,
                 "frac": hbm_gbs / HBM_PEAK_GBS, "ops_per_step": step_ops},
         "roofline": {
-            "kernel": "k_gateup (gate/up Q8_0 grouped GEMV + SwiGLU)",
+            "kernel": dom_name,
             "bound": "hbm",
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": None,
-            "bytes_per_launch": gu_bytes,
-            "avg_launch_us": gu_avg_s * 1e6,
+            "bytes_per_launch": dom_bytes,
+            "avg_launch_us": dom_avg_s * 1e6,
         },
+        "path": ("persistent decode kernel" if persistent else "one launch per stage"),
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

@@ -83,6 +83,23 @@ int mia_moe_stack(mia_moe *m, int l0, int l1, float *x, int T);
 int mia_moe_layer_dev(mia_moe *m, int layer, float *d_x, int T, const float *d_bias);
 int mia_moe_stack_dev(mia_moe *m, int l0, int l1, float *d_x, int T);
 
+/* Decode of one token through layers [l0, l1) in a single persistent launch
+ * (the Qwen3-30B-A3B shape on a 256-CU MI355X; mhip_decode_stack). x[dim]
+ * (host) is updated in place; idx/w ([l1-l0][K]) receive the routing when
+ * not NULL; bias (E floats) applies to every layer when not NULL. Expert
+ * indices are bit-equal to the reference; the output is within ~1e-6
+ * relative of it (the gate weights come from the parallel router logits). */
+int mia_moe_decode(mia_moe *m, int l0, int l1, float *x, const float *bias, int *idx, float *w);
+/* Same on device memory, queued on the handle's stream; check
+ * mia_moe_decode_status after the stream completes. */
+int mia_moe_decode_dev(mia_moe *m, int l0, int l1, float *d_x, const float *d_bias);
+/* status[0] abort bits (nonzero: the output is invalid), [1] rmsnorm
+ * fallbacks, [2] layers routed by the exact fallback. Waits for the stream. */
+int mia_moe_decode_status(mia_moe *m, int status[4]);
+/* Stage timestamps of the last decode call made with MHIP_DECODE_TRACE
+ * (see mhip_decode_trace). */
+int mia_moe_decode_trace(mia_moe *m, unsigned long long *out);
+
 /* The handle's device context (memory, copies, stream marks of mia_hip.h)
  * and the scratch of the last call (routing, dispatch, intermediates). */
 mhip_ctx *mia_moe_gpu(mia_moe *m);

@@ -73,7 +73,8 @@ int mhip_elapsed(mhip_ctx *c, int slot0, int slot1, float *ms);
 #define MHIP_STAGE_GATEUP 3
 #define MHIP_STAGE_DOWN 4
 #define MHIP_STAGE_COMBINE 5
-#define MHIP_N_STAGES 6
+#define MHIP_STAGE_DECODE 6 /* the persistent decode-stack kernel */
+#define MHIP_N_STAGES 7
 int mhip_stage_timing(mhip_ctx *c, unsigned mask, int max_launches);
 int mhip_stage_time(mhip_ctx *c, int stage, double *ms, int *launches);
 
@@ -92,9 +93,10 @@ int mhip_table_unpack(mhip_ctx *c, const mhip_dims *s, const void *d_table,
  * to include/mia/synth.h quantized on the host. */
 int mhip_table_synth(mhip_ctx *c, const mhip_dims *s, void *d_table,
                      uint64_t seed, int l0, int l1);
-/* Router of layer l, transposed: d_router_t[i*E + e] = W[e][i]. */
+/* Router of layer l, transposed (d_router_t[i*E + e] = W[e][i]) and, when
+ * d_router is not NULL, row-major (d_router[e*d + i] = W[e][i]). */
 int mhip_router_synth(mhip_ctx *c, const mhip_dims *s, float *d_router_t,
-                      uint64_t seed, int layer);
+                      float *d_router, uint64_t seed, int layer);
 int mhip_router_transpose(mhip_ctx *c, const mhip_dims *s, float *d_router_t,
                           const float *d_router);
 int mhip_synth_f32(mhip_ctx *c, float *d_out, size_t n, uint64_t seed,
@@ -124,8 +126,10 @@ size_t mhip_scratch_bytes(const mhip_dims *s, int max_tokens);
 int mhip_scratch_carve(const mhip_dims *s, int max_tokens, void *d_base,
                        mhip_scratch *out);
 
-/* Flags for mhip_moe_layer. */
-#define MHIP_FORCE_SEQ_RMS 1 /* always take the sequential rmsnorm sum */
+/* Flags for mhip_moe_layer and mhip_decode_stack. */
+#define MHIP_FORCE_SEQ_RMS 1      /* always take the sequential rmsnorm sum */
+#define MHIP_FORCE_EXACT_ROUTER 2 /* decode stack: always the exact router chain */
+#define MHIP_DECODE_TRACE 4       /* decode stack: record stage timestamps */
 
 /*
  * One MoE layer (rmsnorm -> router/top-K -> dispatch -> gate/up+SwiGLU ->
@@ -137,6 +141,32 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
                    const void *d_table_layer, const float *d_router_t,
                    const float *d_norm, const float *d_bias, float *d_x, int T,
                    const mhip_scratch *sc, int flags);
+
+/*
+ * Decode (one token) through L consecutive layers in one persistent launch:
+ * the Qwen3-30B-A3B shape only (dim 2048, 128 experts, n_active <= 8,
+ * expert_hidden 768) on a 256-CU MI355X. d_table/d_router ([L][E][d])/
+ * d_router_t ([L][d][E])/d_norm ([L][d]) start at the first layer; d_bias
+ * (E floats, every layer) may be NULL; d_x[d] is updated in place. d_ws is a
+ * workspace of mhip_decode_ws_bytes() bytes (not shared by concurrent
+ * launches). d_idx/d_w ([L][n_active]) receive the routing when non-NULL.
+ * Expert indices are bit-equal to the reference (certified parallel router,
+ * exact fallback); the gate weights come from the parallel logits, within
+ * ~1e-6 relative of the reference's. After the stream completes,
+ * mhip_decode_status reports [0] abort bits (1: workgroups not on the
+ * expected XCDs, 2: a wait timed out; the output is then invalid),
+ * [1] rmsnorm fallbacks, [2] layers routed by the exact fallback.
+ */
+size_t mhip_decode_ws_bytes(void);
+int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
+                      const void *d_table, const float *d_router, const float *d_router_t,
+                      const float *d_norm, const float *d_bias, float *d_x, int L,
+                      void *d_ws, int *d_idx, float *d_w, int flags);
+int mhip_decode_status(mhip_ctx *c, const void *d_ws, int status[4]);
+/* With MHIP_DECODE_TRACE set: the 100 MHz real-time counter at 12 stage
+ * boundaries of the first 64 layers, for workgroups 0 and 1
+ * (out[2][64][12]). Diagnostic. */
+int mhip_decode_trace(mhip_ctx *c, const void *d_ws, unsigned long long *out);
 
 /* ---- reference tensor ops on device pointers ---------------------------- */
 /* Q8_0 blocks in the reference's 36-byte format. */

@@ -23,7 +23,9 @@ _sz = ctypes.c_size_t
 _u64 = ctypes.c_uint64
 
 MHIP_FORCE_SEQ_RMS = 1
-STAGES = ["rmsnorm", "router", "dispatch", "gateup", "down", "combine"]
+MHIP_FORCE_EXACT_ROUTER = 2
+MHIP_DECODE_TRACE = 4
+STAGES = ["rmsnorm", "router", "dispatch", "gateup", "down", "combine", "decode"]
 
 
 class MoeConfig(ctypes.Structure):
@@ -71,7 +73,7 @@ SIGNATURES = {
                                _sz, _sz, _sz]),
     "mhip_table_unpack": (_i, [_p, ctypes.POINTER(Dims), _p, _i, _i, _p, _sz, _sz, _sz]),
     "mhip_table_synth": (_i, [_p, ctypes.POINTER(Dims), _p, _u64, _i, _i]),
-    "mhip_router_synth": (_i, [_p, ctypes.POINTER(Dims), _p, _u64, _i]),
+    "mhip_router_synth": (_i, [_p, ctypes.POINTER(Dims), _p, _p, _u64, _i]),
     "mhip_router_transpose": (_i, [_p, ctypes.POINTER(Dims), _p, _p]),
     "mhip_synth_f32": (_i, [_p, _p, _sz, _u64, _u64, ctypes.c_double]),
     "mhip_fill_f32": (_i, [_p, _p, _sz, _f]),
@@ -79,6 +81,11 @@ SIGNATURES = {
     "mhip_scratch_carve": (_i, [ctypes.POINTER(Dims), _i, _p, ctypes.POINTER(Scratch)]),
     "mhip_moe_layer": (_i, [_p, ctypes.POINTER(Dims), ctypes.POINTER(Layout), _p, _p, _p, _p,
                             _p, _i, ctypes.POINTER(Scratch), _i]),
+    "mhip_decode_ws_bytes": (_sz, []),
+    "mhip_decode_stack": (_i, [_p, ctypes.POINTER(Dims), ctypes.POINTER(Layout), _p, _p, _p, _p,
+                               _p, _p, _i, _p, _p, _p, _i]),
+    "mhip_decode_status": (_i, [_p, _p, ctypes.POINTER(_i)]),
+    "mhip_decode_trace": (_i, [_p, _p, _p]),
     "mhip_quantize_q8": (_i, [_p, _p, _p, _i]),
     "mhip_dequantize_q8": (_i, [_p, _p, _p, _i]),
     "mhip_matvec": (_i, [_p, _p, _p, _i, _p, _p, _i, _i]),
@@ -105,6 +112,10 @@ SIGNATURES = {
     "mia_moe_stack": (_i, [_p, _i, _i, _p, _i]),
     "mia_moe_layer_dev": (_i, [_p, _i, _p, _i, _p]),
     "mia_moe_stack_dev": (_i, [_p, _i, _i, _p, _i]),
+    "mia_moe_decode": (_i, [_p, _i, _i, _p, _p, _p, _p]),
+    "mia_moe_decode_dev": (_i, [_p, _i, _i, _p, _p]),
+    "mia_moe_decode_status": (_i, [_p, ctypes.POINTER(_i)]),
+    "mia_moe_decode_trace": (_i, [_p, _p]),
     "mia_moe_gpu": (_p, [_p]),
     "mia_moe_scratch": (ctypes.POINTER(Scratch), [_p]),
     "mia_moe_set_flags": (None, [_p, _i]),
@@ -250,6 +261,31 @@ class Moe:
 
     def stack_dev(self, l0, l1, d_x, T):
         self._check(lib().mia_moe_stack_dev(self.h, l0, l1, d_x, T), "mia_moe_stack_dev")
+
+    def decode(self, l0, l1, x, bias=None):
+        """One token through layers [l0, l1) in one persistent launch.
+        Returns (x_out, idx[l1-l0][K], w[l1-l0][K])."""
+        x = np.array(x, dtype=np.float32).reshape(-1).copy()
+        K = self.shape["n_active"]
+        idx = np.zeros((l1 - l0, K), dtype=np.int32)
+        w = np.zeros((l1 - l0, K), dtype=np.float32)
+        bias = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        self._check(lib().mia_moe_decode(self.h, l0, l1, _ptr(x), _ptr(bias), _ptr(idx), _ptr(w)),
+                    "mia_moe_decode")
+        return x, idx, w
+
+    def decode_trace(self):
+        out = np.zeros((2, 64, 12), dtype=np.uint64)
+        self._check(lib().mia_moe_decode_trace(self.h, out.ctypes.data), "mia_moe_decode_trace")
+        return out
+
+    def decode_dev(self, l0, l1, d_x, d_bias=None):
+        self._check(lib().mia_moe_decode_dev(self.h, l0, l1, d_x, d_bias), "mia_moe_decode_dev")
+
+    def decode_status(self):
+        st = (_i * 4)()
+        self._check(lib().mia_moe_decode_status(self.h, st), "mia_moe_decode_status")
+        return list(st)
 
     def scratch(self):
         return lib().mia_moe_scratch(self.h).contents

@@ -152,12 +152,16 @@ __global__ __launch_bounds__(256) void k_unpack(ExpertGeom g, const uint8_t *exp
     dst[8] = (uint32_t)c1.w;
 }
 
-// Router of one layer, stored transposed: out[i*E + e] = W[e][i].
-__global__ __launch_bounds__(256) void k_router_synth(float *out, int d, int E, uint64_t key) {
+// Router of one layer, transposed (out_t[i*E + e] = W[e][i]) and, when
+// out_rm is not null, row-major (out_rm[e*d + i] = W[e][i]).
+__global__ __launch_bounds__(256) void k_router_synth(float *out_t, float *out_rm, int d, int E,
+                                                      uint64_t key) {
     const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (q >= (size_t)d * E) return;
     const int e = (int)(q / d), i = (int)(q % d);
-    out[(size_t)i * E + e] = mia_synth_f32(key, q, 0.02);
+    const float v = mia_synth_f32(key, q, 0.02);
+    out_t[(size_t)i * E + e] = v;
+    if (out_rm) out_rm[q] = v;
 }
 
 __global__ __launch_bounds__(256) void k_transpose(float *out, const float *in, int E, int d) {
@@ -263,12 +267,12 @@ int mhip_table_unpack(mhip_ctx *c, const mhip_dims *s, const void *d_table, int 
     return mhip::check_launch(c, "unpack");
 }
 
-int mhip_router_synth(mhip_ctx *c, const mhip_dims *s, float *d_router_t, uint64_t seed,
-                      int layer) {
+int mhip_router_synth(mhip_ctx *c, const mhip_dims *s, float *d_router_t, float *d_router,
+                      uint64_t seed, int layer) {
     if (mhip::check_dims(c, s) || mhip::use_device(c)) return -1;
     const size_t n = (size_t)s->dim * s->n_experts;
     const uint64_t key = mia_synth_key(seed, MIA_STREAM_ROUTER + (uint64_t)layer);
-    k_router_synth<<<mhip::blocks_for(n, 256), 256, 0, c->stream>>>(d_router_t, s->dim,
+    k_router_synth<<<mhip::blocks_for(n, 256), 256, 0, c->stream>>>(d_router_t, d_router, s->dim,
                                                                      s->n_experts, key);
     return mhip::check_launch(c, "router_synth");
 }

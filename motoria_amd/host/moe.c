@@ -17,6 +17,10 @@ struct mia_moe {
     size_t blob_bytes, off_up, off_down;
     void *d_table;      /* [L][E] experts, lay.expert_bytes apart */
     float *d_router_t;  /* [L][dim][E] */
+    float *d_router_rm; /* [L][E][dim] */
+    void *d_dws;        /* persistent decode workspace */
+    int *d_didx;        /* [L][K] routing of the last decode-stack call */
+    float *d_dw;        /* [L][K] */
     float *d_norm;      /* [L][dim] */
     float *d_router;    /* [E][dim] upload staging */
     void *d_scratch;
@@ -54,6 +58,10 @@ void mia_moe_close(mia_moe *m) {
         mhip_sync(m->gpu);
         mhip_free(m->gpu, m->d_table);
         mhip_free(m->gpu, m->d_router_t);
+        mhip_free(m->gpu, m->d_router_rm);
+        mhip_free(m->gpu, m->d_dws);
+        mhip_free(m->gpu, m->d_didx);
+        mhip_free(m->gpu, m->d_dw);
         mhip_free(m->gpu, m->d_norm);
         mhip_free(m->gpu, m->d_router);
         mhip_free(m->gpu, m->d_scratch);
@@ -104,6 +112,10 @@ int mia_moe_open(mia_moe **out, const mia_moe_config *cfg, char *err, size_t err
         const size_t scratch = mhip_scratch_bytes(&m->dims, cfg->max_tokens);
         m->d_table = mhip_malloc(m->gpu, table);
         m->d_router_t = mhip_malloc(m->gpu, (size_t)cfg->n_layers * d * E * 4);
+        m->d_router_rm = mhip_malloc(m->gpu, (size_t)cfg->n_layers * d * E * 4);
+        m->d_dws = mhip_malloc(m->gpu, mhip_decode_ws_bytes());
+        m->d_didx = mhip_malloc(m->gpu, (size_t)cfg->n_layers * cfg->n_active * 4);
+        m->d_dw = mhip_malloc(m->gpu, (size_t)cfg->n_layers * cfg->n_active * 4);
         m->d_norm = mhip_malloc(m->gpu, (size_t)cfg->n_layers * d * 4);
         m->d_router = mhip_malloc(m->gpu, d * E * 4);
         m->d_scratch = mhip_malloc(m->gpu, scratch);
@@ -111,8 +123,9 @@ int mia_moe_open(mia_moe **out, const mia_moe_config *cfg, char *err, size_t err
         m->d_bias = mhip_malloc(m->gpu, E * 4);
         m->d_blob = mhip_malloc(m->gpu, m->blob_bytes);
         m->h_blob = malloc(m->blob_bytes);
-        if (!m->d_table || !m->d_router_t || !m->d_norm || !m->d_router || !m->d_scratch ||
-            !m->d_x || !m->d_bias || !m->d_blob)
+        if (!m->d_table || !m->d_router_t || !m->d_router_rm || !m->d_dws || !m->d_didx ||
+            !m->d_dw || !m->d_norm || !m->d_router || !m->d_scratch || !m->d_x || !m->d_bias ||
+            !m->d_blob)
             rc = fail(m, "HBM allocation (%.2f GiB table): %s", table / 1073741824.0,
                       mhip_error(m->gpu));
         else if (!m->h_blob)
@@ -122,6 +135,7 @@ int mia_moe_open(mia_moe **out, const mia_moe_config *cfg, char *err, size_t err
             if (mhip_zero(m->gpu, m->sc.status, 16) ||
                 mhip_zero(m->gpu, m->d_table, table) ||
                 mhip_zero(m->gpu, m->d_router_t, (size_t)cfg->n_layers * d * E * 4) ||
+                mhip_zero(m->gpu, m->d_router_rm, (size_t)cfg->n_layers * d * E * 4) ||
                 mhip_fill_f32(m->gpu, m->d_norm, (size_t)cfg->n_layers * d, 1.0f) ||
                 mhip_sync(m->gpu))
                 rc = gpu_fail(m);
@@ -177,6 +191,7 @@ int mia_moe_set_layer(mia_moe *m, int layer, const float *ffn_norm, const float 
     const size_t d = (size_t)m->dims.dim, E = (size_t)m->dims.n_experts;
     if (mhip_h2d(m->gpu, m->d_norm + layer * d, ffn_norm, d * 4) ||
         mhip_h2d(m->gpu, m->d_router, router, d * E * 4) ||
+        mhip_d2d(m->gpu, m->d_router_rm + layer * d * E, m->d_router, d * E * 4) ||
         mhip_router_transpose(m->gpu, &m->dims, m->d_router_t + layer * d * E, m->d_router) ||
         mhip_sync(m->gpu))
         return gpu_fail(m);
@@ -187,7 +202,8 @@ int mia_moe_synth(mia_moe *m, uint64_t seed) {
     const size_t d = (size_t)m->dims.dim, E = (size_t)m->dims.n_experts;
     if (mhip_table_synth(m->gpu, &m->dims, m->d_table, seed, 0, m->n_layers)) return gpu_fail(m);
     for (int l = 0; l < m->n_layers; l++)
-        if (mhip_router_synth(m->gpu, &m->dims, m->d_router_t + l * d * E, seed, l))
+        if (mhip_router_synth(m->gpu, &m->dims, m->d_router_t + l * d * E,
+                              m->d_router_rm + l * d * E, seed, l))
             return gpu_fail(m);
     if (mhip_fill_f32(m->gpu, m->d_norm, (size_t)m->n_layers * d, 1.0f) || mhip_sync(m->gpu))
         return gpu_fail(m);
@@ -216,6 +232,47 @@ int mia_moe_stack_dev(mia_moe *m, int l0, int l1, float *d_x, int T) {
         return fail(m, "layer range [%d, %d) outside [0, %d)", l0, l1, m->n_layers);
     for (int l = l0; l < l1; l++)
         if (run_layer(m, l, d_x, T, NULL)) return -1;
+    return 0;
+}
+
+int mia_moe_decode_dev(mia_moe *m, int l0, int l1, float *d_x, const float *d_bias) {
+    if (l0 < 0 || l1 > m->n_layers || l0 > l1)
+        return fail(m, "layer range [%d, %d) outside [0, %d)", l0, l1, m->n_layers);
+    const size_t d = (size_t)m->dims.dim, E = (size_t)m->dims.n_experts,
+                 K = (size_t)m->dims.n_active;
+    if (mhip_decode_stack(m->gpu, &m->dims, &m->lay,
+                          (const unsigned char *)m->d_table + (size_t)l0 * E * m->lay.expert_bytes,
+                          m->d_router_rm + l0 * d * E, m->d_router_t + l0 * d * E,
+                          m->d_norm + l0 * d, d_bias, d_x, l1 - l0, m->d_dws, m->d_didx + l0 * K,
+                          m->d_dw + l0 * K, m->flags))
+        return gpu_fail(m);
+    return 0;
+}
+
+int mia_moe_decode_status(mia_moe *m, int status[4]) {
+    if (mhip_decode_status(m->gpu, m->d_dws, status)) return gpu_fail(m);
+    return 0;
+}
+
+int mia_moe_decode_trace(mia_moe *m, unsigned long long *out) {
+    if (mhip_decode_trace(m->gpu, m->d_dws, out)) return gpu_fail(m);
+    return 0;
+}
+
+int mia_moe_decode(mia_moe *m, int l0, int l1, float *x, const float *bias, int *idx, float *w) {
+    const size_t d = (size_t)m->dims.dim, E = (size_t)m->dims.n_experts,
+                 K = (size_t)m->dims.n_active;
+    if (mhip_h2d(m->gpu, m->d_x, x, d * 4)) return gpu_fail(m);
+    if (bias && mhip_h2d(m->gpu, m->d_bias, bias, E * 4)) return gpu_fail(m);
+    if (mia_moe_decode_dev(m, l0, l1, m->d_x, bias ? m->d_bias : NULL)) return -1;
+    int st[4];
+    if (mhip_sync(m->gpu) || mhip_decode_status(m->gpu, m->d_dws, st)) return gpu_fail(m);
+    if (st[0]) return fail(m, "decode stack aborted (status %d: %s)", st[0],
+                           (st[0] & 1) ? "workgroups not on the expected XCDs" : "a wait timed out");
+    if (mhip_d2h(m->gpu, x, m->d_x, d * 4) ||
+        (idx && mhip_d2h(m->gpu, idx, m->d_didx + l0 * K, (size_t)(l1 - l0) * K * 4)) ||
+        (w && mhip_d2h(m->gpu, w, m->d_dw + l0 * K, (size_t)(l1 - l0) * K * 4)))
+        return gpu_fail(m);
     return 0;
 }
 

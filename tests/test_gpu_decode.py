@@ -1,0 +1,139 @@
+"""GPU parity of the persistent decode-stack kernel (one token, many layers).
+
+Expert indices must be bit-equal to the oracle; the layer outputs must be
+within the north-star tolerance (max|diff| / max|ref| <= 1e-3; the kernel's
+gate weights come from the parallel router logits, so ~1e-6 is expected).
+With the exact router forced, the output must be bit-equal to the oracle.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import motoria_amd as M
+from motoria_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+LAYERS = 6
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
+
+
+@pytest.fixture(scope="module")
+def moe():
+    say("open decode handle: %d layers" % LAYERS)
+    m = M.Moe(n_layers=LAYERS, max_tokens=4, device=0, **W.SHAPE)
+    m.synth(W.WEIGHT_SEED)
+    m.sync()
+    yield m
+    m.close()
+
+
+def run_oracle_layer(O, moe, d, layer, x, bias=None):
+    router = O.synth_router(W.WEIGHT_SEED, layer, d)
+    norm = np.ones(d.dim, np.float32)
+    x1 = np.array(x, np.float32).reshape(1, -1)
+    # the oracle's own routing prologue tells which experts to fetch
+    xn = O.rmsnorm(x1[0], norm, d.norm_eps)
+    lg = O.matvec(router, 0, xn, d.n_experts, d.dim)
+    if bias is not None:
+        lg = (lg + bias).astype(np.float32)
+    idx, _, _ = O.route(lg, d.n_active)
+    blobs = [None] * d.n_experts
+    for e in idx.tolist():
+        blobs[e] = moe.read_expert(layer, e)
+    return O.moe_layer(d, x1, norm, router, blobs, bias=bias)
+
+
+def test_decode_layer_by_layer_matches_oracle(oracle, qwen_dims, moe):
+    say("test_decode_layer_by_layer_matches_oracle")
+    d = qwen_dims
+    x = oracle.synth_x(W.X_SEED, 1, d.dim)[0]
+    worst = 0.0
+    for l in range(LAYERS):
+        xo, io, wo, _, _ = run_oracle_layer(oracle, moe, d, l, x)
+        xg, ig, wg = moe.decode(l, l + 1, x)
+        st = moe.decode_status()
+        assert st[0] == 0, "decode aborted: %s" % st
+        assert np.array_equal(ig[0], io[0]), "layer %d: expert indices %s vs %s" % (l, ig[0], io[0])
+        e_out = rel(xg - x, xo[0] - x)
+        e_w = rel(wg[0], wo[0])
+        worst = max(worst, e_out)
+        say("  layer %d: idx %s  rel err delta %.2e  w %.2e  status %s" % (l, ig[0].tolist(), e_out,
+                                                                           e_w, st))
+        assert e_out <= TOL and e_w <= TOL
+        x = xo[0]
+    say("  worst rel err %.2e" % worst)
+
+
+def test_decode_full_stack_matches_oracle(oracle, qwen_dims, moe):
+    say("test_decode_full_stack_matches_oracle")
+    d = qwen_dims
+    x0 = oracle.synth_x(W.X_SEED + 7, 1, d.dim)[0]
+    xg, ig, wg = moe.decode(0, LAYERS, x0)
+    assert moe.decode_status()[0] == 0
+    x = x0
+    for l in range(LAYERS):
+        xo, io, _, _, _ = run_oracle_layer(oracle, moe, d, l, x)
+        assert np.array_equal(ig[l], io[0]), "layer %d routing differs" % l
+        x = xo[0]
+    e = rel(xg - x0, x - x0)
+    say("  %d-layer stack rel err %.2e" % (LAYERS, e))
+    assert e <= TOL
+
+
+def test_decode_exact_router_is_bit_equal(oracle, qwen_dims, moe):
+    say("test_decode_exact_router_is_bit_equal")
+    d = qwen_dims
+    x = oracle.synth_x(W.X_SEED + 11, 1, d.dim)[0]
+    moe.set_flags(M.MHIP_FORCE_EXACT_ROUTER)
+    try:
+        for l in range(2):
+            xo, io, wo, _, _ = run_oracle_layer(oracle, moe, d, l, x)
+            xg, ig, wg = moe.decode(l, l + 1, x)
+            st = moe.decode_status()
+            assert st[0] == 0 and st[2] >= 1, st
+            assert np.array_equal(ig[0], io[0])
+            assert np.array_equal(wg[0].view(np.uint32), wo[0].view(np.uint32))
+            assert np.array_equal(xg.view(np.uint32), xo[0].view(np.uint32)), \
+                "layer %d rel err %.2e" % (l, rel(xg - x, xo[0] - x))
+            x = xo[0]
+    finally:
+        moe.set_flags(0)
+
+
+def test_decode_forced_sequential_rmsnorm(oracle, qwen_dims, moe):
+    say("test_decode_forced_sequential_rmsnorm")
+    x = oracle.synth_x(W.X_SEED + 13, 1, qwen_dims.dim)[0]
+    a = moe.decode(0, 3, x)
+    moe.set_flags(M.MHIP_FORCE_SEQ_RMS)
+    try:
+        b = moe.decode(0, 3, x)
+        assert moe.decode_status()[1] >= 3
+    finally:
+        moe.set_flags(0)
+    for u, v in zip(a, b):
+        assert np.array_equal(np.asarray(u).view(np.uint32), np.asarray(v).view(np.uint32))
+
+
+def test_decode_with_bias_and_repeats(oracle, qwen_dims, moe):
+    say("test_decode_with_bias_and_repeats")
+    d = qwen_dims
+    bias = W.zipf_bias(d.n_experts)
+    x = oracle.synth_x(W.X_SEED + 17, 1, d.dim)[0]
+    xo, io, _, _, _ = run_oracle_layer(oracle, moe, d, 0, x, bias=bias)
+    for rep in range(3):  # repeated launches reuse the workspace
+        xg, ig, _ = moe.decode(0, 1, x, bias=bias)
+        assert np.array_equal(ig[0], io[0])
+        assert rel(xg - x, xo[0] - x) <= TOL
