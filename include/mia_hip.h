@@ -163,9 +163,14 @@ int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
                       const float *d_norm, const float *d_bias, float *d_x, int L,
                       void *d_ws, int *d_idx, float *d_w, int flags);
 int mhip_decode_status(mhip_ctx *c, const void *d_ws, int status[4]);
-/* With MHIP_DECODE_TRACE set: the 100 MHz real-time counter at 12 stage
- * boundaries of the first 64 layers, for workgroups 0 and 1
- * (out[2][64][12]). Diagnostic. */
+/* With MHIP_DECODE_TRACE set: the 100 MHz real-time counter read by thread 0
+ * of each of the 256 workgroups at up to MHIP_TRACE_SLOTS stage boundaries
+ * of layers MHIP_TRACE_L0 .. MHIP_TRACE_L0 + MHIP_TRACE_NL - 1
+ * (out[MHIP_TRACE_NL][256][MHIP_TRACE_SLOTS]; slots not reached stay 0).
+ * Diagnostic. */
+#define MHIP_TRACE_L0 8
+#define MHIP_TRACE_NL 8
+#define MHIP_TRACE_SLOTS 16
 int mhip_decode_trace(mhip_ctx *c, const void *d_ws, unsigned long long *out);
 
 /* ---- reference tensor ops on device pointers ---------------------------- */

@@ -25,6 +25,7 @@ _u64 = ctypes.c_uint64
 MHIP_FORCE_SEQ_RMS = 1
 MHIP_FORCE_EXACT_ROUTER = 2
 MHIP_DECODE_TRACE = 4
+TRACE_L0, TRACE_NL, TRACE_SLOTS = 8, 8, 16  # decode trace window (MHIP_TRACE_* in mia_hip.h)
 STAGES = ["rmsnorm", "router", "dispatch", "gateup", "down", "combine", "decode"]
 
 
@@ -275,7 +276,7 @@ class Moe:
         return x, idx, w
 
     def decode_trace(self):
-        out = np.zeros((2, 64, 12), dtype=np.uint64)
+        out = np.zeros((TRACE_NL, 256, TRACE_SLOTS), dtype=np.uint64)
         self._check(lib().mia_moe_decode_trace(self.h, out.ctypes.data), "mia_moe_decode_trace")
         return out
 

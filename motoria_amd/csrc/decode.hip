@@ -11,13 +11,20 @@
 // (tiny) router and top-K itself, so the only cross-XCD traffic per layer is
 // the K expert outputs (K x 8 KB) gathered by the combine.
 //
+// Inside a workgroup the waves have two roles. Waves 0-3 stream the gate/up
+// rows and finish their h values without a workgroup barrier. Waves 4-7 hold
+// the workgroup's down rows and the next layer's router rows in registers:
+// they issue those loads during the gate/up pass and never wait for them at a
+// synchronisation, so the h exchange overlaps the rest of the weight stream.
+//
 // Per layer, on every XCD:
 //   A  x (8 KB) -> certified rmsnorm -> xn, Q8(xn) in LDS; 4 router logits per
-//      workgroup by a parallel sum with a rigorous bound on the distance to
-//      the reference's sequential fp32 chain                 [XCD sync]
-//   B  all 128 logits -> top-K + certification -> gate weights (if the
-//      ordering is not certified, the exact sequential logits are computed
-//      and routing follows the reference bit for bit)
+//      workgroup (one per down wave) by a parallel sum with a rigorous bound
+//      on the distance to the reference's sequential fp32 chain  [XCD sync]
+//   B  all 128 logits -> ranks (LDS, 512 threads) -> top-K + certification
+//      -> gate weights (if the ordering is not certified, the exact
+//      sequential logits are computed and routing follows the reference bit
+//      for bit)
 //   C  gate/up rows of expert idx[k] + SwiGLU -> h (768 floats) [XCD sync]
 //      (the down rows and the next layer's router rows are loaded meanwhile)
 //   D  Q8(h) -> down rows -> the expert's output rows, published device-wide
@@ -43,11 +50,14 @@ constexpr int NT = 512;          // threads per workgroup
 constexpr int NWAVE = NT / 64;
 constexpr int D = 2048, E = 128, EH = 768, KMAX = 8;
 constexpr int NB = D / 32, NBH = EH / 32;
-constexpr int HROWS = EH / WPX;             // 24 h rows per workgroup
-constexpr int GU_RW = 2 * HROWS / NWAVE;    // 6 weight rows per wave (3 gate, 3 up)
-constexpr int DROWS = D / WPX;              // 64 down rows per workgroup
-constexpr int DPK = DROWS * NBH / NT;       // 3 (row, block) pairs per thread
-constexpr int LPW = E / WPX;                // 4 logits per workgroup
+constexpr int HROWS = EH / WPX;                 // 24 h rows per workgroup
+constexpr int DROWS = D / WPX;                  // 64 down rows per workgroup
+constexpr int LPW = E / WPX;                    // 4 logits per workgroup
+constexpr int NGU = 4;                          // waves 0..3: gate/up
+constexpr int NDN = NWAVE - NGU;                // waves 4..7: down + router rows
+constexpr int GU_H = HROWS / NGU;               // 6 h rows per gate/up wave
+constexpr int GU_R = 2 * GU_H;                  // its 12 weight rows
+constexpr int DPK = DROWS * NBH / (NDN * 64);   // 6 (row, block) pairs per down thread
 constexpr long SPIN = 1L << 18;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -57,20 +67,22 @@ __device__ __forceinline__ int4 ld_stream(const void *p) {
 }
 
 static_assert(NB == 64, "one 32-block per lane");
-static_assert(GU_RW * NWAVE == 2 * HROWS && DPK * NT == DROWS * NBH, "tiling");
+static_assert(LPW == NDN, "one router row per down wave");
+static_assert(GU_H * NGU == HROWS && DPK * NDN * 64 == DROWS * NBH, "tiling");
+static_assert(NT == 4 * E, "ranks: four threads per expert");
 
 struct DecodeWs {
     unsigned gstart[64];          // start barrier (device scope)
     unsigned cnt[NX][64];         // intra-XCD counters, monotonic
     unsigned tflag[NWG][16];      // expert-output rows published (layer + 1)
-    unsigned xflag[NX][16];       // exact logits published (layer + 1)
     int status[16];               // [0] abort bits, [1] rms fallbacks, [2] router fallbacks
     float x[NX][D];
     double lg[NX][E][2];          // parallel logit sum S and bound B
     float lx[NX][E];              // exact logits (fallback)
     float h[NX][EH];
     float out[2][KMAX][D];        // expert outputs, double-buffered by layer parity
-    unsigned long long trace[2][64][12];  // stage timestamps of two workgroups (diagnostic)
+    // stage timestamps of every workgroup for layers MHIP_TRACE_L0 .. +MHIP_TRACE_NL (diagnostic)
+    unsigned long long trace[MHIP_TRACE_NL][NWG][MHIP_TRACE_SLOTS];
 };
 
 struct DecodeArgs {
@@ -116,14 +128,22 @@ __device__ __forceinline__ bool aborted(DecodeWs *ws) {
     return ld_dev((const unsigned *)&ws->status[0]) != 0;
 }
 
-// All of this workgroup's stores complete, then one arrival on the XCD
-// counter; wait until all WPX workgroups of the XCD arrived `phase` times.
-__device__ void xcd_sync(DecodeWs *ws, int xcd, unsigned phase) {
-    __builtin_amdgcn_s_waitcnt(0);
+// One arrival of this workgroup on the XCD counter, then wait until all WPX
+// workgroups of the XCD arrived `phase` times. Waves with `drain` set first
+// wait for all their memory operations (their stores become visible before
+// the arrival); waves without it keep their loads in flight (they must have
+// stored nothing that other workgroups read after this sync).
+// The sync is split in two halves so that work which depends on no other
+// workgroup can run between the arrival and the wait.
+__device__ void xcd_arrive(DecodeWs *ws, int xcd, bool drain) {
+    if (drain) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(&ws->cnt[xcd][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ void xcd_wait(DecodeWs *ws, int xcd, unsigned phase) {
     if (threadIdx.x == 0) {
-        unsigned *c = &ws->cnt[xcd][0];
-        __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const unsigned *c = &ws->cnt[xcd][0];
         long s = 0;
         while (ld_dev(c) < phase * WPX) {
             if (++s > SPIN || ((s & 255) == 0 && aborted(ws))) {
@@ -134,6 +154,10 @@ __device__ void xcd_sync(DecodeWs *ws, int xcd, unsigned phase) {
     }
     __syncthreads();
 }
+__device__ void xcd_sync(DecodeWs *ws, int xcd, unsigned phase, bool drain) {
+    xcd_arrive(ws, xcd, drain);
+    xcd_wait(ws, xcd, phase);
+}
 
 __device__ void wait_flag(DecodeWs *ws, const unsigned *flag, unsigned value) {
     long s = 0;
@@ -143,6 +167,15 @@ __device__ void wait_flag(DecodeWs *ws, const unsigned *flag, unsigned value) {
             break;
         }
     }
+}
+
+// Orders LDS traffic between the lanes of one wavefront (LDS operations of a
+// wavefront execute in program order; this keeps the compiler from moving
+// them across the point).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // Wavefront-wide inclusive prefix sum with DPP (row_shr 1/2/4/8 inside each
@@ -185,32 +218,15 @@ __device__ __forceinline__ double wave_max_d(double v) {
     v = fmax(v, dpp_keep_d<0x143, 0xc>(v));
     return lane63_d(v);
 }
-__device__ __forceinline__ float lanef(float v, int lane) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
-__device__ __forceinline__ double laned(double v, int lane) {
-    return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), lane),
-                            __builtin_amdgcn_readlane(__double2loint(v), lane));
-}
-
-// One round of "largest untaken value, lowest index on ties" over the 128
-// values held two per lane (v0 for index lane, v1 for index lane + 64), in
-// one wavefront. Returns the winning index (uniform); -1 if none (all taken
-// or NaN).
-__device__ __forceinline__ int wave_argmax_d(double v0, double v1, bool t0, bool t1, int lane) {
-    const double ninf = -__builtin_inf();
-    const double a0 = t0 ? ninf : v0, a1 = t1 ? ninf : v1;
-    const double m = wave_max_d(fmax(a0, a1));
-    const unsigned long long lo = __ballot(!t0 && a0 == m);
-    if (lo) return __builtin_ctzll(lo);
-    const unsigned long long hi = __ballot(!t1 && a1 == m);
-    if (hi) return 64 + __builtin_ctzll(hi);
-    return -1;
-}
 
 __device__ __forceinline__ float wave_sum_f(float v) {
     // through double: exact for the wave-wide sum of 64 floats' partials
     return (float)lane63_d(wave_scan_d((double)v));
+}
+
+__device__ __forceinline__ float4 i4_as_f4(const int4 v) {
+    return make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z),
+                       __int_as_float(v.w));
 }
 
 // LDS. `scr` is reused by stages that never overlap: the exact-router
@@ -219,7 +235,8 @@ __device__ __forceinline__ float wave_sum_f(float v) {
 constexpr int GU_LD = NB + 4;     // 16-byte aligned rows
 constexpr int DN_LD = NBH + 4;
 constexpr int SCR = 8192;         // floats
-static_assert(NWAVE * GU_RW * GU_LD <= SCR && DROWS * DN_LD <= SCR && LPW * D <= SCR, "scr");
+static_assert(NGU * GU_R * GU_LD <= SCR && DROWS * DN_LD <= SCR && LPW * D <= SCR &&
+              DROWS * KMAX <= SCR, "scr");
 
 struct Lds {
     alignas(16) float x[D];
@@ -230,20 +247,25 @@ struct Lds {
     alignas(16) int8_t hq[EH];
     float xs[NB];
     float hsc[NBH];
-    float gu[NWAVE][GU_RW];
-    alignas(16) float p[E];       // probabilities (or exp values)
-    float lf[E];                  // fp32 logits
-    double c[E];                  // ranking centre of each logit
+    float gu[NGU][GU_R];
+    alignas(16) uint64_t key[E];  // ranking key: S + bias made monotone, expert index in the low bits
+    double c[E];                  // S + bias
     double r[E];                  // its bound
-    double part[NT];
-    double wtot[LPW][64];
-    double wabs[LPW][64];
-    int order[KMAX + 1];
+    double bmax;
+    float lf[E];                  // fp32 logits (+ bias)
+    alignas(16) float p[E];       // probabilities (fallback)
+    float bias[E];
+    uint64_t etab[32];            // expf table
+    int rk[4][E];                 // partial ranks
+    double part[NWAVE];
+    int order[E];                 // expert of each rank (ranks 0..K used)
+    float pk[KMAX];
     float inv;
     float sum;
     int idx[KMAX];
     float w[KMAX];
     int fallback;
+    int nanflag;
 };
 
 // Sequential fp32 sum of n (multiple of 4) LDS floats starting at p, in
@@ -261,21 +283,53 @@ __device__ __forceinline__ float lds_seq_sum(const float *p, int n, float s) {
     return s;
 }
 
-// Diagnostic: workgroups 0 and 1 (XCDs 0 and 1) record the 100 MHz real-time
-// counter at each stage boundary of the first 64 layers.
-#define TRACE(slot)                                                                       \
-    do {                                                                                  \
-        if ((a.flags & MHIP_DECODE_TRACE) && blockIdx.x < 2 && tid == 0 && l < 64)       \
-            ws->trace[blockIdx.x][l][slot] = __builtin_amdgcn_s_memrealtime();            \
+// Q8_0 of one 32-block (quant.c:11-27) from LDS into LDS.
+__device__ __forceinline__ void q8_block(const float *src, int8_t *dst, float *dscale) {
+    const float4 *v4 = (const float4 *)src;
+    float v[32];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const float4 q = v4[k];
+        v[4 * k] = q.x;
+        v[4 * k + 1] = q.y;
+        v[4 * k + 2] = q.z;
+        v[4 * k + 3] = q.w;
+    }
+    float am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) am = fmaxf(am, fabsf(v[i]));
+    const float d = am / 127.0f;
+    const float qi = d != 0.0f ? 1.0f / d : 0.0f;
+    union {
+        int8_t c[32];
+        int4 v4[2];
+    } q;
+#pragma unroll
+    for (int i = 0; i < 32; i++) q.c[i] = (int8_t)roundf(v[i] * qi);
+    ((int4 *)dst)[0] = q.v4[0];
+    ((int4 *)dst)[1] = q.v4[1];
+    *dscale = d;
+}
+
+// Diagnostic: thread 0 of every workgroup records the 100 MHz real-time
+// counter at the stage boundaries of a window of layers.
+#define TRACE(slot)                                                                        \
+    do {                                                                                   \
+        if ((a.flags & MHIP_DECODE_TRACE) && tid == 0 && l >= MHIP_TRACE_L0 &&             \
+            l < MHIP_TRACE_L0 + MHIP_TRACE_NL)                                             \
+            ws->trace[l - MHIP_TRACE_L0][blockIdx.x][slot] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
 
 __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
     __shared__ Lds sh;
     DecodeWs *ws = a.ws;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int xcd = blockIdx.x % NX, rank = blockIdx.x / NX;
     const int K = a.K;
+    const int need = K < E ? K + 1 : K;     // ranks certified: K and the first not taken
     const size_t layer_bytes = (size_t)E * a.lay.expert_bytes;
+    const bool gu_wave = wave < NGU;
 
     // Start: every workgroup checks its XCD, then a device-wide barrier.
     if (tid == 0) {
@@ -288,24 +342,48 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
     if (aborted(ws)) return;
 
     unsigned phase = 0;
-    // Router rows of this workgroup's logits (waves 0..LPW-1), next layer first.
-    float4 rrow[8];
+    // One register array serves both roles. A gate/up wave holds its GU_R
+    // weight rows in wq0/wq1/wsc during stage C. A down wave holds its DPK
+    // down (row, block) pairs in slots 0..DPK-1 from stage C to D, and the
+    // router row of its logit (8 x 16 bytes per lane, as int bits) in the
+    // slots above: wq0[DPK..GU_R), then wq1[DPK..). Sharing the registers
+    // keeps the compiler from copying loads still in flight (which would wait
+    // for them) where the two roles' code paths meet.
+    constexpr int NR0 = GU_R - DPK;
+    static_assert(2 * NR0 >= 8, "router row slots");
+    int4 wq0[GU_R], wq1[GU_R];
+    float wsc[GU_R];
 #define LOAD_ROUTER(layer)                                                                 \
     do {                                                                                   \
-        if (wave < LPW) {                                                                  \
-            const float4 *src_ = (const float4 *)(a.router +                               \
-                                                  ((size_t)(layer) * E + rank * LPW + wave) * D + \
-                                                  lane * 32);                              \
-            _Pragma("unroll") for (int k_ = 0; k_ < 8; k_++) rrow[k_] = src_[k_];          \
-        }                                                                                  \
+        const int4 *src_ = (const int4 *)(a.router +                                       \
+                                          ((size_t)(layer) * E + rank * LPW + wave - NGU) * D + \
+                                          lane * 32);                                      \
+        _Pragma("unroll") for (int k_ = 0; k_ < NR0; k_++) wq0[DPK + k_] = src_[k_];       \
+        _Pragma("unroll") for (int k_ = 0; k_ < 8 - NR0; k_++) wq1[DPK + k_] = src_[NR0 + k_]; \
     } while (0)
-    LOAD_ROUTER(0);
+#define RROW(k)                                                                            \
+    i4_as_f4((k) < NR0 ? wq0[DPK + ((k) < NR0 ? (k) : 0)] : wq1[DPK + ((k) < NR0 ? 0 : (k) - NR0)])
+    // rmsnorm weights of the next layer at this thread's 4 positions.
+    float wn[D / NT];
+#define LOAD_NORM(layer)                                                                   \
+    do {                                                                                   \
+        _Pragma("unroll") for (int k_ = 0; k_ < D / NT; k_++)                              \
+            wn[k_] = a.norm[(size_t)(layer) * D + tid + NT * k_];                          \
+    } while (0)
+    if (!gu_wave) LOAD_ROUTER(0);
+    LOAD_NORM(0);
     for (int i = tid; i < D; i += NT) sh.x[i] = a.x[i];
+    if (tid < E) sh.bias[tid] = a.bias ? a.bias[tid] : 0.0f;
+    if (tid < 32) sh.etab[tid] = mia_expf_tab[tid];
 
     for (int l = 0; l < a.L; l++) {
-        const float *wnorm = a.norm + (size_t)l * D;
+        // Per-thread addresses are recomputed in every layer rather than held
+        // in registers across the loop (the thread index is made opaque).
+        asm volatile("" : "+v"(tid));
+        lane = tid & 63;
+        const int dt = tid - NGU * 64;          // index among the down waves' threads
         TRACE(0);
-        // ---- A: rmsnorm (certified), xn, Q8(xn) -----------------------------------
+        // ---- A: rmsnorm (certified), xn, Q8(xn), logits -----------------------------
         __syncthreads();
         {
             double ss = 0.0;
@@ -334,6 +412,7 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                 if (blockIdx.x == 0) atomicAdd(&ws->status[1], 1);
             }
             sh.inv = inv;
+            sh.nanflag = 0;
         }
         __syncthreads();
         {
@@ -341,48 +420,20 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
 #pragma unroll
             for (int k = 0; k < D / NT; k++) {
                 const int i = tid + NT * k;
-                sh.xn[i] = (sh.x[i] * inv) * wnorm[i];
+                sh.xn[i] = (sh.x[i] * inv) * wn[k];
             }
         }
         __syncthreads();
-        if (tid < NB) {
-            // Q8_0 of one 32-block (quant.c:11-27)
-            const float4 *v4 = (const float4 *)&sh.xn[tid * 32];
-            float v[32];
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const float4 q = v4[k];
-                v[4 * k] = q.x;
-                v[4 * k + 1] = q.y;
-                v[4 * k + 2] = q.z;
-                v[4 * k + 3] = q.w;
-            }
-            float am = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 32; i++) am = fmaxf(am, fabsf(v[i]));
-            const float dsc = am / 127.0f;
-            const float qi = dsc != 0.0f ? 1.0f / dsc : 0.0f;
-            union {
-                int8_t c[32];
-                int4 v4[2];
-            } q;
-#pragma unroll
-            for (int i = 0; i < 32; i++) q.c[i] = (int8_t)roundf(v[i] * qi);
-            ((int4 *)&sh.xq[tid * 32])[0] = q.v4[0];
-            ((int4 *)&sh.xq[tid * 32])[1] = q.v4[1];
-            sh.xs[tid] = dsc;
-        }
+        if (tid < NB) q8_block(&sh.xn[tid * 32], &sh.xq[tid * 32], &sh.xs[tid]);
         // Parallel logits with a bound. The reference's logit is the
         // sequential fp32 chain over p_i = fl(W_ei * xn_i); S = sum p_i in
         // double, and |chain - S| <= 2^-24 * sum_k |S_k| (S_k the prefix sums).
-        // p_i = fl(W_ei * xn_i) for this lane's 32 elements (recomputed in the
-        // second pass rather than held across the barrier)
-        if (wave < LPW) {
+        if (!gu_wave) {
             const float4 *xv4 = (const float4 *)&sh.xn[lane * 32];
             double tot = 0.0;
 #pragma unroll
             for (int k = 0; k < 8; k++) {
-                const float4 wv = rrow[k], xv = xv4[k];
+                const float4 wv = RROW(k), xv = xv4[k];
                 tot = tot + (double)(wv.x * xv.x);
                 tot = tot + (double)(wv.y * xv.y);
                 tot = tot + (double)(wv.z * xv.z);
@@ -393,7 +444,7 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             double absum = 0.0;
 #pragma unroll
             for (int k = 0; k < 8; k++) {
-                const float4 wv = rrow[k], xv = xv4[k];
+                const float4 wv = RROW(k), xv = xv4[k];
                 run = run + (double)(wv.x * xv.x);
                 absum = absum + fabs(run);
                 run = run + (double)(wv.y * xv.y);
@@ -406,113 +457,104 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             const double S = lane63_d(incl);
             const double A = lane63_d(wave_scan_d(absum));
             if (lane == 0) {
-                const int e = rank * LPW + wave;
+                const int e = rank * LPW + wave - NGU;
                 st_devd(&ws->lg[xcd][e][0], S);
                 st_devd(&ws->lg[xcd][e][1], A * 0x1p-24 * (1.0 + 0x1p-8) + 1e-30);
             }
         }
         TRACE(1);
-        xcd_sync(ws, xcd, ++phase);
+        xcd_sync(ws, xcd, ++phase, true);
         TRACE(2);
 
-        // ---- B: top-K, certification, gate weights (wavefront 0, registers) --------
+        // ---- B: ranks, certification ------------------------------------------------
+        if (tid < E) {
+            const double S = ld_devd(&ws->lg[xcd][tid][0]);
+            const double B = ld_devd(&ws->lg[xcd][tid][1]);
+            const float bs = sh.bias[tid];
+            const double c = S + (double)bs;
+            // monotone 64-bit image of c with the low 7 bits replaced by
+            // 127 - e: distinct keys, lower index first among (near-)equal
+            // values; an order that differs from c's fails the gap test below
+            uint64_t u = (uint64_t)__double_as_longlong(c);
+            u = (u >> 63) ? ~u : (u | (1ull << 63));
+            sh.key[tid] = ((u >> 7) << 7) | (uint64_t)(E - 1 - tid);
+            sh.c[tid] = c;
+            sh.r[tid] = B;
+            sh.lf[tid] = a.bias ? (float)S + bs : (float)S;
+            if (c != c) sh.nanflag = 1;
+        }
+        __syncthreads();
+        TRACE(10);
+        {
+            // rank of expert e among the 32 keys of quarter q
+            const int e = tid & (E - 1), q = tid >> 7;
+            const uint64_t ke = sh.key[e];
+            const ulonglong2 *kv = (const ulonglong2 *)&sh.key[q * 32];
+            int rk = 0;
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const ulonglong2 v = kv[k];
+                rk += (int)(v.x > ke) + (int)(v.y > ke);
+            }
+            sh.rk[q][e] = rk;
+            if (wave == 0) {
+                const double bm = wave_max_d(fmax(sh.r[lane], sh.r[lane + 64]));
+                if (lane == 0) sh.bmax = bm;
+            }
+        }
+        __syncthreads();
+        if (tid < E) {
+            const int rk = sh.rk[0][tid] + sh.rk[1][tid] + sh.rk[2][tid] + sh.rk[3][tid];
+            if (rk < need) sh.order[rk] = tid;
+        }
+        __syncthreads();
+        TRACE(11);
         if (wave == 0) {
-            // lane holds experts lane and lane + 64
-            const double S0 = ld_devd(&ws->lg[xcd][lane][0]);
-            const double S1 = ld_devd(&ws->lg[xcd][lane + 64][0]);
-            const double B0 = ld_devd(&ws->lg[xcd][lane][1]);
-            const double B1 = ld_devd(&ws->lg[xcd][lane + 64][1]);
-            const float bias0 = a.bias ? a.bias[lane] : 0.0f;
-            const float bias1 = a.bias ? a.bias[lane + 64] : 0.0f;
-            const double c0 = S0 + (double)bias0, c1 = S1 + (double)bias1;
-            const float lf0 = a.bias ? (float)S0 + bias0 : (float)S0;
-            const float lf1 = a.bias ? (float)S1 + bias1 : (float)S1;
-            TRACE(10);
-            const double bmax = wave_max_d(fmax(B0, B1));
-            bool t0 = false, t1 = false, ok = (a.flags & MHIP_FORCE_EXACT_ROUTER) == 0;
-            const int need = K < E ? K + 1 : K;
-            double top = 0.0, prev = 0.0;
-            int sel[KMAX + 1];
-            bool valid = true;
-#pragma unroll
-            for (int j = 0; j < KMAX + 1; j++) {
-                sel[j] = 0;
-                if (j < need && valid) {
-                    const int win = wave_argmax_d(c0, c1, t0, t1, lane);
-                    if (win < 0) {  // NaN logits: take the exact path
-                        ok = false;
-                        valid = false;
-                    } else {
-                        sel[j] = win;
-                        if (win == lane) t0 = true;
-                        if (win == lane + 64) t1 = true;
-                        const double cw = laned(win < 64 ? c0 : c1, win & 63);
-                        if (j == 0) top = cw;
-                        if (j > 0) {
-                            // Margin for the fp32 roundings between the logit and
-                            // the probability (logit+bias, l-mx, expf, division).
-                            const double tau = 0x1p-19 * (2.0 + fabs(top) + fabs(prev));
-                            if (!(prev - cw > 2.0 * bmax + tau)) ok = false;
-                        }
-                        prev = cw;
-                    }
-                }
-            }
-            TRACE(11);
+            // Without NaN keys the ranks are a permutation, so order[0..need)
+            // is set. The order is the reference's when every consecutive gap
+            // exceeds twice the largest bound plus a margin for the fp32
+            // roundings between the logit and the probability (logit + bias,
+            // l - mx, expf, division). The gate weights are computed later,
+            // while the XCD waits for h.
+            bool ok = (a.flags & MHIP_FORCE_EXACT_ROUTER) == 0 && sh.nanflag == 0;
             if (ok) {
-                // Softmax of the parallel logits (forward.c:95-101 in shape; the
-                // gate weights only need the 1e-3 tolerance).
-                const float mx = lanef(sel[0] < 64 ? lf0 : lf1, sel[0] & 63);
-                const float e0 = mhip_dev::expf_glibc(lf0 - mx);
-                const float e1 = mhip_dev::expf_glibc(lf1 - mx);
-                const float sum = wave_sum_f(e0 + e1);
-                float pj[KMAX], wsum = 0.0f;
-#pragma unroll
-                for (int j = 0; j < KMAX; j++) {
-                    if (j < K) {
-                        pj[j] = lanef(sel[j] < 64 ? e0 : e1, sel[j] & 63) / sum;
-                        wsum = wsum + pj[j];
-                    }
+                const double top = sh.c[sh.order[0]], bmax = sh.bmax;
+                int bad = 0;
+                if (lane >= 1 && lane < need) {
+                    const double prev = sh.c[sh.order[lane - 1]], cw = sh.c[sh.order[lane]];
+                    const double tau = 0x1p-19 * (2.0 + fabs(top) + fabs(prev));
+                    bad = !(prev - cw > 2.0 * bmax + tau);
                 }
-                if (lane == 0) {
-#pragma unroll
-                    for (int j = 0; j < KMAX; j++) {
-                        if (j < K) {
-                            sh.idx[j] = sel[j];
-                            sh.w[j] = a.norm_topk ? pj[j] / wsum : pj[j];
-                        }
-                    }
-                }
+                ok = __ballot(bad) == 0;
             }
+            if (ok && lane < K) sh.idx[lane] = sh.order[lane];
             if (lane == 0) sh.fallback = ok ? 0 : 1;
         }
         __syncthreads();
         if (sh.fallback) {
-            // Exact logits, the reference's sequential chain: each workgroup
-            // computes its 4 (one per wave: products to LDS, lane 0 sums them
-            // in order), then the XCD exchanges them.
-            if (wave < LPW) {
-                const int e = rank * LPW + wave;
-                const float4 *src = (const float4 *)(a.router + ((size_t)l * E + e) * D + lane * 32);
-                float *pw = &sh.scr[wave * D];
+            // Exact logits, the reference's sequential chain: each down wave
+            // computes one (products to LDS, lane 0 sums them in order), then
+            // the XCD exchanges them.
+            if (!gu_wave) {
+                float *pw = &sh.scr[(wave - NGU) * D];
+                const float *xv = &sh.xn[lane * 32];
 #pragma unroll
                 for (int k = 0; k < 8; k++) {
-                    const float4 wv = src[k];
-                    const float *xv = &sh.xn[lane * 32 + 4 * k];
-                    pw[lane * 32 + 4 * k + 0] = wv.x * xv[0];
-                    pw[lane * 32 + 4 * k + 1] = wv.y * xv[1];
-                    pw[lane * 32 + 4 * k + 2] = wv.z * xv[2];
-                    pw[lane * 32 + 4 * k + 3] = wv.w * xv[3];
+                    const float4 wv = RROW(k);
+                    pw[lane * 32 + 4 * k + 0] = wv.x * xv[4 * k + 0];
+                    pw[lane * 32 + 4 * k + 1] = wv.y * xv[4 * k + 1];
+                    pw[lane * 32 + 4 * k + 2] = wv.z * xv[4 * k + 2];
+                    pw[lane * 32 + 4 * k + 3] = wv.w * xv[4 * k + 3];
+                }
+                wave_lds_sync();
+                if (lane == 0) {
+                    const int e = rank * LPW + wave - NGU;
+                    float s = lds_seq_sum(pw, D, 0.0f);
+                    if (a.bias) s = s + sh.bias[e];
+                    st_devf(&ws->lx[xcd][e], s);
                 }
             }
-            __syncthreads();
-            if (wave < LPW && lane == 0) {
-                const int e = rank * LPW + wave;
-                float s = lds_seq_sum(&sh.scr[wave * D], D, 0.0f);
-                if (a.bias) s = s + a.bias[e];
-                st_devf(&ws->lx[xcd][e], s);
-            }
-            xcd_sync(ws, xcd, ++phase);
+            xcd_sync(ws, xcd, ++phase, true);
             if (tid < E) sh.lf[tid] = ld_devf(&ws->lx[xcd][tid]);
             __syncthreads();
             if (tid == 0) {
@@ -522,13 +564,32 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                 sh.inv = mx;
             }
             __syncthreads();
-            if (tid < E) sh.p[tid] = mhip_dev::expf_glibc(sh.lf[tid] - sh.inv);
+            if (tid < E) sh.p[tid] = mia_expf_glibc_tab(sh.lf[tid] - sh.inv, sh.etab);
             __syncthreads();
             if (tid == 0) sh.sum = lds_seq_sum(sh.p, E, 0.0f);
             __syncthreads();
-            if (tid < E) sh.p[tid] = sh.p[tid] / sh.sum;
-            __syncthreads();
             if (tid < E) {
+                const float pe = sh.p[tid] / sh.sum;
+                sh.p[tid] = pe;
+                if (pe != pe) sh.nanflag = 2;
+            }
+            if (tid < KMAX) sh.idx[tid] = 0;
+            __syncthreads();
+            if (sh.nanflag == 2) {
+                // forward.c:104-114 literally (a NaN probability never wins a
+                // comparison; the first untaken index stands in for it).
+                if (tid == 0) {
+                    for (int j = 0; j < K; j++) {
+                        int best = -1;
+                        for (int i = 0; i < E; i++) {
+                            int taken = 0;
+                            for (int t = 0; t < j; t++) taken |= sh.idx[t] == i;
+                            if (!taken && (best < 0 || sh.p[i] > sh.p[best])) best = i;
+                        }
+                        sh.idx[j] = best;
+                    }
+                }
+            } else if (tid < E) {
                 // forward.c:104-114: descending p, lowest index on ties
                 const float pe = sh.p[tid];
                 int rk = 0;
@@ -549,120 +610,122 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
         }
         __syncthreads();
         TRACE(3);
+
+        // ---- C: gate/up + SwiGLU for expert slot `xcd` -----------------------------
+        const bool active = xcd < K;
+        const int ex = min(max(sh.idx[active ? xcd : 0], 0), E - 1);
+        const uint8_t *eb = a.table + (size_t)l * layer_bytes + (size_t)ex * a.lay.expert_bytes;
+        // The next layer's rmsnorm weights are requested first: they arrive
+        // before this wave's weight rows, so no later wait is held up by them.
+        // The prefetches below are issued on every path (the last layer
+        // reloads its own rows) so that the compiler's wait counts stay exact
+        // and a wait for the down rows never covers the router rows.
+        const int lnext = min(l + 1, a.L - 1);
+        LOAD_NORM(lnext);
+        if (gu_wave) {
+            if (active) {
+                // this wave's rows: gate h0..h0+GU_H-1, then up h0..h0+GU_H-1
+                const int h0 = rank * HROWS + wave * GU_H;
+                const int4 *xv = (const int4 *)&sh.xq[lane * 32];
+                const int4 x0 = xv[0], x1 = xv[1];
+                const float dx = sh.xs[lane];
+#pragma unroll
+                for (int r = 0; r < GU_R; r++) {
+                    const int row = h0 + (r % GU_H);
+                    const size_t qoff = (r < GU_H ? a.lay.gate_q : a.lay.up_q) + (size_t)row * D +
+                                        (size_t)lane * 32;
+                    const size_t soff = (r < GU_H ? a.lay.gate_s : a.lay.up_s);
+                    const int4 *src = (const int4 *)(eb + qoff);
+                    wq0[r] = ld_stream(src);
+                    wq1[r] = ld_stream(src + 1);
+                    wsc[r] = ((const float *)(eb + soff))[(size_t)row * NB + lane];
+                }
+                float *terms = &sh.scr[wave * GU_R * GU_LD];
+#pragma unroll
+                for (int r = 0; r < GU_R; r++)
+                    terms[r * GU_LD + lane] = mhip_dev::block_term(
+                        mhip_dev::dot32_i8(wq0[r], wq1[r], x0, x1), wsc[r], dx);
+                TRACE(12);
+                wave_lds_sync();
+                if (lane < GU_R) sh.gu[wave][lane] = lds_seq_sum(&terms[lane * GU_LD], NB, 0.0f);
+                wave_lds_sync();
+                if (lane < GU_H) {
+                    const float g = sh.gu[wave][lane], u = sh.gu[wave][GU_H + lane];
+                    st_devf(&ws->h[xcd][h0 + lane],
+                            (g / (1.0f + mia_expf_glibc_tab(-g, sh.etab))) * u);
+                }
+            }
+        } else {
+            // the down rows of this workgroup (used after the next sync; an
+            // XCD without a routed slot loads them too and never uses them)
+#pragma unroll
+            for (int k = 0; k < DPK; k++) {
+                const int pidx = dt + NDN * 64 * k;
+                const int row = rank * DROWS + pidx / NBH, blk = pidx % NBH;
+                const int4 *src =
+                    (const int4 *)(eb + a.lay.down_q + (size_t)row * EH + (size_t)blk * 32);
+                wq0[k] = ld_stream(src);
+                wq1[k] = ld_stream(src + 1);
+                wsc[k] = ((const float *)(eb + a.lay.down_s))[(size_t)row * NBH + blk];
+            }
+            LOAD_ROUTER(lnext);
+        }
+        TRACE(4);
+        // The down waves keep their loads in flight across this sync; wave 1
+        // computes the gate weights while the XCD's h values arrive.
+        xcd_arrive(ws, xcd, gu_wave);
+        if (wave == 1 && !sh.fallback) {
+            // Softmax of the parallel logits (forward.c:95-101 in shape; the
+            // gate weights only need the 1e-3 tolerance), renormalised as
+            // forward.c:178-181.
+            const float mx = sh.lf[sh.idx[0]];
+            const float e0 = mia_expf_glibc_tab(sh.lf[lane] - mx, sh.etab);
+            const float e1 = mia_expf_glibc_tab(sh.lf[lane + 64] - mx, sh.etab);
+            const float sum = wave_sum_f(e0 + e1);
+            if (lane < K) sh.pk[lane] = mia_expf_glibc_tab(sh.lf[sh.idx[lane]] - mx, sh.etab) / sum;
+            wave_lds_sync();
+            if (lane == 0) {
+                float wsum = 0.0f;
+                for (int j = 0; j < K; j++) wsum = wsum + sh.pk[j];
+                for (int j = 0; j < K; j++) sh.w[j] = a.norm_topk ? sh.pk[j] / wsum : sh.pk[j];
+            }
+        }
+        xcd_wait(ws, xcd, ++phase);
+        TRACE(5);
         if (blockIdx.x == 0 && tid < K) {
             if (a.idx_out) a.idx_out[(size_t)l * K + tid] = sh.idx[tid];
             if (a.w_out) a.w_out[(size_t)l * K + tid] = sh.w[tid];
         }
 
-        // ---- C: gate/up + SwiGLU for expert slot `xcd` -----------------------------
-        const bool active = xcd < K;
-        int4 dq0[DPK], dq1[DPK];
-        float dsc[DPK];
-        if (active) {
-            const int ex = sh.idx[xcd];
-            const uint8_t *eb = a.table + (size_t)l * layer_bytes + (size_t)ex * a.lay.expert_bytes;
-            // this wave's rows: gate h0..h0+2, then up h0..h0+2
-            const int h0 = rank * HROWS + wave * (GU_RW / 2);
-            int4 gq0[GU_RW], gq1[GU_RW];
-            float gs[GU_RW];
-#pragma unroll
-            for (int r = 0; r < GU_RW; r++) {
-                const int row = h0 + (r % (GU_RW / 2));
-                const size_t qoff = (r < GU_RW / 2 ? a.lay.gate_q : a.lay.up_q) + (size_t)row * D +
-                                    (size_t)lane * 32;
-                const size_t soff = (r < GU_RW / 2 ? a.lay.gate_s : a.lay.up_s);
-                const int4 *src = (const int4 *)(eb + qoff);
-                gq0[r] = ld_stream(src);
-                gq1[r] = ld_stream(src + 1);
-                gs[r] = ((const float *)(eb + soff))[(size_t)row * NB + lane];
-            }
-            // down rows of this workgroup (used after the next sync)
-#pragma unroll
-            for (int k = 0; k < DPK; k++) {
-                const int pidx = tid + NT * k;
-                const int row = rank * DROWS + pidx / NBH, blk = pidx % NBH;
-                const int4 *src =
-                    (const int4 *)(eb + a.lay.down_q + (size_t)row * EH + (size_t)blk * 32);
-                dq0[k] = ld_stream(src);
-                dq1[k] = ld_stream(src + 1);
-                dsc[k] = ((const float *)(eb + a.lay.down_s))[(size_t)row * NBH + blk];
-            }
-            if (l + 1 < a.L) LOAD_ROUTER(l + 1);
-            const int4 *xv = (const int4 *)&sh.xq[lane * 32];
-            const int4 x0 = xv[0], x1 = xv[1];
-            const float dx = sh.xs[lane];
-            float *terms = &sh.scr[wave * GU_RW * GU_LD];
-#pragma unroll
-            for (int r = 0; r < GU_RW; r++)
-                terms[r * GU_LD + lane] =
-                    mhip_dev::block_term(mhip_dev::dot32_i8(gq0[r], gq1[r], x0, x1), gs[r], dx);
-            __syncthreads();
-            if (lane < GU_RW) sh.gu[wave][lane] = lds_seq_sum(&terms[lane * GU_LD], NB, 0.0f);
-            __syncthreads();
-            if (lane < GU_RW / 2) {
-                const float g = sh.gu[wave][lane], u = sh.gu[wave][GU_RW / 2 + lane];
-                st_devf(&ws->h[xcd][h0 + lane], (g / (1.0f + mhip_dev::expf_glibc(-g))) * u);
-            }
-        } else if (l + 1 < a.L) {
-            LOAD_ROUTER(l + 1);
-        }
-        TRACE(4);
-        xcd_sync(ws, xcd, ++phase);
-        TRACE(5);
-
         // ---- D: Q8(h) and down ------------------------------------------------------
         const int par = l & 1;
         if (active) {
-            {
-                const float h0 = ld_devf(&ws->h[xcd][tid]);
-                const float h1 = tid + NT < EH ? ld_devf(&ws->h[xcd][tid + NT]) : 0.0f;
-                sh.hs[tid] = h0;
-                if (tid + NT < EH) sh.hs[tid + NT] = h1;
-            }
+            // loaded by the gate/up waves, which have no loads in flight
+            if (gu_wave)
+                for (int i = tid; i < EH; i += NGU * 64) sh.hs[i] = ld_devf(&ws->h[xcd][i]);
             __syncthreads();
-            if (tid < NBH) {
-                const float4 *v4 = (const float4 *)&sh.hs[tid * 32];
-                float v[32];
-#pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    const float4 q = v4[k];
-                    v[4 * k] = q.x;
-                    v[4 * k + 1] = q.y;
-                    v[4 * k + 2] = q.z;
-                    v[4 * k + 3] = q.w;
-                }
-                float am = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 32; i++) am = fmaxf(am, fabsf(v[i]));
-                const float d = am / 127.0f;
-                const float qi = d != 0.0f ? 1.0f / d : 0.0f;
-                union {
-                    int8_t c[32];
-                    int4 v4[2];
-                } q;
-#pragma unroll
-                for (int i = 0; i < 32; i++) q.c[i] = (int8_t)roundf(v[i] * qi);
-                ((int4 *)&sh.hq[tid * 32])[0] = q.v4[0];
-                ((int4 *)&sh.hq[tid * 32])[1] = q.v4[1];
-                sh.hsc[tid] = d;
-            }
+            if (tid < NBH) q8_block(&sh.hs[tid * 32], &sh.hq[tid * 32], &sh.hsc[tid]);
             __syncthreads();
+            TRACE(13);
             float *dterm = sh.scr;
+            if (!gu_wave) {
 #pragma unroll
-            for (int k = 0; k < DPK; k++) {
-                const int pidx = tid + NT * k;
-                const int row = pidx / NBH, blk = pidx % NBH;
-                const int4 *hv = (const int4 *)&sh.hq[blk * 32];
-                dterm[row * DN_LD + blk] = mhip_dev::block_term(
-                    mhip_dev::dot32_i8(dq0[k], dq1[k], hv[0], hv[1]), dsc[k], sh.hsc[blk]);
+                for (int k = 0; k < DPK; k++) {
+                    const int pidx = dt + NDN * 64 * k;
+                    const int row = pidx / NBH, blk = pidx % NBH;
+                    const int4 *hv = (const int4 *)&sh.hq[blk * 32];
+                    dterm[row * DN_LD + blk] = mhip_dev::block_term(
+                        mhip_dev::dot32_i8(wq0[k], wq1[k], hv[0], hv[1]), wsc[k], sh.hsc[blk]);
+                }
             }
             __syncthreads();
-            if (tid < DROWS)
-                st_devf(&ws->out[par][xcd][rank * DROWS + tid],
-                        lds_seq_sum(&dterm[tid * DN_LD], NBH, 0.0f));
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-            if (tid == 0) st_dev(&ws->tflag[blockIdx.x][0], (unsigned)(l + 1));
+            if (wave == 0) {
+                st_devf(&ws->out[par][xcd][rank * DROWS + lane],
+                        lds_seq_sum(&dterm[lane * DN_LD], NBH, 0.0f));
+                // the wavefront's row stores complete before the flag
+                __builtin_amdgcn_s_waitcnt(0);
+                if (lane == 0) st_dev(&ws->tflag[blockIdx.x][0], (unsigned)(l + 1));
+            }
         }
         TRACE(6);
 
@@ -685,7 +748,7 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             if (l == a.L - 1 && xcd == 0) a.x[r] = v;
         }
         TRACE(8);
-        xcd_sync(ws, xcd, ++phase);
+        xcd_sync(ws, xcd, ++phase, true);
         TRACE(9);
         if (l + 1 < a.L) {
             float xv[D / NT];
@@ -693,6 +756,7 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             for (int k = 0; k < D / NT; k++) xv[k] = ld_devf(&ws->x[xcd][tid + NT * k]);
 #pragma unroll
             for (int k = 0; k < D / NT; k++) sh.x[tid + NT * k] = xv[k];
+            TRACE(14);
         }
     }
 }

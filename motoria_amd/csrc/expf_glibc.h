@@ -40,7 +40,9 @@ MIA_EXPF_TABLE uint64_t mia_expf_tab[32] = {
     0x3fef3720dcef9069ULL, 0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL,
     0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
 
-MIA_EXPF_FN float mia_expf_glibc(float x) {
+/* The algorithm with the table passed in (device code may keep a copy in
+ * LDS, where a lookup costs far less than a global-memory load). */
+MIA_EXPF_FN float mia_expf_glibc_tab(float x, const uint64_t *tab) {
     uint32_t ux;
     memcpy(&ux, &x, 4);
     const uint32_t abstop = (ux >> 20) & 0x7ff;
@@ -67,7 +69,7 @@ MIA_EXPF_FN float mia_expf_glibc(float x) {
     memcpy(&ki, &kd, 8);
     kd = kd - shift;
     const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    uint64_t t = mia_expf_tab[ki % 32];
+    uint64_t t = tab[ki % 32];
     t += ki << 47;
     double s;
     memcpy(&s, &t, 8);
@@ -78,5 +80,7 @@ MIA_EXPF_FN float mia_expf_glibc(float x) {
     y = y * s;
     return (float)y;
 }
+
+MIA_EXPF_FN float mia_expf_glibc(float x) { return mia_expf_glibc_tab(x, mia_expf_tab); }
 
 #endif
