@@ -120,7 +120,13 @@ typedef struct {
     float *h;         /* [T*K][eh] SwiGLU output, bucketed order */
     float *tmp;       /* [T*K][d]  down output, bucketed order */
     int *status;      /* [4] device-side error/diagnostic words */
+    void *xdq;        /* [T][d]    fp16: the Q8 codes of xn (matrix-core path) */
+    void *hdq;        /* [T*K][eh] fp16: d_h * q_h of Q8(h), bucketed (matrix-core path) */
+    int *gtile;       /* [E+1]     tiles of MHIP_GEMM_TM rows before each group */
 } mhip_scratch;
+
+/* Rows of one expert bucket per matrix-core tile. */
+#define MHIP_GEMM_TM 128
 
 size_t mhip_scratch_bytes(const mhip_dims *s, int max_tokens);
 int mhip_scratch_carve(const mhip_dims *s, int max_tokens, void *d_base,
@@ -130,13 +136,23 @@ int mhip_scratch_carve(const mhip_dims *s, int max_tokens, void *d_base,
 #define MHIP_FORCE_SEQ_RMS 1      /* always take the sequential rmsnorm sum */
 #define MHIP_FORCE_EXACT_ROUTER 2 /* decode stack: always the exact router chain */
 #define MHIP_DECODE_TRACE 4       /* decode stack: record stage timestamps */
+#define MHIP_EXACT_EXPERTS 8      /* layer: bit-exact expert products at every T */
 
 /*
  * One MoE layer (rmsnorm -> router/top-K -> dispatch -> gate/up+SwiGLU ->
  * down -> combine) in place on d_x[T][d]. d_table/d_router_t/d_norm point to
  * this layer's experts, transposed router and ffn_norm. d_bias (E floats) is
  * added to the logits when non-NULL.
+ *
+ * Routing (indices, order, gate weights) is bit-equal to the reference at
+ * every T. The expert products are bit-equal too for small batches; from
+ * MHIP_GEMM_MIN_A assignments on (and when the shape allows: d a multiple of
+ * 128, expert_hidden of 64) they run on the matrix cores: gate/up, SwiGLU
+ * and Q8(h) stay bit-equal, the down product takes fp16 operands and is
+ * within ~1e-4 relative of the reference. MHIP_EXACT_EXPERTS keeps the
+ * bit-exact down product at every T.
  */
+#define MHIP_GEMM_MIN_A 2048
 int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
                    const void *d_table_layer, const float *d_router_t,
                    const float *d_norm, const float *d_bias, float *d_x, int T,

@@ -25,6 +25,8 @@ _u64 = ctypes.c_uint64
 MHIP_FORCE_SEQ_RMS = 1
 MHIP_FORCE_EXACT_ROUTER = 2
 MHIP_DECODE_TRACE = 4
+MHIP_EXACT_EXPERTS = 8
+GEMM_MIN_A = 2048  # MHIP_GEMM_MIN_A
 TRACE_L0, TRACE_NL, TRACE_SLOTS = 8, 8, 16  # decode trace window (MHIP_TRACE_* in mia_hip.h)
 STAGES = ["rmsnorm", "router", "dispatch", "gateup", "down", "combine", "decode"]
 
@@ -47,7 +49,8 @@ class Layout(ctypes.Structure):
 
 class Scratch(ctypes.Structure):
     _fields_ = [(n, _p) for n in ("xn", "xq", "xs", "logits", "idx", "w", "counts", "offsets",
-                                  "perm", "pos", "groups", "h", "tmp", "status")]
+                                  "perm", "pos", "groups", "h", "tmp", "status", "xdq",
+                                  "hdq", "gtile")]
 
 
 # Every function the library exports, with its ctypes signature. tests check

@@ -43,6 +43,14 @@ inline unsigned blocks_for(size_t n, unsigned per) {
     return (unsigned)((n + per - 1) / per);
 }
 
+// Matrix-core expert products (moe_gemm.hip).
+bool gemm_path_fits(const mhip_dims *s);
+int gemm_max_tiles(int A, int E);
+int launch_gateup_mfma(hipStream_t st, const mhip_dims *s, const mhip_layout *lay,
+                       const void *d_table_layer, const mhip_scratch *sc, int A);
+int launch_down_mfma(hipStream_t st, const mhip_dims *s, const mhip_layout *lay,
+                     const void *d_table_layer, const mhip_scratch *sc, int A);
+
 }  // namespace mhip
 
 // ---- device helpers --------------------------------------------------------

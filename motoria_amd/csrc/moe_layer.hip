@@ -11,7 +11,10 @@
 // results are bit-equal to the reference C path (src/model/forward.c:167-197
 // on x86): block dots are exact int32, the per-row sums over 32-value blocks
 // run in block order, and sums the reference takes in double are either
-// reproduced exactly or certified (see k_rmsnorm_q8).
+// reproduced exactly or certified (see k_rmsnorm_q8). For large batches the
+// gate/up and down stages switch to the matrix-core kernels of moe_gemm.hip
+// (gate/up and h still bit-exact, down within ~1e-4 of the reference);
+// routing and dispatch stay bit-exact.
 #include "mhip_internal.h"
 
 namespace {
@@ -36,7 +39,8 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_q8(const float *__restrict__ x,
                                                    const float *__restrict__ w,
                                                    float *__restrict__ xn,
                                                    int8_t *__restrict__ xq,
-                                                   float *__restrict__ xs, int d, float eps,
+                                                   float *__restrict__ xs,
+                                                   _Float16 *__restrict__ xq16, int d, float eps,
                                                    int force_seq, int *status) {
     __shared__ double part[NT / 64];
     __shared__ float inv_sh;
@@ -79,8 +83,10 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_q8(const float *__restrict__ x,
         const float dsc = a / 127.0f;
         const float qi = dsc != 0.0f ? 1.0f / dsc : 0.0f;
         if (in) {
+            const float q = roundf(v * qi);
             xn[(size_t)t * d + i] = v;
-            xq[(size_t)t * d + i] = (int8_t)roundf(v * qi);
+            xq[(size_t)t * d + i] = (int8_t)q;
+            if (xq16) xq16[(size_t)t * d + i] = (_Float16)q;
             if ((i & 31) == 0) xs[(size_t)t * nb + i / QK] = dsc;
         }
     }
@@ -197,13 +203,16 @@ __global__ __launch_bounds__(256) void k_router(const float *__restrict__ xn,
 // exclusive scan per expert over the threads, then each thread scatters its
 // chunk in order. Within an expert the order is by t (then j), the order in
 // which the reference visits tokens. Also emits the list of non-empty
-// experts as (expert, begin, end) groups. status[0] |= 1 on a bad index.
+// experts as (expert, begin, end) groups, and gtile[g], the number of
+// tm-row tiles before group g (gtile[n_groups] = all tiles). status[0] |= 1
+// on a bad index.
 __global__ __launch_bounds__(256) void k_dispatch(const int *__restrict__ idx, int A, int E,
                                                   int *__restrict__ counts,
                                                   int *__restrict__ offsets,
                                                   int *__restrict__ perm,
                                                   int *__restrict__ pos,
-                                                  int *__restrict__ groups, int *status) {
+                                                  int *__restrict__ groups,
+                                                  int *__restrict__ gtile, int tm, int *status) {
     extern __shared__ unsigned char lds[];
     const int nt = blockDim.x;
     const int tid = threadIdx.x;
@@ -238,7 +247,7 @@ __global__ __launch_bounds__(256) void k_dispatch(const int *__restrict__ idx, i
     }
     __syncthreads();
     if (tid == 0) {
-        int acc = 0, g = 0;
+        int acc = 0, g = 0, tiles = 0;
         for (int e = 0; e < E; e++) {
             const int cnt = off[e];
             counts[e] = cnt;
@@ -248,6 +257,8 @@ __global__ __launch_bounds__(256) void k_dispatch(const int *__restrict__ idx, i
                 groups[1 + 3 * g] = e;
                 groups[2 + 3 * g] = acc;
                 groups[3 + 3 * g] = acc + cnt;
+                gtile[g] = tiles;
+                tiles += (cnt + tm - 1) / tm;
                 g++;
             }
             acc += cnt;
@@ -255,6 +266,7 @@ __global__ __launch_bounds__(256) void k_dispatch(const int *__restrict__ idx, i
         off[E] = acc;
         offsets[E] = acc;
         groups[0] = g;
+        gtile[g] = tiles;
     }
     __syncthreads();
     for (int a = a0; a < a1; a++) {
@@ -492,6 +504,9 @@ size_t mhip_scratch_bytes(const mhip_dims *s, int T) {
     n += align256(A * eh * 4);         // h
     n += align256(A * d * 4);          // tmp
     n += align256(4 * 4);              // status
+    n += align256(T * d * 2);          // xdq
+    n += align256(A * eh * 2);         // hdq
+    n += align256((E + 1) * 4);        // gtile
     return n;
 }
 
@@ -518,6 +533,9 @@ int mhip_scratch_carve(const mhip_dims *s, int T, void *d_base, mhip_scratch *o)
     o->h = (float *)take(A * eh * 4);
     o->tmp = (float *)take(A * d * 4);
     o->status = (int *)take(4 * 4);
+    o->xdq = take(T * d * 2);
+    o->hdq = take(A * eh * 2);
+    o->gtile = (int *)take((E + 1) * 4);
     return 0;
 }
 
@@ -531,9 +549,12 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     if (A > 65535) return mhip::fail(c, "T*K=%d exceeds 65535 assignments", A);
     const int nb = d / QK, nbh = eh / QK;
     hipStream_t st = c->stream;
+    const bool mfma = !(flags & MHIP_EXACT_EXPERTS) && A >= MHIP_GEMM_MIN_A &&
+                      mhip::gemm_path_fits(s);
 
     int slot = mhip::stage_begin(c, MHIP_STAGE_RMSNORM);
-    k_rmsnorm_q8<<<T, NT, 0, st>>>(d_x, d_norm, sc->xn, sc->xq, sc->xs, d, s->norm_eps,
+    k_rmsnorm_q8<<<T, NT, 0, st>>>(d_x, d_norm, sc->xn, sc->xq, sc->xs,
+                                   mfma ? (_Float16 *)sc->xdq : nullptr, d, s->norm_eps,
                                    (flags & MHIP_FORCE_SEQ_RMS) ? 1 : 0, sc->status);
     mhip::stage_end(c, slot);
     if (mhip::check_launch(c, "rmsnorm_q8")) return -1;
@@ -555,9 +576,25 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
         return -1;
     slot = mhip::stage_begin(c, MHIP_STAGE_DISPATCH);
     k_dispatch<<<1, dnt, dsh, st>>>(sc->idx, A, E, sc->counts, sc->offsets, sc->perm, sc->pos,
-                                    sc->groups, sc->status);
+                                    sc->groups, sc->gtile, MHIP_GEMM_TM, sc->status);
     mhip::stage_end(c, slot);
     if (mhip::check_launch(c, "dispatch")) return -1;
+
+    if (mfma) {
+        slot = mhip::stage_begin(c, MHIP_STAGE_GATEUP);
+        int e = mhip::launch_gateup_mfma(st, s, lay, d_table_layer, sc, A);
+        mhip::stage_end(c, slot);
+        if (mhip::check(c, (hipError_t)e, "gateup_mfma launch")) return -1;
+        slot = mhip::stage_begin(c, MHIP_STAGE_DOWN);
+        e = mhip::launch_down_mfma(st, s, lay, d_table_layer, sc, A);
+        mhip::stage_end(c, slot);
+        if (mhip::check(c, (hipError_t)e, "down_mfma launch")) return -1;
+        dim3 cg(mhip::blocks_for(d, 256), T);
+        slot = mhip::stage_begin(c, MHIP_STAGE_COMBINE);
+        k_combine<<<cg, 256, 0, st>>>(d_x, sc->w, sc->pos, sc->tmp, d, K);
+        mhip::stage_end(c, slot);
+        return mhip::check_launch(c, "combine");
+    }
 
     const int G = A < E ? A : E;  // at most this many non-empty experts
     const int Rg = rows_gateup(nb);
