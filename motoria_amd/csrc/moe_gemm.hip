@@ -20,12 +20,19 @@
 // accumulation: ~1e-4 relative of the reference, within the path's 1e-3.
 //
 // Tiles: 128 assignments (rows of one expert's bucket) x 128 weight rows, one
-// 32-value Q8_0 block of k per step (one 16x16x32 product per 16x16 tile).
-// Wavefront w owns assignment rows 32w..32w+31 against all 128 weight rows:
-// 2 x 8 tiles of 16x16, 64 accumulators per lane. Weight codes become fp16
-// on the way into LDS (a byte permute and one packed fp16 subtract per two
-// codes); the k loop double-buffers LDS and keeps the global loads two
-// blocks ahead in registers.
+// 32-value Q8_0 block of k per step. Wavefront w owns weight rows
+// 32w..32w+31 against all 128 assignment rows: 8 x 2 tiles of 16x16 (one
+// 16x16x32 product each per step), 64 accumulators per lane, and it alone
+// turns those weight codes into fp16 operands.
+//
+// Operands move from global memory straight into an NS-stage LDS ring with
+// global_load_lds (no registers on the way), NS-1 steps ahead of the
+// products. Each wavefront issues exactly four such loads per step, so a
+// wait for the oldest step is one immediate vmcnt count. The loads are
+// issued from inline assembly (which sets M0, the LDS base they use) so the
+// compiler does not wait for all of them before every LDS read; the waits
+// are explicit. Rows past a bucket's end load a valid row; their results are
+// never stored.
 #include "mhip_internal.h"
 
 namespace {
@@ -38,27 +45,25 @@ constexpr int GT = 256;           // threads per workgroup (4 wavefronts)
 constexpr int TM = MHIP_GEMM_TM;  // assignment rows per tile
 constexpr int TN = 128;           // weight rows per tile
 constexpr int KB = 32;            // k per step: one Q8_0 block
-constexpr int LDK = KB;           // LDS row: 32 halves = 4 chunks of 16 bytes, swizzled
+constexpr int MI = TM / 16;       // 16-row tiles of assignments (8)
+constexpr int NJ = 2;             // 16-row tiles of weights per wavefront
 constexpr int HLD = TN / 2 + 4;   // epilogue h tile row stride (floats)
-constexpr int MT = 2, NTL = TN / 16;  // 16x16 tiles per wavefront: 2 (rows) x 8 (weight rows)
+constexpr int DMA_PER_STEP = 4;   // global_load_lds per wavefront per step
 
-static_assert(TM == 128 && GT == 256, "4 wavefronts x 32 assignment rows");
-static_assert(TM <= GT && TN == GT / 2, "staging: one thread per scale, two per B row");
+static_assert(TM == 128 && TN == 128 && GT == 256, "tiling");
 
-// LDS: two buffers of two k steps each ([buffer][step][row][k]). The 16-byte
-// chunk c of row r is stored at chunk c ^ ((r >> 2) & 3), so the 16 lanes of
-// an operand read (16 consecutive rows, one chunk) hit 16 distinct groups of
-// 4 banks.
-struct KLds {
-    alignas(16) _Float16 a[2][2][TM][LDK];
-    alignas(16) _Float16 b[2][2][TN][LDK];
-    alignas(16) float sa[2][2][TM];   // activation block scales (gate/up)
-    alignas(16) float sb[2][2][TN];   // weight block scales (gate/up)
+// One step of the ring: A rows of 32 fp16 (4 chunks of 16 bytes; chunk c of
+// row r at slot c ^ ((r >> 2) & 3)), B rows of 32 int8 codes, and block
+// scales of the weight rows (sb) and of the assignment rows (sa).
+struct alignas(16) Step {
+    _Float16 a[TM][KB];  // 8 KB
+    int8_t b[TN][KB];    // 4 KB
+    float sb[TN];
+    float sa[TM];
 };
-union alignas(16) GemmLds {
-    KLds k;
-    alignas(16) float h[TM][HLD];
-};
+static_assert(sizeof(Step) == 13312, "step layout");
+
+__device__ __forceinline__ int aslot(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
 
 // The group g with gtile[g] <= mt < gtile[g + 1] (gtile is non-decreasing).
 __device__ __forceinline__ int find_group(const int *gtile, int G, int mt) {
@@ -71,6 +76,58 @@ __device__ __forceinline__ int find_group(const int *gtile, int G, int mt) {
             hi = mid;
     }
     return lo;
+}
+
+// Tile coordinates shared by both kernels.
+//
+// The 1-D grid is ordered for the XCDs' L2 caches: workgroup b runs on XCD
+// b % 8, and XCD k takes a contiguous share of the row tiles (consecutive
+// tiles of one expert share its weights), each row tile's ny weight-row
+// tiles back to back (they share its A rows). The share is computed from
+// the number of row tiles the dispatch produced; workgroups beyond it exit.
+struct TileRef {
+    int e, base, nrows, y;
+};
+constexpr int NXCD = 8;
+__device__ __forceinline__ bool tile_of(const int *groups, const int *gtile, int ny,
+                                        TileRef &t) {
+    const int G = groups[0];
+    if (G == 0) return false;
+    const int nreal = gtile[G];
+    const int b = blockIdx.x, xcd = b % NXCD, r = b / NXCD;
+    const int share = (nreal + NXCD - 1) / NXCD;
+    const int q = r / ny;
+    if (q >= share) return false;
+    const int mt = xcd * share + q;
+    if (mt >= nreal) return false;
+    t.y = r % ny;
+    const int g = find_group(gtile, G, mt);
+    t.e = groups[1 + 3 * g];
+    t.base = groups[2 + 3 * g] + (mt - gtile[g]) * TM;
+    t.nrows = min(TM, groups[3 + 3 * g] - t.base);
+    return true;
+}
+
+// global -> LDS, 16 (resp. 4) bytes per lane; lane i writes LDS at
+// lds + 16 i (resp. 4 i). lds must be wavefront-uniform.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(unsigned lds, const void *g) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(unsigned lds, const void *g) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(g)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ unsigned lds_addr(const void *p) {
+    return (unsigned)(uintptr_t)p;
 }
 
 // 8 Q8_0 codes (two little-endian words) as fp16 integers, in byte order:
@@ -93,217 +150,180 @@ __device__ __forceinline__ h8 codes8(unsigned w0, unsigned w1) {
     return r;
 }
 
-__device__ __forceinline__ int swz(int row, int chunk) { return (chunk ^ ((row >> 2) & 3)) * 8; }
-
-// v if keep, else zeros (a value select: no address is taken).
-__device__ __forceinline__ int4 keep4(bool keep, const int4 v) {
-    return make_int4(keep ? v.x : 0, keep ? v.y : 0, keep ? v.z : 0, keep ? v.w : 0);
-}
-
-// Generic grouped GEMM over one tile; EXACT selects gate/up (codes as fp16
-// integers, exact per-block epilogue) or down (dequantized operands).
-// A rows come from arow0/arow1 (fp16, KB halves per step; always readable:
-// rows past the bucket's end point at a valid row and are zeroed by aval);
-// B rows are Q8_0 codes bq with scales bs; ascale (gate/up) is the
-// block-scale row of assignment row tid (threads < TM; always readable,
-// zeroed by sval); nk = k steps.
-// On return acc[i][j][r] holds
-//   C[32*wave + 16*i + 4*(lane/16) + r][16*j + lane%16].
-//
-// Each iteration takes two k steps: it issues the global loads of the next
-// two steps into registers, runs its own two steps from one LDS buffer, then
-// stores the loaded steps into the other buffer and synchronises. No load is
-// in flight across the loop's back edge, so the compiler's wait counts are
-// exact, and the loads have two steps of products to arrive. Every load is
-// unconditional (the step index is clamped to the last step).
-template <bool EXACT>
-__device__ __forceinline__ void gemm_tile(GemmLds &L, const _Float16 *arow0,
-                                          const _Float16 *arow1, bool aval0, bool aval1,
-                                          int am0, int ap0, int am1, int ap1,
-                                          const int8_t *bq, const float *bs, int brow, int bh,
-                                          const float *ascale, bool sval, int nk,
-                                          f4v acc[MT][NTL]) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    int4 a0[2], a1[2], bw[2];
-    float sw[2], sa[2];
-#define GEMM_LOAD(S, KB_)                                                             \
-    do {                                                                              \
-        const size_t k_ = (size_t)min((KB_), nk - 1);                                 \
-        a0[S] = *(const int4 *)(arow0 + k_ * KB);                                     \
-        a1[S] = *(const int4 *)(arow1 + k_ * KB);                                     \
-        bw[S] = *(const int4 *)(bq + k_ * KB);                                        \
-        sw[S] = bs[k_];                                                               \
-        if (EXACT) sa[S] = ascale[k_];                                                \
-    } while (0)
-#define GEMM_STORE(S, P)                                                              \
-    do {                                                                              \
-        *(int4 *)&L.k.a[P][S][am0][swz(am0, ap0)] = keep4(aval0, a0[S]);              \
-        *(int4 *)&L.k.a[P][S][am1][swz(am1, ap1)] = keep4(aval1, a1[S]);              \
-        h8 lo_ = codes8((unsigned)bw[S].x, (unsigned)bw[S].y);                        \
-        h8 hi_ = codes8((unsigned)bw[S].z, (unsigned)bw[S].w);                        \
-        if (EXACT) {                                                                  \
-            if (bh == 0) L.k.sb[P][S][brow] = sw[S];                                  \
-            if (tid < TM) L.k.sa[P][S][tid] = sval ? sa[S] : 0.0f;                    \
-        } else {                                                                      \
-            const _Float16 s_ = (_Float16)sw[S];                                      \
-            const h8 s8_ = {s_, s_, s_, s_, s_, s_, s_, s_};                          \
-            lo_ = lo_ * s8_;                                                          \
-            hi_ = hi_ * s8_;                                                          \
-        }                                                                             \
-        *(h8 *)&L.k.b[P][S][brow][swz(brow, 2 * bh)] = lo_;                           \
-        *(h8 *)&L.k.b[P][S][brow][swz(brow, 2 * bh + 1)] = hi_;                       \
-    } while (0)
-#define GEMM_MMA(P, S)                                                                 \
-    do {                                                                              \
-        const int ck = lane >> 4;                                                     \
-        h8 av[MT];                                                                    \
-        _Pragma("unroll") for (int i = 0; i < MT; i++) av[i] =                        \
-            *(const h8 *)&L.k.a[P][S][32 * wave + 16 * i + (lane & 15)]               \
-                                  [swz(32 * wave + 16 * i + (lane & 15), ck)];        \
-        if (EXACT) {                                                                  \
-            /* tile j's products are issued while tile j-1's are scaled and    */    \
-            /* added; scheduling barriers keep two tiles' products live at most */   \
-            float4 sx[MT];                                                            \
-            _Pragma("unroll") for (int i = 0; i < MT; i++) sx[i] =                    \
-                *(const float4 *)&L.k.sa[P][S][32 * wave + 16 * i + 4 * (lane >> 4)];    \
-            f4v pc[MT], pn[MT];                                                       \
-            float wc = 0.0f, wn = 0.0f;                                               \
-            _Pragma("unroll") for (int j = 0; j <= NTL; j++) {                        \
-                if (j < NTL) {                                                        \
-                    const h8 bv = *(const h8 *)&L.k.b[P][S][16 * j + (lane & 15)]      \
-                                                     [swz(16 * j + (lane & 15), ck)]; \
-                    wn = L.k.sb[P][S][16 * j + (lane & 15)];                          \
-                    _Pragma("unroll") for (int i = 0; i < MT; i++) {                  \
-                        const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};                       \
-                        pn[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv, z, 0, 0, 0); \
-                    }                                                                 \
-                }                                                                     \
-                if (j > 0) {                                                          \
-                    _Pragma("unroll") for (int i = 0; i < MT; i++) {                  \
-                        f4v &c = acc[i][j - 1];                                       \
-                        c[0] = c[0] + (pc[i][0] * wc) * sx[i].x;                      \
-                        c[1] = c[1] + (pc[i][1] * wc) * sx[i].y;                      \
-                        c[2] = c[2] + (pc[i][2] * wc) * sx[i].z;                      \
-                        c[3] = c[3] + (pc[i][3] * wc) * sx[i].w;                      \
-                    }                                                                 \
-                }                                                                     \
-                _Pragma("unroll") for (int i = 0; i < MT; i++) pc[i] = pn[i];         \
-                wc = wn;                                                              \
-                __builtin_amdgcn_sched_barrier(0);                                    \
-            }                                                                         \
-        } else {                                                                      \
-            _Pragma("unroll") for (int j = 0; j < NTL; j++) {                         \
-                const h8 bv = *(const h8 *)&L.k.b[P][S][16 * j + (lane & 15)]          \
-                                                 [swz(16 * j + (lane & 15), ck)];     \
-                _Pragma("unroll") for (int i = 0; i < MT; i++) acc[i][j] =            \
-                    __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv, acc[i][j], 0, 0, 0); \
-            }                                                                         \
-        }                                                                             \
-    } while (0)
-    // nk is even (gemm_path_fits): the loop moves in pairs of steps.
-    GEMM_LOAD(0, 0);
-    GEMM_LOAD(1, 1);
-    GEMM_STORE(0, 0);
-    GEMM_STORE(1, 0);
-    __syncthreads();
-    for (int kb = 0; kb < nk; kb += 2) {
-        const int p = (kb >> 1) & 1;
-        GEMM_LOAD(0, kb + 2);
-        GEMM_LOAD(1, kb + 3);
-        asm volatile("" ::: "memory");  // the prefetch goes out before this pair's work
-        GEMM_MMA(p, 0);
-        asm volatile("" ::: "memory");  // one step's operands and products at a time
-        GEMM_MMA(p, 1);
-        asm volatile("" ::: "memory");
-        GEMM_STORE(0, p ^ 1);
-        GEMM_STORE(1, p ^ 1);
-        __syncthreads();
-    }
-#undef GEMM_LOAD
-#undef GEMM_STORE
-#undef GEMM_MMA
-}
-
-// Tile coordinates shared by both kernels.
-struct TileRef {
-    int e, base, nrows;
+// Per-thread global sources of one tile, advanced by one block per step.
+struct Src {
+    const _Float16 *a0, *a1;  // A chunks of rows ar0, ar1 (fp16, KB halves per step)
+    const int8_t *b;          // B 16-byte half of weight row br (KB bytes per step)
+    const float *s;           // a block-scale row (one float per step)
 };
-__device__ __forceinline__ bool tile_of(const int *groups, const int *gtile, int mt, TileRef &t) {
-    const int G = groups[0];
-    if (G == 0 || mt >= gtile[G]) return false;
-    const int g = find_group(gtile, G, mt);
-    t.e = groups[1 + 3 * g];
-    t.base = groups[2 + 3 * g] + (mt - gtile[g]) * TM;
-    t.nrows = min(TM, groups[3 + 3 * g] - t.base);
-    return true;
+
+// The k loop over nk steps (nk >= NS - 1). On return acc[i][j][r] holds
+//   C[16*i + 4*(lane/16) + r][32*wave + 16*j + lane%16].
+template <int NS, bool EXACT>
+__device__ __forceinline__ void gemm_tile(Step *ring, const Src &src, int nk, f4v acc[MI][NJ]) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // LDS destinations of this wavefront's four loads within a step
+    const unsigned ring0 = lds_addr(ring);
+    const unsigned oa0 = (unsigned)offsetof(Step, a) + (2 * wave) * 1024;
+    const unsigned oa1 = oa0 + 1024;
+    const unsigned ob = (unsigned)offsetof(Step, b) + wave * 1024;
+    // waves 0, 1: the weight rows' scales; waves 2, 3: the assignment rows'
+    const unsigned os = (wave < 2 ? (unsigned)offsetof(Step, sb) : (unsigned)offsetof(Step, sa)) +
+                        (wave & 1) * 256;
+    auto issue = [&](int kb) {
+        const int k = min(kb, nk - 1);  // past the end: reload the last step
+        const unsigned st = ring0 + (unsigned)((kb % NS) * sizeof(Step));
+        dma16(st + oa0, src.a0 + (size_t)k * KB);
+        dma16(st + oa1, src.a1 + (size_t)k * KB);
+        dma16(st + ob, src.b + (size_t)k * KB);
+        dma4(st + os, src.s + k);
+    };
+#pragma unroll
+    for (int s = 0; s < NS - 1; s++) issue(s);
+    for (int kb = 0; kb < nk; kb++) {
+        // this wavefront's loads of step kb are done (NS - 2 later steps may
+        // still be in flight); then every wavefront's are
+        wait_vm<(NS - 2) * DMA_PER_STEP>();
+        __syncthreads();
+        // step kb + NS - 1 reuses the slot read in step kb - 1, which every
+        // wavefront has finished with (the LDS reads completed before the
+        // barrier)
+        issue(kb + NS - 1);
+        const Step &S = ring[kb % NS];
+        const int ck = lane >> 4;
+        h8 bv[NJ];
+        float sw[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int n = 32 * wave + 16 * j + (lane & 15);
+            const uint2 q = *(const uint2 *)&S.b[n][8 * ck];
+            bv[j] = codes8(q.x, q.y);
+            sw[j] = S.sb[n];
+            if (!EXACT) {
+                const _Float16 s = (_Float16)sw[j];
+                const h8 s8 = {s, s, s, s, s, s, s, s};
+                bv[j] = bv[j] * s8;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < MI; i++) {
+            const int m = 16 * i + (lane & 15);
+            const h8 av = *(const h8 *)&S.a[m][8 * aslot(m, ck)];
+            if (EXACT) {
+                const float4 sx = *(const float4 *)&S.sa[16 * i + 4 * ck];
+#pragma unroll
+                for (int j = 0; j < NJ; j++) {
+                    const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};
+                    const f4v blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv[j], z, 0, 0, 0);
+                    acc[i][j][0] = acc[i][j][0] + (blk[0] * sw[j]) * sx.x;
+                    acc[i][j][1] = acc[i][j][1] + (blk[1] * sw[j]) * sx.y;
+                    acc[i][j][2] = acc[i][j][2] + (blk[2] * sw[j]) * sx.z;
+                    acc[i][j][3] = acc[i][j][3] + (blk[3] * sw[j]) * sx.w;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < NJ; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+    wait_vm<0>();  // the reloads past the end
+    __syncthreads();
+}
+
+// The A rows this thread loads: rows 32*wave + 16*q + lane/4 (q = 0, 1), in
+// the chunk that lands in LDS slot lane % 4.
+__device__ __forceinline__ void a_rows(int &r0, int &c0, int &r1, int &c1) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    r0 = 32 * wave + (lane >> 2);
+    r1 = r0 + 16;
+    c0 = aslot(r0, lane & 3);  // slot ^ swizzle = the chunk stored there
+    c1 = aslot(r1, lane & 3);
 }
 
 // ---- gate/up + SwiGLU + Q8(h) ----------------------------------------------------
 //
 // blockIdx.x = tile of assignment rows (gtile numbering), blockIdx.y = 64
-// consecutive h columns; the tile's 128 weight rows are those 64 gate rows
-// and the 64 up rows of the same h columns, so SwiGLU pairs accumulator
-// tiles j and j + 4 of a wavefront lane by lane.
+// consecutive h columns h0..h0+63. Wavefront w's 32 weight rows are the gate
+// rows then the up rows of h columns h0+16w..h0+16w+15, so SwiGLU pairs its
+// accumulator tiles 0 and 1 lane by lane.
+constexpr int NS_GU = 4;
+constexpr int NS_DN = 6;
+
+union alignas(16) GateUpLds {
+    Step ring[NS_GU];
+    float h[TM][HLD];
+};
+union alignas(16) DownLds {
+    Step ring[NS_DN];
+};
+
 __global__ __launch_bounds__(GT, 1) void k_gateup_mfma(
     const uint8_t *__restrict__ table, mhip_layout lay, const _Float16 *__restrict__ xq16,
     const float *__restrict__ xs, const int *__restrict__ groups, const int *__restrict__ gtile,
     const int *__restrict__ perm, _Float16 *__restrict__ hdq, int d, int eh, int K) {
-    __shared__ GemmLds L;
+    __shared__ GateUpLds L;
     TileRef tr;
-    if (!tile_of(groups, gtile, blockIdx.x, tr)) return;
+    if (!tile_of(groups, gtile, eh / (TN / 2), tr)) return;
     const int base = tr.base, nrows = tr.nrows;
-    const int h0 = blockIdx.y * (TN / 2);
+    const int h0 = tr.y * (TN / 2);
     const uint8_t *ex = table + (size_t)tr.e * lay.expert_bytes;
     const int nb = d / KB;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-    // A: this thread's two 16-byte chunks per step (rows am, parts ap); rows
-    // past the bucket's end read its first row and are zeroed
-    const int am0 = tid >> 2, ap0 = tid & 3, am1 = (tid + GT) >> 2, ap1 = (tid + GT) & 3;
-    const bool aval0 = am0 < nrows, aval1 = am1 < nrows;
-    const int t0 = perm[base + (aval0 ? am0 : 0)] / K;
-    const int t1 = perm[base + (aval1 ? am1 : 0)] / K;
-    const _Float16 *arow0 = xq16 + (size_t)t0 * d + ap0 * 8;
-    const _Float16 *arow1 = xq16 + (size_t)t1 * d + ap1 * 8;
-    // block scales of assignment row tid (threads 0..TM-1; zeroed past the end)
-    const bool sval = tid < nrows;
-    const float *ascale = xs + (size_t)(perm[base + (sval ? tid : 0)] / K) * nb;
-    // B: weight row brow (gate rows first, then up rows), 16-byte half bh
-    const int brow = tid >> 1, bh = tid & 1;
-    const bool isg = brow < TN / 2;
-    const int wr = h0 + (isg ? brow : brow - TN / 2);
-    const int8_t *bq = (const int8_t *)(ex + (isg ? lay.gate_q : lay.up_q)) + (size_t)wr * d + bh * 16;
-    const float *bs = (const float *)(ex + (isg ? lay.gate_s : lay.up_s)) + (size_t)wr * nb;
+    Src src;
+    {
+        int r0, c0, r1, c1;
+        a_rows(r0, c0, r1, c1);
+        const int t0 = perm[base + min(r0, nrows - 1)] / K;
+        const int t1 = perm[base + min(r1, nrows - 1)] / K;
+        src.a0 = xq16 + (size_t)t0 * d + c0 * 8;
+        src.a1 = xq16 + (size_t)t1 * d + c1 * 8;
+        // weight row of B row 32*wave + lane/2: gate rows then up rows
+        const int bj = (lane >> 1) >> 4, br = (lane >> 1) & 15;
+        const int wr = h0 + 16 * wave + br;
+        src.b = (const int8_t *)(ex + (bj == 0 ? lay.gate_q : lay.up_q)) + (size_t)wr * d +
+                (lane & 1) * 16;
+        if (wave < 2) {
+            // scale of B row 64*wave + lane
+            const int b = 64 * wave + lane;
+            const int sw = h0 + 16 * (b >> 5) + (b & 15);
+            src.s = (const float *)(ex + (((b >> 4) & 1) == 0 ? lay.gate_s : lay.up_s)) +
+                    (size_t)sw * nb;
+        } else {
+            // scale of assignment row 64*(wave-2) + lane
+            const int m = 64 * (wave - 2) + lane;
+            src.s = xs + (size_t)(perm[base + min(m, nrows - 1)] / K) * nb;
+        }
+    }
 
-    f4v acc[MT][NTL];
+    f4v acc[MI][NJ];
 #pragma unroll
-    for (int i = 0; i < MT; i++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
-        for (int j = 0; j < NTL; j++) acc[i][j] = (f4v){0.0f, 0.0f, 0.0f, 0.0f};
-    gemm_tile<true>(L, arow0, arow1, aval0, aval1, am0, ap0, am1, ap1, bq, bs, brow, bh, ascale,
-                    sval, nb, acc);
+        for (int j = 0; j < NJ; j++) acc[i][j] = (f4v){0.0f, 0.0f, 0.0f, 0.0f};
+    gemm_tile<NS_GU, true>(L.ring, src, nb, acc);
 
-    __syncthreads();  // every wavefront is done with the k-loop LDS
+    // SwiGLU into the h tile (LDS, reused), then Q8_0 per 32-block
 #pragma unroll
-    for (int i = 0; i < MT; i++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
-        for (int j = 0; j < NTL / 2; j++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = 32 * wave + 16 * i + 4 * (lane >> 4) + r;
-                const float gv = acc[i][j][r], uv = acc[i][j + NTL / 2][r];
-                L.h[m][16 * j + (lane & 15)] = (gv / (1.0f + mia_expf_glibc(-gv))) * uv;
-            }
+        for (int r = 0; r < 4; r++) {
+            const int m = 16 * i + 4 * (lane >> 4) + r;
+            const float gv = acc[i][0][r], uv = acc[i][1][r];
+            L.h[m][16 * wave + (lane & 15)] = (gv / (1.0f + mia_expf_glibc(-gv))) * uv;
+        }
     __syncthreads();
     {
         // Q8_0 of one 32-block of h (quant.c:11-27), stored dequantized
         const int m = tid >> 1, i = tid & 1;
         if (m < nrows) {
-            const float4 *src = (const float4 *)&L.h[m][32 * i];
+            const float4 *hs = (const float4 *)&L.h[m][32 * i];
             float v[32];
 #pragma unroll
             for (int k = 0; k < 8; k++) {
-                const float4 q = src[k];
+                const float4 q = hs[k];
                 v[4 * k] = q.x;
                 v[4 * k + 1] = q.y;
                 v[4 * k + 2] = q.z;
@@ -334,40 +354,44 @@ __global__ __launch_bounds__(GT, 2) void k_down_mfma(const uint8_t *__restrict__
                                                      const int *__restrict__ groups,
                                                      const int *__restrict__ gtile,
                                                      float *__restrict__ tmp, int d, int eh) {
-    __shared__ GemmLds L;
+    __shared__ DownLds L;
     TileRef tr;
-    if (!tile_of(groups, gtile, blockIdx.x, tr)) return;
+    if (!tile_of(groups, gtile, d / TN, tr)) return;
     const int base = tr.base, nrows = tr.nrows;
-    const int n0 = blockIdx.y * TN;
+    const int n0 = tr.y * TN;
     const uint8_t *ex = table + (size_t)tr.e * lay.expert_bytes;
     const int nbh = eh / KB;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-    const int am0 = tid >> 2, ap0 = tid & 3, am1 = (tid + GT) >> 2, ap1 = (tid + GT) & 3;
-    const bool aval0 = am0 < nrows, aval1 = am1 < nrows;
-    const _Float16 *arow0 = hdq + (size_t)(base + (aval0 ? am0 : 0)) * eh + ap0 * 8;
-    const _Float16 *arow1 = hdq + (size_t)(base + (aval1 ? am1 : 0)) * eh + ap1 * 8;
-    const int brow = tid >> 1, bh = tid & 1;
-    const int8_t *bq = (const int8_t *)(ex + lay.down_q) + (size_t)(n0 + brow) * eh + bh * 16;
-    const float *bs = (const float *)(ex + lay.down_s) + (size_t)(n0 + brow) * nbh;
+    Src src;
+    {
+        int r0, c0, r1, c1;
+        a_rows(r0, c0, r1, c1);
+        src.a0 = hdq + (size_t)(base + min(r0, nrows - 1)) * eh + c0 * 8;
+        src.a1 = hdq + (size_t)(base + min(r1, nrows - 1)) * eh + c1 * 8;
+        const int row = n0 + 32 * wave + (lane >> 1);
+        src.b = (const int8_t *)(ex + lay.down_q) + (size_t)row * eh + (lane & 1) * 16;
+        // scales of weight rows 64*(wave&1) + lane (waves 2, 3 repeat waves
+        // 0, 1 into the unused assignment-scale slot)
+        src.s = (const float *)(ex + lay.down_s) + (size_t)(n0 + 64 * (wave & 1) + lane) * nbh;
+    }
 
-    f4v acc[MT][NTL];
+    f4v acc[MI][NJ];
 #pragma unroll
-    for (int i = 0; i < MT; i++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
-        for (int j = 0; j < NTL; j++) acc[i][j] = (f4v){0.0f, 0.0f, 0.0f, 0.0f};
-    gemm_tile<false>(L, arow0, arow1, aval0, aval1, am0, ap0, am1, ap1, bq, bs, brow, bh, bs,
-                     false, nbh, acc);
+        for (int j = 0; j < NJ; j++) acc[i][j] = (f4v){0.0f, 0.0f, 0.0f, 0.0f};
+    gemm_tile<NS_DN, false>(L.ring, src, nbh, acc);
 
 #pragma unroll
-    for (int i = 0; i < MT; i++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const int m = 32 * wave + 16 * i + 4 * (lane >> 4) + r;
+            const int m = 16 * i + 4 * (lane >> 4) + r;
             if (m < nrows) {
-                float *dst = tmp + (size_t)(base + m) * d + n0 + (lane & 15);
+                float *dst = tmp + (size_t)(base + m) * d + n0 + 32 * wave + (lane & 15);
 #pragma unroll
-                for (int j = 0; j < NTL; j++) dst[16 * j] = acc[i][j][r];
+                for (int j = 0; j < NJ; j++) dst[16 * j] = acc[i][j][r];
             }
         }
 }
@@ -377,17 +401,23 @@ __global__ __launch_bounds__(GT, 2) void k_down_mfma(const uint8_t *__restrict__
 namespace mhip {
 
 bool gemm_path_fits(const mhip_dims *s) {
-    // whole tiles of weight rows, and an even number of k steps
-    return s->dim % TN == 0 && s->expert_hidden % (TN / 2) == 0 && s->dim % (2 * KB) == 0 &&
-           s->expert_hidden % (2 * KB) == 0;
+    // whole tiles of weight rows, and enough k steps to fill the rings
+    return s->dim % TN == 0 && s->expert_hidden % (TN / 2) == 0 &&
+           s->dim / KB >= NS_GU - 1 && s->expert_hidden / KB >= NS_DN - 1;
 }
 
 int gemm_max_tiles(int A, int E) { return (A + TM - 1) / TM + (A < E ? A : E); }
 
+// Workgroups for ny weight-row tiles: every XCD's share can hold all row tiles.
+static unsigned gemm_grid(int A, int E, int ny) {
+    const int share = (gemm_max_tiles(A, E) + NXCD - 1) / NXCD;
+    return (unsigned)(NXCD * share * ny);
+}
+
 int launch_gateup_mfma(hipStream_t st, const mhip_dims *s, const mhip_layout *lay,
                        const void *d_table_layer, const mhip_scratch *sc, int A) {
     const int d = s->dim, eh = s->expert_hidden;
-    dim3 grid((unsigned)gemm_max_tiles(A, s->n_experts), (unsigned)(eh / (TN / 2)));
+    const unsigned grid = gemm_grid(A, s->n_experts, eh / (TN / 2));
     k_gateup_mfma<<<grid, GT, 0, st>>>((const uint8_t *)d_table_layer, *lay,
                                        (const _Float16 *)sc->xdq, sc->xs, sc->groups,
                                        sc->gtile, sc->perm, (_Float16 *)sc->hdq, d, eh,
@@ -398,7 +428,7 @@ int launch_gateup_mfma(hipStream_t st, const mhip_dims *s, const mhip_layout *la
 int launch_down_mfma(hipStream_t st, const mhip_dims *s, const mhip_layout *lay,
                      const void *d_table_layer, const mhip_scratch *sc, int A) {
     const int d = s->dim, eh = s->expert_hidden;
-    dim3 grid((unsigned)gemm_max_tiles(A, s->n_experts), (unsigned)(d / TN));
+    const unsigned grid = gemm_grid(A, s->n_experts, d / TN);
     k_down_mfma<<<grid, GT, 0, st>>>((const uint8_t *)d_table_layer, *lay,
                                      (const _Float16 *)sc->hdq, sc->groups, sc->gtile, sc->tmp,
                                      d, eh);
