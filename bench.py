@@ -27,6 +27,7 @@ import motoria_amd as M  # noqa: E402
 from motoria_amd import workloads as W  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 matrix peak
 METRIC = "MoE tokens/s + achieved HBM GB/s (% of peak), Qwen3-30B-A3B shape, 1 GPU"
 
 
@@ -62,6 +63,13 @@ def gateup_bytes(n_touched, T, shape):
     d, eh, K = shape["dim"], shape["expert_hidden"], shape["n_active"]
     w = n_touched * 2 * eh * (d // 32) * 36
     return w + T * d + T * (d // 32) * 4 + T * K * eh * 4
+
+
+def gateup_flops(T, shape):
+    """Algorithmic flops of one gate/up launch: 2 * assignments * (gate + up
+    rows) * dim multiply-adds."""
+    d, eh, K = shape["dim"], shape["expert_hidden"], shape["n_active"]
+    return 2.0 * T * K * 2 * eh * d
 
 
 def cpu_baseline(moe, wl, shape, sample_layers, sample_tokens):
@@ -199,6 +207,14 @@ def main():
         dom_bytes = sum(gateup_bytes(n, T, shape) for n in touched) / len(touched)
         dom_name = "k_gateup (gate/up Q8_0 grouped GEMV + SwiGLU)"
     achieved = dom_bytes / dom_avg_s / 1e9
+    # Large batches run the expert products on the matrix cores: the gate/up
+    # kernel is then priced against the fp16 matrix peak.
+    matrix = not persistent and T * shape["n_active"] >= M.GEMM_MIN_A
+    if matrix:
+        dom_name = ("k_gateup_mfma (gate/up on fp16 MFMA with the exact per-block Q8_0 "
+                    "epilogue, SwiGLU, Q8(h))")
+        dom_flops = gateup_flops(T, shape)
+        achieved_tf = dom_flops / dom_avg_s / 1e12
     for s in M.STAGES:
         ms, n = diag[s]
         if n:
@@ -242,7 +258,18 @@ def main():
         },
         "hbm": {"bytes_per_step": step_bytes, "achieved_gbs": hbm_gbs,
                 "frac": hbm_gbs / HBM_PEAK_GBS, "ops_per_step": step_ops},
-        "roofline": {
+        "roofline": ({
+            "kernel": dom_name,
+            "bound": "mfma",
+            "achieved": achieved_tf,
+            "peak": MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved_tf / MFMA_PEAK_TFLOPS,
+            "traffic": None,
+            "flops_per_launch": dom_flops,
+            "avg_launch_us": dom_avg_s * 1e6,
+            "layer_ops_tflops": step_ops / (ms_step / 1e3) / 1e12,
+        } if matrix else {
             "kernel": dom_name,
             "bound": "hbm",
             "achieved": achieved,
@@ -252,8 +279,10 @@ def main():
             "traffic": None,
             "bytes_per_launch": dom_bytes,
             "avg_launch_us": dom_avg_s * 1e6,
-        },
-        "path": ("persistent decode kernel" if persistent else "one launch per stage"),
+        }),
+        "path": ("persistent decode kernel" if persistent else
+                 "one launch per stage, expert products on the matrix cores" if matrix else
+                 "one launch per stage"),
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

@@ -100,26 +100,33 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_q8(const float *__restrict__ x,
 // restated glibc expf and a sequential sum; top-K (forward.c:104-114) takes
 // the largest untaken probability, lowest index on ties; the gate weights
 // are renormalised as forward.c:178-181.
+//
+// With have_logits set, the logits (bias included) were already computed by
+// k_router_logits and only the selection runs.
 __global__ __launch_bounds__(256) void k_router(const float *__restrict__ xn,
                                                 const float *__restrict__ wt,
                                                 const float *__restrict__ bias,
                                                 float *__restrict__ logits,
                                                 int *__restrict__ idx_out,
                                                 float *__restrict__ w_out, int d, int E, int K,
-                                                int norm_topk) {
+                                                int norm_topk, int have_logits) {
     extern __shared__ float sh[];
-    float *xs = sh;       // [d]
-    float *p = sh + d;    // [E]
+    float *p = sh;        // [E]
+    float *xs = sh + E;   // [d] (chains computed here)
     __shared__ float red[4];
     __shared__ float sum_sh;
     __shared__ int top[64];
     const int t = blockIdx.x;
     const int tid = threadIdx.x;
-    for (int i = tid; i < d; i += blockDim.x) xs[i] = xn[(size_t)t * d + i];
-    __syncthreads();
+    if (!have_logits) {
+        for (int i = tid; i < d; i += blockDim.x) xs[i] = xn[(size_t)t * d + i];
+        __syncthreads();
+    }
 
     float l = -__builtin_inff();
-    if (tid < E) {
+    if (tid < E && have_logits) {
+        l = logits[(size_t)t * E + tid];
+    } else if (tid < E) {
         const float *col = wt + tid;
         float s = 0.0f;
         int i = 0;
@@ -194,6 +201,96 @@ __global__ __launch_bounds__(256) void k_router(const float *__restrict__ xn,
             }
         }
     }
+}
+
+// ---- router logits for many tokens ----------------------------------------------
+//
+// The same sequential fp32 chains (matmul.c:13-17, plus the bias), tiled:
+// a workgroup takes 2C tokens, thread (e, g) runs the chains of expert e for
+// tokens g*C .. g*C+C-1 (C independent chains, one weight read for all).
+// The workgroup's xn rows sit in LDS (transposed) for the whole kernel; the
+// transposed router streams through an RL_NS-stage LDS ring of RL_I rows,
+// loaded straight from global memory (global_load_lds, issued from inline
+// assembly that sets M0) RL_NS-1 chunks ahead, with explicit waits. Each
+// wavefront issues four 1 KB loads per chunk. Needs E == 128.
+constexpr int RL_I = 32;
+constexpr int RL_NS = 4;
+constexpr int RL_E = 128;
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void rl_dma16(unsigned lds, const void *g) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <int C>
+__global__ __launch_bounds__(256) void k_router_logits(const float *__restrict__ xn,
+                                                       const float *__restrict__ wt,
+                                                       const float *__restrict__ bias,
+                                                       float *__restrict__ logits, int T, int d) {
+    constexpr int TT = 2 * C;
+    extern __shared__ __align__(16) float rl_sh[];
+    float (*Wr)[RL_I][RL_E] = (float (*)[RL_I][RL_E])rl_sh;  // [stage][i][e]
+    float *Xs = rl_sh + RL_NS * RL_I * RL_E;                  // [i][TT]
+    const int tid = threadIdx.x, e = tid & (RL_E - 1), g = tid >> 7;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int t0 = blockIdx.x * TT;
+    const int nch = d / RL_I;
+    // chunk ch -> stage ch % RL_NS; wavefront w loads rows 8w..8w+7 of the
+    // chunk, two 512-byte rows per instruction
+    const unsigned ring = (unsigned)(uintptr_t)rl_sh;
+    auto issue = [&](int ch) {
+        const int k = min(ch, nch - 1);
+        const unsigned st = ring + (unsigned)((ch % RL_NS) * RL_I * RL_E * 4);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int row = 8 * wave + 2 * q;
+            rl_dma16(st + (unsigned)(row * RL_E * 4),
+                     wt + (size_t)(k * RL_I + row + (lane >> 5)) * RL_E + 4 * (lane & 31));
+        }
+    };
+#pragma unroll
+    for (int c = 0; c < RL_NS - 1; c++) issue(c);
+    // xn of the workgroup's tokens, transposed, while the first chunks load
+    for (int f = tid; f < TT * (d / 4); f += 256) {
+        const int t = f / (d / 4), i4 = f % (d / 4);
+        const float4 v = t0 + t < T ? *(const float4 *)(xn + (size_t)(t0 + t) * d + 4 * i4)
+                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        Xs[(4 * i4 + 0) * TT + t] = v.x;
+        Xs[(4 * i4 + 1) * TT + t] = v.y;
+        Xs[(4 * i4 + 2) * TT + t] = v.z;
+        Xs[(4 * i4 + 3) * TT + t] = v.w;
+    }
+    float s[C];
+#pragma unroll
+    for (int c = 0; c < C; c++) s[c] = 0.0f;
+    for (int ch = 0; ch < nch; ch++) {
+        // this wavefront's loads of chunk ch are done (later ones may still
+        // be in flight), then every wavefront's (and the xn staging)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((RL_NS - 2) * 4) : "memory");
+        __syncthreads();
+        issue(ch + RL_NS - 1);  // into the stage read in chunk ch - 1
+        const float(*W)[RL_E] = Wr[ch % RL_NS];
+        const float *X = Xs + (size_t)ch * RL_I * TT + g * C;
+#pragma unroll 8
+        for (int ii = 0; ii < RL_I; ii++) {
+            const float w = W[ii][e];
+#pragma unroll
+            for (int c = 0; c < C; c++) s[c] = s[c] + w * X[ii * TT + c];
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the reloads past the end
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        const int t = t0 + g * C + c;
+        if (t < T) logits[(size_t)t * RL_E + e] = bias ? s[c] + bias[e] : s[c];
+    }
+}
+
+size_t router_logits_lds(int C, int d) {
+    return ((size_t)RL_NS * RL_I * RL_E + (size_t)d * 2 * C) * sizeof(float);
 }
 
 // ---- dispatch -------------------------------------------------------------
@@ -560,10 +657,30 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     if (mhip::check_launch(c, "rmsnorm_q8")) return -1;
 
     const int rthreads = E <= 64 ? 64 : E <= 128 ? 128 : 256;
-    const size_t rsh = (size_t)(d + E) * sizeof(float);
+    // The tiled chains for more than one token; one workgroup per token else.
+    const bool tiled = T > 1 && E == RL_E && d % RL_I == 0 && d / RL_I >= RL_NS - 1;
+    const size_t rsh = (size_t)(E + (tiled ? 0 : d)) * sizeof(float);
     slot = mhip::stage_begin(c, MHIP_STAGE_ROUTER);
+    if (tiled) {
+        const int C = T >= 4096 ? 4 : T >= 2048 ? 2 : 1;
+        const size_t lsh = router_logits_lds(C, d);
+        const void *fn = C == 4 ? (const void *)k_router_logits<4>
+                         : C == 2 ? (const void *)k_router_logits<2>
+                                  : (const void *)k_router_logits<1>;
+        if (lsh > 65536 &&
+            mhip::check(c, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)lsh),
+                        "router LDS attribute"))
+            return -1;
+        if (C == 4)
+            k_router_logits<4><<<(T + 7) / 8, 256, lsh, st>>>(sc->xn, d_router_t, d_bias, sc->logits, T, d);
+        else if (C == 2)
+            k_router_logits<2><<<(T + 3) / 4, 256, lsh, st>>>(sc->xn, d_router_t, d_bias, sc->logits, T, d);
+        else
+            k_router_logits<1><<<(T + 1) / 2, 256, lsh, st>>>(sc->xn, d_router_t, d_bias, sc->logits, T, d);
+    }
     k_router<<<T, rthreads, rsh, st>>>(sc->xn, d_router_t, d_bias, sc->logits, sc->idx, sc->w, d,
-                                       E, K, s->norm_topk);
+                                       E, K, s->norm_topk, tiled ? 1 : 0);
     mhip::stage_end(c, slot);
     if (mhip::check_launch(c, "router")) return -1;
 
