@@ -30,9 +30,12 @@
 //   D  Q8(h) -> down rows -> the expert's output rows, published device-wide
 //   E  combine x_r += w_j * out_j,r in top-K order for 64 rows [XCD sync]
 //
-// Intra-XCD synchronisation is an L2 atomic counter; cross-XCD data is written
-// with device-scope stores and read with device-scope loads after a
-// point-to-point flag. No agent-scope cache maintenance is issued.
+// Exchanged data carries its own readiness: every value goes out as one
+// 64-bit device-scope store of (fp32 value, tag), the tag naming the launch
+// and the layer, and its readers poll those words until the tag matches. No
+// separate flag, barrier or store acknowledgement sits between a producer
+// and its readers, and no agent-scope cache maintenance is issued. (The rare
+// exact-router fallback uses an L2 atomic counter per XCD.)
 //
 // Results: top-K indices bit-equal to the reference (certified, with an exact
 // fallback); expert products, SwiGLU, Q8(h), down and combine follow the
@@ -71,19 +74,26 @@ static_assert(LPW == NDN, "one router row per down wave");
 static_assert(GU_H * NGU == HROWS && DPK * NDN * 64 == DROWS * NBH, "tiling");
 static_assert(NT == 4 * E, "ranks: four threads per expert");
 
+// Tagged words: (tag << 32) | fp32 bits.
+typedef unsigned long long tw;
+
 struct DecodeWs {
     unsigned gstart[64];          // start barrier (device scope)
-    unsigned cnt[NX][64];         // intra-XCD counters, monotonic
-    unsigned tflag[NWG][16];      // expert-output rows published (layer + 1)
-    int status[16];               // [0] abort bits, [1] rms fallbacks, [2] router fallbacks
-    float x[NX][D];
-    double lg[NX][E][2];          // parallel logit sum S and bound B
-    float lx[NX][E];              // exact logits (fallback)
-    float h[NX][EH];
-    float out[2][KMAX][D];        // expert outputs, double-buffered by layer parity
+    int status[64];               // [0] abort bits, [1] rms fallbacks, [2] router fallbacks
+    // Every per-XCD array starts on a 256-byte boundary, so no cache line
+    // holds data of two XCDs.
+    alignas(256) tw x[NX][D];     // residual stream after each layer, per XCD
+    alignas(256) tw lgs[NX][E];   // parallel logit sum S, rounded to fp32
+    alignas(256) tw lgb[NX][E];   // its bound, widened for that rounding
+    alignas(256) tw lx[NX][E];    // exact logits (fallback)
+    alignas(256) tw h[NX][EH];    // SwiGLU output of the XCD's expert
+    alignas(256) tw out[2][KMAX][D];  // expert outputs, double-buffered by layer parity
     // stage timestamps of every workgroup for layers MHIP_TRACE_L0 .. +MHIP_TRACE_NL (diagnostic)
     unsigned long long trace[MHIP_TRACE_NL][NWG][MHIP_TRACE_SLOTS];
 };
+
+static_assert(offsetof(DecodeWs, lgb) == offsetof(DecodeWs, lgs) + NX * E * sizeof(tw),
+              "lgb follows lgs");
 
 struct DecodeArgs {
     const uint8_t *table;         // layer 0, experts expert_bytes apart, layers E*expert_bytes
@@ -98,6 +108,7 @@ struct DecodeArgs {
     float *w_out;                 // [L][K] or null
     int L, K, norm_topk, flags;
     float eps;
+    unsigned epoch;               // tag of this launch (bits 8..31 of every tag)
 };
 
 __device__ __forceinline__ unsigned xcc_id() {
@@ -106,57 +117,93 @@ __device__ __forceinline__ unsigned xcc_id() {
 __device__ __forceinline__ unsigned ld_dev(const unsigned *p) {
     return __hip_atomic_load((unsigned *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float ld_devf(const float *p) {
-    return __uint_as_float(ld_dev((const unsigned *)p));
-}
-__device__ __forceinline__ double ld_devd(const double *p) {
-    unsigned long long v = __hip_atomic_load((unsigned long long *)p, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-    return __longlong_as_double((long long)v);
-}
-__device__ __forceinline__ void st_dev(unsigned *p, unsigned v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_devf(float *p, float v) { st_dev((unsigned *)p, __float_as_uint(v)); }
-__device__ __forceinline__ void st_devd(double *p, double v) {
-    __hip_atomic_store((unsigned long long *)p, (unsigned long long)__double_as_longlong(v),
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // Abort bits: 1 = workgroup not on the expected XCD, 2 = a wait timed out.
 __device__ __forceinline__ bool aborted(DecodeWs *ws) {
     return ld_dev((const unsigned *)&ws->status[0]) != 0;
 }
 
-// One arrival of this workgroup on the XCD counter, then wait until all WPX
-// workgroups of the XCD arrived `phase` times. Waves with `drain` set first
-// wait for all their memory operations (their stores become visible before
-// the arrival); waves without it keep their loads in flight (they must have
-// stored nothing that other workgroups read after this sync).
-// The sync is split in two halves so that work which depends on no other
-// workgroup can run between the arrival and the wait.
-__device__ void xcd_arrive(DecodeWs *ws, int xcd, bool drain) {
-    if (drain) __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0)
-        __hip_atomic_fetch_add(&ws->cnt[xcd][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+// Two kinds of exchange. Data read only inside the writer's XCD (x, logits,
+// h) meets in that XCD's L2: workgroup-scope stores (the L1 writes through)
+// and non-temporal loads, which the L1 does not keep, so every poll reads the
+// L2 (a scope-0/1 load may hit a stale L1 line and never see the store).
+// Measured hand-off between two CUs of one XCD: ~290 ns one way, against
+// ~460 ns with device-scope accesses. Expert outputs, read by every XCD, use
+// device-scope (sc1) stores and loads.
+template <bool LOCAL>
+__device__ __forceinline__ void put_tagged(tw *p, float v, unsigned tag) {
+    const tw w = ((tw)tag << 32) | __float_as_uint(v);
+    if (LOCAL)
+        __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    else
+        __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ void xcd_wait(DecodeWs *ws, int xcd, unsigned phase) {
-    if (threadIdx.x == 0) {
-        const unsigned *c = &ws->cnt[xcd][0];
-        long s = 0;
-        while (ld_dev(c) < phase * WPX) {
-            if (++s > SPIN || ((s & 255) == 0 && aborted(ws))) {
-                atomicOr(&ws->status[0], 2);
-                break;
-            }
-        }
+// N words p[0], p[stride], ... read from the L2 (one wait for all of them).
+template <int N> struct L2Load;
+template <> struct L2Load<1> {
+    __device__ static void run(tw *v, const tw *p, int) {
+        asm volatile("global_load_dwordx2 %0, %1, off nt\n\ts_waitcnt vmcnt(0)"
+                     : "=&v"(v[0]) : "v"(p) : "memory");
     }
-    __syncthreads();
+};
+template <> struct L2Load<2> {
+    __device__ static void run(tw *v, const tw *p, int s) {
+        asm volatile("global_load_dwordx2 %0, %2, off nt\n\t"
+                     "global_load_dwordx2 %1, %3, off nt\n\ts_waitcnt vmcnt(0)"
+                     : "=&v"(v[0]), "=&v"(v[1]) : "v"(p), "v"(p + s) : "memory");
+    }
+};
+template <> struct L2Load<3> {
+    __device__ static void run(tw *v, const tw *p, int s) {
+        asm volatile("global_load_dwordx2 %0, %3, off nt\n\t"
+                     "global_load_dwordx2 %1, %4, off nt\n\t"
+                     "global_load_dwordx2 %2, %5, off nt\n\ts_waitcnt vmcnt(0)"
+                     : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2])
+                     : "v"(p), "v"(p + s), "v"(p + 2 * s) : "memory");
+    }
+};
+template <> struct L2Load<4> {
+    __device__ static void run(tw *v, const tw *p, int s) {
+        asm volatile("global_load_dwordx2 %0, %4, off nt\n\t"
+                     "global_load_dwordx2 %1, %5, off nt\n\t"
+                     "global_load_dwordx2 %2, %6, off nt\n\t"
+                     "global_load_dwordx2 %3, %7, off nt\n\ts_waitcnt vmcnt(0)"
+                     : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+                     : "v"(p), "v"(p + s), "v"(p + 2 * s), "v"(p + 3 * s) : "memory");
+    }
+};
+template <int N, bool LOCAL>
+__device__ __forceinline__ void load_words(tw *v, const tw *p, int stride) {
+    if (LOCAL) {
+        L2Load<N>::run(v, p, stride);
+    } else {
+#pragma unroll
+        for (int k = 0; k < N; k++)
+            v[k] = __hip_atomic_load((tw *)(p + k * stride), __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
-__device__ void xcd_sync(DecodeWs *ws, int xcd, unsigned phase, bool drain) {
-    xcd_arrive(ws, xcd, drain);
-    xcd_wait(ws, xcd, phase);
+// The values of the N words p[0], p[stride], ... once each carries `tag`
+// (polled together). After SPIN rounds, or once the launch has aborted, sets
+// abort bit 2 and returns whatever is there.
+template <int N, bool LOCAL>
+__device__ __forceinline__ void get_tagged(DecodeWs *ws, const tw *p, int stride, unsigned tag,
+                                           float *out) {
+    tw v[N];
+    load_words<N, LOCAL>(v, p, stride);
+    long s = 0;
+    for (;;) {
+        bool ready = true;
+#pragma unroll
+        for (int k = 0; k < N; k++) ready = ready && (unsigned)(v[k] >> 32) == tag;
+        if (ready) break;
+        if (++s > SPIN || ((s & 255) == 0 && aborted(ws))) {
+            atomicOr(&ws->status[0], 2);
+            break;
+        }
+        load_words<N, LOCAL>(v, p, stride);
+    }
+#pragma unroll
+    for (int k = 0; k < N; k++) out[k] = __uint_as_float((unsigned)v[k]);
 }
 
 __device__ void wait_flag(DecodeWs *ws, const unsigned *flag, unsigned value) {
@@ -339,9 +386,9 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
         wait_flag(ws, &ws->gstart[0], NWG);
     }
     __syncthreads();
-    if (aborted(ws)) return;
+    // An XCD without a routed slot has nothing that another XCD reads.
+    if (aborted(ws) || xcd >= K) return;
 
-    unsigned phase = 0;
     // One register array serves both roles. A gate/up wave holds its GU_R
     // weight rows in wq0/wq1/wsc during stage C. A down wave holds its DPK
     // down (row, block) pairs in slots 0..DPK-1 from stage C to D, and the
@@ -382,6 +429,7 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
         asm volatile("" : "+v"(tid));
         lane = tid & 63;
         const int dt = tid - NGU * 64;          // index among the down waves' threads
+        const unsigned tag = (a.epoch << 8) | (unsigned)(l & 255);
         TRACE(0);
         // ---- A: rmsnorm (certified), xn, Q8(xn), logits -----------------------------
         __syncthreads();
@@ -457,19 +505,24 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             const double S = lane63_d(incl);
             const double A = lane63_d(wave_scan_d(absum));
             if (lane == 0) {
+                // S goes out rounded to fp32 (|S - Sf| <= 2^-24 |Sf|, plus an
+                // absolute 2^-150 for subnormals); the bound grows by that and
+                // is rounded upwards to fp32 by the (1 + 2^-22) factor.
                 const int e = rank * LPW + wave - NGU;
-                st_devd(&ws->lg[xcd][e][0], S);
-                st_devd(&ws->lg[xcd][e][1], A * 0x1p-24 * (1.0 + 0x1p-8) + 1e-30);
+                const float Sf = (float)S;
+                const double B = A * 0x1p-24 * (1.0 + 0x1p-8) + 0x1p-24 * fabs((double)Sf) + 1e-30;
+                put_tagged<true>(&ws->lgs[xcd][e], Sf, tag);
+                put_tagged<true>(&ws->lgb[xcd][e], (float)(B * (1.0 + 0x1p-22)), tag);
             }
         }
         TRACE(1);
-        xcd_sync(ws, xcd, ++phase, true);
         TRACE(2);
 
         // ---- B: ranks, certification ------------------------------------------------
         if (tid < E) {
-            const double S = ld_devd(&ws->lg[xcd][tid][0]);
-            const double B = ld_devd(&ws->lg[xcd][tid][1]);
+            float sb[2];
+            get_tagged<2, true>(ws, &ws->lgs[xcd][tid], NX * E, tag, sb);
+            const double S = (double)sb[0], B = (double)sb[1];
             const float bs = sh.bias[tid];
             const double c = S + (double)bs;
             // monotone 64-bit image of c with the low 7 bits replaced by
@@ -480,7 +533,7 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             sh.key[tid] = ((u >> 7) << 7) | (uint64_t)(E - 1 - tid);
             sh.c[tid] = c;
             sh.r[tid] = B;
-            sh.lf[tid] = a.bias ? (float)S + bs : (float)S;
+            sh.lf[tid] = a.bias ? sb[0] + bs : sb[0];
             if (c != c) sh.nanflag = 1;
         }
         __syncthreads();
@@ -551,11 +604,10 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                     const int e = rank * LPW + wave - NGU;
                     float s = lds_seq_sum(pw, D, 0.0f);
                     if (a.bias) s = s + sh.bias[e];
-                    st_devf(&ws->lx[xcd][e], s);
+                    put_tagged<true>(&ws->lx[xcd][e], s, tag);
                 }
             }
-            xcd_sync(ws, xcd, ++phase, true);
-            if (tid < E) sh.lf[tid] = ld_devf(&ws->lx[xcd][tid]);
+            if (tid < E) get_tagged<1, true>(ws, &ws->lx[xcd][tid], 0, tag, &sh.lf[tid]);
             __syncthreads();
             if (tid == 0) {
                 // forward.c:95-101 exactly: first maximum, sequential sum.
@@ -651,8 +703,8 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                 wave_lds_sync();
                 if (lane < GU_H) {
                     const float g = sh.gu[wave][lane], u = sh.gu[wave][GU_H + lane];
-                    st_devf(&ws->h[xcd][h0 + lane],
-                            (g / (1.0f + mia_expf_glibc_tab(-g, sh.etab))) * u);
+                    put_tagged<true>(&ws->h[xcd][h0 + lane],
+                               (g / (1.0f + mia_expf_glibc_tab(-g, sh.etab))) * u, tag);
                 }
             }
         } else {
@@ -671,9 +723,8 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             LOAD_ROUTER(lnext);
         }
         TRACE(4);
-        // The down waves keep their loads in flight across this sync; wave 1
-        // computes the gate weights while the XCD's h values arrive.
-        xcd_arrive(ws, xcd, gu_wave);
+        // Wave 1 computes the gate weights while the XCD's h values arrive;
+        // the down waves keep their loads in flight meanwhile.
         if (wave == 1 && !sh.fallback) {
             // Softmax of the parallel logits (forward.c:95-101 in shape; the
             // gate weights only need the 1e-3 tolerance), renormalised as
@@ -690,20 +741,22 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                 for (int j = 0; j < K; j++) sh.w[j] = a.norm_topk ? sh.pk[j] / wsum : sh.pk[j];
             }
         }
-        xcd_wait(ws, xcd, ++phase);
-        TRACE(5);
-        if (blockIdx.x == 0 && tid < K) {
-            if (a.idx_out) a.idx_out[(size_t)l * K + tid] = sh.idx[tid];
-            if (a.w_out) a.w_out[(size_t)l * K + tid] = sh.w[tid];
-        }
-
         // ---- D: Q8(h) and down ------------------------------------------------------
         const int par = l & 1;
         if (active) {
-            // loaded by the gate/up waves, which have no loads in flight
-            if (gu_wave)
-                for (int i = tid; i < EH; i += NGU * 64) sh.hs[i] = ld_devf(&ws->h[xcd][i]);
+            // polled by the gate/up waves, which have no loads in flight
+            if (gu_wave) {
+                float hv[EH / (NGU * 64)];
+                get_tagged<EH / (NGU * 64), true>(ws, &ws->h[xcd][tid], NGU * 64, tag, hv);
+#pragma unroll
+                for (int k = 0; k < EH / (NGU * 64); k++) sh.hs[tid + NGU * 64 * k] = hv[k];
+            }
             __syncthreads();
+            TRACE(5);
+            if (blockIdx.x == 0 && tid < K) {
+                if (a.idx_out) a.idx_out[(size_t)l * K + tid] = sh.idx[tid];
+                if (a.w_out) a.w_out[(size_t)l * K + tid] = sh.w[tid];
+            }
             if (tid < NBH) q8_block(&sh.hs[tid * 32], &sh.hq[tid * 32], &sh.hsc[tid]);
             __syncthreads();
             TRACE(13);
@@ -719,44 +772,37 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                 }
             }
             __syncthreads();
-            if (wave == 0) {
-                st_devf(&ws->out[par][xcd][rank * DROWS + lane],
-                        lds_seq_sum(&dterm[lane * DN_LD], NBH, 0.0f));
-                // the wavefront's row stores complete before the flag
-                __builtin_amdgcn_s_waitcnt(0);
-                if (lane == 0) st_dev(&ws->tflag[blockIdx.x][0], (unsigned)(l + 1));
-            }
+            if (wave == 0)
+                put_tagged<false>(&ws->out[par][xcd][rank * DROWS + lane],
+                           lds_seq_sum(&dterm[lane * DN_LD], NBH, 0.0f), tag);
         }
         TRACE(6);
 
         // ---- E: combine rows rank*64 .. +64 in top-K order ---------------------------
-        if (tid < K) wait_flag(ws, &ws->tflag[rank * NX + tid][0], (unsigned)(l + 1));
-        __syncthreads();
-        TRACE(7);
         {
             // thread (j, r) fetches expert j's output row r; then one thread
             // per row adds them in top-K order
             const int j = tid / DROWS, r = tid % DROWS;
-            if (j < K) sh.scr[r * KMAX + j] = ld_devf(&ws->out[par][j][rank * DROWS + r]);
+            if (j < K) get_tagged<1, false>(ws, &ws->out[par][j][rank * DROWS + r], 0, tag, &sh.scr[r * KMAX + j]);
         }
         __syncthreads();
+        TRACE(7);
         if (tid < DROWS) {
             const int r = rank * DROWS + tid;
             float v = sh.x[r];
             for (int j = 0; j < K; j++) v = v + sh.w[j] * sh.scr[tid * KMAX + j];
-            st_devf(&ws->x[xcd][r], v);
-            if (l == a.L - 1 && xcd == 0) a.x[r] = v;
+            if (l + 1 < a.L) put_tagged<true>(&ws->x[xcd][r], v, tag);
+            else if (xcd == 0) a.x[r] = v;
         }
         TRACE(8);
-        xcd_sync(ws, xcd, ++phase, true);
-        TRACE(9);
         if (l + 1 < a.L) {
+            // the XCD's new residual stream; a row is written only after its
+            // old value was read above, so no barrier is needed before this
             float xv[D / NT];
-#pragma unroll
-            for (int k = 0; k < D / NT; k++) xv[k] = ld_devf(&ws->x[xcd][tid + NT * k]);
+            get_tagged<D / NT, true>(ws, &ws->x[xcd][tid], NT, tag, xv);
 #pragma unroll
             for (int k = 0; k < D / NT; k++) sh.x[tid + NT * k] = xv[k];
-            TRACE(14);
+            TRACE(9);
         }
     }
 }
@@ -788,9 +834,20 @@ int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
         return mhip::fail(c, "decode stack needs %d CUs with one %d-thread workgroup each "
                              "(device has %d CUs, occupancy %d)", NWG, NT,
                           prop.multiProcessorCount, occ);
+    if ((uintptr_t)d_ws % 256)
+        return mhip::fail(c, "decode stack: workspace %p is not 256-byte aligned", d_ws);
     DecodeWs *ws = (DecodeWs *)d_ws;
-    // Counters, flags and status start at zero (fill kernel, no memset).
-    if (mhip_zero(c, ws, offsetof(DecodeWs, x))) return -1;
+    // The start barrier and status start at zero (fill kernel, no memset).
+    // Exchanged words are tagged with this launch's epoch, so stale words of
+    // earlier launches never match; a workspace this context has not used
+    // last (or an epoch about to leave its 24 bits) is cleared whole first.
+    if (ws != c->decode_ws || c->decode_epoch >= (1u << 24) - 1) {
+        if (mhip_zero(c, ws, offsetof(DecodeWs, trace))) return -1;
+        c->decode_ws = ws;
+        c->decode_epoch = 0;
+    } else if (mhip_zero(c, ws, offsetof(DecodeWs, x))) {
+        return -1;
+    }
     DecodeArgs a;
     a.table = (const uint8_t *)d_table;
     a.lay = *lay;
@@ -807,6 +864,7 @@ int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     a.norm_topk = s->norm_topk;
     a.flags = flags;
     a.eps = s->norm_eps;
+    a.epoch = ++c->decode_epoch;
     void *args[] = {&a};
     int slot = mhip::stage_begin(c, MHIP_STAGE_DECODE);
     hipError_t e = hipLaunchCooperativeKernel((const void *)k_decode_stack, dim3(NWG), dim3(NT),

@@ -18,6 +18,8 @@ struct mhip_ctx {
     int st_cap, st_n;
     hipEvent_t *st_ev;  // [2 * st_cap]
     int *st_stage;      // [st_cap]
+    unsigned decode_epoch;  // launches of the decode kernel (tags its exchanged data)
+    const void *decode_ws;  // workspace those tags were written to
     char err[512];
 };
 
