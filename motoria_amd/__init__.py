@@ -27,7 +27,7 @@ MHIP_FORCE_EXACT_ROUTER = 2
 MHIP_DECODE_TRACE = 4
 MHIP_EXACT_EXPERTS = 8
 GEMM_MIN_A = 2048  # MHIP_GEMM_MIN_A
-TRACE_L0, TRACE_NL, TRACE_SLOTS = 8, 8, 16  # decode trace window (MHIP_TRACE_* in mia_hip.h)
+TRACE_L0, TRACE_NL, TRACE_SLOTS = 8, 8, 32  # decode trace window (MHIP_TRACE_* in mia_hip.h)
 STAGES = ["rmsnorm", "router", "dispatch", "gateup", "down", "combine", "decode"]
 
 

@@ -266,6 +266,13 @@ __device__ __forceinline__ double wave_max_d(double v) {
     return lane63_d(v);
 }
 
+// v from the lane DPP control CTRL names (every lane has a source).
+template <int CTRL>
+__device__ __forceinline__ float dpp_keep_f(float v) {
+    const int b = __float_as_int(v);
+    return __int_as_float(__builtin_amdgcn_update_dpp(b, b, CTRL, 0xf, 0xf, false));
+}
+
 __device__ __forceinline__ float wave_sum_f(float v) {
     // through double: exact for the wave-wide sum of 64 floats' partials
     return (float)lane63_d(wave_scan_d((double)v));
@@ -279,6 +286,10 @@ __device__ __forceinline__ float4 i4_as_f4(const int4 v) {
 // LDS. `scr` is reused by stages that never overlap: the exact-router
 // products (B, fallback), the gate/up terms (C) and the down terms and
 // gathered expert outputs (D, E).
+// A lane reading its own 32-block of xn with 16-byte reads: blocks 36
+// floats apart put eight consecutive lanes on distinct banks (a 128-byte
+// stride would put every lane on the same four banks).
+constexpr int XN_LD = 36;
 constexpr int GU_LD = NB + 4;     // 16-byte aligned rows
 constexpr int DN_LD = NBH + 4;
 constexpr int SCR = 8192;         // floats
@@ -287,18 +298,16 @@ static_assert(NGU * GU_R * GU_LD <= SCR && DROWS * DN_LD <= SCR && LPW * D <= SC
 
 struct Lds {
     alignas(16) float x[D];
-    alignas(16) float xn[D];
+    alignas(16) float xn[NB * XN_LD];  // 32-blocks XN_LD floats apart
     alignas(16) int8_t xq[D];
     alignas(16) float scr[SCR];
-    alignas(16) float hs[EH];
     alignas(16) int8_t hq[EH];
     float xs[NB];
     float hsc[NBH];
     float gu[NGU][GU_R];
     alignas(16) uint64_t key[E];  // ranking key: S + bias made monotone, expert index in the low bits
     double c[E];                  // S + bias
-    double r[E];                  // its bound
-    double bmax;
+    double bpart[E / 64];         // largest bound among each 64 experts
     float lf[E];                  // fp32 logits (+ bias)
     alignas(16) float p[E];       // probabilities (fallback)
     float bias[E];
@@ -330,41 +339,20 @@ __device__ __forceinline__ float lds_seq_sum(const float *p, int n, float s) {
     return s;
 }
 
-// Q8_0 of one 32-block (quant.c:11-27) from LDS into LDS.
-__device__ __forceinline__ void q8_block(const float *src, int8_t *dst, float *dscale) {
-    const float4 *v4 = (const float4 *)src;
-    float v[32];
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const float4 q = v4[k];
-        v[4 * k] = q.x;
-        v[4 * k + 1] = q.y;
-        v[4 * k + 2] = q.z;
-        v[4 * k + 3] = q.w;
-    }
-    float am = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; i++) am = fmaxf(am, fabsf(v[i]));
-    const float d = am / 127.0f;
-    const float qi = d != 0.0f ? 1.0f / d : 0.0f;
-    union {
-        int8_t c[32];
-        int4 v4[2];
-    } q;
-#pragma unroll
-    for (int i = 0; i < 32; i++) q.c[i] = (int8_t)roundf(v[i] * qi);
-    ((int4 *)dst)[0] = q.v4[0];
-    ((int4 *)dst)[1] = q.v4[1];
-    *dscale = d;
-}
-
-// Diagnostic: thread 0 of every workgroup records the 100 MHz real-time
-// counter at the stage boundaries of a window of layers.
-#define TRACE(slot)                                                                        \
+// Diagnostic: one thread of every workgroup (thread 0 unless named) records
+// the 100 MHz real-time counter at the stage boundaries of a window of layers.
+#define TRACE_BY(slot, who)                                                                \
+    do {                                                                                   \
+        if ((a.flags & MHIP_DECODE_TRACE) && tid == (who) && l >= MHIP_TRACE_L0 &&         \
+            l < MHIP_TRACE_L0 + MHIP_TRACE_NL)                                             \
+            ws->trace[l - MHIP_TRACE_L0][blockIdx.x][slot] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#define TRACE(slot) TRACE_BY(slot, 0)
+#define TRACE_CLK(slot)                                                                    \
     do {                                                                                   \
         if ((a.flags & MHIP_DECODE_TRACE) && tid == 0 && l >= MHIP_TRACE_L0 &&             \
             l < MHIP_TRACE_L0 + MHIP_TRACE_NL)                                             \
-            ws->trace[l - MHIP_TRACE_L0][blockIdx.x][slot] = __builtin_amdgcn_s_memrealtime(); \
+            ws->trace[l - MHIP_TRACE_L0][blockIdx.x][slot] = __builtin_amdgcn_s_memtime();  \
     } while (0)
 
 __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
@@ -431,8 +419,10 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
         const int dt = tid - NGU * 64;          // index among the down waves' threads
         const unsigned tag = (a.epoch << 8) | (unsigned)(l & 255);
         TRACE(0);
+        TRACE_CLK(30);
         // ---- A: rmsnorm (certified), xn, Q8(xn), logits -----------------------------
         __syncthreads();
+        TRACE(14);
         {
             double ss = 0.0;
 #pragma unroll
@@ -444,66 +434,86 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             if (lane == 0) sh.part[wave] = ss;
         }
         __syncthreads();
-        if (tid == 0) {
-            // Any summation order is within (n + log2 n) 2^-53 S of the
-            // reference's sequential sum (all terms >= 0); S -/+ m brackets it.
+        float inv;
+        {
+            // Every thread brackets the scale itself (same partials, same
+            // order, same result). Any summation order is within
+            // (n + log2 n) 2^-53 S of the reference's sequential sum (all
+            // terms >= 0); S -/+ m brackets it.
             double S = 0.0;
             for (int k = 0; k < NWAVE; k++) S = S + sh.part[k];
             const double m = S * ((double)(D + 64) * 0x1p-52);
             const float lo = (float)(1.0 / sqrt((S + m) / D + (double)a.eps));
             const float hi = (float)(1.0 / sqrt((S - m) / D + (double)a.eps));
-            float inv = lo;
-            if ((a.flags & MHIP_FORCE_SEQ_RMS) || lo != hi) {
-                double sq = 0.0;
-                for (int i = 0; i < D; i++) sq = sq + (double)sh.x[i] * (double)sh.x[i];
-                inv = (float)(1.0 / sqrt(sq / D + (double)a.eps));
-                if (blockIdx.x == 0) atomicAdd(&ws->status[1], 1);
+            inv = lo;
+            if ((a.flags & MHIP_FORCE_SEQ_RMS) || lo != hi) {   // the same branch in every thread
+                if (tid == 0) {
+                    double sq = 0.0;
+                    for (int i = 0; i < D; i++) sq = sq + (double)sh.x[i] * (double)sh.x[i];
+                    sh.inv = (float)(1.0 / sqrt(sq / D + (double)a.eps));
+                    if (blockIdx.x == 0) atomicAdd(&ws->status[1], 1);
+                }
+                __syncthreads();
+                inv = sh.inv;
             }
-            sh.inv = inv;
-            sh.nanflag = 0;
+            if (tid == 0) sh.nanflag = 0;
         }
-        __syncthreads();
+        TRACE(15);
         {
-            const float inv = sh.inv;
 #pragma unroll
             for (int k = 0; k < D / NT; k++) {
                 const int i = tid + NT * k;
-                sh.xn[i] = (sh.x[i] * inv) * wn[k];
+                sh.xn[(i / 32) * XN_LD + i % 32] = (sh.x[i] * inv) * wn[k];
             }
         }
         __syncthreads();
-        if (tid < NB) q8_block(&sh.xn[tid * 32], &sh.xq[tid * 32], &sh.xs[tid]);
+        TRACE_BY(20, NGU * 64);
         // Parallel logits with a bound. The reference's logit is the
         // sequential fp32 chain over p_i = fl(W_ei * xn_i); S = sum p_i in
         // double, and |chain - S| <= 2^-24 * sum_k |S_k| (S_k the prefix sums).
         if (!gu_wave) {
-            const float4 *xv4 = (const float4 *)&sh.xn[lane * 32];
-            double tot = 0.0;
+            // This lane's 32 products (the reference's, fp32), summed in
+            // four independent stretches of 8; the prefix sums of the
+            // second pass restart each stretch from its own offset, so no
+            // dependency chain is longer than 8 additions.
+            const float4 *xv4 = (const float4 *)&sh.xn[lane * XN_LD];
+            float pr[32];
 #pragma unroll
             for (int k = 0; k < 8; k++) {
                 const float4 wv = RROW(k), xv = xv4[k];
-                tot = tot + (double)(wv.x * xv.x);
-                tot = tot + (double)(wv.y * xv.y);
-                tot = tot + (double)(wv.z * xv.z);
-                tot = tot + (double)(wv.w * xv.w);
+                pr[4 * k + 0] = wv.x * xv.x;
+                pr[4 * k + 1] = wv.y * xv.y;
+                pr[4 * k + 2] = wv.z * xv.z;
+                pr[4 * k + 3] = wv.w * xv.w;
             }
+            double cs[4];
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                cs[m] = 0.0;
+#pragma unroll
+                for (int j = 0; j < 8; j++) cs[m] = cs[m] + (double)pr[8 * m + j];
+            }
+            const double tot = (cs[0] + cs[1]) + (cs[2] + cs[3]);
             const double incl = wave_scan_d(tot);
-            double run = incl - tot;  // exclusive prefix of this lane
-            double absum = 0.0;
+            TRACE_BY(21, NGU * 64);
+            double run[4], ab[4];
+            run[0] = incl - tot;  // exclusive prefix of this lane
+            run[1] = run[0] + cs[0];
+            run[2] = run[1] + cs[1];
+            run[3] = run[2] + cs[2];
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const float4 wv = RROW(k), xv = xv4[k];
-                run = run + (double)(wv.x * xv.x);
-                absum = absum + fabs(run);
-                run = run + (double)(wv.y * xv.y);
-                absum = absum + fabs(run);
-                run = run + (double)(wv.z * xv.z);
-                absum = absum + fabs(run);
-                run = run + (double)(wv.w * xv.w);
-                absum = absum + fabs(run);
-            }
+            for (int m = 0; m < 4; m++) ab[m] = 0.0;
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    run[m] = run[m] + (double)pr[8 * m + j];
+                    ab[m] = ab[m] + fabs(run[m]);
+                }
+            const double absum = (ab[0] + ab[1]) + (ab[2] + ab[3]);
             const double S = lane63_d(incl);
             const double A = lane63_d(wave_scan_d(absum));
+            TRACE_BY(22, NGU * 64);
             if (lane == 0) {
                 // S goes out rounded to fp32 (|S - Sf| <= 2^-24 |Sf|, plus an
                 // absolute 2^-150 for subnormals); the bound grows by that and
@@ -514,8 +524,32 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                 put_tagged<true>(&ws->lgs[xcd][e], Sf, tag);
                 put_tagged<true>(&ws->lgb[xcd][e], (float)(B * (1.0 + 0x1p-22)), tag);
             }
+            // Q8(xn) for stage C, while the logits travel (quant.c:11-27 per
+            // element): four lanes per 32-block, eight elements each, the
+            // block maximum over the quad by DPP (order-free).
+            {
+                const int blk = dt >> 2, sub = dt & 3;
+                const float4 *src = (const float4 *)&sh.xn[blk * XN_LD + sub * 8];
+                const float4 v0 = src[0], v1 = src[1];
+                const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+                float am = 0.0f;                                 // a NaN counts as 0
+#pragma unroll
+                for (int i = 0; i < 8; i++) am = fmaxf(am, fabsf(v[i]));
+                am = fmaxf(am, dpp_keep_f<0xB1>(am));            // quad_perm [1,0,3,2]
+                am = fmaxf(am, dpp_keep_f<0x4E>(am));            // quad_perm [2,3,0,1]
+                const float d = am / 127.0f;
+                const float qi = d != 0.0f ? 1.0f / d : 0.0f;
+                union {
+                    int8_t c[8];
+                    int2 w;
+                } q;
+#pragma unroll
+                for (int i = 0; i < 8; i++) q.c[i] = (int8_t)roundf(v[i] * qi);
+                *(int2 *)&sh.xq[blk * 32 + sub * 8] = q.w;
+                if (sub == 0) sh.xs[blk] = d;
+            }
         }
-        TRACE(1);
+        TRACE_BY(1, NGU * 64);
         TRACE(2);
 
         // ---- B: ranks, certification ------------------------------------------------
@@ -532,9 +566,10 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             u = (u >> 63) ? ~u : (u | (1ull << 63));
             sh.key[tid] = ((u >> 7) << 7) | (uint64_t)(E - 1 - tid);
             sh.c[tid] = c;
-            sh.r[tid] = B;
             sh.lf[tid] = a.bias ? sb[0] + bs : sb[0];
             if (c != c) sh.nanflag = 1;
+            const double bm = wave_max_d(B);
+            if (lane == 0) sh.bpart[wave] = bm;
         }
         __syncthreads();
         TRACE(10);
@@ -550,10 +585,6 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                 rk += (int)(v.x > ke) + (int)(v.y > ke);
             }
             sh.rk[q][e] = rk;
-            if (wave == 0) {
-                const double bm = wave_max_d(fmax(sh.r[lane], sh.r[lane + 64]));
-                if (lane == 0) sh.bmax = bm;
-            }
         }
         __syncthreads();
         if (tid < E) {
@@ -571,7 +602,7 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             // while the XCD waits for h.
             bool ok = (a.flags & MHIP_FORCE_EXACT_ROUTER) == 0 && sh.nanflag == 0;
             if (ok) {
-                const double top = sh.c[sh.order[0]], bmax = sh.bmax;
+                const double top = sh.c[sh.order[0]], bmax = fmax(sh.bpart[0], sh.bpart[1]);
                 int bad = 0;
                 if (lane >= 1 && lane < need) {
                     const double prev = sh.c[sh.order[lane - 1]], cw = sh.c[sh.order[lane]];
@@ -590,7 +621,7 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             // the XCD exchanges them.
             if (!gu_wave) {
                 float *pw = &sh.scr[(wave - NGU) * D];
-                const float *xv = &sh.xn[lane * 32];
+                const float *xv = &sh.xn[lane * XN_LD];
 #pragma unroll
                 for (int k = 0; k < 8; k++) {
                     const float4 wv = RROW(k);
@@ -659,8 +690,8 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                     sh.w[j] = a.norm_topk ? sh.p[sh.idx[j]] / wsum : sh.p[sh.idx[j]];
                 if (xcd == 0 && rank == 0) atomicAdd(&ws->status[2], 1);
             }
+            __syncthreads();
         }
-        __syncthreads();
         TRACE(3);
 
         // ---- C: gate/up + SwiGLU for expert slot `xcd` -----------------------------
@@ -701,15 +732,17 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                 wave_lds_sync();
                 if (lane < GU_R) sh.gu[wave][lane] = lds_seq_sum(&terms[lane * GU_LD], NB, 0.0f);
                 wave_lds_sync();
+                TRACE(19);
                 if (lane < GU_H) {
                     const float g = sh.gu[wave][lane], u = sh.gu[wave][GU_H + lane];
                     put_tagged<true>(&ws->h[xcd][h0 + lane],
                                (g / (1.0f + mia_expf_glibc_tab(-g, sh.etab))) * u, tag);
                 }
+                TRACE_BY(16, 64);
+                TRACE_BY(17, 192);
             }
         } else {
-            // the down rows of this workgroup (used after the next sync; an
-            // XCD without a routed slot loads them too and never uses them)
+            // the down rows of this workgroup (used once h has arrived)
 #pragma unroll
             for (int k = 0; k < DPK; k++) {
                 const int pidx = dt + NDN * 64 * k;
@@ -721,45 +754,59 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                 wsc[k] = ((const float *)(eb + a.lay.down_s))[(size_t)row * NBH + blk];
             }
             LOAD_ROUTER(lnext);
-        }
-        TRACE(4);
-        // Wave 1 computes the gate weights while the XCD's h values arrive;
-        // the down waves keep their loads in flight meanwhile.
-        if (wave == 1 && !sh.fallback) {
-            // Softmax of the parallel logits (forward.c:95-101 in shape; the
-            // gate weights only need the 1e-3 tolerance), renormalised as
-            // forward.c:178-181.
-            const float mx = sh.lf[sh.idx[0]];
-            const float e0 = mia_expf_glibc_tab(sh.lf[lane] - mx, sh.etab);
-            const float e1 = mia_expf_glibc_tab(sh.lf[lane + 64] - mx, sh.etab);
-            const float sum = wave_sum_f(e0 + e1);
-            if (lane < K) sh.pk[lane] = mia_expf_glibc_tab(sh.lf[sh.idx[lane]] - mx, sh.etab) / sum;
-            wave_lds_sync();
-            if (lane == 0) {
-                float wsum = 0.0f;
-                for (int j = 0; j < K; j++) wsum = wsum + sh.pk[j];
-                for (int j = 0; j < K; j++) sh.w[j] = a.norm_topk ? sh.pk[j] / wsum : sh.pk[j];
+            if (wave == NGU && !sh.fallback) {
+                // The gate weights: softmax of the parallel logits
+                // (forward.c:95-101 in shape; the weights only need the 1e-3
+                // tolerance), renormalised as forward.c:178-181.
+                const float mx = sh.lf[sh.idx[0]];
+                const float e0 = mia_expf_glibc_tab(sh.lf[lane] - mx, sh.etab);
+                const float e1 = mia_expf_glibc_tab(sh.lf[lane + 64] - mx, sh.etab);
+                const float sum = wave_sum_f(e0 + e1);
+                if (lane < K) sh.pk[lane] = mia_expf_glibc_tab(sh.lf[sh.idx[lane]] - mx, sh.etab) / sum;
+                wave_lds_sync();
+                if (lane == 0) {
+                    float wsum = 0.0f;
+                    for (int j = 0; j < K; j++) wsum = wsum + sh.pk[j];
+                    for (int j = 0; j < K; j++) sh.w[j] = a.norm_topk ? sh.pk[j] / wsum : sh.pk[j];
+                }
+                TRACE_BY(18, NGU * 64);
             }
         }
+        TRACE(4);
         // ---- D: Q8(h) and down ------------------------------------------------------
         const int par = l & 1;
         if (active) {
-            // polled by the gate/up waves, which have no loads in flight
+            // h is polled by the gate/up waves, which have no loads in
+            // flight: wave w takes h[192w, 192w + 192), i.e. six Q8 blocks,
+            // two per register with one block per 32-lane half, and
+            // quantizes them in place (quant.c:11-27 per element; the block
+            // maximum is order-free).
             if (gu_wave) {
-                float hv[EH / (NGU * 64)];
-                get_tagged<EH / (NGU * 64), true>(ws, &ws->h[xcd][tid], NGU * 64, tag, hv);
+                constexpr int HPW = EH / (NGU * 64);
+                float hv[HPW];
+                get_tagged<HPW, true>(ws, &ws->h[xcd][wave * 64 * HPW + lane], 64, tag, hv);
 #pragma unroll
-                for (int k = 0; k < EH / (NGU * 64); k++) sh.hs[tid + NGU * 64 * k] = hv[k];
+                for (int k = 0; k < HPW; k++) {
+                    const int i = wave * 64 * HPW + 64 * k + lane;
+                    float am = fmaxf(0.0f, fabsf(hv[k]));   // a NaN counts as 0, as in the chain
+                    am = fmaxf(am, dpp_keep_f<0x121>(am));  // row_ror 1, 2, 4, 8: 16-lane max
+                    am = fmaxf(am, dpp_keep_f<0x122>(am));
+                    am = fmaxf(am, dpp_keep_f<0x124>(am));
+                    am = fmaxf(am, dpp_keep_f<0x128>(am));
+                    am = fmaxf(am, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(am), 0x401f)));
+                    const float d = am / 127.0f;
+                    const float qi = d != 0.0f ? 1.0f / d : 0.0f;
+                    sh.hq[i] = (int8_t)roundf(hv[k] * qi);
+                    if ((lane & 31) == 0) sh.hsc[i / 32] = d;
+                }
             }
             __syncthreads();
             TRACE(5);
+            TRACE(13);
             if (blockIdx.x == 0 && tid < K) {
                 if (a.idx_out) a.idx_out[(size_t)l * K + tid] = sh.idx[tid];
                 if (a.w_out) a.w_out[(size_t)l * K + tid] = sh.w[tid];
             }
-            if (tid < NBH) q8_block(&sh.hs[tid * 32], &sh.hq[tid * 32], &sh.hsc[tid]);
-            __syncthreads();
-            TRACE(13);
             float *dterm = sh.scr;
             if (!gu_wave) {
 #pragma unroll
@@ -783,14 +830,14 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             // thread (j, r) fetches expert j's output row r; then one thread
             // per row adds them in top-K order
             const int j = tid / DROWS, r = tid % DROWS;
-            if (j < K) get_tagged<1, false>(ws, &ws->out[par][j][rank * DROWS + r], 0, tag, &sh.scr[r * KMAX + j]);
+            if (j < K) get_tagged<1, false>(ws, &ws->out[par][j][rank * DROWS + r], 0, tag, &sh.scr[j * DROWS + r]);
         }
         __syncthreads();
         TRACE(7);
         if (tid < DROWS) {
             const int r = rank * DROWS + tid;
             float v = sh.x[r];
-            for (int j = 0; j < K; j++) v = v + sh.w[j] * sh.scr[tid * KMAX + j];
+            for (int j = 0; j < K; j++) v = v + sh.w[j] * sh.scr[j * DROWS + tid];
             if (l + 1 < a.L) put_tagged<true>(&ws->x[xcd][r], v, tag);
             else if (xcd == 0) a.x[r] = v;
         }
@@ -848,6 +895,7 @@ int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     } else if (mhip_zero(c, ws, offsetof(DecodeWs, x))) {
         return -1;
     }
+    if ((flags & MHIP_DECODE_TRACE) && mhip_zero(c, ws->trace, sizeof(ws->trace))) return -1;
     DecodeArgs a;
     a.table = (const uint8_t *)d_table;
     a.lay = *lay;
