@@ -45,6 +45,20 @@ def cpu_model():
     return platform.processor() or "unknown"
 
 
+def profiled_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` on `workload` from the committed
+    rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, each scaled by the
+    same counter's reading over a copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "%s_%s_traffic.md" % (workload, kernel))
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def routing_census(moe, d_x, d_x0, layers, T, nbytes, d_bias):
     """One untimed pass layer by layer: distinct experts touched per layer."""
     moe.sync()
@@ -152,10 +166,14 @@ def main():
     persistent = T == 1 and not args.multi_kernel
 
     def step():
-        M.lib().mhip_d2d(moe.gpu, d_x, d_x0, nbytes)
         if persistent:
+            # decode: each step takes the previous step's output as its
+            # token (K experts per layer whatever x is, so the bytes per step
+            # do not depend on it)
             moe.decode_dev(0, L, d_x, d_bias)
-        elif d_bias is None:
+            return
+        M.lib().mhip_d2d(moe.gpu, d_x, d_x0, nbytes)
+        if d_bias is None:
             moe.stack_dev(0, L, d_x, T)
         else:
             for l in range(L):
@@ -165,15 +183,18 @@ def main():
     step_bytes = W.bytes_per_step(L, T, touched, shape)
     step_ops = W.ops_per_step(L, T, shape)
 
+    M.lib().mhip_d2d(moe.gpu, d_x, d_x0, nbytes)
     for _ in range(args.warmup):
         step()
     moe.sync()
 
     # Timed region: host clock between two stream synchronisations, HIP events
     # on the library stream, and events around every launch of the dominant
-    # kernel (the persistent decode kernel, or k_gateup per layer).
+    # kernel (k_gateup per layer). A persistent decode step is one launch of
+    # the dominant kernel, so the two region events time it (launch gaps
+    # included); per-launch events would add their own gaps to the step.
     dom = "decode" if persistent else "gateup"
-    moe.stage_timing([dom], max_launches=(1 if persistent else L) * args.steps + 16)
+    moe.stage_timing([] if persistent else [dom], max_launches=L * args.steps + 16)
     moe.sync()
     t0 = time.perf_counter()
     moe.mark(0)
@@ -183,7 +204,7 @@ def main():
     moe.sync()
     t1 = time.perf_counter()
     ev_ms = moe.elapsed_ms(0, 1)
-    stage = {dom: moe.stage_time(dom)}
+    stage = {dom: (ev_ms, args.steps) if persistent else moe.stage_time(dom)}
     dstat = moe.decode_status() if persistent else None
     # Untimed diagnostic pass: every stage bracketed by events.
     diag_steps = min(args.steps, 5)
@@ -247,7 +268,8 @@ def main():
         "vs_baseline": None,
         "dtype": "int8 x int8 -> int32 block dots, fp32 scales/accumulation (Q8_0)",
         "data": "synthetic: seeded N(0,0.02) weights quantized to Q8_0, x ~ N(0,1), "
-                "generated in HBM (no checkpoint offline)",
+                "generated in HBM (no checkpoint offline)"
+                + ("; each decode step continues from the previous step's x" if persistent else ""),
         "config": {
             "workload": "%s: %s" % (args.workload, wl["doc"]),
             "layers": L, "tokens_per_step": T, "hidden": d,
@@ -276,7 +298,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": profiled_traffic(args.workload, "k_decode_stack" if persistent else "k_gateup"),
             "bytes_per_launch": dom_bytes,
             "avg_launch_us": dom_avg_s * 1e6,
         }),

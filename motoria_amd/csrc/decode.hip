@@ -78,8 +78,9 @@ static_assert(NT == 4 * E, "ranks: four threads per expert");
 typedef unsigned long long tw;
 
 struct DecodeWs {
-    unsigned gstart[64];          // start barrier (device scope)
-    int status[64];               // [0] abort bits, [1] rms fallbacks, [2] router fallbacks
+    unsigned gstart[64];          // start barrier: NWG arrivals per launch, never reset
+    tw status[32];                // (epoch << 32) | value: [0] abort bits,
+                                  // [1] rms fallbacks, [2] router fallbacks
     // Every per-XCD array starts on a 256-byte boundary, so no cache line
     // holds data of two XCDs.
     alignas(256) tw x[NX][D];     // residual stream after each layer, per XCD
@@ -117,9 +118,30 @@ __device__ __forceinline__ unsigned xcc_id() {
 __device__ __forceinline__ unsigned ld_dev(const unsigned *p) {
     return __hip_atomic_load((unsigned *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
+// Status words carry the epoch of the launch that wrote them in their high
+// half (a word of an earlier launch reads as 0), so they need no clearing
+// between launches.
+enum { ST_ABORT = 0, ST_RMS = 1, ST_ROUTER = 2 };
+__device__ __forceinline__ unsigned status_get(DecodeWs *ws, int i, unsigned epoch) {
+    const tw v = __hip_atomic_load(&ws->status[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return (unsigned)(v >> 32) == epoch ? (unsigned)v : 0u;
+}
+// status[i] |= bits, or += 1 when `add` (device-scope compare-and-swap).
+__device__ void status_update(DecodeWs *ws, int i, unsigned epoch, bool add, unsigned bits) {
+    tw old = __hip_atomic_load(&ws->status[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (;;) {
+        const unsigned cur = (unsigned)(old >> 32) == epoch ? (unsigned)old : 0u;
+        const tw w = ((tw)epoch << 32) | (add ? cur + 1 : (cur | bits));
+        if (w == old) return;
+        const tw prev = atomicCAS(&ws->status[i], old, w);
+        if (prev == old) return;
+        old = prev;
+    }
+}
 // Abort bits: 1 = workgroup not on the expected XCD, 2 = a wait timed out.
-__device__ __forceinline__ bool aborted(DecodeWs *ws) {
-    return ld_dev((const unsigned *)&ws->status[0]) != 0;
+__device__ __forceinline__ bool aborted(DecodeWs *ws, unsigned epoch) {
+    return status_get(ws, ST_ABORT, epoch) != 0;
 }
 
 // Two kinds of exchange. Data read only inside the writer's XCD (x, logits,
@@ -196,8 +218,8 @@ __device__ __forceinline__ void get_tagged(DecodeWs *ws, const tw *p, int stride
 #pragma unroll
         for (int k = 0; k < N; k++) ready = ready && (unsigned)(v[k] >> 32) == tag;
         if (ready) break;
-        if (++s > SPIN || ((s & 255) == 0 && aborted(ws))) {
-            atomicOr(&ws->status[0], 2);
+        if (++s > SPIN || ((s & 255) == 0 && aborted(ws, tag >> 8))) {
+            status_update(ws, ST_ABORT, tag >> 8, false, 2);
             break;
         }
         load_words<N, LOCAL>(v, p, stride);
@@ -206,11 +228,11 @@ __device__ __forceinline__ void get_tagged(DecodeWs *ws, const tw *p, int stride
     for (int k = 0; k < N; k++) out[k] = __uint_as_float((unsigned)v[k]);
 }
 
-__device__ void wait_flag(DecodeWs *ws, const unsigned *flag, unsigned value) {
+__device__ void wait_flag(DecodeWs *ws, const unsigned *flag, unsigned value, unsigned epoch) {
     long s = 0;
     while (ld_dev(flag) < value) {
-        if (++s > SPIN || ((s & 255) == 0 && aborted(ws))) {
-            atomicOr(&ws->status[0], 2);
+        if (++s > SPIN || ((s & 255) == 0 && aborted(ws, epoch))) {
+            status_update(ws, ST_ABORT, epoch, false, 2);
             break;
         }
     }
@@ -315,7 +337,6 @@ struct Lds {
     int rk[4][E];                 // partial ranks
     double part[NWAVE];
     int order[E];                 // expert of each rank (ranks 0..K used)
-    float pk[KMAX];
     float inv;
     float sum;
     int idx[KMAX];
@@ -366,16 +387,18 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
     const size_t layer_bytes = (size_t)E * a.lay.expert_bytes;
     const bool gu_wave = wave < NGU;
 
-    // Start: every workgroup checks its XCD, then a device-wide barrier.
+    // Start: every workgroup checks its XCD, then a device-wide barrier
+    // (the counter gains NWG per launch; epochs count launches since the
+    // workspace was cleared).
     if (tid == 0) {
-        if (xcc_id() != (unsigned)xcd) atomicOr(&ws->status[0], 1);
+        if (xcc_id() != (unsigned)xcd) status_update(ws, ST_ABORT, a.epoch, false, 1);
         __builtin_amdgcn_s_waitcnt(0);
         __hip_atomic_fetch_add(&ws->gstart[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        wait_flag(ws, &ws->gstart[0], NWG);
+        wait_flag(ws, &ws->gstart[0], NWG * a.epoch, a.epoch);
     }
     __syncthreads();
     // An XCD without a routed slot has nothing that another XCD reads.
-    if (aborted(ws) || xcd >= K) return;
+    if (aborted(ws, a.epoch) || xcd >= K) return;
 
     // One register array serves both roles. A gate/up wave holds its GU_R
     // weight rows in wq0/wq1/wsc during stage C. A down wave holds its DPK
@@ -451,7 +474,7 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                     double sq = 0.0;
                     for (int i = 0; i < D; i++) sq = sq + (double)sh.x[i] * (double)sh.x[i];
                     sh.inv = (float)(1.0 / sqrt(sq / D + (double)a.eps));
-                    if (blockIdx.x == 0) atomicAdd(&ws->status[1], 1);
+                    if (blockIdx.x == 0) status_update(ws, ST_RMS, a.epoch, true, 0);
                 }
                 __syncthreads();
                 inv = sh.inv;
@@ -688,7 +711,7 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                 for (int j = 0; j < K; j++) wsum = wsum + sh.p[sh.idx[j]];
                 for (int j = 0; j < K; j++)
                     sh.w[j] = a.norm_topk ? sh.p[sh.idx[j]] / wsum : sh.p[sh.idx[j]];
-                if (xcd == 0 && rank == 0) atomicAdd(&ws->status[2], 1);
+                if (xcd == 0 && rank == 0) status_update(ws, ST_ROUTER, a.epoch, true, 0);
             }
             __syncthreads();
         }
@@ -743,6 +766,26 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             }
         } else {
             // the down rows of this workgroup (used once h has arrived)
+            if (wave == NGU && !sh.fallback) {
+                // The gate weights, before this wave's loads (a wave waiting
+                // to issue a load runs nothing else, and the CU takes its
+                // vector memory instructions in order). Softmax of the
+                // parallel logits (forward.c:95-101 in shape; the weights
+                // only need the 1e-3 tolerance); with renormalisation
+                // (forward.c:178-181) the full sum cancels and only the
+                // top K exponentials are needed.
+                const float mx = sh.lf[sh.idx[0]];
+                const float ek = mia_expf_glibc_tab(sh.lf[sh.idx[min(lane, K - 1)]] - mx, sh.etab);
+                const float ej = lane < K ? ek : 0.0f;
+                float den;
+                if (a.norm_topk)
+                    den = wave_sum_f(ej);
+                else
+                    den = wave_sum_f(mia_expf_glibc_tab(sh.lf[lane] - mx, sh.etab) +
+                                     mia_expf_glibc_tab(sh.lf[lane + 64] - mx, sh.etab));
+                if (lane < K) sh.w[lane] = ej / den;
+                TRACE_BY(18, NGU * 64);
+            }
 #pragma unroll
             for (int k = 0; k < DPK; k++) {
                 const int pidx = dt + NDN * 64 * k;
@@ -754,23 +797,6 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                 wsc[k] = ((const float *)(eb + a.lay.down_s))[(size_t)row * NBH + blk];
             }
             LOAD_ROUTER(lnext);
-            if (wave == NGU && !sh.fallback) {
-                // The gate weights: softmax of the parallel logits
-                // (forward.c:95-101 in shape; the weights only need the 1e-3
-                // tolerance), renormalised as forward.c:178-181.
-                const float mx = sh.lf[sh.idx[0]];
-                const float e0 = mia_expf_glibc_tab(sh.lf[lane] - mx, sh.etab);
-                const float e1 = mia_expf_glibc_tab(sh.lf[lane + 64] - mx, sh.etab);
-                const float sum = wave_sum_f(e0 + e1);
-                if (lane < K) sh.pk[lane] = mia_expf_glibc_tab(sh.lf[sh.idx[lane]] - mx, sh.etab) / sum;
-                wave_lds_sync();
-                if (lane == 0) {
-                    float wsum = 0.0f;
-                    for (int j = 0; j < K; j++) wsum = wsum + sh.pk[j];
-                    for (int j = 0; j < K; j++) sh.w[j] = a.norm_topk ? sh.pk[j] / wsum : sh.pk[j];
-                }
-                TRACE_BY(18, NGU * 64);
-            }
         }
         TRACE(4);
         // ---- D: Q8(h) and down ------------------------------------------------------
@@ -870,30 +896,34 @@ int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
                              "2048/128/<=8/768", s->dim, s->n_experts, s->n_active,
                           s->expert_hidden);
     if (L <= 0) return L == 0 ? 0 : mhip::fail(c, "decode stack: L=%d", L);
-    hipDeviceProp_t prop;
-    if (mhip::check(c, hipGetDeviceProperties(&prop, c->device), "hipGetDeviceProperties"))
-        return -1;
-    int occ = 0;
-    if (mhip::check(c, hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_decode_stack, NT, 0),
-                    "occupancy"))
-        return -1;
-    if (prop.multiProcessorCount != NWG || occ < 1)
-        return mhip::fail(c, "decode stack needs %d CUs with one %d-thread workgroup each "
-                             "(device has %d CUs, occupancy %d)", NWG, NT,
-                          prop.multiProcessorCount, occ);
+    if (!c->decode_checked) {
+        // once per context: the device properties query is slow
+        hipDeviceProp_t prop;
+        if (mhip::check(c, hipGetDeviceProperties(&prop, c->device), "hipGetDeviceProperties"))
+            return -1;
+        int occ = 0;
+        if (mhip::check(c,
+                        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_decode_stack, NT, 0),
+                        "occupancy"))
+            return -1;
+        if (prop.multiProcessorCount != NWG || occ < 1)
+            return mhip::fail(c, "decode stack needs %d CUs with one %d-thread workgroup each "
+                                 "(device has %d CUs, occupancy %d)", NWG, NT,
+                              prop.multiProcessorCount, occ);
+        c->decode_checked = 1;
+    }
     if ((uintptr_t)d_ws % 256)
         return mhip::fail(c, "decode stack: workspace %p is not 256-byte aligned", d_ws);
     DecodeWs *ws = (DecodeWs *)d_ws;
-    // The start barrier and status start at zero (fill kernel, no memset).
-    // Exchanged words are tagged with this launch's epoch, so stale words of
-    // earlier launches never match; a workspace this context has not used
-    // last (or an epoch about to leave its 24 bits) is cleared whole first.
+    // Exchanged words and status words are tagged with the launch's epoch,
+    // so stale words of earlier launches never match, and the start counter
+    // grows by NWG per launch: nothing is cleared between launches. A
+    // workspace this context has not used last (or an epoch about to leave
+    // its 24 bits) is cleared whole first (fill kernel, no memset).
     if (ws != c->decode_ws || c->decode_epoch >= (1u << 24) - 1) {
         if (mhip_zero(c, ws, offsetof(DecodeWs, trace))) return -1;
         c->decode_ws = ws;
         c->decode_epoch = 0;
-    } else if (mhip_zero(c, ws, offsetof(DecodeWs, x))) {
-        return -1;
     }
     if ((flags & MHIP_DECODE_TRACE) && mhip_zero(c, ws->trace, sizeof(ws->trace))) return -1;
     DecodeArgs a;
@@ -913,17 +943,27 @@ int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     a.flags = flags;
     a.eps = s->norm_eps;
     a.epoch = ++c->decode_epoch;
-    void *args[] = {&a};
+    // An ordinary launch: one 512-thread workgroup fits each of the 256 CUs
+    // (checked above), so on an otherwise idle device all of them are
+    // resident at once. Should one not be, the start barrier times out and
+    // the launch reports abort bit 2 instead of waiting for ever.
     int slot = mhip::stage_begin(c, MHIP_STAGE_DECODE);
-    hipError_t e = hipLaunchCooperativeKernel((const void *)k_decode_stack, dim3(NWG), dim3(NT),
-                                              args, 0, c->stream);
+    k_decode_stack<<<NWG, NT, 0, c->stream>>>(a);
+    const hipError_t e = hipGetLastError();
     mhip::stage_end(c, slot);
+    if (e != hipSuccess) c->decode_epoch--;   // nothing arrived at the start counter
     return mhip::check(c, e, "decode stack launch");
 }
 
 int mhip_decode_status(mhip_ctx *c, const void *d_ws, int status[4]) {
     const DecodeWs *ws = (const DecodeWs *)d_ws;
-    return mhip_d2h(c, status, ws->status, 4 * sizeof(int));
+    tw st[3];
+    if (mhip_d2h(c, st, ws->status, sizeof st)) return -1;
+    for (int i = 0; i < 3; i++)
+        status[i] = (d_ws == c->decode_ws && (unsigned)(st[i] >> 32) == c->decode_epoch)
+                        ? (int)(unsigned)st[i] : 0;
+    status[3] = 0;
+    return 0;
 }
 
 int mhip_decode_trace(mhip_ctx *c, const void *d_ws, unsigned long long *out) {

@@ -20,6 +20,7 @@ struct mhip_ctx {
     int *st_stage;      // [st_cap]
     unsigned decode_epoch;  // launches of the decode kernel (tags its exchanged data)
     const void *decode_ws;  // workspace those tags were written to
+    int decode_checked;     // the device was checked for the decode launch shape
     char err[512];
 };
 
