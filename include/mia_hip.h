@@ -36,12 +36,15 @@ typedef struct {
  * 256-byte aligned). Codes are row-major int8, scales row-major fp32 with one
  * scale per 32-value block; values and bytes-per-weight are those of the
  * reference's 36-byte Q8_0 blocks, only regrouped (codes apart from scales)
- * so that rows load as aligned 16-byte vectors.
+ * so that rows load as aligned 16-byte vectors. A second, block-major copy
+ * of the scales serves the matrix-core kernels, which read one block of
+ * many rows at a time.
  */
 typedef struct {
-    size_t gate_q, up_q, down_q; /* [eh][d], [eh][d], [d][eh] int8 */
-    size_t gate_s, up_s, down_s; /* [eh][d/32], [eh][d/32], [d][eh/32] fp32 */
-    size_t expert_bytes;         /* stride between experts */
+    size_t gate_q, up_q, down_q;    /* [eh][d], [eh][d], [d][eh] int8 */
+    size_t gate_s, up_s, down_s;    /* [eh][d/32], [eh][d/32], [d][eh/32] fp32 */
+    size_t gate_st, up_st, down_st; /* [d/32][eh], [d/32][eh], [eh/32][d] fp32 (same values) */
+    size_t expert_bytes;            /* stride between experts */
 } mhip_layout;
 
 int mhip_layout_of(const mhip_dims *s, mhip_layout *out);
@@ -123,6 +126,7 @@ typedef struct {
     void *xdq;        /* [T][d]    fp16: the Q8 codes of xn (matrix-core path) */
     void *hdq;        /* [T*K][eh] fp16: d_h * q_h of Q8(h), bucketed (matrix-core path) */
     int *gtile;       /* [E+1]     tiles of MHIP_GEMM_TM rows before each group */
+    float *xsb;       /* [d/32][T*K] Q8 scales of xn per assignment, bucketed (matrix-core path) */
 } mhip_scratch;
 
 /* Rows of one expert bucket per matrix-core tile. */

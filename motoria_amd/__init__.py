@@ -44,13 +44,14 @@ class Dims(ctypes.Structure):
 
 class Layout(ctypes.Structure):
     _fields_ = [("gate_q", _sz), ("up_q", _sz), ("down_q", _sz), ("gate_s", _sz),
-                ("up_s", _sz), ("down_s", _sz), ("expert_bytes", _sz)]
+                ("up_s", _sz), ("down_s", _sz), ("gate_st", _sz), ("up_st", _sz),
+                ("down_st", _sz), ("expert_bytes", _sz)]
 
 
 class Scratch(ctypes.Structure):
     _fields_ = [(n, _p) for n in ("xn", "xq", "xs", "logits", "idx", "w", "counts", "offsets",
                                   "perm", "pos", "groups", "h", "tmp", "status", "xdq",
-                                  "hdq", "gtile")]
+                                  "hdq", "gtile", "xsb")]
 
 
 # Every function the library exports, with its ctypes signature. tests check

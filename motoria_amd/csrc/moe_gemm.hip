@@ -154,7 +154,8 @@ __device__ __forceinline__ h8 codes8(unsigned w0, unsigned w1) {
 struct Src {
     const _Float16 *a0, *a1;  // A chunks of rows ar0, ar1 (fp16, KB halves per step)
     const int8_t *b;          // B 16-byte half of weight row br (KB bytes per step)
-    const float *s;           // a block-scale row (one float per step)
+    const float *s;           // a block scale in a block-major array ...
+    int sstep;                // ... whose blocks are sstep floats apart
 };
 
 // The k loop over nk steps (nk >= NS - 1). On return acc[i][j][r] holds
@@ -177,7 +178,7 @@ __device__ __forceinline__ void gemm_tile(Step *ring, const Src &src, int nk, f4
         dma16(st + oa0, src.a0 + (size_t)k * KB);
         dma16(st + oa1, src.a1 + (size_t)k * KB);
         dma16(st + ob, src.b + (size_t)k * KB);
-        dma4(st + os, src.s + k);
+        dma4(st + os, src.s + (size_t)k * src.sstep);
     };
 #pragma unroll
     for (int s = 0; s < NS - 1; s++) issue(s);
@@ -242,6 +243,17 @@ __device__ __forceinline__ void a_rows(int &r0, int &c0, int &r1, int &c1) {
     c1 = aslot(r1, lane & 3);
 }
 
+// ---- x block scales in bucketed, block-major order --------------------------------
+//
+// xsb[k][p] = xs[t][k] for the assignment p = (t, j) in bucketed order, so a
+// tile's 128 rows read their scales of block k as one contiguous run.
+__global__ __launch_bounds__(256) void k_xs_bucket(const float *__restrict__ xs,
+                                                   const int *__restrict__ perm,
+                                                   float *__restrict__ xsb, int A, int nb, int K) {
+    const int p = blockIdx.x * 256 + threadIdx.x, k = blockIdx.y;
+    if (p < A) xsb[(size_t)k * A + p] = xs[(size_t)(perm[p] / K) * nb + k];
+}
+
 // ---- gate/up + SwiGLU + Q8(h) ----------------------------------------------------
 //
 // blockIdx.x = tile of assignment rows (gtile numbering), blockIdx.y = 64
@@ -261,8 +273,8 @@ union alignas(16) DownLds {
 
 __global__ __launch_bounds__(GT, 1) void k_gateup_mfma(
     const uint8_t *__restrict__ table, mhip_layout lay, const _Float16 *__restrict__ xq16,
-    const float *__restrict__ xs, const int *__restrict__ groups, const int *__restrict__ gtile,
-    const int *__restrict__ perm, _Float16 *__restrict__ hdq, int d, int eh, int K) {
+    const float *__restrict__ xsb, const int *__restrict__ groups, const int *__restrict__ gtile,
+    const int *__restrict__ perm, _Float16 *__restrict__ hdq, int d, int eh, int K, int A) {
     __shared__ GateUpLds L;
     TileRef tr;
     if (!tile_of(groups, gtile, eh / (TN / 2), tr)) return;
@@ -285,16 +297,19 @@ __global__ __launch_bounds__(GT, 1) void k_gateup_mfma(
         const int wr = h0 + 16 * wave + br;
         src.b = (const int8_t *)(ex + (bj == 0 ? lay.gate_q : lay.up_q)) + (size_t)wr * d +
                 (lane & 1) * 16;
+        // block-major scales: the 128 rows of a step are 4 (waves 0, 1) or
+        // 1 (waves 2, 3) contiguous runs
         if (wave < 2) {
             // scale of B row 64*wave + lane
             const int b = 64 * wave + lane;
             const int sw = h0 + 16 * (b >> 5) + (b & 15);
-            src.s = (const float *)(ex + (((b >> 4) & 1) == 0 ? lay.gate_s : lay.up_s)) +
-                    (size_t)sw * nb;
+            src.s = (const float *)(ex + (((b >> 4) & 1) == 0 ? lay.gate_st : lay.up_st)) + sw;
+            src.sstep = eh;
         } else {
             // scale of assignment row 64*(wave-2) + lane
             const int m = 64 * (wave - 2) + lane;
-            src.s = xs + (size_t)(perm[base + min(m, nrows - 1)] / K) * nb;
+            src.s = xsb + base + min(m, nrows - 1);
+            src.sstep = A;
         }
     }
 
@@ -371,9 +386,10 @@ __global__ __launch_bounds__(GT, 2) void k_down_mfma(const uint8_t *__restrict__
         src.a1 = hdq + (size_t)(base + min(r1, nrows - 1)) * eh + c1 * 8;
         const int row = n0 + 32 * wave + (lane >> 1);
         src.b = (const int8_t *)(ex + lay.down_q) + (size_t)row * eh + (lane & 1) * 16;
-        // scales of weight rows 64*(wave&1) + lane (waves 2, 3 repeat waves
-        // 0, 1 into the unused assignment-scale slot)
-        src.s = (const float *)(ex + lay.down_s) + (size_t)(n0 + 64 * (wave & 1) + lane) * nbh;
+        // scales of weight rows 64*(wave&1) + lane, block-major (waves 2, 3
+        // repeat waves 0, 1 into the unused assignment-scale slot)
+        src.s = (const float *)(ex + lay.down_st) + n0 + 64 * (wave & 1) + lane;
+        src.sstep = d;
     }
 
     f4v acc[MI][NJ];
@@ -417,11 +433,13 @@ static unsigned gemm_grid(int A, int E, int ny) {
 int launch_gateup_mfma(hipStream_t st, const mhip_dims *s, const mhip_layout *lay,
                        const void *d_table_layer, const mhip_scratch *sc, int A) {
     const int d = s->dim, eh = s->expert_hidden;
+    k_xs_bucket<<<dim3((A + 255) / 256, d / KB), 256, 0, st>>>(sc->xs, sc->perm, sc->xsb, A,
+                                                              d / KB, s->n_active);
     const unsigned grid = gemm_grid(A, s->n_experts, eh / (TN / 2));
     k_gateup_mfma<<<grid, GT, 0, st>>>((const uint8_t *)d_table_layer, *lay,
-                                       (const _Float16 *)sc->xdq, sc->xs, sc->groups,
+                                       (const _Float16 *)sc->xdq, sc->xsb, sc->groups,
                                        sc->gtile, sc->perm, (_Float16 *)sc->hdq, d, eh,
-                                       s->n_active);
+                                       s->n_active, A);
     return (int)hipGetLastError();
 }
 

@@ -296,81 +296,232 @@ size_t router_logits_lds(int C, int d) {
 // ---- dispatch -------------------------------------------------------------
 //
 // Stable counting sort of the A = T*K assignments a = t*K + j by expert
-// idx[a] in one workgroup: per-thread histograms of contiguous chunks, an
-// exclusive scan per expert over the threads, then each thread scatters its
-// chunk in order. Within an expert the order is by t (then j), the order in
-// which the reference visits tokens. Also emits the list of non-empty
-// experts as (expert, begin, end) groups, and gtile[g], the number of
-// tm-row tiles before group g (gtile[n_groups] = all tiles). status[0] |= 1
-// on a bad index.
-__global__ __launch_bounds__(256) void k_dispatch(const int *__restrict__ idx, int A, int E,
-                                                  int *__restrict__ counts,
-                                                  int *__restrict__ offsets,
-                                                  int *__restrict__ perm,
-                                                  int *__restrict__ pos,
-                                                  int *__restrict__ groups,
-                                                  int *__restrict__ gtile, int tm, int *status) {
-    extern __shared__ unsigned char lds[];
-    const int nt = blockDim.x;
-    const int tid = threadIdx.x;
-    unsigned short *hist = (unsigned short *)lds;           // [nt][E]
-    int *off = (int *)(lds + align256((size_t)nt * E * 2));   // [E+1]
-    unsigned char *key = (unsigned char *)(off + E + 1);     // [A]
-    for (int i = tid; i < nt * E; i += nt) hist[i] = 0;
-    int bad = 0;
-    for (int a = tid; a < A; a += nt) {
-        int e = idx[a];
-        if (e < 0 || e >= E) {
-            bad = 1;
-            e = 0;
-        }
-        key[a] = (unsigned char)e;
+// idx[a]: within an expert the order is by t (then j), the order in which
+// the reference visits tokens. Three small kernels over chunks of DCH
+// consecutive assignments, one wavefront per chunk:
+//   k_disp_count    per-chunk expert counts           -> hist[e][chunk]
+//   k_disp_scan     per expert, exclusive scan over the chunks; counts
+//   k_disp_scatter  offsets, the list of non-empty experts as (expert,
+//                   begin, end) groups and gtile[g], the number of tm-row
+//                   tiles before group g (gtile[n_groups] = all tiles); then
+//                   each chunk in order, 64 assignments per step: the rank
+//                   of a lane among the step's lanes with the same expert
+//                   comes from one ballot per bit of the expert index.
+// Up to DSMALL chunks, one workgroup does all three (k_disp_small).
+// status[0] |= 1 on a bad index (the assignment is then counted as expert 0).
+constexpr int DCH = 256;               // assignments per chunk (4 steps of 64)
+constexpr int DWG = 4;                 // chunks (wavefronts) per workgroup
+
+// Keeps the compiler from moving LDS accesses across this point; a
+// wavefront's own LDS operations execute in program order.
+__device__ __forceinline__ void wave_order() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ int disp_key(const int *idx, int a, int A, int E, int *status) {
+    if (a >= A) return -1;
+    const int e = idx[a];
+    if (e < 0 || e >= E) {
+        atomicOr(&status[0], 1);
+        return 0;
     }
-    if (bad) atomicOr(&status[0], 1);
-    __syncthreads();
-    const int chunk = (A + nt - 1) / nt;
-    const int a0 = tid * chunk < A ? tid * chunk : A;
-    const int a1 = a0 + chunk < A ? a0 + chunk : A;
-    for (int a = a0; a < a1; a++) hist[tid * E + key[a]]++;
-    __syncthreads();
-    for (int e = tid; e < E; e += nt) {
-        int run = 0;
-        for (int q = 0; q < nt; q++) {
-            const int cnt = hist[q * E + e];
-            hist[q * E + e] = (unsigned short)run;
-            run += cnt;
-        }
-        off[e] = run;
+    return e;
+}
+
+// Lanes of the wavefront whose key equals this lane's (keys < 2^bits; -1
+// matches no lane).
+__device__ __forceinline__ uint64_t same_key_lanes(int key, int bits) {
+    uint64_t m = __ballot(key >= 0);
+    for (int b = 0; b < bits; b++) {
+        const uint64_t on = __ballot(key >= 0 && ((key >> b) & 1));
+        m &= ((key >> b) & 1) ? on : ~on;
     }
+    return key >= 0 ? m : 0ull;
+}
+
+// One wavefront counts chunk ch into cnt[E] (zeroed by the caller).
+__device__ __forceinline__ void disp_count_chunk(const int *idx, int A, int E, int ch, int *cnt,
+                                                 int *status) {
+    const int lane = threadIdx.x & 63;
+    for (int s = 0; s < DCH / 64; s++) {
+        const int k = disp_key(idx, ch * DCH + s * 64 + lane, A, E, status);
+        if (k >= 0) atomicAdd(&cnt[k], 1);
+    }
+}
+
+// One wavefront places chunk ch in order; bs[E] holds each expert's next
+// position and is advanced.
+__device__ __forceinline__ void disp_scatter_chunk(const int *idx, int A, int E, int ch, int bits,
+                                                   int *bs, int *perm, int *pos, int *status) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t below = (1ull << lane) - 1;
+    for (int s = 0; s < DCH / 64; s++) {
+        const int a = ch * DCH + s * 64 + lane;
+        const int k = disp_key(idx, a, A, E, status);
+        const uint64_t m = same_key_lanes(k, bits);
+        if (k >= 0) {
+            const int p = bs[k] + __popcll(m & below);
+            perm[p] = a;
+            pos[a] = p;
+        }
+        wave_order();
+        // the highest lane of each key advances that key's position
+        if (k >= 0 && (m >> lane) == 1ull) bs[k] += __popcll(m);
+        wave_order();
+    }
+}
+
+__global__ __launch_bounds__(64 * DWG) void k_disp_count(const int *__restrict__ idx, int A, int E,
+                                                         int nch, int *__restrict__ hist,
+                                                         int *status) {
+    extern __shared__ int cnt[];  // [DWG][E]
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int ch = blockIdx.x * DWG + w;
+    int *c = cnt + w * E;
+    for (int e = lane; e < E; e += 64) c[e] = 0;
     __syncthreads();
-    if (tid == 0) {
-        int acc = 0, g = 0, tiles = 0;
+    if (ch < nch) disp_count_chunk(idx, A, E, ch, c, status);
+    __syncthreads();
+    if (ch < nch)
+        for (int e = lane; e < E; e += 64) hist[(size_t)e * nch + ch] = c[e];
+}
+
+// counts, offsets, groups and gtile from the expert totals (one thread).
+__device__ void disp_groups(int E, const int *tot, int *counts, int *offsets, int *groups,
+                            int *gtile, int tm) {
+    int acc = 0, g = 0, tiles = 0;
+    for (int x = 0; x < E; x++) {
+        const int n = tot[x];
+        counts[x] = n;
+        offsets[x] = acc;
+        if (n > 0) {
+            groups[1 + 3 * g] = x;
+            groups[2 + 3 * g] = acc;
+            groups[3 + 3 * g] = acc + n;
+            gtile[g] = tiles;
+            tiles += (n + tm - 1) / tm;
+            g++;
+        }
+        acc += n;
+    }
+    offsets[E] = acc;
+    groups[0] = g;
+    gtile[g] = tiles;
+}
+
+// Workgroup e: exclusive prefix of expert e's counts over the chunks, in
+// place; the total goes to counts[e].
+__global__ __launch_bounds__(256) void k_disp_scan(int nch, int *__restrict__ hist,
+                                                   int *__restrict__ counts) {
+    __shared__ int wsum[4];
+    __shared__ int carry;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    int *row = hist + (size_t)blockIdx.x * nch;
+    if (threadIdx.x == 0) carry = 0;
+    for (int c0 = 0; c0 < nch; c0 += 256) {
+        const int c = c0 + threadIdx.x;
+        const int v = c < nch ? row[c] : 0;
+        int inc = v;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int u = __shfl_up(inc, o);
+            if (lane >= o) inc += u;
+        }
+        if (lane == 63) wsum[w] = inc;
+        __syncthreads();
+        int pre = carry;
+        for (int k = 0; k < w; k++) pre += wsum[k];
+        if (c < nch) row[c] = pre + inc - v;
+        __syncthreads();
+        if (threadIdx.x == 255) carry = pre + inc;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) counts[blockIdx.x] = carry;
+}
+
+// Every workgroup derives the experts' first positions from counts[];
+// workgroup 0 also writes offsets, groups and gtile.
+__global__ __launch_bounds__(64 * DWG) void k_disp_scatter(const int *__restrict__ idx, int A,
+                                                           int E, int nch, int bits,
+                                                           const int *__restrict__ hist,
+                                                           int *__restrict__ counts,
+                                                           int *__restrict__ offsets,
+                                                           int *__restrict__ groups,
+                                                           int *__restrict__ gtile, int tm,
+                                                           int *__restrict__ perm,
+                                                           int *__restrict__ pos,
+                                                           int *status) {
+    extern __shared__ int lds_s[];
+    int *base = lds_s;                 // [DWG][E]: next position of each expert
+    int *tot = lds_s + DWG * E;        // [E]
+    int *off = tot + E;                // [E]
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) tot[e] = counts[e];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int acc = 0;
         for (int e = 0; e < E; e++) {
-            const int cnt = off[e];
-            counts[e] = cnt;
-            offsets[e] = acc;
             off[e] = acc;
-            if (cnt > 0) {
-                groups[1 + 3 * g] = e;
-                groups[2 + 3 * g] = acc;
-                groups[3 + 3 * g] = acc + cnt;
-                gtile[g] = tiles;
-                tiles += (cnt + tm - 1) / tm;
-                g++;
-            }
-            acc += cnt;
+            acc += tot[e];
         }
-        off[E] = acc;
-        offsets[E] = acc;
-        groups[0] = g;
-        gtile[g] = tiles;
+        if (blockIdx.x == 0) disp_groups(E, tot, counts, offsets, groups, gtile, tm);
     }
     __syncthreads();
-    for (int a = a0; a < a1; a++) {
-        const int e = key[a];
-        const int p = off[e] + hist[tid * E + e]++;
-        perm[p] = a;
-        pos[a] = p;
+    const int ch = blockIdx.x * DWG + w;
+    if (ch >= nch) return;  // a whole wavefront: no workgroup barrier follows
+    int *bs = base + w * E;
+    for (int e = lane; e < E; e += 64) bs[e] = off[e] + hist[(size_t)e * nch + ch];
+    wave_order();
+    disp_scatter_chunk(idx, A, E, ch, bits, bs, perm, pos, status);
+}
+
+// All three steps in one workgroup, one wavefront per chunk, for up to
+// DSMALL chunks.
+constexpr int DSMALL = 16;
+__global__ __launch_bounds__(64 * DSMALL) void k_disp_small(const int *__restrict__ idx, int A,
+                                                            int E, int nch, int bits,
+                                                            int *__restrict__ counts,
+                                                            int *__restrict__ offsets,
+                                                            int *__restrict__ perm,
+                                                            int *__restrict__ pos,
+                                                            int *__restrict__ groups,
+                                                            int *__restrict__ gtile, int tm,
+                                                            int *status) {
+    extern __shared__ int lds_i[];
+    int *hist = lds_i;                 // [DSMALL][E]
+    int *tot = lds_i + DSMALL * E;     // [E]
+    int *off = tot + E;                // [E + 1]
+    const int w = threadIdx.x >> 6;
+    for (int i = threadIdx.x; i < DSMALL * E; i += blockDim.x) hist[i] = 0;
+    __syncthreads();
+    if (w < nch) disp_count_chunk(idx, A, E, w, hist + w * E, status);
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        int run = 0;
+        for (int c = 0; c < nch; c++) {
+            const int v = hist[c * E + e];
+            hist[c * E + e] = run;
+            run += v;
+        }
+        tot[e] = run;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        disp_groups(E, tot, counts, offsets, groups, gtile, tm);
+        int acc = 0;
+        for (int e = 0; e < E; e++) {
+            off[e] = acc;
+            acc += tot[e];
+        }
+    }
+    __syncthreads();
+    if (w < nch) {
+        int *bs = hist + w * E;
+        for (int e = threadIdx.x & 63; e < E; e += 64) bs[e] += off[e];
+        wave_order();
+        disp_scatter_chunk(idx, A, E, w, bits, bs, perm, pos, status);
     }
 }
 
@@ -604,6 +755,7 @@ size_t mhip_scratch_bytes(const mhip_dims *s, int T) {
     n += align256(T * d * 2);          // xdq
     n += align256(A * eh * 2);         // hdq
     n += align256((E + 1) * 4);        // gtile
+    n += align256(A * (d / QK) * 4);   // xsb
     return n;
 }
 
@@ -633,6 +785,7 @@ int mhip_scratch_carve(const mhip_dims *s, int T, void *d_base, mhip_scratch *o)
     o->xdq = take(T * d * 2);
     o->hdq = take(A * eh * 2);
     o->gtile = (int *)take((E + 1) * 4);
+    o->xsb = (float *)take(A * (d / QK) * 4);
     return 0;
 }
 
@@ -684,16 +837,25 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     mhip::stage_end(c, slot);
     if (mhip::check_launch(c, "router")) return -1;
 
-    const int dnt = E <= 128 ? 256 : 128;
-    const size_t dsh = align256((size_t)dnt * E * 2) + (size_t)(E + 1) * 4 + (size_t)A;
-    if (dsh > 65536 &&
-        mhip::check(c, hipFuncSetAttribute((const void *)k_dispatch,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)dsh),
-                    "dispatch LDS attribute"))
-        return -1;
+    // dispatch; the per-chunk counts live in tmp, which the down stage
+    // writes only later
+    const int nch = (A + DCH - 1) / DCH;
+    const int dgrid = (nch + DWG - 1) / DWG;
+    int bits = 0;
+    while ((1 << bits) < E) bits++;
+    int *dhist = (int *)sc->tmp;
     slot = mhip::stage_begin(c, MHIP_STAGE_DISPATCH);
-    k_dispatch<<<1, dnt, dsh, st>>>(sc->idx, A, E, sc->counts, sc->offsets, sc->perm, sc->pos,
-                                    sc->groups, sc->gtile, MHIP_GEMM_TM, sc->status);
+    if (nch <= DSMALL) {
+        k_disp_small<<<1, 64 * DSMALL, (DSMALL * E + 2 * E + 1) * 4, st>>>(
+            sc->idx, A, E, nch, bits, sc->counts, sc->offsets, sc->perm, sc->pos, sc->groups,
+            sc->gtile, MHIP_GEMM_TM, sc->status);
+    } else {
+        k_disp_count<<<dgrid, 64 * DWG, DWG * E * 4, st>>>(sc->idx, A, E, nch, dhist, sc->status);
+        k_disp_scan<<<E, 256, 0, st>>>(nch, dhist, sc->counts);
+        k_disp_scatter<<<dgrid, 64 * DWG, (DWG + 2) * E * 4, st>>>(
+            sc->idx, A, E, nch, bits, dhist, sc->counts, sc->offsets, sc->groups, sc->gtile,
+            MHIP_GEMM_TM, sc->perm, sc->pos, sc->status);
+    }
     mhip::stage_end(c, slot);
     if (mhip::check_launch(c, "dispatch")) return -1;
 

@@ -5,7 +5,8 @@
 // through an LRU cache (src/storage/expert_cache.c:59-85,
 // src/storage/mia_file.c:121-126). Here every blob of every layer sits in one
 // HBM allocation, regrouped once at upload: int8 codes of a matrix form a
-// dense row-major array, the fp32 block scales a second array beside it.
+// dense row-major array, the fp32 block scales a second array beside it, and
+// a block-major copy of those scales a third (for the matrix-core kernels).
 #include "mhip_internal.h"
 #include "mia/synth.h"
 
@@ -17,7 +18,7 @@ inline size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
 struct ExpertGeom {
     int d, eh, E;
-    size_t gate_q, up_q, down_q, gate_s, up_s, down_s, expert_bytes;
+    size_t gate_q, up_q, down_q, gate_s, up_s, down_s, gate_st, up_st, down_st, expert_bytes;
 };
 
 ExpertGeom geom_of(const mhip_dims *s, const mhip_layout &l) {
@@ -31,6 +32,9 @@ ExpertGeom geom_of(const mhip_dims *s, const mhip_layout &l) {
     g.gate_s = l.gate_s;
     g.up_s = l.up_s;
     g.down_s = l.down_s;
+    g.gate_st = l.gate_st;
+    g.up_st = l.up_st;
+    g.down_st = l.down_st;
     g.expert_bytes = l.expert_bytes;
     return g;
 }
@@ -62,13 +66,18 @@ __device__ __forceinline__ BlockRef block_ref(const ExpertGeom &g, size_t q) {
     return b;
 }
 
+// Codes and scale of a block; *scale_t is the scale's block-major copy (may
+// be null when not wanted).
 __device__ __forceinline__ void block_addr(const ExpertGeom &g, uint8_t *expert,
-                                           const BlockRef &b, int8_t **codes,
-                                           float **scale) {
-    size_t qoff = b.m == 0 ? g.gate_q : b.m == 1 ? g.up_q : g.down_q;
-    size_t soff = b.m == 0 ? g.gate_s : b.m == 1 ? g.up_s : g.down_s;
+                                           const BlockRef &b, int8_t **codes, float **scale,
+                                           float **scale_t) {
+    const size_t qoff = b.m == 0 ? g.gate_q : b.m == 1 ? g.up_q : g.down_q;
+    const size_t soff = b.m == 0 ? g.gate_s : b.m == 1 ? g.up_s : g.down_s;
+    const size_t toff = b.m == 0 ? g.gate_st : b.m == 1 ? g.up_st : g.down_st;
+    const int rows = b.m == 2 ? g.d : g.eh;
     *codes = (int8_t *)(expert + qoff + (size_t)b.row * b.cols + (size_t)b.blk * QK);
     *scale = (float *)(expert + soff) + (size_t)b.row * b.nb + b.blk;
+    if (scale_t) *scale_t = (float *)(expert + toff) + (size_t)b.blk * rows + b.row;
 }
 
 // One thread per 32-value block: draw 32 N(0, 0.02) values, quantize them
@@ -100,11 +109,12 @@ __global__ __launch_bounds__(256) void k_table_synth(ExpertGeom g, uint8_t *tabl
 #pragma unroll
     for (int i = 0; i < QK; i++) out.c[i] = (int8_t)roundf(v[i] * inv);
     int8_t *codes;
-    float *scale;
-    block_addr(g, table + ((size_t)l * g.E + e) * g.expert_bytes, b, &codes, &scale);
+    float *scale, *scale_t;
+    block_addr(g, table + ((size_t)l * g.E + e) * g.expert_bytes, b, &codes, &scale, &scale_t);
     ((int4 *)codes)[0] = out.v4[0];
     ((int4 *)codes)[1] = out.v4[1];
     *scale = dsc;
+    *scale_t = dsc;
 }
 
 // Reference blob (36-byte blocks) -> table slot.
@@ -118,9 +128,10 @@ __global__ __launch_bounds__(256) void k_repack(ExpertGeom g, uint8_t *expert,
     const uint8_t *src = blob + moff + ((size_t)b.row * b.nb + b.blk) * 36;
     const uint32_t *s32 = (const uint32_t *)src;  // blocks are 4-byte aligned
     int8_t *codes;
-    float *scale;
-    block_addr(g, expert, b, &codes, &scale);
+    float *scale, *scale_t;
+    block_addr(g, expert, b, &codes, &scale, &scale_t);
     *scale = __uint_as_float(s32[0]);
+    *scale_t = __uint_as_float(s32[0]);
     int4 c0 = make_int4((int)s32[1], (int)s32[2], (int)s32[3], (int)s32[4]);
     int4 c1 = make_int4((int)s32[5], (int)s32[6], (int)s32[7], (int)s32[8]);
     ((int4 *)codes)[0] = c0;
@@ -138,7 +149,7 @@ __global__ __launch_bounds__(256) void k_unpack(ExpertGeom g, const uint8_t *exp
     uint32_t *dst = (uint32_t *)(blob + moff + ((size_t)b.row * b.nb + b.blk) * 36);
     int8_t *codes;
     float *scale;
-    block_addr(g, (uint8_t *)expert, b, &codes, &scale);
+    block_addr(g, (uint8_t *)expert, b, &codes, &scale, nullptr);
     const int4 c0 = ((const int4 *)codes)[0];
     const int4 c1 = ((const int4 *)codes)[1];
     dst[0] = __float_as_uint(*scale);
@@ -201,6 +212,12 @@ int mhip_layout_of(const mhip_dims *s, mhip_layout *out) {
     out->up_s = off;
     off = align256(off + eh * (d / QK) * 4);
     out->down_s = off;
+    off = align256(off + d * (eh / QK) * 4);
+    out->gate_st = off;
+    off = align256(off + eh * (d / QK) * 4);
+    out->up_st = off;
+    off = align256(off + eh * (d / QK) * 4);
+    out->down_st = off;
     off = align256(off + d * (eh / QK) * 4);
     out->expert_bytes = off;
     return 0;

@@ -58,9 +58,13 @@ def test_layout_matches_blob_size():
     d = M.Dims(2048, 128, 8, 768, 1, 1e-6)
     lay = M.Layout()
     assert M.lib().mhip_layout_of(ctypes.byref(d), ctypes.byref(lay)) == 0
-    # Regrouping keeps 1.125 bytes per weight: the .mia blob size exactly.
-    assert lay.expert_bytes == 5308416
-    for off in (lay.gate_q, lay.up_q, lay.down_q, lay.gate_s, lay.up_s, lay.down_s):
+    # Regrouping keeps 1.125 bytes per weight (the .mia blob size exactly, up
+    # to the start of the block-major scale copy), plus that copy.
+    assert lay.gate_st == 5308416
+    scales = 2 * 768 * 64 * 4 + 2048 * 24 * 4
+    assert lay.expert_bytes == 5308416 + scales
+    for off in (lay.gate_q, lay.up_q, lay.down_q, lay.gate_s, lay.up_s, lay.down_s,
+                lay.gate_st, lay.up_st, lay.down_st):
         assert off % 256 == 0
 
 
