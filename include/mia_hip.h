@@ -97,11 +97,17 @@ int mhip_table_unpack(mhip_ctx *c, const mhip_dims *s, const void *d_table,
 int mhip_table_synth(mhip_ctx *c, const mhip_dims *s, void *d_table,
                      uint64_t seed, int l0, int l1);
 /* Router of layer l, transposed (d_router_t[i*E + e] = W[e][i]) and, when
- * d_router is not NULL, row-major (d_router[e*d + i] = W[e][i]). */
+ * d_router_dl is not NULL, in the decode layout (below). */
 int mhip_router_synth(mhip_ctx *c, const mhip_dims *s, float *d_router_t,
-                      float *d_router, uint64_t seed, int layer);
+                      float *d_router_dl, uint64_t seed, int layer);
 int mhip_router_transpose(mhip_ctx *c, const mhip_dims *s, float *d_router_t,
                           const float *d_router);
+/* Decode layout of one layer's router from the row-major W[E][d]: within
+ * each expert row, element i = 32 L + 4 k + c (L < d/32, k < 8, c < 4) is
+ * stored at (k * d/32 + L) * 4 + c, so the decode kernel's lane L reads its
+ * 32 consecutive elements as 8 fully contiguous 1 KB loads. */
+int mhip_router_decode_layout(mhip_ctx *c, const mhip_dims *s, float *d_router_dl,
+                              const float *d_router);
 int mhip_synth_f32(mhip_ctx *c, float *d_out, size_t n, uint64_t seed,
                    uint64_t stream, double sigma);
 int mhip_fill_f32(mhip_ctx *c, float *d_out, size_t n, float value);
@@ -165,7 +171,8 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
 /*
  * Decode (one token) through L consecutive layers in one persistent launch:
  * the Qwen3-30B-A3B shape only (dim 2048, 128 experts, n_active <= 8,
- * expert_hidden 768) on a 256-CU MI355X. d_table/d_router ([L][E][d])/
+ * expert_hidden 768) on a 256-CU MI355X. d_table/d_router ([L][E][d], each
+ * layer in the decode layout of mhip_router_decode_layout)/
  * d_router_t ([L][d][E])/d_norm ([L][d]) start at the first layer; d_bias
  * (E floats, every layer) may be NULL; d_x[d] is updated in place. d_ws is a
  * workspace of mhip_decode_ws_bytes() bytes (not shared by concurrent

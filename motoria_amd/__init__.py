@@ -80,6 +80,7 @@ SIGNATURES = {
     "mhip_table_synth": (_i, [_p, ctypes.POINTER(Dims), _p, _u64, _i, _i]),
     "mhip_router_synth": (_i, [_p, ctypes.POINTER(Dims), _p, _p, _u64, _i]),
     "mhip_router_transpose": (_i, [_p, ctypes.POINTER(Dims), _p, _p]),
+    "mhip_router_decode_layout": (_i, [_p, ctypes.POINTER(Dims), _p, _p]),
     "mhip_synth_f32": (_i, [_p, _p, _sz, _u64, _u64, ctypes.c_double]),
     "mhip_fill_f32": (_i, [_p, _p, _sz, _f]),
     "mhip_scratch_bytes": (_sz, [ctypes.POINTER(Dims), _i]),

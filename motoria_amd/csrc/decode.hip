@@ -99,7 +99,7 @@ static_assert(offsetof(DecodeWs, lgb) == offsetof(DecodeWs, lgs) + NX * E * size
 struct DecodeArgs {
     const uint8_t *table;         // layer 0, experts expert_bytes apart, layers E*expert_bytes
     mhip_layout lay;
-    const float *router;          // [L][E][D]
+    const float *router;          // [L][E][D], decode layout
     const float *router_t;        // [L][D][E]
     const float *norm;            // [L][D]
     const float *bias;            // [E] or null
@@ -300,6 +300,16 @@ __device__ __forceinline__ float wave_sum_f(float v) {
     return (float)lane63_d(wave_scan_d((double)v));
 }
 
+// Exact int32 dot of 16 int8 codes (four v_dot4).
+__device__ __forceinline__ int dot16_i8(const int4 a, const int4 b) {
+    int acc = 0;
+    acc = __builtin_amdgcn_sdot4(a.x, b.x, acc, false);
+    acc = __builtin_amdgcn_sdot4(a.y, b.y, acc, false);
+    acc = __builtin_amdgcn_sdot4(a.z, b.z, acc, false);
+    acc = __builtin_amdgcn_sdot4(a.w, b.w, acc, false);
+    return acc;
+}
+
 __device__ __forceinline__ float4 i4_as_f4(const int4 v) {
     return make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z),
                        __int_as_float(v.w));
@@ -411,13 +421,15 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
     static_assert(2 * NR0 >= 8, "router row slots");
     int4 wq0[GU_R], wq1[GU_R];
     float wsc[GU_R];
+    // In the decode layout, load k of the row (1 KB, contiguous) gives lane
+    // L its elements 32 L + 4 k .. + 3.
 #define LOAD_ROUTER(layer)                                                                 \
     do {                                                                                   \
         const int4 *src_ = (const int4 *)(a.router +                                       \
-                                          ((size_t)(layer) * E + rank * LPW + wave - NGU) * D + \
-                                          lane * 32);                                      \
-        _Pragma("unroll") for (int k_ = 0; k_ < NR0; k_++) wq0[DPK + k_] = src_[k_];       \
-        _Pragma("unroll") for (int k_ = 0; k_ < 8 - NR0; k_++) wq1[DPK + k_] = src_[NR0 + k_]; \
+                                          ((size_t)(layer) * E + rank * LPW + wave - NGU) * D) + \
+                           lane;                                                           \
+        _Pragma("unroll") for (int k_ = 0; k_ < NR0; k_++) wq0[DPK + k_] = src_[64 * k_];  \
+        _Pragma("unroll") for (int k_ = 0; k_ < 8 - NR0; k_++) wq1[DPK + k_] = src_[64 * (NR0 + k_)]; \
     } while (0)
 #define RROW(k)                                                                            \
     i4_as_f4((k) < NR0 ? wq0[DPK + ((k) < NR0 ? (k) : 0)] : wq1[DPK + ((k) < NR0 ? 0 : (k) - NR0)])
@@ -730,27 +742,36 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
         LOAD_NORM(lnext);
         if (gu_wave) {
             if (active) {
-                // this wave's rows: gate h0..h0+GU_H-1, then up h0..h0+GU_H-1
+                // this wave's rows: gate h0..h0+GU_H-1, then up h0..h0+GU_H-1.
+                // A row's 2 KB of codes arrive as two contiguous 1 KB loads:
+                // lane l holds half (l & 1) of block l/2 and of block 32 + l/2;
+                // the lane pair adds its two half dots, and lane l keeps
+                // block blk = l/2 (l even) or 32 + l/2 (l odd).
                 const int h0 = rank * HROWS + wave * GU_H;
-                const int4 *xv = (const int4 *)&sh.xq[lane * 32];
-                const int4 x0 = xv[0], x1 = xv[1];
-                const float dx = sh.xs[lane];
+                const int hf = lane & 1, bm = lane >> 1;
+                const int blk = hf ? NB / 2 + bm : bm;
+                const int4 xa = *(const int4 *)&sh.xq[bm * 32 + 16 * hf];
+                const int4 xb = *(const int4 *)&sh.xq[(NB / 2 + bm) * 32 + 16 * hf];
+                const float dx = sh.xs[blk];
 #pragma unroll
                 for (int r = 0; r < GU_R; r++) {
                     const int row = h0 + (r % GU_H);
                     const size_t qoff = (r < GU_H ? a.lay.gate_q : a.lay.up_q) + (size_t)row * D +
-                                        (size_t)lane * 32;
+                                        (size_t)lane * 16;
                     const size_t soff = (r < GU_H ? a.lay.gate_s : a.lay.up_s);
                     const int4 *src = (const int4 *)(eb + qoff);
                     wq0[r] = ld_stream(src);
-                    wq1[r] = ld_stream(src + 1);
-                    wsc[r] = ((const float *)(eb + soff))[(size_t)row * NB + lane];
+                    wq1[r] = ld_stream(src + 64);
+                    wsc[r] = ((const float *)(eb + soff))[(size_t)row * NB + blk];
                 }
                 float *terms = &sh.scr[wave * GU_R * GU_LD];
 #pragma unroll
-                for (int r = 0; r < GU_R; r++)
-                    terms[r * GU_LD + lane] = mhip_dev::block_term(
-                        mhip_dev::dot32_i8(wq0[r], wq1[r], x0, x1), wsc[r], dx);
+                for (int r = 0; r < GU_R; r++) {
+                    const int pa = dot16_i8(wq0[r], xa), pb = dot16_i8(wq1[r], xb);
+                    const int other = __builtin_amdgcn_update_dpp(0, hf ? pa : pb, 0xB1, 0xf, 0xf, false);
+                    terms[r * GU_LD + blk] =
+                        mhip_dev::block_term((hf ? pb : pa) + other, wsc[r], dx);
+                }
                 TRACE(12);
                 wave_lds_sync();
                 if (lane < GU_R) sh.gu[wave][lane] = lds_seq_sum(&terms[lane * GU_LD], NB, 0.0f);
@@ -788,13 +809,15 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             }
 #pragma unroll
             for (int k = 0; k < DPK; k++) {
-                const int pidx = dt + NDN * 64 * k;
-                const int row = rank * DROWS + pidx / NBH, blk = pidx % NBH;
-                const int4 *src =
-                    (const int4 *)(eb + a.lay.down_q + (size_t)row * EH + (size_t)blk * 32);
-                wq0[k] = ld_stream(src);
-                wq1[k] = ld_stream(src + 1);
-                wsc[k] = ((const float *)(eb + a.lay.down_s))[(size_t)row * NBH + blk];
+                // The workgroup's 64 rows are one contiguous 48 KB run, read
+                // as 16-byte pieces q = dt + 256 j (j < 12): the two halves of
+                // block q/2 sit in a lane pair. Loads 2k, 2k + 1 go to
+                // wq0[k], wq1[k]; the pair later keeps block P(2k + (dt & 1)).
+                const int4 *run = (const int4 *)(eb + a.lay.down_q + (size_t)rank * DROWS * EH);
+                wq0[k] = ld_stream(run + dt + NDN * 64 * (2 * k));
+                wq1[k] = ld_stream(run + dt + NDN * 64 * (2 * k + 1));
+                const int p = (dt >> 1) + (NDN * 32) * (2 * k + (dt & 1));
+                wsc[k] = ((const float *)(eb + a.lay.down_s))[(size_t)rank * DROWS * NBH + p];
             }
             LOAD_ROUTER(lnext);
         }
@@ -837,11 +860,18 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             if (!gu_wave) {
 #pragma unroll
                 for (int k = 0; k < DPK; k++) {
-                    const int pidx = dt + NDN * 64 * k;
-                    const int row = pidx / NBH, blk = pidx % NBH;
-                    const int4 *hv = (const int4 *)&sh.hq[blk * 32];
-                    dterm[row * DN_LD + blk] = mhip_dev::block_term(
-                        mhip_dev::dot32_i8(wq0[k], wq1[k], hv[0], hv[1]), wsc[k], sh.hsc[blk]);
+                    // blocks pa, pb = pa + 128 of the workgroup's rows (row
+                    // p / 24, block p % 24); this lane keeps pa if even, pb if odd
+                    const int hf = dt & 1;
+                    const int pa = (dt >> 1) + (NDN * 32) * (2 * k), pb = pa + NDN * 32;
+                    const int4 ha = *(const int4 *)&sh.hq[(pa % NBH) * 32 + 16 * hf];
+                    const int4 hb = *(const int4 *)&sh.hq[(pb % NBH) * 32 + 16 * hf];
+                    const int da = dot16_i8(wq0[k], ha), db = dot16_i8(wq1[k], hb);
+                    const int other = __builtin_amdgcn_update_dpp(0, hf ? da : db, 0xB1, 0xf, 0xf, false);
+                    const int p = hf ? pb : pa;
+                    const int row = p / NBH, blk = p % NBH;
+                    dterm[row * DN_LD + blk] = mhip_dev::block_term((hf ? db : da) + other, wsc[k],
+                                                                    sh.hsc[blk]);
                 }
             }
             __syncthreads();

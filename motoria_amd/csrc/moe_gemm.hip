@@ -53,8 +53,9 @@ constexpr int DMA_PER_STEP = 4;   // global_load_lds per wavefront per step
 static_assert(TM == 128 && TN == 128 && GT == 256, "tiling");
 
 // One step of the ring: A rows of 32 fp16 (4 chunks of 16 bytes; chunk c of
-// row r at slot c ^ ((r >> 2) & 3)), B rows of 32 int8 codes, and block
-// scales of the weight rows (sb) and of the assignment rows (sa).
+// row r at slot c ^ ((r >> 1) & 3), so the eight rows that eight consecutive
+// lanes read at one chunk fall on distinct banks), B rows of 32 int8 codes,
+// and block scales of the weight rows (sb) and of the assignment rows (sa).
 struct alignas(16) Step {
     _Float16 a[TM][KB];  // 8 KB
     int8_t b[TN][KB];    // 4 KB
@@ -63,7 +64,7 @@ struct alignas(16) Step {
 };
 static_assert(sizeof(Step) == 13312, "step layout");
 
-__device__ __forceinline__ int aslot(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
+__device__ __forceinline__ int aslot(int row, int chunk) { return chunk ^ ((row >> 1) & 3); }
 
 // The group g with gtile[g] <= mt < gtile[g + 1] (gtile is non-decreasing).
 __device__ __forceinline__ int find_group(const int *gtile, int G, int mt) {

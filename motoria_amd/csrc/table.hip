@@ -163,16 +163,29 @@ __global__ __launch_bounds__(256) void k_unpack(ExpertGeom g, const uint8_t *exp
     dst[8] = (uint32_t)c1.w;
 }
 
+// Position of element i of a router row in the decode layout: i = 32 L +
+// 4 k + c goes to (k * d/32 + L) * 4 + c.
+__device__ __forceinline__ int router_dl_pos(int i, int d) {
+    return (((i & 31) >> 2) * (d / 32) + (i >> 5)) * 4 + (i & 3);
+}
+
 // Router of one layer, transposed (out_t[i*E + e] = W[e][i]) and, when
-// out_rm is not null, row-major (out_rm[e*d + i] = W[e][i]).
-__global__ __launch_bounds__(256) void k_router_synth(float *out_t, float *out_rm, int d, int E,
+// out_dl is not null, in the decode layout.
+__global__ __launch_bounds__(256) void k_router_synth(float *out_t, float *out_dl, int d, int E,
                                                       uint64_t key) {
     const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (q >= (size_t)d * E) return;
     const int e = (int)(q / d), i = (int)(q % d);
     const float v = mia_synth_f32(key, q, 0.02);
     out_t[(size_t)i * E + e] = v;
-    if (out_rm) out_rm[q] = v;
+    if (out_dl) out_dl[(size_t)e * d + router_dl_pos(i, d)] = v;
+}
+
+__global__ __launch_bounds__(256) void k_router_dl(float *out, const float *in, int E, int d) {
+    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= (size_t)d * E) return;
+    const int e = (int)(q / d), i = (int)(q % d);
+    out[(size_t)e * d + router_dl_pos(i, d)] = in[q];
 }
 
 __global__ __launch_bounds__(256) void k_transpose(float *out, const float *in, int E, int d) {
@@ -284,14 +297,23 @@ int mhip_table_unpack(mhip_ctx *c, const mhip_dims *s, const void *d_table, int 
     return mhip::check_launch(c, "unpack");
 }
 
-int mhip_router_synth(mhip_ctx *c, const mhip_dims *s, float *d_router_t, float *d_router,
+int mhip_router_synth(mhip_ctx *c, const mhip_dims *s, float *d_router_t, float *d_router_dl,
                       uint64_t seed, int layer) {
     if (mhip::check_dims(c, s) || mhip::use_device(c)) return -1;
     const size_t n = (size_t)s->dim * s->n_experts;
     const uint64_t key = mia_synth_key(seed, MIA_STREAM_ROUTER + (uint64_t)layer);
-    k_router_synth<<<mhip::blocks_for(n, 256), 256, 0, c->stream>>>(d_router_t, d_router, s->dim,
-                                                                     s->n_experts, key);
+    k_router_synth<<<mhip::blocks_for(n, 256), 256, 0, c->stream>>>(d_router_t, d_router_dl,
+                                                                     s->dim, s->n_experts, key);
     return mhip::check_launch(c, "router_synth");
+}
+
+int mhip_router_decode_layout(mhip_ctx *c, const mhip_dims *s, float *d_router_dl,
+                              const float *d_router) {
+    if (mhip::check_dims(c, s) || mhip::use_device(c)) return -1;
+    const size_t n = (size_t)s->dim * s->n_experts;
+    k_router_dl<<<mhip::blocks_for(n, 256), 256, 0, c->stream>>>(d_router_dl, d_router,
+                                                                  s->n_experts, s->dim);
+    return mhip::check_launch(c, "router_decode_layout");
 }
 
 int mhip_router_transpose(mhip_ctx *c, const mhip_dims *s, float *d_router_t,

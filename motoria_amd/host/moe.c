@@ -17,7 +17,7 @@ struct mia_moe {
     size_t blob_bytes, off_up, off_down;
     void *d_table;      /* [L][E] experts, lay.expert_bytes apart */
     float *d_router_t;  /* [L][dim][E] */
-    float *d_router_rm; /* [L][E][dim] */
+    float *d_router_dl; /* [L][E][dim], decode layout (mhip_router_decode_layout) */
     void *d_dws;        /* persistent decode workspace */
     int *d_didx;        /* [L][K] routing of the last decode-stack call */
     float *d_dw;        /* [L][K] */
@@ -58,7 +58,7 @@ void mia_moe_close(mia_moe *m) {
         mhip_sync(m->gpu);
         mhip_free(m->gpu, m->d_table);
         mhip_free(m->gpu, m->d_router_t);
-        mhip_free(m->gpu, m->d_router_rm);
+        mhip_free(m->gpu, m->d_router_dl);
         mhip_free(m->gpu, m->d_dws);
         mhip_free(m->gpu, m->d_didx);
         mhip_free(m->gpu, m->d_dw);
@@ -112,7 +112,7 @@ int mia_moe_open(mia_moe **out, const mia_moe_config *cfg, char *err, size_t err
         const size_t scratch = mhip_scratch_bytes(&m->dims, cfg->max_tokens);
         m->d_table = mhip_malloc(m->gpu, table);
         m->d_router_t = mhip_malloc(m->gpu, (size_t)cfg->n_layers * d * E * 4);
-        m->d_router_rm = mhip_malloc(m->gpu, (size_t)cfg->n_layers * d * E * 4);
+        m->d_router_dl = mhip_malloc(m->gpu, (size_t)cfg->n_layers * d * E * 4);
         m->d_dws = mhip_malloc(m->gpu, mhip_decode_ws_bytes());
         m->d_didx = mhip_malloc(m->gpu, (size_t)cfg->n_layers * cfg->n_active * 4);
         m->d_dw = mhip_malloc(m->gpu, (size_t)cfg->n_layers * cfg->n_active * 4);
@@ -123,7 +123,7 @@ int mia_moe_open(mia_moe **out, const mia_moe_config *cfg, char *err, size_t err
         m->d_bias = mhip_malloc(m->gpu, E * 4);
         m->d_blob = mhip_malloc(m->gpu, m->blob_bytes);
         m->h_blob = malloc(m->blob_bytes);
-        if (!m->d_table || !m->d_router_t || !m->d_router_rm || !m->d_dws || !m->d_didx ||
+        if (!m->d_table || !m->d_router_t || !m->d_router_dl || !m->d_dws || !m->d_didx ||
             !m->d_dw || !m->d_norm || !m->d_router || !m->d_scratch || !m->d_x || !m->d_bias ||
             !m->d_blob)
             rc = fail(m, "HBM allocation (%.2f GiB table): %s", table / 1073741824.0,
@@ -135,7 +135,7 @@ int mia_moe_open(mia_moe **out, const mia_moe_config *cfg, char *err, size_t err
             if (mhip_zero(m->gpu, m->sc.status, 16) ||
                 mhip_zero(m->gpu, m->d_table, table) ||
                 mhip_zero(m->gpu, m->d_router_t, (size_t)cfg->n_layers * d * E * 4) ||
-                mhip_zero(m->gpu, m->d_router_rm, (size_t)cfg->n_layers * d * E * 4) ||
+                mhip_zero(m->gpu, m->d_router_dl, (size_t)cfg->n_layers * d * E * 4) ||
                 mhip_fill_f32(m->gpu, m->d_norm, (size_t)cfg->n_layers * d, 1.0f) ||
                 mhip_sync(m->gpu))
                 rc = gpu_fail(m);
@@ -191,7 +191,7 @@ int mia_moe_set_layer(mia_moe *m, int layer, const float *ffn_norm, const float 
     const size_t d = (size_t)m->dims.dim, E = (size_t)m->dims.n_experts;
     if (mhip_h2d(m->gpu, m->d_norm + layer * d, ffn_norm, d * 4) ||
         mhip_h2d(m->gpu, m->d_router, router, d * E * 4) ||
-        mhip_d2d(m->gpu, m->d_router_rm + layer * d * E, m->d_router, d * E * 4) ||
+        mhip_router_decode_layout(m->gpu, &m->dims, m->d_router_dl + layer * d * E, m->d_router) ||
         mhip_router_transpose(m->gpu, &m->dims, m->d_router_t + layer * d * E, m->d_router) ||
         mhip_sync(m->gpu))
         return gpu_fail(m);
@@ -203,7 +203,7 @@ int mia_moe_synth(mia_moe *m, uint64_t seed) {
     if (mhip_table_synth(m->gpu, &m->dims, m->d_table, seed, 0, m->n_layers)) return gpu_fail(m);
     for (int l = 0; l < m->n_layers; l++)
         if (mhip_router_synth(m->gpu, &m->dims, m->d_router_t + l * d * E,
-                              m->d_router_rm + l * d * E, seed, l))
+                              m->d_router_dl + l * d * E, seed, l))
             return gpu_fail(m);
     if (mhip_fill_f32(m->gpu, m->d_norm, (size_t)m->n_layers * d, 1.0f) || mhip_sync(m->gpu))
         return gpu_fail(m);
@@ -242,7 +242,7 @@ int mia_moe_decode_dev(mia_moe *m, int l0, int l1, float *d_x, const float *d_bi
                  K = (size_t)m->dims.n_active;
     if (mhip_decode_stack(m->gpu, &m->dims, &m->lay,
                           (const unsigned char *)m->d_table + (size_t)l0 * E * m->lay.expert_bytes,
-                          m->d_router_rm + l0 * d * E, m->d_router_t + l0 * d * E,
+                          m->d_router_dl + l0 * d * E, m->d_router_t + l0 * d * E,
                           m->d_norm + l0 * d, d_bias, d_x, l1 - l0, m->d_dws, m->d_didx + l0 * K,
                           m->d_dw + l0 * K, m->flags))
         return gpu_fail(m);
