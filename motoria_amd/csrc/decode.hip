@@ -316,8 +316,7 @@ __device__ __forceinline__ float4 i4_as_f4(const int4 v) {
 }
 
 // LDS. `scr` is reused by stages that never overlap: the exact-router
-// products (B, fallback), the gate/up terms (C) and the down terms and
-// gathered expert outputs (D, E).
+// products (B, fallback), the gate/up terms (C) and the down terms (D).
 // A lane reading its own 32-block of xn with 16-byte reads: blocks 36
 // floats apart put eight consecutive lanes on distinct banks (a 128-byte
 // stride would put every lane on the same four banks).
@@ -325,14 +324,16 @@ constexpr int XN_LD = 36;
 constexpr int GU_LD = NB + 4;     // 16-byte aligned rows
 constexpr int DN_LD = NBH + 4;
 constexpr int SCR = 8192;         // floats
-static_assert(NGU * GU_R * GU_LD <= SCR && DROWS * DN_LD <= SCR && LPW * D <= SCR &&
-              DROWS * KMAX <= SCR, "scr");
+static_assert(NGU * GU_R * GU_LD <= SCR && DROWS * DN_LD <= SCR && LPW * D <= SCR, "scr");
 
 struct Lds {
     alignas(16) float x[D];
     alignas(16) float xn[NB * XN_LD];  // 32-blocks XN_LD floats apart
     alignas(16) int8_t xq[D];
     alignas(16) float scr[SCR];
+    // expert outputs gathered for the combine; apart from scr, because rows
+    // of other XCDs can arrive while wave 0 still sums this XCD's down terms
+    alignas(16) float og[KMAX * DROWS];
     alignas(16) int8_t hq[EH];
     float xs[NB];
     float hsc[NBH];
@@ -886,14 +887,14 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             // thread (j, r) fetches expert j's output row r; then one thread
             // per row adds them in top-K order
             const int j = tid / DROWS, r = tid % DROWS;
-            if (j < K) get_tagged<1, false>(ws, &ws->out[par][j][rank * DROWS + r], 0, tag, &sh.scr[j * DROWS + r]);
+            if (j < K) get_tagged<1, false>(ws, &ws->out[par][j][rank * DROWS + r], 0, tag, &sh.og[j * DROWS + r]);
         }
         __syncthreads();
         TRACE(7);
         if (tid < DROWS) {
             const int r = rank * DROWS + tid;
             float v = sh.x[r];
-            for (int j = 0; j < K; j++) v = v + sh.w[j] * sh.scr[j * DROWS + tid];
+            for (int j = 0; j < K; j++) v = v + sh.w[j] * sh.og[j * DROWS + tid];
             if (l + 1 < a.L) put_tagged<true>(&ws->x[xcd][r], v, tag);
             else if (xcd == 0) a.x[r] = v;
         }
