@@ -6,29 +6,31 @@
 //   k_gateup_mfma  h = SwiGLU(Wg x, Wu x), then Q8_0(h)   forward.c:186-192
 //   k_down_mfma    tmp = Wd Q8(h)                           forward.c:192-193
 //
-// gate/up is bit-exact. Its operands are the Q8_0 codes themselves, as fp16
-// integers: v_mfma_f32_16x16x32_f16 over one 32-value block gives the exact
-// int32 block dot (every partial sum is an integer below 2^24), and the
-// reference's term ((float)acc * d_w) * d_x is added to the row sum in block
-// order by the vector ALUs (matmul.c:19-28). h, and so Q8(h), are therefore
-// the reference's bits. (Q8(h) is sensitive: an h off by 1e-4 moves ~3 % of
-// its codes by one step, and one code step on a large down weight is a
-// 1e-3 change of the output.)
+// gate/up: the operands are the Q8_0 codes themselves, as fp16 integers, so
+// v_mfma_f32_16x16x32_f16 over one 32-value block gives the exact int32
+// block dot (every partial sum is an integer below 2^24). The reference's
+// block term ((float)acc * d_w) * d_x is added to the row sum in block order
+// by the vector ALUs (matmul.c:19-28) with one fused multiply-add: the term's
+// last rounding and the addition's become one, so h is the reference's to
+// within a few fp32 ulps (~1e-7 relative). Q8(h) then differs from the
+// reference's in the rare code whose h sits within that distance of a
+// rounding boundary (one code step moves an output by < 1e-4 relative).
 //
 // down takes the reference's dequantized values (d * q for the weights,
 // d_h * q_h for h) rounded to fp16 on the matrix cores with fp32
 // accumulation: ~1e-4 relative of the reference, within the path's 1e-3.
 //
-// Tiles: 128 assignments (rows of one expert's bucket) x 128 weight rows, one
-// 32-value Q8_0 block of k per step. Wavefront w owns weight rows
-// 32w..32w+31 against all 128 assignment rows: 8 x 2 tiles of 16x16 (one
-// 16x16x32 product each per step), 64 accumulators per lane, and it alone
-// turns those weight codes into fp16 operands.
+// Tiles: 256 weight rows x 128 assignments (rows of one expert's bucket),
+// one 32-value Q8_0 block of k per step. Wavefront w owns weight rows
+// 64w..64w+63 against all 128 assignments: 4 x 8 tiles of 16x16 with the
+// weights as the A operand, so each lane's four results share one
+// assignment (one x scale) and four consecutive weight rows (one float4 of
+// weight scales). Two workgroups share a CU.
 //
 // Operands move from global memory straight into an NS-stage LDS ring with
 // global_load_lds (no registers on the way), NS-1 steps ahead of the
-// products. Each wavefront issues exactly four such loads per step, so a
-// wait for the oldest step is one immediate vmcnt count. The loads are
+// products. Each wavefront issues a fixed number of such loads per step, so
+// a wait for the oldest step is one immediate vmcnt count. The loads are
 // issued from inline assembly (which sets M0, the LDS base they use) so the
 // compiler does not wait for all of them before every LDS read; the waits
 // are explicit. Rows past a bucket's end load a valid row; their results are
@@ -43,28 +45,34 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 
 constexpr int GT = 256;           // threads per workgroup (4 wavefronts)
 constexpr int TM = MHIP_GEMM_TM;  // assignment rows per tile
-constexpr int TN = 128;           // weight rows per tile
+constexpr int TN = 256;           // weight rows per tile
 constexpr int KB = 32;            // k per step: one Q8_0 block
-constexpr int MI = TM / 16;       // 16-row tiles of assignments (8)
-constexpr int NJ = 2;             // 16-row tiles of weights per wavefront
-constexpr int HLD = TN / 2 + 4;   // epilogue h tile row stride (floats)
-constexpr int DMA_PER_STEP = 4;   // global_load_lds per wavefront per step
+constexpr int WN = TN / 4;        // weight rows per wavefront (64)
+constexpr int MI = WN / 16;       // 16-row weight tiles per wavefront (4)
+constexpr int NJ = TM / 16;       // 16-row assignment tiles (8)
+constexpr int NS = 4;             // ring stages
+constexpr int OLD = TM + 4;       // epilogue tile row stride (floats): 128 columns + pad
 
-static_assert(TM == 128 && TN == 128 && GT == 256, "tiling");
+static_assert(TM == 128 && TN == 256 && GT == 256, "tiling");
 
-// One step of the ring: A rows of 32 fp16 (4 chunks of 16 bytes; chunk c of
-// row r at slot c ^ ((r >> 1) & 3), so the eight rows that eight consecutive
-// lanes read at one chunk fall on distinct banks), B rows of 32 int8 codes,
-// and block scales of the weight rows (sb) and of the assignment rows (sa).
+// One step of the ring.
+//   x:  assignment rows, 32 fp16 codes/values = 4 chunks of 16 bytes; chunk c
+//       of row m sits at slot c ^ ((m >> 1) & 3), so the eight rows that
+//       eight consecutive lanes read at one chunk fall on distinct banks;
+//   w:  weight rows, 32 int8 codes = 2 halves of 16 bytes; half h of row n
+//       sits at slot h ^ ((n >> 3) & 1), so the sixteen rows that sixteen
+//       consecutive lanes read (8 bytes each) fall on distinct banks;
+//   sw: block scales of the weight rows, sx: of the assignment rows.
 struct alignas(16) Step {
-    _Float16 a[TM][KB];  // 8 KB
-    int8_t b[TN][KB];    // 4 KB
-    float sb[TN];
-    float sa[TM];
+    _Float16 x[TM][KB];  // 8 KB
+    int8_t w[TN][KB];    // 8 KB
+    float sw[TN];        // 1 KB
+    float sx[TM];        // 512 B
 };
-static_assert(sizeof(Step) == 13312, "step layout");
+static_assert(sizeof(Step) == 17920, "step layout");
 
-__device__ __forceinline__ int aslot(int row, int chunk) { return chunk ^ ((row >> 1) & 3); }
+__device__ __forceinline__ int xslot(int m, int chunk) { return chunk ^ ((m >> 1) & 3); }
+__device__ __forceinline__ int wslot(int n, int half) { return half ^ ((n >> 3) & 1); }
 
 // The group g with gtile[g] <= mt < gtile[g + 1] (gtile is non-decreasing).
 __device__ __forceinline__ int find_group(const int *gtile, int G, int mt) {
@@ -153,95 +161,133 @@ __device__ __forceinline__ h8 codes8(unsigned w0, unsigned w1) {
 
 // Per-thread global sources of one tile, advanced by one block per step.
 struct Src {
-    const _Float16 *a0, *a1;  // A chunks of rows ar0, ar1 (fp16, KB halves per step)
-    const int8_t *b;          // B 16-byte half of weight row br (KB bytes per step)
-    const float *s;           // a block scale in a block-major array ...
-    int sstep;                // ... whose blocks are sstep floats apart
+    const _Float16 *x0, *x1;  // assignment-row chunks (KB halves per step)
+    const int8_t *w0, *w1;    // weight-row halves (KB bytes per step)
+    const float *sw;          // this lane's weight-row scale, block-major ...
+    int swstep;               // ... blocks swstep floats apart
+    const float *sx;          // this lane's assignment-row scale (lanes < 32)
+    int sxstep;
 };
 
+// This thread's four 16-byte pieces of a step: x rows 32 w + lane / 4 and
+// 32 w + 16 + lane / 4 (the chunk that lands in slot lane % 4), weight rows
+// 64 w + lane / 2 and 64 w + 32 + lane / 2 (the half that lands in slot
+// lane % 2).
+struct Pieces {
+    int xr0, xc0, xr1, xc1, wr0, wh0, wr1, wh1;
+};
+__device__ __forceinline__ Pieces pieces() {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    Pieces p;
+    p.xr0 = 32 * wave + (lane >> 2);
+    p.xr1 = p.xr0 + 16;
+    p.xc0 = xslot(p.xr0, lane & 3);  // slot ^ swizzle = the chunk stored there
+    p.xc1 = xslot(p.xr1, lane & 3);
+    p.wr0 = 64 * wave + (lane >> 1);
+    p.wr1 = p.wr0 + 32;
+    p.wh0 = wslot(p.wr0, lane & 1);
+    p.wh1 = wslot(p.wr1, lane & 1);
+    return p;
+}
+
 // The k loop over nk steps (nk >= NS - 1). On return acc[i][j][r] holds
-//   C[16*i + 4*(lane/16) + r][32*wave + 16*j + lane%16].
-template <int NS, bool EXACT>
+//   C[64*wave + 16*i + 4*(lane/16) + r][16*j + lane%16]
+// (weight row, assignment row). GATEUP: exact block dots, and the block
+// terms added with their scales; otherwise fp16 dequantized weights
+// (d_w * q) accumulated on the matrix cores.
+template <bool GATEUP>
 __device__ __forceinline__ void gemm_tile(Step *ring, const Src &src, int nk, f4v acc[MI][NJ]) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // LDS destinations of this wavefront's four loads within a step
+    constexpr int NLOAD = GATEUP ? 6 : 5;  // global_load_lds per wavefront per step
     const unsigned ring0 = lds_addr(ring);
-    const unsigned oa0 = (unsigned)offsetof(Step, a) + (2 * wave) * 1024;
-    const unsigned oa1 = oa0 + 1024;
-    const unsigned ob = (unsigned)offsetof(Step, b) + wave * 1024;
-    // waves 0, 1: the weight rows' scales; waves 2, 3: the assignment rows'
-    const unsigned os = (wave < 2 ? (unsigned)offsetof(Step, sb) : (unsigned)offsetof(Step, sa)) +
-                        (wave & 1) * 256;
+    const unsigned ox = (unsigned)offsetof(Step, x) + (2 * wave) * 1024;
+    const unsigned ow = (unsigned)offsetof(Step, w) + (2 * wave) * 1024;
+    const unsigned osw = (unsigned)offsetof(Step, sw) + wave * 256;
+    const unsigned osx = (unsigned)offsetof(Step, sx) + wave * 128;
     auto issue = [&](int kb) {
         const int k = min(kb, nk - 1);  // past the end: reload the last step
         const unsigned st = ring0 + (unsigned)((kb % NS) * sizeof(Step));
-        dma16(st + oa0, src.a0 + (size_t)k * KB);
-        dma16(st + oa1, src.a1 + (size_t)k * KB);
-        dma16(st + ob, src.b + (size_t)k * KB);
-        dma4(st + os, src.s + (size_t)k * src.sstep);
+        dma16(st + ox, src.x0 + (size_t)k * KB);
+        dma16(st + ox + 1024, src.x1 + (size_t)k * KB);
+        dma16(st + ow, src.w0 + (size_t)k * KB);
+        dma16(st + ow + 1024, src.w1 + (size_t)k * KB);
+        dma4(st + osw, src.sw + (size_t)k * src.swstep);
+        if (GATEUP && lane < 32) dma4(st + osx, src.sx + (size_t)k * src.sxstep);
     };
 #pragma unroll
     for (int s = 0; s < NS - 1; s++) issue(s);
+    const int c = lane >> 4, l16 = lane & 15;
     for (int kb = 0; kb < nk; kb++) {
         // this wavefront's loads of step kb are done (NS - 2 later steps may
         // still be in flight); then every wavefront's are
-        wait_vm<(NS - 2) * DMA_PER_STEP>();
+        wait_vm<(NS - 2) * NLOAD>();
         __syncthreads();
         // step kb + NS - 1 reuses the slot read in step kb - 1, which every
         // wavefront has finished with (the LDS reads completed before the
         // barrier)
         issue(kb + NS - 1);
         const Step &S = ring[kb % NS];
-        const int ck = lane >> 4;
-        h8 bv[NJ];
-        float sw[NJ];
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const int n = 32 * wave + 16 * j + (lane & 15);
-            const uint2 q = *(const uint2 *)&S.b[n][8 * ck];
-            bv[j] = codes8(q.x, q.y);
-            sw[j] = S.sb[n];
-            if (!EXACT) {
-                const _Float16 s = (_Float16)sw[j];
-                const h8 s8 = {s, s, s, s, s, s, s, s};
-                bv[j] = bv[j] * s8;
-            }
-        }
+        h8 av[MI];
+        f4v s4[MI];
 #pragma unroll
         for (int i = 0; i < MI; i++) {
-            const int m = 16 * i + (lane & 15);
-            const h8 av = *(const h8 *)&S.a[m][8 * aslot(m, ck)];
-            if (EXACT) {
-                const float4 sx = *(const float4 *)&S.sa[16 * i + 4 * ck];
-#pragma unroll
-                for (int j = 0; j < NJ; j++) {
-                    const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};
-                    const f4v blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv[j], z, 0, 0, 0);
-                    acc[i][j][0] = acc[i][j][0] + (blk[0] * sw[j]) * sx.x;
-                    acc[i][j][1] = acc[i][j][1] + (blk[1] * sw[j]) * sx.y;
-                    acc[i][j][2] = acc[i][j][2] + (blk[2] * sw[j]) * sx.z;
-                    acc[i][j][3] = acc[i][j][3] + (blk[3] * sw[j]) * sx.w;
-                }
+            // weight row n, codes 8c .. 8c+7
+            const int n = WN * wave + 16 * i + l16;
+            const uint2 q = *(const uint2 *)&S.w[n][16 * wslot(n, c >> 1) + 8 * (c & 1)];
+            av[i] = codes8(q.x, q.y);
+            if (GATEUP) {
+                s4[i] = *(const f4v *)&S.sw[WN * wave + 16 * i + 4 * c];
             } else {
+                const _Float16 sc = (_Float16)S.sw[n];
+                const h8 s8 = {sc, sc, sc, sc, sc, sc, sc, sc};
+                av[i] = av[i] * s8;
+            }
+        }
+        if (GATEUP) {
+            // The block dots of assignment tile j + 1 are started before the
+            // terms of tile j are added, so the vector ALUs never wait for
+            // the product they consume.
+            const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};
+            f4v blk[2][MI];
+            {
+                const h8 bv = *(const h8 *)&S.x[l16][8 * xslot(l16, c)];
 #pragma unroll
-                for (int j = 0; j < NJ; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv[j], acc[i][j], 0, 0, 0);
+                for (int i = 0; i < MI; i++)
+                    blk[0][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv, z, 0, 0, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                if (j + 1 < NJ) {
+                    const int m1 = 16 * (j + 1) + l16;
+                    const h8 bv = *(const h8 *)&S.x[m1][8 * xslot(m1, c)];
+#pragma unroll
+                    for (int i = 0; i < MI; i++)
+                        blk[(j + 1) & 1][i] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv, z, 0, 0, 0);
+                }
+                const float sx = S.sx[16 * j + l16];
+#pragma unroll
+                for (int i = 0; i < MI; i++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        acc[i][j][r] =
+                            __builtin_fmaf(blk[j & 1][i][r] * s4[i][r], sx, acc[i][j][r]);
+            }
+        }
+        if (!GATEUP) {
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const int m = 16 * j + l16;
+                const h8 bv = *(const h8 *)&S.x[m][8 * xslot(m, c)];
+#pragma unroll
+                for (int i = 0; i < MI; i++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv, acc[i][j], 0, 0, 0);
             }
         }
     }
     wait_vm<0>();  // the reloads past the end
     __syncthreads();
-}
-
-// The A rows this thread loads: rows 32*wave + 16*q + lane/4 (q = 0, 1), in
-// the chunk that lands in LDS slot lane % 4.
-__device__ __forceinline__ void a_rows(int &r0, int &c0, int &r1, int &c1) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    r0 = 32 * wave + (lane >> 2);
-    r1 = r0 + 16;
-    c0 = aslot(r0, lane & 3);  // slot ^ swizzle = the chunk stored there
-    c1 = aslot(r1, lane & 3);
 }
 
 // ---- x block scales in bucketed, block-major order --------------------------------
@@ -255,63 +301,54 @@ __global__ __launch_bounds__(256) void k_xs_bucket(const float *__restrict__ xs,
     if (p < A) xsb[(size_t)k * A + p] = xs[(size_t)(perm[p] / K) * nb + k];
 }
 
+union alignas(16) TileLds {
+    Step ring[NS];
+    float o[TM][OLD];  // epilogue: 128 assignment rows x 128 columns
+};
+static_assert(sizeof(TileLds) == NS * sizeof(Step), "epilogue tile fits the ring");
+
 // ---- gate/up + SwiGLU + Q8(h) ----------------------------------------------------
 //
-// blockIdx.x = tile of assignment rows (gtile numbering), blockIdx.y = 64
-// consecutive h columns h0..h0+63. Wavefront w's 32 weight rows are the gate
-// rows then the up rows of h columns h0+16w..h0+16w+15, so SwiGLU pairs its
-// accumulator tiles 0 and 1 lane by lane.
-constexpr int NS_GU = 4;
-constexpr int NS_DN = 6;
-
-union alignas(16) GateUpLds {
-    Step ring[NS_GU];
-    float h[TM][HLD];
-};
-union alignas(16) DownLds {
-    Step ring[NS_DN];
-};
-
-__global__ __launch_bounds__(GT, 1) void k_gateup_mfma(
+// blockIdx.x = tile of assignment rows (gtile numbering) x 6 column tiles of
+// 128 consecutive h columns h0..h0+127. Wavefront w's 64 weight rows are the
+// gate rows then the up rows of h columns h0+32w..h0+32w+31, so SwiGLU pairs
+// its accumulator tiles i and i + 2 lane by lane.
+__global__ __launch_bounds__(GT, 2) void k_gateup_mfma(
     const uint8_t *__restrict__ table, mhip_layout lay, const _Float16 *__restrict__ xq16,
     const float *__restrict__ xsb, const int *__restrict__ groups, const int *__restrict__ gtile,
     const int *__restrict__ perm, _Float16 *__restrict__ hdq, int d, int eh, int K, int A) {
-    __shared__ GateUpLds L;
+    __shared__ TileLds L;
     TileRef tr;
     if (!tile_of(groups, gtile, eh / (TN / 2), tr)) return;
     const int base = tr.base, nrows = tr.nrows;
     const int h0 = tr.y * (TN / 2);
     const uint8_t *ex = table + (size_t)tr.e * lay.expert_bytes;
-    const int nb = d / KB;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
     Src src;
     {
-        int r0, c0, r1, c1;
-        a_rows(r0, c0, r1, c1);
-        const int t0 = perm[base + min(r0, nrows - 1)] / K;
-        const int t1 = perm[base + min(r1, nrows - 1)] / K;
-        src.a0 = xq16 + (size_t)t0 * d + c0 * 8;
-        src.a1 = xq16 + (size_t)t1 * d + c1 * 8;
-        // weight row of B row 32*wave + lane/2: gate rows then up rows
-        const int bj = (lane >> 1) >> 4, br = (lane >> 1) & 15;
-        const int wr = h0 + 16 * wave + br;
-        src.b = (const int8_t *)(ex + (bj == 0 ? lay.gate_q : lay.up_q)) + (size_t)wr * d +
-                (lane & 1) * 16;
-        // block-major scales: the 128 rows of a step are 4 (waves 0, 1) or
-        // 1 (waves 2, 3) contiguous runs
-        if (wave < 2) {
-            // scale of B row 64*wave + lane
-            const int b = 64 * wave + lane;
-            const int sw = h0 + 16 * (b >> 5) + (b & 15);
-            src.s = (const float *)(ex + (((b >> 4) & 1) == 0 ? lay.gate_st : lay.up_st)) + sw;
-            src.sstep = eh;
-        } else {
-            // scale of assignment row 64*(wave-2) + lane
-            const int m = 64 * (wave - 2) + lane;
-            src.s = xsb + base + min(m, nrows - 1);
-            src.sstep = A;
+        const Pieces p = pieces();
+        const int t0 = perm[base + min(p.xr0, nrows - 1)] / K;
+        const int t1 = perm[base + min(p.xr1, nrows - 1)] / K;
+        src.x0 = xq16 + (size_t)t0 * d + p.xc0 * 8;
+        src.x1 = xq16 + (size_t)t1 * d + p.xc1 * 8;
+        // tile row n: wavefront n / 64; within it gate rows then up rows
+        auto wrow = [&](int n, int half) {
+            const int r = n % WN;
+            const int hc = h0 + (n / WN) * (WN / 2) + r % (WN / 2);
+            return (const int8_t *)(ex + (r < WN / 2 ? lay.gate_q : lay.up_q)) + (size_t)hc * d +
+                   16 * half;
+        };
+        src.w0 = wrow(p.wr0, p.wh0);
+        src.w1 = wrow(p.wr1, p.wh1);
+        {
+            // scale of tile row 64 wave + lane
+            const int hc = h0 + wave * (WN / 2) + lane % (WN / 2);
+            src.sw = (const float *)(ex + (lane < WN / 2 ? lay.gate_st : lay.up_st)) + hc;
+            src.swstep = eh;
         }
+        src.sx = xsb + base + min(32 * wave + (lane & 31), nrows - 1);
+        src.sxstep = A;
     }
 
     f4v acc[MI][NJ];
@@ -319,78 +356,89 @@ __global__ __launch_bounds__(GT, 1) void k_gateup_mfma(
     for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = (f4v){0.0f, 0.0f, 0.0f, 0.0f};
-    gemm_tile<NS_GU, true>(L.ring, src, nb, acc);
+    gemm_tile<true>(L.ring, src, d / KB, acc);
 
-    // SwiGLU into the h tile (LDS, reused), then Q8_0 per 32-block
+    // SwiGLU into the h tile (LDS, reused): row = assignment, column = h - h0
+    const int c = lane >> 4, l16 = lane & 15;
 #pragma unroll
-    for (int i = 0; i < MI; i++)
+    for (int i = 0; i < MI / 2; i++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int m = 16 * i + 4 * (lane >> 4) + r;
-            const float gv = acc[i][0][r], uv = acc[i][1][r];
-            L.h[m][16 * wave + (lane & 15)] = (gv / (1.0f + mia_expf_glibc(-gv))) * uv;
+        for (int j = 0; j < NJ; j++) {
+            f4v hv;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float gv = acc[i][j][r], uv = acc[i + 2][j][r];
+                hv[r] = (gv / (1.0f + mia_expf_glibc(-gv))) * uv;
+            }
+            *(f4v *)&L.o[16 * j + l16][(WN / 2) * wave + 16 * i + 4 * c] = hv;
         }
     __syncthreads();
     {
-        // Q8_0 of one 32-block of h (quant.c:11-27), stored dequantized
-        const int m = tid >> 1, i = tid & 1;
+        // Q8_0 of 32-blocks of h (quant.c:11-27), stored dequantized: thread
+        // (m, b2) does blocks 2 b2 and 2 b2 + 1 of row m
+        const int m = tid >> 1, b2 = tid & 1;
         if (m < nrows) {
-            const float4 *hs = (const float4 *)&L.h[m][32 * i];
-            float v[32];
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const float4 q = hs[k];
-                v[4 * k] = q.x;
-                v[4 * k + 1] = q.y;
-                v[4 * k + 2] = q.z;
-                v[4 * k + 3] = q.w;
+            for (int bb = 0; bb < 2; bb++) {
+                const int blk = 2 * b2 + bb;
+                const f4v *hs = (const f4v *)&L.o[m][32 * blk];
+                float v[32];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const f4v q = hs[k];
+                    v[4 * k] = q[0];
+                    v[4 * k + 1] = q[1];
+                    v[4 * k + 2] = q[2];
+                    v[4 * k + 3] = q[3];
+                }
+                float amax = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 32; k++) amax = fmaxf(amax, fabsf(v[k]));
+                const float dsc = amax / 127.0f;
+                const float qi = dsc != 0.0f ? 1.0f / dsc : 0.0f;
+                h8 o[4];
+#pragma unroll
+                for (int k = 0; k < 32; k++) o[k >> 3][k & 7] = (_Float16)(roundf(v[k] * qi) * dsc);
+                h8 *dst = (h8 *)(hdq + (size_t)(base + m) * eh + h0 + 32 * blk);
+#pragma unroll
+                for (int k = 0; k < 4; k++) dst[k] = o[k];
             }
-            float amax = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 32; k++) amax = fmaxf(amax, fabsf(v[k]));
-            const float dsc = amax / 127.0f;
-            const float qi = dsc != 0.0f ? 1.0f / dsc : 0.0f;
-            h8 o[4];
-#pragma unroll
-            for (int k = 0; k < 32; k++) o[k >> 3][k & 7] = (_Float16)(roundf(v[k] * qi) * dsc);
-            h8 *dst = (h8 *)(hdq + (size_t)(base + m) * eh + h0 + 32 * i);
-#pragma unroll
-            for (int k = 0; k < 4; k++) dst[k] = o[k];
         }
     }
 }
 
 // ---- down -----------------------------------------------------------------------------
 //
-// blockIdx.x = tile of assignment rows, blockIdx.y = 128 consecutive down
-// rows. A rows are the tile's Q8(h) (fp16, bucketed order, contiguous).
+// blockIdx.x = tile of assignment rows x 8 column tiles of 256 consecutive
+// down rows n0..n0+255. The x operand is the tile's Q8(h) (fp16, bucketed
+// order, contiguous). Results go out through LDS in two halves of 128
+// columns, so every assignment row is written as 512 contiguous bytes.
 __global__ __launch_bounds__(GT, 2) void k_down_mfma(const uint8_t *__restrict__ table,
                                                      mhip_layout lay,
                                                      const _Float16 *__restrict__ hdq,
                                                      const int *__restrict__ groups,
                                                      const int *__restrict__ gtile,
                                                      float *__restrict__ tmp, int d, int eh) {
-    __shared__ DownLds L;
+    __shared__ TileLds L;
     TileRef tr;
     if (!tile_of(groups, gtile, d / TN, tr)) return;
     const int base = tr.base, nrows = tr.nrows;
     const int n0 = tr.y * TN;
     const uint8_t *ex = table + (size_t)tr.e * lay.expert_bytes;
-    const int nbh = eh / KB;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
     Src src;
     {
-        int r0, c0, r1, c1;
-        a_rows(r0, c0, r1, c1);
-        src.a0 = hdq + (size_t)(base + min(r0, nrows - 1)) * eh + c0 * 8;
-        src.a1 = hdq + (size_t)(base + min(r1, nrows - 1)) * eh + c1 * 8;
-        const int row = n0 + 32 * wave + (lane >> 1);
-        src.b = (const int8_t *)(ex + lay.down_q) + (size_t)row * eh + (lane & 1) * 16;
-        // scales of weight rows 64*(wave&1) + lane, block-major (waves 2, 3
-        // repeat waves 0, 1 into the unused assignment-scale slot)
-        src.s = (const float *)(ex + lay.down_st) + n0 + 64 * (wave & 1) + lane;
-        src.sstep = d;
+        const Pieces p = pieces();
+        src.x0 = hdq + (size_t)(base + min(p.xr0, nrows - 1)) * eh + p.xc0 * 8;
+        src.x1 = hdq + (size_t)(base + min(p.xr1, nrows - 1)) * eh + p.xc1 * 8;
+        const int8_t *dq = (const int8_t *)(ex + lay.down_q);
+        src.w0 = dq + (size_t)(n0 + p.wr0) * eh + 16 * p.wh0;
+        src.w1 = dq + (size_t)(n0 + p.wr1) * eh + 16 * p.wh1;
+        src.sw = (const float *)(ex + lay.down_st) + n0 + WN * wave + lane;
+        src.swstep = d;
+        src.sx = nullptr;
+        src.sxstep = 0;
     }
 
     f4v acc[MI][NJ];
@@ -398,19 +446,30 @@ __global__ __launch_bounds__(GT, 2) void k_down_mfma(const uint8_t *__restrict__
     for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = (f4v){0.0f, 0.0f, 0.0f, 0.0f};
-    gemm_tile<NS_DN, false>(L.ring, src, nbh, acc);
+    gemm_tile<false>(L.ring, src, eh / KB, acc);
 
+    const int c = lane >> 4, l16 = lane & 15;
 #pragma unroll
-    for (int i = 0; i < MI; i++)
+    for (int half = 0; half < 2; half++) {
+        // wavefronts 2 half, 2 half + 1 own columns 128 half .. + 127
+        if ((wave >> 1) == half) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int m = 16 * i + 4 * (lane >> 4) + r;
-            if (m < nrows) {
-                float *dst = tmp + (size_t)(base + m) * d + n0 + 32 * wave + (lane & 15);
+            for (int i = 0; i < MI; i++)
 #pragma unroll
-                for (int j = 0; j < NJ; j++) dst[16 * j] = acc[i][j][r];
-            }
+                for (int j = 0; j < NJ; j++)
+                    *(f4v *)&L.o[16 * j + l16][WN * (wave & 1) + 16 * i + 4 * c] = acc[i][j];
         }
+        __syncthreads();
+        // 128 rows x 32 float4: thread tid writes float4 tid % 32 of rows tid / 32 + 8 k
+#pragma unroll
+        for (int k = 0; k < TM / 8; k++) {
+            const int m = tid / 32 + 8 * k, f = tid % 32;
+            if (m < nrows)
+                *(f4v *)(tmp + (size_t)(base + m) * d + n0 + 128 * half + 4 * f) =
+                    *(const f4v *)&L.o[m][4 * f];
+        }
+        __syncthreads();
+    }
 }
 
 }  // namespace
@@ -419,8 +478,8 @@ namespace mhip {
 
 bool gemm_path_fits(const mhip_dims *s) {
     // whole tiles of weight rows, and enough k steps to fill the rings
-    return s->dim % TN == 0 && s->expert_hidden % (TN / 2) == 0 &&
-           s->dim / KB >= NS_GU - 1 && s->expert_hidden / KB >= NS_DN - 1;
+    return s->dim % TN == 0 && s->expert_hidden % (TN / 2) == 0 && s->dim / KB >= NS - 1 &&
+           s->expert_hidden / KB >= NS - 1;
 }
 
 int gemm_max_tiles(int A, int E) { return (A + TM - 1) / TM + (A < E ? A : E); }
