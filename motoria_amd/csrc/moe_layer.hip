@@ -293,6 +293,85 @@ size_t router_logits_lds(int C, int d) {
     return ((size_t)RL_NS * RL_I * RL_E + (size_t)d * 2 * C) * sizeof(float);
 }
 
+// ---- router logits for prefill-sized T ----------------------------------------------
+//
+// The same chains with the tokens across the lanes: a workgroup takes RW_T = 64
+// tokens (lane = token) and RW_E = 16 experts (wavefront w: experts 4w..4w+3),
+// so every lane runs four chains over one token and every router value is a
+// wavefront-wide broadcast. xn (transposed, rows padded to 65 floats so the
+// transposing stores and the row reads are conflict-free) and the router
+// rows go through LDS in chunks of RW_I values of i, double-buffered through
+// registers. Needs d % RW_I == 0 and E % RW_E == 0.
+constexpr int RW_T = 64, RW_E = 16, RW_I = 64;
+
+__global__ __launch_bounds__(256, 2) void k_router_logits_wide(const float *__restrict__ xn,
+                                                               const float *__restrict__ wt,
+                                                               const float *__restrict__ bias,
+                                                               float *__restrict__ logits, int T,
+                                                               int d, int E) {
+    __shared__ float Xs[2][RW_I][RW_T + 1];
+    __shared__ float4 Ws[2][RW_I][RW_E / 4];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t0 = blockIdx.x * RW_T, e0 = blockIdx.y * RW_E;
+    // this thread's loads of a chunk: 16 values of xn row tt (from i0 + 16 q),
+    // and the 4 router values of row i0 + tid / 4, experts e0 + 4 (tid % 4) ..
+    const int tt = tid >> 2, q = tid & 3;
+    const float *xsrc = xn + (size_t)min(t0 + tt, T - 1) * d + 16 * q;
+    const float *wsrc = wt + (size_t)(tid >> 2) * E + e0 + 4 * (tid & 3);
+    float4 xr[4], wr;
+    auto gload = [&](int ch) {
+        const int i0 = ch * RW_I;
+#pragma unroll
+        for (int k = 0; k < 4; k++) xr[k] = *(const float4 *)(xsrc + i0 + 4 * k);
+        wr = *(const float4 *)(wsrc + (size_t)i0 * E);
+    };
+    auto lstore = [&](int b) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            Xs[b][16 * q + 4 * k + 0][tt] = xr[k].x;
+            Xs[b][16 * q + 4 * k + 1][tt] = xr[k].y;
+            Xs[b][16 * q + 4 * k + 2][tt] = xr[k].z;
+            Xs[b][16 * q + 4 * k + 3][tt] = xr[k].w;
+        }
+        Ws[b][tid >> 2][tid & 3] = wr;
+    };
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    const int nch = d / RW_I;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int ch = 0; ch < nch; ch++) {
+        const int b = ch & 1;
+        if (ch + 1 < nch) gload(ch + 1);
+#pragma unroll 16
+        for (int ii = 0; ii < RW_I; ii++) {
+            const float x = Xs[b][ii][lane];
+            const float4 w = Ws[b][ii][wave];
+            s0 = s0 + w.x * x;
+            s1 = s1 + w.y * x;
+            s2 = s2 + w.z * x;
+            s3 = s3 + w.w * x;
+        }
+        // buffer b ^ 1 was last read in the previous chunk, before the
+        // barrier that ended it
+        if (ch + 1 < nch) lstore(b ^ 1);
+        __syncthreads();
+    }
+    const int t = t0 + lane;
+    if (t < T) {
+        const int e = e0 + 4 * wave;
+        float4 o = make_float4(s0, s1, s2, s3);
+        if (bias) {
+            o.x = s0 + bias[e];
+            o.y = s1 + bias[e + 1];
+            o.z = s2 + bias[e + 2];
+            o.w = s3 + bias[e + 3];
+        }
+        *(float4 *)(logits + (size_t)t * E + e) = o;
+    }
+}
+
 // ---- dispatch -------------------------------------------------------------
 //
 // Stable counting sort of the A = T*K assignments a = t*K + j by expert
@@ -814,7 +893,11 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     const bool tiled = T > 1 && E == RL_E && d % RL_I == 0 && d / RL_I >= RL_NS - 1;
     const size_t rsh = (size_t)(E + (tiled ? 0 : d)) * sizeof(float);
     slot = mhip::stage_begin(c, MHIP_STAGE_ROUTER);
-    if (tiled) {
+    const bool wide = tiled && T >= 2048 && d % RW_I == 0 && E % RW_E == 0;
+    if (wide) {
+        k_router_logits_wide<<<dim3((T + RW_T - 1) / RW_T, E / RW_E), 256, 0, st>>>(
+            sc->xn, d_router_t, d_bias, sc->logits, T, d, E);
+    } else if (tiled) {
         const int C = T >= 4096 ? 4 : T >= 2048 ? 2 : 1;
         const size_t lsh = router_logits_lds(C, d);
         const void *fn = C == 4 ? (const void *)k_router_logits<4>
