@@ -25,7 +25,7 @@
 // 64w..64w+63 against all 128 assignments: 4 x 8 tiles of 16x16 with the
 // weights as the A operand, so each lane's four results share one
 // assignment (one x scale) and four consecutive weight rows (one float4 of
-// weight scales). Two workgroups share a CU.
+// weight scales). Two gate/up or three down workgroups share a CU.
 //
 // Operands move from global memory straight into an NS-stage LDS ring with
 // global_load_lds (no registers on the way), NS-1 steps ahead of the
@@ -50,8 +50,10 @@ constexpr int KB = 32;            // k per step: one Q8_0 block
 constexpr int WN = TN / 4;        // weight rows per wavefront (64)
 constexpr int MI = WN / 16;       // 16-row weight tiles per wavefront (4)
 constexpr int NJ = TM / 16;       // 16-row assignment tiles (8)
-constexpr int NS = 4;             // ring stages
-constexpr int OLD = TM + 4;       // epilogue tile row stride (floats): 128 columns + pad
+constexpr int NS_GU = 4;          // ring stages: gate/up (two workgroups per CU)
+constexpr int NS_DN = 3;          // down (three workgroups per CU)
+constexpr int OLD = TM + 4;       // gate/up epilogue tile row stride (floats): 128 columns + pad
+constexpr int DLD = WN + 4;       // down epilogue tile row stride: 64 columns + pad
 
 static_assert(TM == 128 && TN == 256 && GT == 256, "tiling");
 
@@ -195,7 +197,7 @@ __device__ __forceinline__ Pieces pieces() {
 // (weight row, assignment row). GATEUP: exact block dots, and the block
 // terms added with their scales; otherwise fp16 dequantized weights
 // (d_w * q) accumulated on the matrix cores.
-template <bool GATEUP>
+template <bool GATEUP, int NS>
 __device__ __forceinline__ void gemm_tile(Step *ring, const Src &src, int nk, f4v acc[MI][NJ]) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -301,11 +303,17 @@ __global__ __launch_bounds__(256) void k_xs_bucket(const float *__restrict__ xs,
     if (p < A) xsb[(size_t)k * A + p] = xs[(size_t)(perm[p] / K) * nb + k];
 }
 
-union alignas(16) TileLds {
-    Step ring[NS];
-    float o[TM][OLD];  // epilogue: 128 assignment rows x 128 columns
+union alignas(16) GateUpLds {
+    Step ring[NS_GU];
+    float o[TM][OLD];  // epilogue: 128 assignment rows x 128 h columns
 };
-static_assert(sizeof(TileLds) == NS * sizeof(Step), "epilogue tile fits the ring");
+union alignas(16) DownLds {
+    Step ring[NS_DN];
+    float o[TM][DLD];  // epilogue: 128 assignment rows x 64 down rows
+};
+static_assert(sizeof(GateUpLds) == NS_GU * sizeof(Step) && sizeof(DownLds) == NS_DN * sizeof(Step),
+              "epilogue tiles fit the rings");
+static_assert(3 * sizeof(DownLds) <= 160 * 1024, "three down workgroups per CU");
 
 // ---- gate/up + SwiGLU + Q8(h) ----------------------------------------------------
 //
@@ -317,7 +325,7 @@ __global__ __launch_bounds__(GT, 2) void k_gateup_mfma(
     const uint8_t *__restrict__ table, mhip_layout lay, const _Float16 *__restrict__ xq16,
     const float *__restrict__ xsb, const int *__restrict__ groups, const int *__restrict__ gtile,
     const int *__restrict__ perm, _Float16 *__restrict__ hdq, int d, int eh, int K, int A) {
-    __shared__ TileLds L;
+    __shared__ GateUpLds L;
     TileRef tr;
     if (!tile_of(groups, gtile, eh / (TN / 2), tr)) return;
     const int base = tr.base, nrows = tr.nrows;
@@ -356,7 +364,7 @@ __global__ __launch_bounds__(GT, 2) void k_gateup_mfma(
     for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = (f4v){0.0f, 0.0f, 0.0f, 0.0f};
-    gemm_tile<true>(L.ring, src, d / KB, acc);
+    gemm_tile<true, NS_GU>(L.ring, src, d / KB, acc);
 
     // SwiGLU into the h tile (LDS, reused): row = assignment, column = h - h0
     const int c = lane >> 4, l16 = lane & 15;
@@ -413,13 +421,13 @@ __global__ __launch_bounds__(GT, 2) void k_gateup_mfma(
 // down rows n0..n0+255. The x operand is the tile's Q8(h) (fp16, bucketed
 // order, contiguous). Results go out through LDS in two halves of 128
 // columns, so every assignment row is written as 512 contiguous bytes.
-__global__ __launch_bounds__(GT, 2) void k_down_mfma(const uint8_t *__restrict__ table,
+__global__ __launch_bounds__(GT, 3) void k_down_mfma(const uint8_t *__restrict__ table,
                                                      mhip_layout lay,
                                                      const _Float16 *__restrict__ hdq,
                                                      const int *__restrict__ groups,
                                                      const int *__restrict__ gtile,
                                                      float *__restrict__ tmp, int d, int eh) {
-    __shared__ TileLds L;
+    __shared__ DownLds L;
     TileRef tr;
     if (!tile_of(groups, gtile, d / TN, tr)) return;
     const int base = tr.base, nrows = tr.nrows;
@@ -446,26 +454,26 @@ __global__ __launch_bounds__(GT, 2) void k_down_mfma(const uint8_t *__restrict__
     for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = (f4v){0.0f, 0.0f, 0.0f, 0.0f};
-    gemm_tile<false>(L.ring, src, eh / KB, acc);
+    gemm_tile<false, NS_DN>(L.ring, src, eh / KB, acc);
 
     const int c = lane >> 4, l16 = lane & 15;
 #pragma unroll
-    for (int half = 0; half < 2; half++) {
-        // wavefronts 2 half, 2 half + 1 own columns 128 half .. + 127
-        if ((wave >> 1) == half) {
+    for (int qw = 0; qw < 4; qw++) {
+        // wavefront qw's 64 columns, then every thread writes them out
+        if (wave == qw) {
 #pragma unroll
             for (int i = 0; i < MI; i++)
 #pragma unroll
                 for (int j = 0; j < NJ; j++)
-                    *(f4v *)&L.o[16 * j + l16][WN * (wave & 1) + 16 * i + 4 * c] = acc[i][j];
+                    *(f4v *)&L.o[16 * j + l16][16 * i + 4 * c] = acc[i][j];
         }
         __syncthreads();
-        // 128 rows x 32 float4: thread tid writes float4 tid % 32 of rows tid / 32 + 8 k
+        // 128 rows x 16 float4: thread tid writes float4 tid % 16 of rows tid / 16 + 16 k
 #pragma unroll
-        for (int k = 0; k < TM / 8; k++) {
-            const int m = tid / 32 + 8 * k, f = tid % 32;
+        for (int k = 0; k < TM / 16; k++) {
+            const int m = tid / 16 + 16 * k, f = tid % 16;
             if (m < nrows)
-                *(f4v *)(tmp + (size_t)(base + m) * d + n0 + 128 * half + 4 * f) =
+                *(f4v *)(tmp + (size_t)(base + m) * d + n0 + WN * qw + 4 * f) =
                     *(const f4v *)&L.o[m][4 * f];
         }
         __syncthreads();
@@ -478,8 +486,8 @@ namespace mhip {
 
 bool gemm_path_fits(const mhip_dims *s) {
     // whole tiles of weight rows, and enough k steps to fill the rings
-    return s->dim % TN == 0 && s->expert_hidden % (TN / 2) == 0 && s->dim / KB >= NS - 1 &&
-           s->expert_hidden / KB >= NS - 1;
+    return s->dim % TN == 0 && s->expert_hidden % (TN / 2) == 0 && s->dim / KB >= NS_GU - 1 &&
+           s->expert_hidden / KB >= NS_DN - 1;
 }
 
 int gemm_max_tiles(int A, int E) { return (A + TM - 1) / TM + (A < E ? A : E); }

@@ -778,19 +778,33 @@ __global__ __launch_bounds__(NT) void k_down(const uint8_t *__restrict__ table, 
 
 // ---- combine -------------------------------------------------------------------
 // x_i = x_i + w_j * tmp_j,i for j = 0..K-1 in top-K order (forward.c:194).
+// Four consecutive elements per thread (d % 4 == 0); the K rows of a token
+// are requested before the ordered sum consumes them.
 __global__ __launch_bounds__(256) void k_combine(float *__restrict__ x,
                                                  const float *__restrict__ w,
                                                  const int *__restrict__ pos,
                                                  const float *__restrict__ tmp, int d, int K) {
     const int t = blockIdx.y;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int i = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
     if (i >= d) return;
-    float v = x[(size_t)t * d + i];
-    for (int j = 0; j < K; j++) {
-        const int a = t * K + j;
-        v = v + w[a] * tmp[(size_t)pos[a] * d + i];
+    float4 *xp = (float4 *)(x + (size_t)t * d + i);
+    float4 v = *xp;
+    for (int j0 = 0; j0 < K; j0 += 8) {
+        float4 tv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (j0 + j < K) tv[j] = *(const float4 *)(tmp + (size_t)pos[t * K + j0 + j] * d + i);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (j0 + j < K) {
+                const float wj = w[t * K + j0 + j];
+                v.x = v.x + wj * tv[j].x;
+                v.y = v.y + wj * tv[j].y;
+                v.z = v.z + wj * tv[j].z;
+                v.w = v.w + wj * tv[j].w;
+            }
     }
-    x[(size_t)t * d + i] = v;
+    *xp = v;
 }
 
 // Rows per workgroup: the largest power of two <= 32 with 2R*nb <= PK*NT
@@ -951,7 +965,7 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
         e = mhip::launch_down_mfma(st, s, lay, d_table_layer, sc, A);
         mhip::stage_end(c, slot);
         if (mhip::check(c, (hipError_t)e, "down_mfma launch")) return -1;
-        dim3 cg(mhip::blocks_for(d, 256), T);
+        dim3 cg(mhip::blocks_for(d, 1024), T);
         slot = mhip::stage_begin(c, MHIP_STAGE_COMBINE);
         k_combine<<<cg, 256, 0, st>>>(d_x, sc->w, sc->pos, sc->tmp, d, K);
         mhip::stage_end(c, slot);
@@ -977,7 +991,7 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     mhip::stage_end(c, slot);
     if (mhip::check_launch(c, "down")) return -1;
 
-    dim3 cg(mhip::blocks_for(d, 256), T);
+    dim3 cg(mhip::blocks_for(d, 1024), T);
     slot = mhip::stage_begin(c, MHIP_STAGE_COMBINE);
     k_combine<<<cg, 256, 0, st>>>(d_x, sc->w, sc->pos, sc->tmp, d, K);
     mhip::stage_end(c, slot);
