@@ -194,11 +194,13 @@ __device__ __forceinline__ Pieces pieces() {
 
 // The k loop over nk steps (nk >= NS - 1). On return acc[i][j][r] holds
 //   C[64*wave + 16*i + 4*(lane/16) + r][16*j + lane%16]
-// (weight row, assignment row). GATEUP: exact block dots, and the block
+// (weight row, assignment row) for the assignment tiles j < NJA (the tiles
+// that hold rows of the bucket; the others are not computed). GATEUP: exact block dots, and the block
 // terms added with their scales; otherwise fp16 dequantized weights
 // (d_w * q) accumulated on the matrix cores.
-template <bool GATEUP, int NS>
+template <bool GATEUP, int NS, int NJA>
 __device__ __forceinline__ void gemm_tile(Step *ring, const Src &src, int nk, f4v acc[MI][NJ]) {
+    static_assert(NJA >= 1 && NJA <= NJ, "assignment tiles");
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     constexpr int NLOAD = GATEUP ? 6 : 5;  // global_load_lds per wavefront per step
@@ -259,8 +261,8 @@ __device__ __forceinline__ void gemm_tile(Step *ring, const Src &src, int nk, f4
                     blk[0][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv, z, 0, 0, 0);
             }
 #pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                if (j + 1 < NJ) {
+            for (int j = 0; j < NJA; j++) {
+                if (j + 1 < NJA) {
                     const int m1 = 16 * (j + 1) + l16;
                     const h8 bv = *(const h8 *)&S.x[m1][8 * xslot(m1, c)];
 #pragma unroll
@@ -279,7 +281,7 @@ __device__ __forceinline__ void gemm_tile(Step *ring, const Src &src, int nk, f4
         }
         if (!GATEUP) {
 #pragma unroll
-            for (int j = 0; j < NJ; j++) {
+            for (int j = 0; j < NJA; j++) {
                 const int m = 16 * j + l16;
                 const h8 bv = *(const h8 *)&S.x[m][8 * xslot(m, c)];
 #pragma unroll
@@ -364,7 +366,16 @@ __global__ __launch_bounds__(GT, 2) void k_gateup_mfma(
     for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = (f4v){0.0f, 0.0f, 0.0f, 0.0f};
-    gemm_tile<true, NS_GU>(L.ring, src, d / KB, acc);
+    // a bucket's last tile may hold few rows: only its assignment tiles run
+    const int nj = (nrows + 15) / 16;
+    if (nj > 4)
+        gemm_tile<true, NS_GU, 8>(L.ring, src, d / KB, acc);
+    else if (nj > 2)
+        gemm_tile<true, NS_GU, 4>(L.ring, src, d / KB, acc);
+    else if (nj > 1)
+        gemm_tile<true, NS_GU, 2>(L.ring, src, d / KB, acc);
+    else
+        gemm_tile<true, NS_GU, 1>(L.ring, src, d / KB, acc);
 
     // SwiGLU into the h tile (LDS, reused): row = assignment, column = h - h0
     const int c = lane >> 4, l16 = lane & 15;
@@ -454,7 +465,15 @@ __global__ __launch_bounds__(GT, 3) void k_down_mfma(const uint8_t *__restrict__
     for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = (f4v){0.0f, 0.0f, 0.0f, 0.0f};
-    gemm_tile<false, NS_DN>(L.ring, src, eh / KB, acc);
+    const int nj = (nrows + 15) / 16;
+    if (nj > 4)
+        gemm_tile<false, NS_DN, 8>(L.ring, src, eh / KB, acc);
+    else if (nj > 2)
+        gemm_tile<false, NS_DN, 4>(L.ring, src, eh / KB, acc);
+    else if (nj > 1)
+        gemm_tile<false, NS_DN, 2>(L.ring, src, eh / KB, acc);
+    else
+        gemm_tile<false, NS_DN, 1>(L.ring, src, eh / KB, acc);
 
     const int c = lane >> 4, l16 = lane & 15;
 #pragma unroll

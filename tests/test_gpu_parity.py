@@ -234,6 +234,42 @@ def test_layer_skewed_2048(oracle, qwen_dims, qwen_moe):
     assert 0.35 < share4 < 0.5 and 20 <= zero <= 40
 
 
+def test_layer_prefill_4096_routing_and_sample(oracle, qwen_dims):
+    """T=4096, the prefill benchmark shape (matrix-core experts, tokens-across-
+    lanes router): every token's logits, expert indices and gate weights
+    bit-equal to the oracle's (rmsnorm, router chain and routing per token),
+    and the layer output of a seeded sample of 96 tokens within TOL (the
+    oracle's layer is per token, so the sample checks the full-size launch)."""
+    say("test_layer_prefill_4096_routing_and_sample")
+    d = qwen_dims
+    T = 4096
+    moe = M.Moe(n_layers=1, max_tokens=T, device=0, **W.SHAPE)
+    try:
+        moe.synth(W.WEIGHT_SEED)
+        moe.sync()
+        x = oracle.synth_x(W.X_SEED + 11, T, d.dim)
+        router = oracle.synth_router(W.WEIGHT_SEED, 0, d)
+        xm, im, wm, lm = _gpu_layer(moe, 0, x, None, 0)
+        norm = np.ones(d.dim, np.float32)
+        for t in range(T):
+            xn = oracle.rmsnorm(x[t], norm, d.norm_eps)
+            lo = oracle.matvec(router, 0, xn, d.n_experts, d.dim)
+            io, wo, _ = oracle.route(lo, d.n_active, d.norm_topk)
+            assert np.array_equal(bits(lm[t]), bits(lo)), "token %d logits" % t
+            assert np.array_equal(im[t], io), "token %d expert indices" % t
+            assert np.array_equal(bits(wm[t]), bits(wo)), "token %d gate weights" % t
+        sample = np.sort(np.random.default_rng(5).choice(T, 96, replace=False))
+        xs = x[sample]
+        xo, io, _, _, _ = oracle_layer(oracle, moe, d, 0, xs, router,
+                                       need=im[sample].ravel().tolist())
+        assert np.array_equal(im[sample], io)
+        e_delta, e_out = rel_err(xm[sample] - xs, xo - xs), rel_err(xm[sample], xo)
+        say("  sample of 96: rel err update %.3e, output %.3e" % (e_delta, e_out))
+        assert e_delta <= TOL and e_out <= TOL
+    finally:
+        moe.close()
+
+
 def test_matrix_path_ragged_buckets(oracle, qwen_dims, qwen_moe):
     """T=300: 2400 assignments (above the matrix-core threshold), every
     expert bucket smaller than one 128-row tile; the tile table must count
