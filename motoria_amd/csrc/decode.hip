@@ -370,6 +370,24 @@ __device__ __forceinline__ float lds_seq_sum(const float *p, int n, float s) {
     }
     return s;
 }
+// The same for a compile-time length: every value is read before the first
+// addition, so the chain waits for the LDS once.
+template <int N>
+__device__ __forceinline__ float lds_seq_sum_n(const float *p, float s) {
+    static_assert(N % 4 == 0, "whole float4s");
+    const float4 *v = (const float4 *)p;
+    float4 q[N / 4];
+#pragma unroll
+    for (int k = 0; k < N / 4; k++) q[k] = v[k];
+#pragma unroll
+    for (int k = 0; k < N / 4; k++) {
+        s = s + q[k].x;
+        s = s + q[k].y;
+        s = s + q[k].z;
+        s = s + q[k].w;
+    }
+    return s;
+}
 
 // Diagnostic: one thread of every workgroup (thread 0 unless named) records
 // the 100 MHz real-time counter at the stage boundaries of a window of layers.
@@ -775,7 +793,7 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                 }
                 TRACE(12);
                 wave_lds_sync();
-                if (lane < GU_R) sh.gu[wave][lane] = lds_seq_sum(&terms[lane * GU_LD], NB, 0.0f);
+                if (lane < GU_R) sh.gu[wave][lane] = lds_seq_sum_n<NB>(&terms[lane * GU_LD], 0.0f);
                 wave_lds_sync();
                 TRACE(19);
                 if (lane < GU_H) {
@@ -878,7 +896,7 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             __syncthreads();
             if (wave == 0)
                 put_tagged<false>(&ws->out[par][xcd][rank * DROWS + lane],
-                           lds_seq_sum(&dterm[lane * DN_LD], NBH, 0.0f), tag);
+                           lds_seq_sum_n<NBH>(&dterm[lane * DN_LD], 0.0f), tag);
         }
         TRACE(6);
 
