@@ -293,38 +293,48 @@ size_t router_logits_lds(int C, int d) {
     return ((size_t)RL_NS * RL_I * RL_E + (size_t)d * 2 * C) * sizeof(float);
 }
 
-// ---- router logits for prefill-sized T ----------------------------------------------
+// ---- router logits for batches of tokens --------------------------------------------
 //
 // The same chains with the tokens across the lanes: a workgroup takes RW_T = 64
-// tokens (lane = token) and RW_E = 16 experts (wavefront w: experts 4w..4w+3),
-// so every lane runs four chains over one token and every router value is a
-// wavefront-wide broadcast. xn (transposed, rows padded to 65 floats so the
-// transposing stores and the row reads are conflict-free) and the router
-// rows go through LDS in chunks of RW_I values of i, double-buffered through
-// registers. Needs d % RW_I == 0 and E % RW_E == 0.
-constexpr int RW_T = 64, RW_E = 16, RW_I = 64;
+// tokens (lane = token) and 4 CPL experts (wavefront w: experts CPL w ..
+// CPL w + CPL - 1), so every lane runs CPL chains over one token and every
+// router value is a wavefront-wide broadcast. xn (transposed, rows padded to
+// 65 floats so the transposing stores and the row reads are conflict-free)
+// and the router rows go through LDS in chunks of RW_I values of i,
+// double-buffered through registers. CPL trades chains per lane (latency
+// hiding) against workgroups (CPL = 1 for a few tokens). Needs d % RW_I == 0
+// and E % (4 CPL) == 0.
+constexpr int RW_T = 64, RW_I = 64;
 
+template <int CPL>
+struct alignas(4 * CPL) RwVec {
+    float v[CPL];
+};
+
+template <int CPL>
 __global__ __launch_bounds__(256, 2) void k_router_logits_wide(const float *__restrict__ xn,
                                                                const float *__restrict__ wt,
                                                                const float *__restrict__ bias,
                                                                float *__restrict__ logits, int T,
                                                                int d, int E) {
+    typedef RwVec<CPL> V;
     __shared__ float Xs[2][RW_I][RW_T + 1];
-    __shared__ float4 Ws[2][RW_I][RW_E / 4];
+    __shared__ V Ws[2][RW_I][4];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int t0 = blockIdx.x * RW_T, e0 = blockIdx.y * RW_E;
+    const int t0 = blockIdx.x * RW_T, e0 = blockIdx.y * 4 * CPL;
     // this thread's loads of a chunk: 16 values of xn row tt (from i0 + 16 q),
-    // and the 4 router values of row i0 + tid / 4, experts e0 + 4 (tid % 4) ..
+    // and the CPL router values of row i0 + tid / 4, experts e0 + CPL (tid % 4) ..
     const int tt = tid >> 2, q = tid & 3;
     const float *xsrc = xn + (size_t)min(t0 + tt, T - 1) * d + 16 * q;
-    const float *wsrc = wt + (size_t)(tid >> 2) * E + e0 + 4 * (tid & 3);
-    float4 xr[4], wr;
+    const float *wsrc = wt + (size_t)(tid >> 2) * E + e0 + CPL * (tid & 3);
+    float4 xr[4];
+    V wr;
     auto gload = [&](int ch) {
         const int i0 = ch * RW_I;
 #pragma unroll
         for (int k = 0; k < 4; k++) xr[k] = *(const float4 *)(xsrc + i0 + 4 * k);
-        wr = *(const float4 *)(wsrc + (size_t)i0 * E);
+        wr = *(const V *)(wsrc + (size_t)i0 * E);
     };
     auto lstore = [&](int b) {
 #pragma unroll
@@ -336,7 +346,9 @@ __global__ __launch_bounds__(256, 2) void k_router_logits_wide(const float *__re
         }
         Ws[b][tid >> 2][tid & 3] = wr;
     };
-    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    float s[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; c++) s[c] = 0.0f;
     const int nch = d / RW_I;
     gload(0);
     lstore(0);
@@ -347,11 +359,9 @@ __global__ __launch_bounds__(256, 2) void k_router_logits_wide(const float *__re
 #pragma unroll 16
         for (int ii = 0; ii < RW_I; ii++) {
             const float x = Xs[b][ii][lane];
-            const float4 w = Ws[b][ii][wave];
-            s0 = s0 + w.x * x;
-            s1 = s1 + w.y * x;
-            s2 = s2 + w.z * x;
-            s3 = s3 + w.w * x;
+            const V w = Ws[b][ii][wave];
+#pragma unroll
+            for (int c = 0; c < CPL; c++) s[c] = s[c] + w.v[c] * x;
         }
         // buffer b ^ 1 was last read in the previous chunk, before the
         // barrier that ended it
@@ -360,15 +370,11 @@ __global__ __launch_bounds__(256, 2) void k_router_logits_wide(const float *__re
     }
     const int t = t0 + lane;
     if (t < T) {
-        const int e = e0 + 4 * wave;
-        float4 o = make_float4(s0, s1, s2, s3);
-        if (bias) {
-            o.x = s0 + bias[e];
-            o.y = s1 + bias[e + 1];
-            o.z = s2 + bias[e + 2];
-            o.w = s3 + bias[e + 3];
-        }
-        *(float4 *)(logits + (size_t)t * E + e) = o;
+        const int e = e0 + CPL * wave;
+        V o;
+#pragma unroll
+        for (int c = 0; c < CPL; c++) o.v[c] = bias ? s[c] + bias[e + c] : s[c];
+        *(V *)(logits + (size_t)t * E + e) = o;
     }
 }
 
@@ -905,12 +911,24 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     const int rthreads = E <= 64 ? 64 : E <= 128 ? 128 : 256;
     // The tiled chains for more than one token; one workgroup per token else.
     const bool tiled = T > 1 && E == RL_E && d % RL_I == 0 && d / RL_I >= RL_NS - 1;
-    const size_t rsh = (size_t)(E + (tiled ? 0 : d)) * sizeof(float);
+    // chains per lane of the batched router: the most that still gives every
+    // CU a workgroup
+    const int ntg = (T + RW_T - 1) / RW_T;
+    const int cpl = ntg * (E / 16) >= 256 && E % 16 == 0 ? 4
+                    : ntg * (E / 8) >= 256 && E % 8 == 0 ? 2
+                                                          : 1;
+    const bool wide = T > 1 && d % RW_I == 0 && E % (4 * cpl) == 0;
+    const bool have_logits = wide || tiled;
+    const size_t rsh = (size_t)(E + (have_logits ? 0 : d)) * sizeof(float);
     slot = mhip::stage_begin(c, MHIP_STAGE_ROUTER);
-    const bool wide = tiled && T >= 2048 && d % RW_I == 0 && E % RW_E == 0;
     if (wide) {
-        k_router_logits_wide<<<dim3((T + RW_T - 1) / RW_T, E / RW_E), 256, 0, st>>>(
-            sc->xn, d_router_t, d_bias, sc->logits, T, d, E);
+        const dim3 g(ntg, E / (4 * cpl));
+        if (cpl == 4)
+            k_router_logits_wide<4><<<g, 256, 0, st>>>(sc->xn, d_router_t, d_bias, sc->logits, T, d, E);
+        else if (cpl == 2)
+            k_router_logits_wide<2><<<g, 256, 0, st>>>(sc->xn, d_router_t, d_bias, sc->logits, T, d, E);
+        else
+            k_router_logits_wide<1><<<g, 256, 0, st>>>(sc->xn, d_router_t, d_bias, sc->logits, T, d, E);
     } else if (tiled) {
         const int C = T >= 4096 ? 4 : T >= 2048 ? 2 : 1;
         const size_t lsh = router_logits_lds(C, d);
@@ -930,7 +948,7 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
             k_router_logits<1><<<(T + 1) / 2, 256, lsh, st>>>(sc->xn, d_router_t, d_bias, sc->logits, T, d);
     }
     k_router<<<T, rthreads, rsh, st>>>(sc->xn, d_router_t, d_bias, sc->logits, sc->idx, sc->w, d,
-                                       E, K, s->norm_topk, tiled ? 1 : 0);
+                                       E, K, s->norm_topk, have_logits ? 1 : 0);
     mhip::stage_end(c, slot);
     if (mhip::check_launch(c, "router")) return -1;
 
