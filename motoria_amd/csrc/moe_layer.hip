@@ -473,27 +473,68 @@ __global__ __launch_bounds__(64 * DWG) void k_disp_count(const int *__restrict__
         for (int e = lane; e < E; e += 64) hist[(size_t)e * nch + ch] = c[e];
 }
 
-// counts, offsets, groups and gtile from the expert totals (one thread).
-__device__ void disp_groups(int E, const int *tot, int *counts, int *offsets, int *groups,
-                            int *gtile, int tm) {
-    int acc = 0, g = 0, tiles = 0;
-    for (int x = 0; x < E; x++) {
-        const int n = tot[x];
-        counts[x] = n;
-        offsets[x] = acc;
-        if (n > 0) {
-            groups[1 + 3 * g] = x;
-            groups[2 + 3 * g] = acc;
-            groups[3 + 3 * g] = acc + n;
-            gtile[g] = tiles;
-            tiles += (n + tm - 1) / tm;
-            g++;
+// The dispatch tables (counts, offsets[E+1], the list of non-empty experts as
+// (expert, begin, end) groups and gtile[g], the number of tm-row tiles before
+// group g) from parallel scans: every thread of the workgroup calls
+// (blockDim >= 256, E <= 256); thread x < E owns expert x. Three exclusive
+// scans over the experts (rows, non-empty experts, tiles) give each
+// expert's offset, its group number and its first tile. off[E] (LDS)
+// receives the offsets; with write_tables the global tables are written too.
+// sc: 12 ints of LDS.
+__device__ void disp_tables(int E, const int *tot, int *off, int *sc, bool write_tables,
+                            int *counts, int *offsets, int *groups, int *gtile, int tm) {
+    const int x = threadIdx.x, lane = x & 63, w = x >> 6;
+    const bool in = x < E;
+    const int n = in ? tot[x] : 0;
+    const int ne = n > 0 ? 1 : 0, nt = (n + tm - 1) / tm;
+    int a = n, b = ne, c = nt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int ua = __shfl_up(a, o), ub = __shfl_up(b, o), uc = __shfl_up(c, o);
+        if (lane >= o) {
+            a += ua;
+            b += ub;
+            c += uc;
         }
-        acc += n;
     }
-    offsets[E] = acc;
-    groups[0] = g;
-    gtile[g] = tiles;
+    if (w < 4 && lane == 63) {
+        sc[w] = a;
+        sc[4 + w] = b;
+        sc[8 + w] = c;
+    }
+    __syncthreads();
+    int pa = 0, pb = 0, pc = 0, ta = 0, tb = 0, tc = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        if (k < w) {
+            pa += sc[k];
+            pb += sc[4 + k];
+            pc += sc[8 + k];
+        }
+        ta += sc[k];
+        tb += sc[4 + k];
+        tc += sc[8 + k];
+    }
+    if (in) {
+        const int ea = pa + a - n, eb = pb + b - ne, ec = pc + c - nt;
+        off[x] = ea;
+        if (write_tables) {
+            counts[x] = n;
+            offsets[x] = ea;
+            if (ne) {
+                groups[1 + 3 * eb] = x;
+                groups[2 + 3 * eb] = ea;
+                groups[3 + 3 * eb] = ea + n;
+                gtile[eb] = ec;
+            }
+        }
+    }
+    if (write_tables && x == 0) {
+        offsets[E] = ta;
+        groups[0] = tb;
+        gtile[tb] = tc;
+    }
+    __syncthreads();
 }
 
 // Workgroup e: exclusive prefix of expert e's counts over the chunks, in
@@ -542,18 +583,11 @@ __global__ __launch_bounds__(64 * DWG) void k_disp_scatter(const int *__restrict
     int *base = lds_s;                 // [DWG][E]: next position of each expert
     int *tot = lds_s + DWG * E;        // [E]
     int *off = tot + E;                // [E]
+    int *sc = off + E;                 // [12]
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     for (int e = threadIdx.x; e < E; e += blockDim.x) tot[e] = counts[e];
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int acc = 0;
-        for (int e = 0; e < E; e++) {
-            off[e] = acc;
-            acc += tot[e];
-        }
-        if (blockIdx.x == 0) disp_groups(E, tot, counts, offsets, groups, gtile, tm);
-    }
-    __syncthreads();
+    disp_tables(E, tot, off, sc, blockIdx.x == 0, counts, offsets, groups, gtile, tm);
     const int ch = blockIdx.x * DWG + w;
     if (ch >= nch) return;  // a whole wavefront: no workgroup barrier follows
     int *bs = base + w * E;
@@ -577,7 +611,8 @@ __global__ __launch_bounds__(64 * DSMALL) void k_disp_small(const int *__restric
     extern __shared__ int lds_i[];
     int *hist = lds_i;                 // [DSMALL][E]
     int *tot = lds_i + DSMALL * E;     // [E]
-    int *off = tot + E;                // [E + 1]
+    int *off = tot + E;                // [E]
+    int *sc = off + E;                 // [12]
     const int w = threadIdx.x >> 6;
     for (int i = threadIdx.x; i < DSMALL * E; i += blockDim.x) hist[i] = 0;
     __syncthreads();
@@ -593,15 +628,7 @@ __global__ __launch_bounds__(64 * DSMALL) void k_disp_small(const int *__restric
         tot[e] = run;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        disp_groups(E, tot, counts, offsets, groups, gtile, tm);
-        int acc = 0;
-        for (int e = 0; e < E; e++) {
-            off[e] = acc;
-            acc += tot[e];
-        }
-    }
-    __syncthreads();
+    disp_tables(E, tot, off, sc, true, counts, offsets, groups, gtile, tm);
     if (w < nch) {
         int *bs = hist + w * E;
         for (int e = threadIdx.x & 63; e < E; e += 64) bs[e] += off[e];
@@ -961,13 +988,13 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     int *dhist = (int *)sc->tmp;
     slot = mhip::stage_begin(c, MHIP_STAGE_DISPATCH);
     if (nch <= DSMALL) {
-        k_disp_small<<<1, 64 * DSMALL, (DSMALL * E + 2 * E + 1) * 4, st>>>(
+        k_disp_small<<<1, 64 * DSMALL, (DSMALL * E + 2 * E + 12) * 4, st>>>(
             sc->idx, A, E, nch, bits, sc->counts, sc->offsets, sc->perm, sc->pos, sc->groups,
             sc->gtile, MHIP_GEMM_TM, sc->status);
     } else {
         k_disp_count<<<dgrid, 64 * DWG, DWG * E * 4, st>>>(sc->idx, A, E, nch, dhist, sc->status);
         k_disp_scan<<<E, 256, 0, st>>>(nch, dhist, sc->counts);
-        k_disp_scatter<<<dgrid, 64 * DWG, (DWG + 2) * E * 4, st>>>(
+        k_disp_scatter<<<dgrid, 64 * DWG, ((DWG + 2) * E + 12) * 4, st>>>(
             sc->idx, A, E, nch, bits, dhist, sc->counts, sc->offsets, sc->groups, sc->gtile,
             MHIP_GEMM_TM, sc->perm, sc->pos, sc->status);
     }
