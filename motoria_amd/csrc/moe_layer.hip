@@ -638,14 +638,26 @@ __global__ __launch_bounds__(64 * DSMALL) void k_disp_small(const int *__restric
 }
 
 // ---- gate/up + SwiGLU --------------------------------------------------------
+
+// Float offset of k_gateup's staged codes in its LDS (16-byte aligned) and
+// the kernel's LDS bytes.
+__host__ __device__ inline int gateup_xq_off(int d, int R) {
+    const int nb = d / QK;
+    const int f = TB * 2 * R * (nb + 1) + TB * 2 * R + TB * nb + TB;
+    return (f + 3) / 4 * 4;
+}
+inline size_t gateup_lds(int d, int R) { return (size_t)gateup_xq_off(d, R) * 4 + (size_t)TB * d; }
+
 //
 // Workgroup = (group g of one expert, R consecutive rows of h). Its 2R weight
 // rows (R of gate, R of up) are split into (row, 32-block) pairs, one pair
 // per thread per step, codes held in registers across the expert's tokens.
-// For TB tokens at a time each pair's exact int32 dot is turned into the
-// reference's term ((float)acc*d_w)*d_x and parked in LDS; then one thread
-// per (token, row) adds its row's terms in block order, and SwiGLU
-// g/(1+expf(-g))*u (forward.c:190) produces h, written in bucketed order.
+// For TB tokens at a time the tokens' Q8(xn) rows and scales are staged in
+// LDS (one round of independent loads), each pair's exact int32 dot is
+// turned into the reference's term ((float)acc*d_w)*d_x and parked in LDS;
+// then one thread per (token, row) adds its row's terms in block order, and
+// SwiGLU g/(1+expf(-g))*u (forward.c:190) produces h, written in bucketed
+// order.
 template <int PK>
 __global__ __launch_bounds__(NT) void k_gateup(const uint8_t *__restrict__ table, mhip_layout lay,
                                                const int8_t *__restrict__ xq,
@@ -654,7 +666,9 @@ __global__ __launch_bounds__(NT) void k_gateup(const uint8_t *__restrict__ table
                                                const int *__restrict__ perm,
                                                float *__restrict__ h, int d, int eh, int K,
                                                int R) {
-    extern __shared__ float terms[];  // [TB][2R][nb+1], then gu[TB][2R]
+    // [TB][2R][nb+1] terms, gu[TB][2R], xs_l[TB][nb], tk[TB], then (16-byte
+    // aligned) xq_l[TB][d] codes
+    extern __shared__ float terms[];
     const int nb = d / QK;
     const int nrc = eh / R;
     const int g = blockIdx.x / nrc;
@@ -665,6 +679,9 @@ __global__ __launch_bounds__(NT) void k_gateup(const uint8_t *__restrict__ table
     const int P = 2 * R * nb;
     const int ld = nb + 1;
     float *gu = terms + TB * 2 * R * ld;
+    float *xs_l = gu + TB * 2 * R;
+    int *tk = (int *)(xs_l + TB * nb);
+    int8_t *xq_l = (int8_t *)(terms + gateup_xq_off(d, R));
 
     int4 wc0[PK], wc1[PK];
     float wd[PK];
@@ -688,15 +705,23 @@ __global__ __launch_bounds__(NT) void k_gateup(const uint8_t *__restrict__ table
     }
     for (int base = b0; base < b1; base += TB) {
         const int ntok = b1 - base < TB ? b1 - base : TB;
+        if (threadIdx.x < ntok) tk[threadIdx.x] = perm[base + threadIdx.x] / K;
+        __syncthreads();
+        const int nq = d / 16;
+        for (int c = threadIdx.x; c < ntok * nq; c += NT)
+            ((int4 *)(xq_l + (size_t)(c / nq) * d))[c % nq] =
+                ((const int4 *)(xq + (size_t)tk[c / nq] * d))[c % nq];
+        for (int c = threadIdx.x; c < ntok * nb; c += NT)
+            xs_l[c] = xs[(size_t)tk[c / nb] * nb + c % nb];
+        __syncthreads();
 #pragma unroll
         for (int k = 0; k < PK; k++) {
             if (prow[k] < 0) continue;
             for (int tb = 0; tb < ntok; tb++) {
-                const int t = perm[base + tb] / K;
-                const int4 *xv = (const int4 *)(xq + (size_t)t * d + (size_t)pblk[k] * QK);
+                const int4 *xv = (const int4 *)(xq_l + (size_t)tb * d + (size_t)pblk[k] * QK);
                 const int acc = mhip_dev::dot32_i8(wc0[k], wc1[k], xv[0], xv[1]);
                 terms[(tb * 2 * R + prow[k]) * ld + pblk[k]] =
-                    mhip_dev::block_term(acc, wd[k], xs[(size_t)t * nb + pblk[k]]);
+                    mhip_dev::block_term(acc, wd[k], xs_l[tb * nb + pblk[k]]);
             }
         }
         __syncthreads();
@@ -1019,7 +1044,7 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
 
     const int G = A < E ? A : E;  // at most this many non-empty experts
     const int Rg = rows_gateup(nb);
-    const size_t gsh = ((size_t)TB * 2 * Rg * (nb + 1) + (size_t)TB * 2 * Rg) * sizeof(float);
+    const size_t gsh = gateup_lds(d, Rg);
     slot = mhip::stage_begin(c, MHIP_STAGE_GATEUP);
     k_gateup<PK><<<(unsigned)G * (eh / Rg), NT, gsh, st>>>(
         (const uint8_t *)d_table_layer, *lay, sc->xq, sc->xs, sc->groups, sc->perm, sc->h, d, eh,
