@@ -133,6 +133,8 @@ typedef struct {
     void *hdq;        /* [T*K][eh] fp16: d_h * q_h of Q8(h), bucketed (matrix-core path) */
     int *gtile;       /* [E+1]     tiles of MHIP_GEMM_TM rows before each group */
     float *xsb;       /* [d/32][T*K] Q8 scales of xn per assignment, bucketed (matrix-core path) */
+    int8_t *hq;       /* [T*K][eh] Q8 codes of h, bucketed (vector path) */
+    float *hs;        /* [T*K][eh/32] Q8 scales of h, bucketed (vector path) */
 } mhip_scratch;
 
 /* Rows of one expert bucket per matrix-core tile. */

@@ -743,15 +743,55 @@ __global__ __launch_bounds__(NT) void k_gateup(const uint8_t *__restrict__ table
     }
 }
 
+// ---- Q8(h) -----------------------------------------------------------------------
+//
+// One thread per 32-block of h (quant.c:11-27), once per assignment row:
+// codes to hq, scales to hs, both in bucketed order.
+__global__ __launch_bounds__(256) void k_quant_h(const float *__restrict__ h,
+                                                 int8_t *__restrict__ hq,
+                                                 float *__restrict__ hs, int nblocks) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const float4 *v4 = (const float4 *)(h + (size_t)b * QK);
+    float v[QK];
+#pragma unroll
+    for (int i = 0; i < QK / 4; i++) {
+        const float4 f = v4[i];
+        v[4 * i] = f.x;
+        v[4 * i + 1] = f.y;
+        v[4 * i + 2] = f.z;
+        v[4 * i + 3] = f.w;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < QK; i++) {
+        const float a = fabsf(v[i]);
+        amax = a > amax ? a : amax;
+    }
+    const float dsc = amax / 127.0f;
+    const float qi = dsc != 0.0f ? 1.0f / dsc : 0.0f;
+    union {
+        int8_t c[QK];
+        int4 q[2];
+    } out;
+#pragma unroll
+    for (int i = 0; i < QK; i++) out.c[i] = (int8_t)roundf(v[i] * qi);
+    int4 *dst = (int4 *)(hq + (size_t)b * QK);
+    dst[0] = out.q[0];
+    dst[1] = out.q[1];
+    hs[b] = dsc;
+}
+
 // ---- down ----------------------------------------------------------------------
 //
-// Workgroup = (group g, R rows of down). For TB tokens at a time, h is
-// quantized (one thread per 32-block, quant.c:11-27) into LDS, the
-// (row, block) pairs produce the reference's terms, and one thread per
-// (token, row) sums them in block order into tmp (bucketed order).
+// Workgroup = (group g, R rows of down). For TB tokens at a time the rows'
+// Q8(h) codes and scales (k_quant_h) are staged in LDS, the (row, block)
+// pairs produce the reference's terms, and one thread per (token, row) sums
+// them in block order into tmp (bucketed order).
 template <int PK>
 __global__ __launch_bounds__(NT) void k_down(const uint8_t *__restrict__ table, mhip_layout lay,
-                                             const float *__restrict__ h,
+                                             const int8_t *__restrict__ hq_g,
+                                             const float *__restrict__ hs_g,
                                              const int *__restrict__ groups,
                                              float *__restrict__ tmp, int d, int eh, int R) {
     extern __shared__ float terms[];  // [TB][R][nbh+1], hs[TB][nbh], hq[TB][eh] bytes
@@ -786,31 +826,11 @@ __global__ __launch_bounds__(NT) void k_down(const uint8_t *__restrict__ table, 
     }
     for (int base = b0; base < b1; base += TB) {
         const int ntok = b1 - base < TB ? b1 - base : TB;
-        for (int c = threadIdx.x; c < ntok * nbh; c += NT) {
-            const int tb = c / nbh, blk = c % nbh;
-            const float *v = h + (size_t)(base + tb) * eh + (size_t)blk * QK;
-            float vals[QK];
-            float amax = 0.0f;
-#pragma unroll
-            for (int i = 0; i < QK; i += 4) {
-                const float4 f = *(const float4 *)(v + i);
-                vals[i] = f.x;
-                vals[i + 1] = f.y;
-                vals[i + 2] = f.z;
-                vals[i + 3] = f.w;
-            }
-#pragma unroll
-            for (int i = 0; i < QK; i++) {
-                const float a = fabsf(vals[i]);
-                amax = a > amax ? a : amax;
-            }
-            const float dsc = amax / 127.0f;
-            const float qi = dsc != 0.0f ? 1.0f / dsc : 0.0f;
-            int8_t *dst = hq + (size_t)tb * eh + (size_t)blk * QK;
-#pragma unroll
-            for (int i = 0; i < QK; i++) dst[i] = (int8_t)roundf(vals[i] * qi);
-            hs[tb * nbh + blk] = dsc;
-        }
+        // the bucket's rows base .. base + ntok - 1 are contiguous
+        const int nq = ntok * eh / 16;
+        for (int c = threadIdx.x; c < nq; c += NT)
+            ((int4 *)hq)[c] = ((const int4 *)(hq_g + (size_t)base * eh))[c];
+        for (int c = threadIdx.x; c < ntok * nbh; c += NT) hs[c] = hs_g[(size_t)base * nbh + c];
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < PK; k++) {
@@ -907,6 +927,8 @@ size_t mhip_scratch_bytes(const mhip_dims *s, int T) {
     n += align256(A * eh * 2);         // hdq
     n += align256((E + 1) * 4);        // gtile
     n += align256(A * (d / QK) * 4);   // xsb
+    n += align256(A * eh);             // hq
+    n += align256(A * (eh / QK) * 4);  // hs
     return n;
 }
 
@@ -937,6 +959,8 @@ int mhip_scratch_carve(const mhip_dims *s, int T, void *d_base, mhip_scratch *o)
     o->hdq = take(A * eh * 2);
     o->gtile = (int *)take((E + 1) * 4);
     o->xsb = (float *)take(A * (d / QK) * 4);
+    o->hq = (int8_t *)take(A * eh);
+    o->hs = (float *)take(A * (eh / QK) * 4);
     return 0;
 }
 
@@ -1056,8 +1080,11 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     const size_t dsh2 = ((size_t)TB * Rd * (nbh + 1) + (size_t)TB * nbh) * sizeof(float) +
                         (size_t)TB * eh;
     slot = mhip::stage_begin(c, MHIP_STAGE_DOWN);
+    const int nbq = A * nbh;
+    k_quant_h<<<(nbq + 255) / 256, 256, 0, st>>>(sc->h, sc->hq, sc->hs, nbq);
     k_down<PK><<<(unsigned)G * (d / Rd), NT, dsh2, st>>>((const uint8_t *)d_table_layer, *lay,
-                                                         sc->h, sc->groups, sc->tmp, d, eh, Rd);
+                                                         sc->hq, sc->hs, sc->groups, sc->tmp, d,
+                                                         eh, Rd);
     mhip::stage_end(c, slot);
     if (mhip::check_launch(c, "down")) return -1;
 
