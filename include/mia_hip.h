@@ -159,10 +159,12 @@ int mhip_scratch_carve(const mhip_dims *s, int max_tokens, void *d_base,
  * Routing (indices, order, gate weights) is bit-equal to the reference at
  * every T. The expert products are bit-equal too for small batches; from
  * MHIP_GEMM_MIN_A assignments on (and when the shape allows: d a multiple of
- * 128, expert_hidden of 64) they run on the matrix cores: gate/up, SwiGLU
- * and Q8(h) stay bit-equal, the down product takes fp16 operands and is
- * within ~1e-4 relative of the reference. MHIP_EXACT_EXPERTS keeps the
- * bit-exact down product at every T.
+ * 256, expert_hidden of 128) they run on the matrix cores: the gate/up block
+ * dots stay exact and each block term is added with one fused multiply-add
+ * (h within a few fp32 ulps of the reference's), the down product takes fp16
+ * operands; the layer output stays within 1e-3 relative of the reference
+ * (max|diff| / max|ref|, measured <= 5.5e-4 on the update). MHIP_EXACT_EXPERTS
+ * keeps the bit-exact vector path at every T.
  */
 #define MHIP_GEMM_MIN_A 2048
 int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
