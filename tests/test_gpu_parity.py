@@ -234,40 +234,54 @@ def test_layer_skewed_2048(oracle, qwen_dims, qwen_moe):
     assert 0.35 < share4 < 0.5 and 20 <= zero <= 40
 
 
-def test_layer_prefill_4096_routing_and_sample(oracle, qwen_dims):
-    """T=4096, the prefill benchmark shape (matrix-core experts, tokens-across-
-    lanes router): every token's logits, expert indices and gate weights
-    bit-equal to the oracle's (rmsnorm, router chain and routing per token),
-    and the layer output of a seeded sample of 96 tokens within TOL (the
-    oracle's layer is per token, so the sample checks the full-size launch)."""
-    say("test_layer_prefill_4096_routing_and_sample")
-    d = qwen_dims
-    T = 4096
+def _routing_and_sample(oracle, d, T, seed, bias=None, nsample=96):
+    """One matrix-core layer at T tokens on a fresh one-layer handle: every
+    token's logits, expert indices and gate weights bit-equal to the oracle's
+    (rmsnorm, router chain and routing per token), and the layer output of a
+    seeded sample of tokens within TOL (the oracle's layer is per token, so
+    the sample checks the full-size launch)."""
     moe = M.Moe(n_layers=1, max_tokens=T, device=0, **W.SHAPE)
     try:
         moe.synth(W.WEIGHT_SEED)
         moe.sync()
-        x = oracle.synth_x(W.X_SEED + 11, T, d.dim)
+        x = oracle.synth_x(seed, T, d.dim)
         router = oracle.synth_router(W.WEIGHT_SEED, 0, d)
-        xm, im, wm, lm = _gpu_layer(moe, 0, x, None, 0)
+        xm, im, wm, lm = _gpu_layer(moe, 0, x, bias, 0)
         norm = np.ones(d.dim, np.float32)
         for t in range(T):
             xn = oracle.rmsnorm(x[t], norm, d.norm_eps)
             lo = oracle.matvec(router, 0, xn, d.n_experts, d.dim)
+            if bias is not None:
+                lo = (lo + bias).astype(np.float32)
             io, wo, _ = oracle.route(lo, d.n_active, d.norm_topk)
             assert np.array_equal(bits(lm[t]), bits(lo)), "token %d logits" % t
             assert np.array_equal(im[t], io), "token %d expert indices" % t
             assert np.array_equal(bits(wm[t]), bits(wo)), "token %d gate weights" % t
-        sample = np.sort(np.random.default_rng(5).choice(T, 96, replace=False))
+        sample = np.sort(np.random.default_rng(5).choice(T, nsample, replace=False))
         xs = x[sample]
-        xo, io, _, _, _ = oracle_layer(oracle, moe, d, 0, xs, router,
+        xo, io, _, _, _ = oracle_layer(oracle, moe, d, 0, xs, router, bias=bias,
                                        need=im[sample].ravel().tolist())
         assert np.array_equal(im[sample], io)
         e_delta, e_out = rel_err(xm[sample] - xs, xo - xs), rel_err(xm[sample], xo)
-        say("  sample of 96: rel err update %.3e, output %.3e" % (e_delta, e_out))
+        say("  sample of %d: rel err update %.3e, output %.3e" % (nsample, e_delta, e_out))
         assert e_delta <= TOL and e_out <= TOL
     finally:
         moe.close()
+
+
+def test_layer_prefill_4096_routing_and_sample(oracle, qwen_dims):
+    """T=4096, the prefill benchmark shape (matrix-core experts, four router
+    chains per lane)."""
+    say("test_layer_prefill_4096_routing_and_sample")
+    _routing_and_sample(oracle, qwen_dims, 4096, W.X_SEED + 11)
+
+
+def test_layer_ragged_2111_with_bias(oracle, qwen_dims):
+    """T=2111: the last 64-token router group and the last bucket tiles are
+    partial, four router chains per lane, with the skewed logit bias."""
+    say("test_layer_ragged_2111_with_bias")
+    _routing_and_sample(oracle, qwen_dims, 2111, W.X_SEED + 13,
+                        bias=W.zipf_bias(qwen_dims.n_experts), nsample=64)
 
 
 def test_matrix_path_ragged_buckets(oracle, qwen_dims, qwen_moe):
