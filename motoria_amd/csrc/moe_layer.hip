@@ -1,11 +1,13 @@
 // One Qwen3-MoE FFN layer over T tokens on the resident expert table:
 //
-//   k_rmsnorm_q8   rmsnorm + Q8_0 quantization of xn      forward.c:174, quant.c:11-27
-//   k_router       logits, softmax, top-K, gate weights  forward.c:175-181
-//   k_dispatch     stable bucketing of the T*K assignments by expert
-//   k_gateup       gate/up Q8 products + SwiGLU          forward.c:186-191
-//   k_down         Q8(h) + down Q8 product               forward.c:192-193
-//   k_combine      x += w_j * tmp_j, j in top-K order    forward.c:194
+//   k_rmsnorm_q8          rmsnorm + Q8_0 quantization of xn      forward.c:174, quant.c:11-27
+//   k_router_logits_wide  router chains for T > 1 (tokens across the lanes)
+//   k_router              softmax, top-K, gate weights (and the chains at T = 1)
+//                                                                 forward.c:175-181
+//   k_disp_*              stable bucketing of the T*K assignments by expert
+//   k_gateup              gate/up Q8 products + SwiGLU          forward.c:186-191
+//   k_quant_h, k_down     Q8(h) + down Q8 product               forward.c:192-193
+//   k_combine             x += w_j * tmp_j, j in top-K order    forward.c:194
 //
 // Every fp32 value is produced in the reference's operation order, so the
 // results are bit-equal to the reference C path (src/model/forward.c:167-197
@@ -13,8 +15,9 @@
 // run in block order, and sums the reference takes in double are either
 // reproduced exactly or certified (see k_rmsnorm_q8). For large batches the
 // gate/up and down stages switch to the matrix-core kernels of moe_gemm.hip
-// (gate/up and h still bit-exact, down within ~1e-4 of the reference);
-// routing and dispatch stay bit-exact.
+// (exact block dots with a fused block term for gate/up, fp16 operands for
+// down; the layer within 1e-3 of the reference); routing and dispatch stay
+// bit-exact.
 #include "mhip_internal.h"
 
 namespace {
