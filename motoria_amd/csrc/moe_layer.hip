@@ -104,8 +104,9 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_q8(const float *__restrict__ x,
 // the largest untaken probability, lowest index on ties; the gate weights
 // are renormalised as forward.c:178-181.
 //
-// With have_logits set, the logits (bias included) were already computed by
-// k_router_logits and only the selection runs.
+// With have_logits set (every shape with d % 64 == 0 and E % 4 == 0), the
+// logits (bias included) were already computed by k_router_logits_wide (or
+// k_router_logits) and only the selection runs.
 __global__ __launch_bounds__(256) void k_router(const float *__restrict__ xn,
                                                 const float *__restrict__ wt,
                                                 const float *__restrict__ bias,
@@ -996,7 +997,7 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     const int cpl = ntg * (E / 16) >= 256 && E % 16 == 0 ? 4
                     : ntg * (E / 8) >= 256 && E % 8 == 0 ? 2
                                                           : 1;
-    const bool wide = T > 1 && d % RW_I == 0 && E % (4 * cpl) == 0;
+    const bool wide = d % RW_I == 0 && E % (4 * cpl) == 0;
     const bool have_logits = wide || tiled;
     const size_t rsh = (size_t)(E + (have_logits ? 0 : d)) * sizeof(float);
     slot = mhip::stage_begin(c, MHIP_STAGE_ROUTER);
