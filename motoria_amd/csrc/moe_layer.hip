@@ -305,8 +305,8 @@ size_t router_logits_lds(int C, int d) {
 // router value is a wavefront-wide broadcast. xn (transposed, rows padded to
 // 65 floats so the transposing stores and the row reads are conflict-free)
 // and the router rows go through LDS in chunks of RW_I values of i,
-// double-buffered through registers. CPL trades chains per lane (latency
-// hiding) against workgroups (CPL = 1 for a few tokens). Needs d % RW_I == 0
+// double-buffered in LDS and 4 / CPL chunks ahead in registers. CPL trades
+// chains per lane against workgroups (CPL = 1 for a few tokens). Needs d % RW_I == 0
 // and E % (4 CPL) == 0.
 constexpr int RW_T = 64, RW_I = 64;
 
@@ -322,6 +322,9 @@ __global__ __launch_bounds__(256, 2) void k_router_logits_wide(const float *__re
                                                                float *__restrict__ logits, int T,
                                                                int d, int E) {
     typedef RwVec<CPL> V;
+    // chunks in flight in registers: a chunk's compute shrinks with CPL, so
+    // fewer chains per lane prefetch further ahead
+    constexpr int NP = 4 / CPL;
     __shared__ float Xs[2][RW_I][RW_T + 1];
     __shared__ V Ws[2][RW_I][4];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -332,45 +335,54 @@ __global__ __launch_bounds__(256, 2) void k_router_logits_wide(const float *__re
     const int tt = tid >> 2, q = tid & 3;
     const float *xsrc = xn + (size_t)min(t0 + tt, T - 1) * d + 16 * q;
     const float *wsrc = wt + (size_t)(tid >> 2) * E + e0 + CPL * (tid & 3);
-    float4 xr[4];
-    V wr;
-    auto gload = [&](int ch) {
+    float4 xr[NP][4];
+    V wr[NP];
+    auto gload = [&](int ch, int sl) {
         const int i0 = ch * RW_I;
 #pragma unroll
-        for (int k = 0; k < 4; k++) xr[k] = *(const float4 *)(xsrc + i0 + 4 * k);
-        wr = *(const V *)(wsrc + (size_t)i0 * E);
+        for (int k = 0; k < 4; k++) xr[sl][k] = *(const float4 *)(xsrc + i0 + 4 * k);
+        wr[sl] = *(const V *)(wsrc + (size_t)i0 * E);
     };
-    auto lstore = [&](int b) {
+    auto lstore = [&](int sl, int b) {
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            Xs[b][16 * q + 4 * k + 0][tt] = xr[k].x;
-            Xs[b][16 * q + 4 * k + 1][tt] = xr[k].y;
-            Xs[b][16 * q + 4 * k + 2][tt] = xr[k].z;
-            Xs[b][16 * q + 4 * k + 3][tt] = xr[k].w;
+            Xs[b][16 * q + 4 * k + 0][tt] = xr[sl][k].x;
+            Xs[b][16 * q + 4 * k + 1][tt] = xr[sl][k].y;
+            Xs[b][16 * q + 4 * k + 2][tt] = xr[sl][k].z;
+            Xs[b][16 * q + 4 * k + 3][tt] = xr[sl][k].w;
         }
-        Ws[b][tid >> 2][tid & 3] = wr;
+        Ws[b][tid >> 2][tid & 3] = wr[sl];
     };
     float s[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; c++) s[c] = 0.0f;
     const int nch = d / RW_I;
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int ch = 0; ch < nch; ch++) {
-        const int b = ch & 1;
-        if (ch + 1 < nch) gload(ch + 1);
-#pragma unroll 16
-        for (int ii = 0; ii < RW_I; ii++) {
-            const float x = Xs[b][ii][lane];
-            const V w = Ws[b][ii][wave];
+    // chunk c travels in register slot c % NP, then LDS buffer c & 1
+    gload(0, 0);
+    lstore(0, 0);
 #pragma unroll
-            for (int c = 0; c < CPL; c++) s[c] = s[c] + w.v[c] * x;
+    for (int p = 1; p <= NP; p++)
+        if (p < nch) gload(p, p % NP);
+    __syncthreads();
+    for (int ch = 0; ch < nch; ch += NP) {
+#pragma unroll
+        for (int u = 0; u < NP; u++) {
+            const int c = ch + u;
+            if (c >= nch) break;
+            const int b = c & 1;
+#pragma unroll 16
+            for (int ii = 0; ii < RW_I; ii++) {
+                const float x = Xs[b][ii][lane];
+                const V w = Ws[b][ii][wave];
+#pragma unroll
+                for (int k = 0; k < CPL; k++) s[k] = s[k] + w.v[k] * x;
+            }
+            // buffer b ^ 1 was last read in chunk c - 1, before the barrier
+            // that ended it; slot (u + 1) % NP then takes chunk c + 1 + NP
+            if (c + 1 < nch) lstore((u + 1) % NP, b ^ 1);
+            if (c + 1 + NP < nch) gload(c + 1 + NP, (u + 1) % NP);
+            __syncthreads();
         }
-        // buffer b ^ 1 was last read in the previous chunk, before the
-        // barrier that ended it
-        if (ch + 1 < nch) lstore(b ^ 1);
-        __syncthreads();
     }
     const int t = t0 + lane;
     if (t < T) {
