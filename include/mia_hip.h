@@ -152,7 +152,8 @@ int mhip_scratch_carve(const mhip_dims *s, int max_tokens, void *d_base,
 
 /*
  * One MoE layer (rmsnorm -> router/top-K -> dispatch -> gate/up+SwiGLU ->
- * down -> combine) in place on d_x[T][d]. d_table/d_router_t/d_norm point to
+ * down -> combine) in place on d_x[T][d] (16-byte aligned, as every
+ * mhip_malloc pointer is). d_table/d_router_t/d_norm point to
  * this layer's experts, transposed router and ffn_norm. d_bias (E floats) is
  * added to the logits when non-NULL.
  *

@@ -988,6 +988,7 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     const int d = s->dim, E = s->n_experts, K = s->n_active, eh = s->expert_hidden;
     const int A = T * K;
     if (A > 65535) return mhip::fail(c, "T*K=%d exceeds 65535 assignments", A);
+    if ((uintptr_t)d_x % 16) return mhip::fail(c, "d_x is not 16-byte aligned");
     const int nb = d / QK, nbh = eh / QK;
     hipStream_t st = c->stream;
     const bool mfma = !(flags & MHIP_EXACT_EXPERTS) && A >= MHIP_GEMM_MIN_A &&
