@@ -69,7 +69,7 @@ struct alignas(16) Step {
     _Float16 x[TM][KB];  // 8 KB
     int8_t w[TN][KB];    // 8 KB
     float sw[TN];        // 1 KB
-    float sx[TM];        // 512 B
+    float sx[TM];        // 512 B: the scale of bucket row 16 j + l at 8 l + j
 };
 static_assert(sizeof(Step) == 17920, "step layout");
 
@@ -253,6 +253,8 @@ __device__ __forceinline__ void gemm_tile(Step *ring, const Src &src, int nk, f4
             // terms of tile j are added, so the vector ALUs never wait for
             // the product they consume.
             const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};
+            // x scales of this lane's assignment rows 16 j + l16, j < 8
+            const f4v sxa = *(const f4v *)&S.sx[8 * l16], sxb = *(const f4v *)&S.sx[8 * l16 + 4];
             f4v blk[2][MI];
             {
                 const h8 bv = *(const h8 *)&S.x[l16][8 * xslot(l16, c)];
@@ -270,7 +272,7 @@ __device__ __forceinline__ void gemm_tile(Step *ring, const Src &src, int nk, f4
                         blk[(j + 1) & 1][i] =
                             __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv, z, 0, 0, 0);
                 }
-                const float sx = S.sx[16 * j + l16];
+                const float sx = j < 4 ? sxa[j & 3] : sxb[j & 3];
 #pragma unroll
                 for (int i = 0; i < MI; i++)
 #pragma unroll
@@ -357,7 +359,11 @@ __global__ __launch_bounds__(GT, 2) void k_gateup_mfma(
             src.sw = (const float *)(ex + (lane < WN / 2 ? lay.gate_st : lay.up_st)) + hc;
             src.swstep = eh;
         }
-        src.sx = xsb + base + min(32 * wave + (lane & 31), nrows - 1);
+        {
+            // sx slot p = 32 wave + lane holds bucket row 16 (p % 8) + p / 8
+            const int p = 32 * wave + (lane & 31);
+            src.sx = xsb + base + min(16 * (p & 7) + (p >> 3), nrows - 1);
+        }
         src.sxstep = A;
     }
 
