@@ -8,7 +8,8 @@
  * mia_model_step (src/model/forward.c:210-213), with experts fetched through
  * an LRU cache fed by the mia_expert_loader port. Here the layer is public,
  * takes T tokens at once, and reads every expert of every layer from one
- * HBM-resident table (48 x 128 Q8_0 experts of Qwen3-30B-A3B = 30.4 GiB).
+ * HBM-resident table (48 x 128 Q8_0 experts of Qwen3-30B-A3B, 36.2 GB with the
+ * block-major scale copies).
  *
  * Conventions follow the reference engine: C99, functions return 0 or -1
  * (with a message in mia_moe_error), rich error text at open time through
@@ -68,11 +69,15 @@ int mia_moe_set_layer(mia_moe *m, int layer, const float *ffn_norm, const float 
  * and routers ~ N(0, 0.02), ffn_norm = 1. */
 int mia_moe_synth(mia_moe *m, uint64_t seed);
 
-/* One layer, moe() semantics, in place on host x[T][dim]. */
+/* One layer, moe() semantics, in place on host x[T][dim]. Bit-equal to the
+ * reference (below MHIP_GEMM_MIN_A assignments; within 1e-3 above). One
+ * token (T = 1) runs as one launch of the persistent decode kernel with the
+ * exact router where mhip_decode_supported allows it, else per stage. */
 int mia_moe_layer(mia_moe *m, int layer, float *x, int T);
 /* As mia_moe_layer with an optional logit bias[E] (added after the router,
  * before the softmax) and optional outputs idx[T][K], w[T][K] and
- * logits[T][E]. NULL skips any of them. */
+ * logits[T][E]. NULL skips any of them; asking for the logits keeps the
+ * per-stage path. */
 int mia_moe_layer_ex(mia_moe *m, int layer, float *x, int T, const float *bias, int *idx,
                      float *w, float *logits);
 /* Layers [l0, l1) of RMSNorm -> MoE -> residual, in place on host x[T][dim]. */

@@ -190,6 +190,11 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
  * [1] rmsnorm fallbacks, [2] layers routed by the exact fallback.
  */
 size_t mhip_decode_ws_bytes(void);
+/* 1 when mhip_decode_stack can run this shape on this device (the
+ * Qwen3-30B-A3B expert shape, 2048/128/<=8/768, and one 512-thread workgroup
+ * on every one of 256 CUs), 0 when it cannot (no error is set), -1 when the
+ * device query fails. */
+int mhip_decode_supported(mhip_ctx *c, const mhip_dims *s);
 int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
                       const void *d_table, const float *d_router, const float *d_router_t,
                       const float *d_norm, const float *d_bias, float *d_x, int L,

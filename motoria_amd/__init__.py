@@ -88,6 +88,7 @@ SIGNATURES = {
     "mhip_moe_layer": (_i, [_p, ctypes.POINTER(Dims), ctypes.POINTER(Layout), _p, _p, _p, _p,
                             _p, _i, ctypes.POINTER(Scratch), _i]),
     "mhip_decode_ws_bytes": (_sz, []),
+    "mhip_decode_supported": (_i, [_p, ctypes.POINTER(Dims)]),
     "mhip_decode_stack": (_i, [_p, ctypes.POINTER(Dims), ctypes.POINTER(Layout), _p, _p, _p, _p,
                                _p, _p, _i, _p, _p, _p, _i]),
     "mhip_decode_status": (_i, [_p, _p, ctypes.POINTER(_i)]),

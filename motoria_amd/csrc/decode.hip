@@ -929,24 +929,11 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
     }
 }
 
-}  // namespace
-
-extern "C" {
-
-size_t mhip_decode_ws_bytes(void) { return (sizeof(DecodeWs) + 255) / 256 * 256; }
-
-int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
-                      const void *d_table, const float *d_router, const float *d_router_t,
-                      const float *d_norm, const float *d_bias, float *d_x, int L, void *d_ws,
-                      int *d_idx, float *d_w, int flags) {
-    if (mhip::check_dims(c, s) || mhip::use_device(c)) return -1;
-    if (s->dim != D || s->n_experts != E || s->expert_hidden != EH || s->n_active > KMAX)
-        return mhip::fail(c, "decode stack: shape %d/%d/%d/%d is not the supported "
-                             "2048/128/<=8/768", s->dim, s->n_experts, s->n_active,
-                          s->expert_hidden);
-    if (L <= 0) return L == 0 ? 0 : mhip::fail(c, "decode stack: L=%d", L);
+// Once per context (the device properties query is slow): 1 when every CU
+// holds one workgroup of the kernel, 0 when not (c->decode_cus and
+// c->decode_occ say why), -1 on a failed query.
+int decode_device_fits(mhip_ctx *c) {
     if (!c->decode_checked) {
-        // once per context: the device properties query is slow
         hipDeviceProp_t prop;
         if (mhip::check(c, hipGetDeviceProperties(&prop, c->device), "hipGetDeviceProperties"))
             return -1;
@@ -955,12 +942,46 @@ int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
                         hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_decode_stack, NT, 0),
                         "occupancy"))
             return -1;
-        if (prop.multiProcessorCount != NWG || occ < 1)
-            return mhip::fail(c, "decode stack needs %d CUs with one %d-thread workgroup each "
-                                 "(device has %d CUs, occupancy %d)", NWG, NT,
-                              prop.multiProcessorCount, occ);
-        c->decode_checked = 1;
+        c->decode_cus = prop.multiProcessorCount;
+        c->decode_occ = occ;
+        c->decode_checked = prop.multiProcessorCount == NWG && occ >= 1 ? 1 : 2;
     }
+    return c->decode_checked == 1 ? 1 : 0;
+}
+
+bool decode_shape_fits(const mhip_dims *s) {
+    return s->dim == D && s->n_experts == E && s->expert_hidden == EH && s->n_active >= 1 &&
+           s->n_active <= KMAX;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mhip_decode_ws_bytes(void) { return (sizeof(DecodeWs) + 255) / 256 * 256; }
+
+int mhip_decode_supported(mhip_ctx *c, const mhip_dims *s) {
+    if (mhip::check_dims(c, s) || mhip::use_device(c)) return -1;
+    if (!decode_shape_fits(s)) return 0;
+    return decode_device_fits(c);
+}
+
+int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
+                      const void *d_table, const float *d_router, const float *d_router_t,
+                      const float *d_norm, const float *d_bias, float *d_x, int L, void *d_ws,
+                      int *d_idx, float *d_w, int flags) {
+    if (mhip::check_dims(c, s) || mhip::use_device(c)) return -1;
+    if (!decode_shape_fits(s))
+        return mhip::fail(c, "decode stack: shape %d/%d/%d/%d is not the supported "
+                             "2048/128/<=8/768", s->dim, s->n_experts, s->n_active,
+                          s->expert_hidden);
+    if (L <= 0) return L == 0 ? 0 : mhip::fail(c, "decode stack: L=%d", L);
+    const int fits = decode_device_fits(c);
+    if (fits < 0) return -1;
+    if (!fits)
+        return mhip::fail(c, "decode stack needs %d CUs with one %d-thread workgroup each "
+                             "(device has %d CUs, occupancy %d)", NWG, NT, c->decode_cus,
+                          c->decode_occ);
     if ((uintptr_t)d_ws % 256)
         return mhip::fail(c, "decode stack: workspace %p is not 256-byte aligned", d_ws);
     DecodeWs *ws = (DecodeWs *)d_ws;

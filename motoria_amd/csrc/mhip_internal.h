@@ -20,7 +20,8 @@ struct mhip_ctx {
     int *st_stage;      // [st_cap]
     unsigned decode_epoch;  // launches of the decode kernel (tags its exchanged data)
     const void *decode_ws;  // workspace those tags were written to
-    int decode_checked;     // the device was checked for the decode launch shape
+    int decode_checked;           // 0 unknown, 1 the decode launch fits the device, 2 it does not
+    int decode_cus, decode_occ;   // the CU count and occupancy that check found
     char err[512];
 };
 

@@ -288,11 +288,45 @@ static int check_status(mia_moe *m) {
     return 0;
 }
 
+/* One token through one layer in a launch of the persistent decode kernel
+ * with the exact router (bit-equal to the reference, like the per-stage
+ * path, and several times faster at T = 1). */
+static int decode_one_layer(mia_moe *m, int layer, float *x, const float *bias, int *idx,
+                            float *w) {
+    const size_t d = (size_t)m->dims.dim, E = (size_t)m->dims.n_experts,
+                 K = (size_t)m->dims.n_active;
+    if (layer < 0 || layer >= m->n_layers) return fail(m, "layer %d out of range", layer);
+    if (mhip_h2d(m->gpu, m->d_x, x, d * 4)) return gpu_fail(m);
+    if (bias && mhip_h2d(m->gpu, m->d_bias, bias, E * 4)) return gpu_fail(m);
+    if (mhip_decode_stack(m->gpu, &m->dims, &m->lay,
+                          (const unsigned char *)m->d_table +
+                              (size_t)layer * E * m->lay.expert_bytes,
+                          m->d_router_dl + layer * d * E, m->d_router_t + layer * d * E,
+                          m->d_norm + layer * d, bias ? m->d_bias : NULL, m->d_x, 1, m->d_dws,
+                          m->d_didx + layer * K, m->d_dw + layer * K,
+                          m->flags | MHIP_FORCE_EXACT_ROUTER))
+        return gpu_fail(m);
+    int st[4];
+    if (mhip_sync(m->gpu) || mhip_decode_status(m->gpu, m->d_dws, st)) return gpu_fail(m);
+    if (st[0]) return fail(m, "decode launch aborted (status %d: %s)", st[0],
+                           (st[0] & 1) ? "workgroups not on the expected XCDs" : "a wait timed out");
+    if (mhip_d2h(m->gpu, x, m->d_x, d * 4) ||
+        (idx && mhip_d2h(m->gpu, idx, m->d_didx + layer * K, K * 4)) ||
+        (w && mhip_d2h(m->gpu, w, m->d_dw + layer * K, K * 4)))
+        return gpu_fail(m);
+    return 0;
+}
+
 int mia_moe_layer_ex(mia_moe *m, int layer, float *x, int T, const float *bias, int *idx,
                      float *w, float *logits) {
     if (T < 0 || T > m->max_tokens)
         return fail(m, "T=%d outside [0, max_tokens=%d]", T, m->max_tokens);
     if (T == 0) return 0;
+    if (T == 1 && !logits && !(m->flags & MHIP_EXACT_EXPERTS)) {
+        const int ok = mhip_decode_supported(m->gpu, &m->dims);
+        if (ok < 0) return gpu_fail(m);
+        if (ok) return decode_one_layer(m, layer, x, bias, idx, w);
+    }
     const size_t d = (size_t)m->dims.dim, E = (size_t)m->dims.n_experts,
                  K = (size_t)m->dims.n_active;
     if (mhip_h2d(m->gpu, m->d_x, x, (size_t)T * d * 4)) return gpu_fail(m);

@@ -137,3 +137,26 @@ def test_decode_with_bias_and_repeats(oracle, qwen_dims, moe):
         xg, ig, _ = moe.decode(0, 1, x, bias=bias)
         assert np.array_equal(ig[0], io[0])
         assert rel(xg - x, xo[0] - x) <= TOL
+
+
+def test_host_layer_one_token_uses_decode_launch(oracle, qwen_dims, moe):
+    """mia_moe_layer at T = 1 (no logits asked): one launch of the persistent
+    kernel with the exact router, bit-equal to the oracle's layer."""
+    say("test_host_layer_one_token_uses_decode_launch")
+    d = qwen_dims
+    K = d.n_active
+    for l in (0, LAYERS - 1):
+        x0 = oracle.synth_x(W.X_SEED + 21 + l, 1, d.dim)
+        x = x0.copy()
+        idx = np.zeros(K, np.int32)
+        w = np.zeros(K, np.float32)
+        rc = M.lib().mia_moe_layer_ex(moe.h, l, x.ctypes.data, 1, None, idx.ctypes.data,
+                                      w.ctypes.data, None)
+        assert rc == 0, M.lib().mia_moe_error(moe.h).decode()
+        st = moe.decode_status()
+        assert st[0] == 0 and st[2] == 1, "the layer did not run as an exact-router decode launch"
+        xo, io, wo, _, _ = run_oracle_layer(oracle, moe, d, l, x0[0])
+        assert np.array_equal(idx, io[0]), "layer %d indices" % l
+        assert np.array_equal(w.view(np.uint32), wo[0].view(np.uint32)), "layer %d gate weights" % l
+        assert np.array_equal(x[0].view(np.uint32), xo[0].view(np.uint32)), "layer %d output" % l
+
