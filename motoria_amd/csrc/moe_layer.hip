@@ -95,6 +95,93 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_q8(const float *__restrict__ x,
     }
 }
 
+// The same for d == 2048 with one wavefront per token (four per workgroup):
+// lane b owns the 32-block b of the row, so the Q8_0 block maximum is the
+// lane's own, and only the sum of squares crosses lanes (a wavefront tree
+// with the same certified bracket; lane 0 redoes the sequential sum when the
+// bracket is ambiguous).
+constexpr int RN_D = 2048;
+__global__ __launch_bounds__(256) void k_rmsnorm_q8_w(const float *__restrict__ x,
+                                                     const float *__restrict__ w,
+                                                     float *__restrict__ xn,
+                                                     int8_t *__restrict__ xq,
+                                                     float *__restrict__ xs,
+                                                     _Float16 *__restrict__ xq16, int T,
+                                                     float eps, int force_seq, int *status) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6), b = threadIdx.x & 63;
+    if (t >= T) return;  // a whole wavefront: no workgroup barrier follows
+    const float4 *xr = (const float4 *)(x + (size_t)t * RN_D + 32 * b);
+    const float4 *wr = (const float4 *)(w + 32 * b);
+    float v[32];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const float4 q = xr[k];
+        v[4 * k] = q.x;
+        v[4 * k + 1] = q.y;
+        v[4 * k + 2] = q.z;
+        v[4 * k + 3] = q.w;
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < 32; k++) ss = ss + (double)v[k] * (double)v[k];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss = ss + __shfl_xor(ss, o);
+    ss = __shfl(ss, 0);  // one value for the whole wavefront (lanes summed in different orders)
+    const double m = ss * ((double)(RN_D + 64) * 0x1p-52);
+    const float lo = (float)(1.0 / sqrt((ss + m) / RN_D + (double)eps));
+    const float hi = (float)(1.0 / sqrt((ss - m) / RN_D + (double)eps));
+    float inv = lo;
+    if (force_seq || lo != hi) {  // the same branch in every lane of the wavefront
+        float r = 0.0f;
+        if (b == 0) {
+            const float *xt = x + (size_t)t * RN_D;
+            double sq = 0.0;
+            for (int i = 0; i < RN_D; i++) sq = sq + (double)xt[i] * (double)xt[i];
+            r = (float)(1.0 / sqrt(sq / RN_D + (double)eps));
+            atomicAdd(&status[1], 1);
+        }
+        inv = __shfl(r, 0);
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const float4 q = wr[k];
+        v[4 * k] = (v[4 * k] * inv) * q.x;
+        v[4 * k + 1] = (v[4 * k + 1] * inv) * q.y;
+        v[4 * k + 2] = (v[4 * k + 2] * inv) * q.z;
+        v[4 * k + 3] = (v[4 * k + 3] * inv) * q.w;
+    }
+#pragma unroll
+    for (int k = 0; k < 32; k++) amax = fmaxf(amax, fabsf(v[k]));
+    const float dsc = amax / 127.0f;
+    const float qi = dsc != 0.0f ? 1.0f / dsc : 0.0f;
+    float4 *xo = (float4 *)(xn + (size_t)t * RN_D + 32 * b);
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+        xo[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+    union {
+        int8_t c[32];
+        int4 q[2];
+    } qc;
+#pragma unroll
+    for (int k = 0; k < 32; k++) qc.c[k] = (int8_t)roundf(v[k] * qi);
+    int4 *qo = (int4 *)(xq + (size_t)t * RN_D + 32 * b);
+    qo[0] = qc.q[0];
+    qo[1] = qc.q[1];
+    if (xq16) {
+        typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+        h8v *ho = (h8v *)(xq16 + (size_t)t * RN_D + 32 * b);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            h8v hv;
+#pragma unroll
+            for (int e = 0; e < 8; e++) hv[e] = (_Float16)qc.c[8 * k + e];
+            ho[k] = hv;
+        }
+    }
+    xs[(size_t)t * (RN_D / QK) + b] = dsc;
+}
+
 // ---- router ---------------------------------------------------------------
 //
 // Thread e computes logit e as the reference's sequential fp32 chain
@@ -995,9 +1082,16 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
                       mhip::gemm_path_fits(s);
 
     int slot = mhip::stage_begin(c, MHIP_STAGE_RMSNORM);
-    k_rmsnorm_q8<<<T, NT, 0, st>>>(d_x, d_norm, sc->xn, sc->xq, sc->xs,
-                                   mfma ? (_Float16 *)sc->xdq : nullptr, d, s->norm_eps,
-                                   (flags & MHIP_FORCE_SEQ_RMS) ? 1 : 0, sc->status);
+    if (d == RN_D)
+        k_rmsnorm_q8_w<<<(T + 3) / 4, 256, 0, st>>>(d_x, d_norm, sc->xn, sc->xq, sc->xs,
+                                                    mfma ? (_Float16 *)sc->xdq : nullptr, T,
+                                                    s->norm_eps,
+                                                    (flags & MHIP_FORCE_SEQ_RMS) ? 1 : 0,
+                                                    sc->status);
+    else
+        k_rmsnorm_q8<<<T, NT, 0, st>>>(d_x, d_norm, sc->xn, sc->xq, sc->xs,
+                                       mfma ? (_Float16 *)sc->xdq : nullptr, d, s->norm_eps,
+                                       (flags & MHIP_FORCE_SEQ_RMS) ? 1 : 0, sc->status);
     mhip::stage_end(c, slot);
     if (mhip::check_launch(c, "rmsnorm_q8")) return -1;
 
