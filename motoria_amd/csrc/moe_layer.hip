@@ -201,7 +201,7 @@ __global__ __launch_bounds__(256) void k_router(const float *__restrict__ xn,
                                                 int *__restrict__ idx_out,
                                                 float *__restrict__ w_out, int d, int E, int K,
                                                 int norm_topk, int have_logits) {
-    extern __shared__ float sh[];
+    extern __shared__ __align__(16) float sh[];
     float *p = sh;        // [E]
     float *xs = sh + E;   // [d] (chains computed here)
     __shared__ float red[4];
@@ -243,8 +243,22 @@ __global__ __launch_bounds__(256) void k_router(const float *__restrict__ xn,
     if (tid < E) p[tid] = mhip_dev::expf_glibc(l - mx);
     __syncthreads();
     if (tid == 0) {
+        // in index order, sixteen values read ahead of their additions
         float sum = 0.0f;
-        for (int i = 0; i < E; i++) sum = sum + p[i];
+        int i = 0;
+        for (; i + 16 <= E; i += 16) {
+            float4 q[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) q[k] = *(const float4 *)&p[i + 4 * k];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                sum = sum + q[k].x;
+                sum = sum + q[k].y;
+                sum = sum + q[k].z;
+                sum = sum + q[k].w;
+            }
+        }
+        for (; i < E; i++) sum = sum + p[i];
         sum_sh = sum;
     }
     __syncthreads();
