@@ -1,6 +1,6 @@
 // Expert products of the batched / prefill MoE layer on the matrix cores.
 //
-// For T tokens the T*K assignments are bucketed by expert (k_dispatch); each
+// For T tokens the T*K assignments are bucketed by expert (k_disp_*); each
 // expert's bucket is a dense contraction with that expert's weights:
 //
 //   k_gateup_mfma  h = SwiGLU(Wg x, Wu x), then Q8_0(h)   forward.c:186-192
