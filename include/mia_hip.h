@@ -59,6 +59,13 @@ int mhip_free(mhip_ctx *c, void *d_ptr);
 int mhip_h2d(mhip_ctx *c, void *d_dst, const void *src, size_t bytes);
 int mhip_d2h(mhip_ctx *c, void *dst, const void *d_src, size_t bytes);
 int mhip_d2d(mhip_ctx *c, void *d_dst, const void *d_src, size_t bytes);
+/* Pinned (page-locked) host memory, and copies queued on the context's
+ * stream without waiting (the host buffer must be pinned and stay untouched
+ * until the stream has passed the copy, e.g. until mhip_sync). */
+void *mhip_host_malloc(mhip_ctx *c, size_t bytes);
+int mhip_host_free(mhip_ctx *c, void *h_ptr);
+int mhip_h2d_async(mhip_ctx *c, void *d_dst, const void *h_src, size_t bytes);
+int mhip_d2h_async(mhip_ctx *c, void *h_dst, const void *d_src, size_t bytes);
 int mhip_zero(mhip_ctx *c, void *d_ptr, size_t bytes); /* fill kernel, not memset */
 int mhip_sync(mhip_ctx *c);
 /* Milliseconds between two points of the context's stream (HIP events). */

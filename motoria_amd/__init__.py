@@ -68,6 +68,10 @@ SIGNATURES = {
     "mhip_h2d": (_i, [_p, _p, _p, _sz]),
     "mhip_d2h": (_i, [_p, _p, _p, _sz]),
     "mhip_d2d": (_i, [_p, _p, _p, _sz]),
+    "mhip_host_malloc": (_p, [_p, _sz]),
+    "mhip_host_free": (_i, [_p, _p]),
+    "mhip_h2d_async": (_i, [_p, _p, _p, _sz]),
+    "mhip_d2h_async": (_i, [_p, _p, _p, _sz]),
     "mhip_zero": (_i, [_p, _p, _sz]),
     "mhip_sync": (_i, [_p]),
     "mhip_mark": (_i, [_p, _i]),

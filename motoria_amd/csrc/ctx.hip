@@ -208,6 +208,35 @@ int mhip_d2h(mhip_ctx *c, void *dst, const void *d_src, size_t bytes) {
     return mhip::check(c, hipStreamSynchronize(c->stream), "d2h sync");
 }
 
+void *mhip_host_malloc(mhip_ctx *c, size_t bytes) {
+    if (mhip::use_device(c)) return nullptr;
+    void *p = nullptr;
+    if (mhip::check(c, hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault),
+                    "hipHostMalloc"))
+        return nullptr;
+    return p;
+}
+
+int mhip_host_free(mhip_ctx *c, void *h_ptr) {
+    if (!h_ptr) return 0;
+    if (mhip::use_device(c)) return -1;
+    // Copies queued on the stream may still use the buffer.
+    if (mhip::check(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize")) return -1;
+    return mhip::check(c, hipHostFree(h_ptr), "hipHostFree");
+}
+
+int mhip_h2d_async(mhip_ctx *c, void *d_dst, const void *h_src, size_t bytes) {
+    if (mhip::use_device(c)) return -1;
+    return mhip::check(c, hipMemcpyAsync(d_dst, h_src, bytes, hipMemcpyHostToDevice, c->stream),
+                       "hipMemcpyAsync h2d");
+}
+
+int mhip_d2h_async(mhip_ctx *c, void *h_dst, const void *d_src, size_t bytes) {
+    if (mhip::use_device(c)) return -1;
+    return mhip::check(c, hipMemcpyAsync(h_dst, d_src, bytes, hipMemcpyDeviceToHost, c->stream),
+                       "hipMemcpyAsync d2h");
+}
+
 int mhip_d2d(mhip_ctx *c, void *d_dst, const void *d_src, size_t bytes) {
     if (mhip::use_device(c)) return -1;
     return mhip::check(c, hipMemcpyAsync(d_dst, d_src, bytes, hipMemcpyDeviceToDevice, c->stream),

@@ -20,6 +20,7 @@ struct mia_moe {
     float *d_router_dl; /* [L][E][dim], decode layout (mhip_router_decode_layout) */
     void *d_dws;        /* persistent decode workspace */
     int *d_didx;        /* [L][K] routing of the last decode-stack call */
+    float *h_stage;     /* pinned: x in [dim], x out [dim], idx [K], w [K] of one-token calls */
     float *d_dw;        /* [L][K] */
     float *d_norm;      /* [L][dim] */
     float *d_router;    /* [E][dim] upload staging */
@@ -61,6 +62,7 @@ void mia_moe_close(mia_moe *m) {
         mhip_free(m->gpu, m->d_router_dl);
         mhip_free(m->gpu, m->d_dws);
         mhip_free(m->gpu, m->d_didx);
+        mhip_host_free(m->gpu, m->h_stage);
         mhip_free(m->gpu, m->d_dw);
         mhip_free(m->gpu, m->d_norm);
         mhip_free(m->gpu, m->d_router);
@@ -123,9 +125,10 @@ int mia_moe_open(mia_moe **out, const mia_moe_config *cfg, char *err, size_t err
         m->d_bias = mhip_malloc(m->gpu, E * 4);
         m->d_blob = mhip_malloc(m->gpu, m->blob_bytes);
         m->h_blob = malloc(m->blob_bytes);
+        m->h_stage = (float *)mhip_host_malloc(m->gpu, (2 * d + 2 * (size_t)cfg->n_active) * 4);
         if (!m->d_table || !m->d_router_t || !m->d_router_dl || !m->d_dws || !m->d_didx ||
             !m->d_dw || !m->d_norm || !m->d_router || !m->d_scratch || !m->d_x || !m->d_bias ||
-            !m->d_blob)
+            !m->d_blob || !m->h_stage)
             rc = fail(m, "HBM allocation (%.2f GiB table): %s", table / 1073741824.0,
                       mhip_error(m->gpu));
         else if (!m->h_blob)
@@ -290,13 +293,18 @@ static int check_status(mia_moe *m) {
 
 /* One token through one layer in a launch of the persistent decode kernel
  * with the exact router (bit-equal to the reference, like the per-stage
- * path, and several times faster at T = 1). */
+ * path, and several times faster at T = 1). x and the routing travel through
+ * the pinned staging buffer with queued copies, so the call waits for the
+ * device once (in the status read). */
 static int decode_one_layer(mia_moe *m, int layer, float *x, const float *bias, int *idx,
                             float *w) {
     const size_t d = (size_t)m->dims.dim, E = (size_t)m->dims.n_experts,
                  K = (size_t)m->dims.n_active;
+    float *hx = m->h_stage, *hy = m->h_stage + d, *hw = m->h_stage + 2 * d + K;
+    int *hi = (int *)(m->h_stage + 2 * d);
     if (layer < 0 || layer >= m->n_layers) return fail(m, "layer %d out of range", layer);
-    if (mhip_h2d(m->gpu, m->d_x, x, d * 4)) return gpu_fail(m);
+    memcpy(hx, x, d * 4);
+    if (mhip_h2d_async(m->gpu, m->d_x, hx, d * 4)) return gpu_fail(m);
     if (bias && mhip_h2d(m->gpu, m->d_bias, bias, E * 4)) return gpu_fail(m);
     if (mhip_decode_stack(m->gpu, &m->dims, &m->lay,
                           (const unsigned char *)m->d_table +
@@ -306,14 +314,18 @@ static int decode_one_layer(mia_moe *m, int layer, float *x, const float *bias, 
                           m->d_didx + layer * K, m->d_dw + layer * K,
                           m->flags | MHIP_FORCE_EXACT_ROUTER))
         return gpu_fail(m);
+    if (mhip_d2h_async(m->gpu, hy, m->d_x, d * 4) ||
+        mhip_d2h_async(m->gpu, hi, m->d_didx + layer * K, K * 4) ||
+        mhip_d2h_async(m->gpu, hw, m->d_dw + layer * K, K * 4))
+        return gpu_fail(m);
     int st[4];
-    if (mhip_sync(m->gpu) || mhip_decode_status(m->gpu, m->d_dws, st)) return gpu_fail(m);
+    /* the status read waits for the stream, copies above included */
+    if (mhip_decode_status(m->gpu, m->d_dws, st)) return gpu_fail(m);
     if (st[0]) return fail(m, "decode launch aborted (status %d: %s)", st[0],
                            (st[0] & 1) ? "workgroups not on the expected XCDs" : "a wait timed out");
-    if (mhip_d2h(m->gpu, x, m->d_x, d * 4) ||
-        (idx && mhip_d2h(m->gpu, idx, m->d_didx + layer * K, K * 4)) ||
-        (w && mhip_d2h(m->gpu, w, m->d_dw + layer * K, K * 4)))
-        return gpu_fail(m);
+    memcpy(x, hy, d * 4);
+    if (idx) memcpy(idx, hi, K * 4);
+    if (w) memcpy(w, hw, K * 4);
     return 0;
 }
 
