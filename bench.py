@@ -127,7 +127,7 @@ def main():
     ap.add_argument("--workload", default="decode48", choices=sorted(W.WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-layers", type=int, default=4)
-    ap.add_argument("--cpu-tokens", type=int, default=256)
+    ap.add_argument("--cpu-tokens", type=int, default=768)
     ap.add_argument("--multi-kernel", action="store_true",
                     help="batch-1 workloads: one launch per stage instead of the "
                          "persistent decode kernel")

@@ -142,6 +142,7 @@ typedef struct {
     float *xsb;       /* [d/32][T*K] Q8 scales of xn per assignment, bucketed (matrix-core path) */
     int8_t *hq;       /* [T*K][eh] Q8 codes of h, bucketed (vector path) */
     float *hs;        /* [T*K][eh/32] Q8 scales of h, bucketed (vector path) */
+    int *glight;      /* [E+1]     light tiles (at most MHIP_GEMM_TM/2 rows) before each group */
 } mhip_scratch;
 
 /* Rows of one expert bucket per matrix-core tile. */

@@ -51,7 +51,7 @@ class Layout(ctypes.Structure):
 class Scratch(ctypes.Structure):
     _fields_ = [(n, _p) for n in ("xn", "xq", "xs", "logits", "idx", "w", "counts", "offsets",
                                   "perm", "pos", "groups", "h", "tmp", "status", "xdq",
-                                  "hdq", "gtile", "xsb", "hq", "hs")]
+                                  "hdq", "gtile", "xsb", "hq", "hs", "glight")]
 
 
 # Every function the library exports, with its ctypes signature. tests check

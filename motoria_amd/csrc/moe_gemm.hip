@@ -76,12 +76,14 @@ static_assert(sizeof(Step) == 17920, "step layout");
 __device__ __forceinline__ int xslot(int m, int chunk) { return chunk ^ ((m >> 1) & 3); }
 __device__ __forceinline__ int wslot(int n, int half) { return half ^ ((n >> 3) & 1); }
 
-// The group g with gtile[g] <= mt < gtile[g + 1] (gtile is non-decreasing).
-__device__ __forceinline__ int find_group(const int *gtile, int G, int mt) {
+// The group g < G with f(g) <= p < f(g + 1), for a non-decreasing f over
+// 0..G with f(0) <= p < f(G).
+template <typename F>
+__device__ __forceinline__ int find_group(F f, int G, int p) {
     int lo = 0, hi = G;
     while (hi - lo > 1) {
         const int mid = (lo + hi) >> 1;
-        if (gtile[mid] <= mt)
+        if (f(mid) <= p)
             lo = mid;
         else
             hi = mid;
@@ -91,28 +93,46 @@ __device__ __forceinline__ int find_group(const int *gtile, int G, int mt) {
 
 // Tile coordinates shared by both kernels.
 //
-// The 1-D grid is ordered for the XCDs' L2 caches: workgroup b runs on XCD
-// b % 8, and XCD k takes a contiguous share of the row tiles (consecutive
-// tiles of one expert share its weights), each row tile's ny weight-row
-// tiles back to back (they share its A rows). The share is computed from
-// the number of row tiles the dispatch produced; workgroups beyond it exit.
+// A bucket's row tiles are TM rows each but its last, which holds the rest;
+// that one is light when it has at most TM / 2 rows (its products run on at
+// most four 16-row assignment tiles), heavy otherwise. The 1-D grid is
+// ordered for balance and for the XCDs' L2 caches: workgroup b runs on XCD
+// b % 8, and XCD k takes a contiguous eighth of the heavy row tiles (in
+// bucket order, so consecutive tiles of one expert share its weights), then
+// a contiguous eighth of the light ones, each row tile's ny weight-row tiles
+// back to back (they share its A rows). Every XCD thus starts the same number
+// of heavy tiles (within one) before any light tile, and the light tiles fill
+// the last round. Workgroups beyond an XCD's shares exit.
 struct TileRef {
     int e, base, nrows, y;
 };
 constexpr int NXCD = 8;
-__device__ __forceinline__ bool tile_of(const int *groups, const int *gtile, int ny,
-                                        TileRef &t) {
+__device__ __forceinline__ bool tile_of(const int *groups, const int *gtile, const int *glight,
+                                        int ny, TileRef &t) {
     const int G = groups[0];
     if (G == 0) return false;
-    const int nreal = gtile[G];
+    const int nl = glight[G], nh = gtile[G] - nl;
+    const int hs = (nh + NXCD - 1) / NXCD, ls = (nl + NXCD - 1) / NXCD;
     const int b = blockIdx.x, xcd = b % NXCD, r = b / NXCD;
-    const int share = (nreal + NXCD - 1) / NXCD;
     const int q = r / ny;
-    if (q >= share) return false;
-    const int mt = xcd * share + q;
-    if (mt >= nreal) return false;
+    const int hk = max(0, min(hs, nh - xcd * hs)), lk = max(0, min(ls, nl - xcd * ls));
+    int g, mt;
+    if (q < hk) {
+        // heavy tile p: group g's heavy tiles are its first
+        // (gtile - glight)(g + 1) - (gtile - glight)(g)
+        const int p = xcd * hs + q;
+        auto heavy_before = [&](int k) { return gtile[k] - glight[k]; };
+        g = find_group(heavy_before, G, p);
+        mt = gtile[g] + (p - heavy_before(g));
+    } else if (q < hk + lk) {
+        // light tile p: the last tile of the group with glight(g) == p
+        const int p = xcd * ls + (q - hk);
+        g = find_group([&](int k) { return glight[k]; }, G, p);
+        mt = gtile[g + 1] - 1;
+    } else {
+        return false;
+    }
     t.y = r % ny;
-    const int g = find_group(gtile, G, mt);
     t.e = groups[1 + 3 * g];
     t.base = groups[2 + 3 * g] + (mt - gtile[g]) * TM;
     t.nrows = min(TM, groups[3 + 3 * g] - t.base);
@@ -328,10 +348,11 @@ static_assert(3 * sizeof(DownLds) <= 160 * 1024, "three down workgroups per CU")
 __global__ __launch_bounds__(GT, 2) void k_gateup_mfma(
     const uint8_t *__restrict__ table, mhip_layout lay, const _Float16 *__restrict__ xq16,
     const float *__restrict__ xsb, const int *__restrict__ groups, const int *__restrict__ gtile,
-    const int *__restrict__ perm, _Float16 *__restrict__ hdq, int d, int eh, int K, int A) {
+    const int *__restrict__ glight, const int *__restrict__ perm, _Float16 *__restrict__ hdq, int d,
+    int eh, int K, int A) {
     __shared__ GateUpLds L;
     TileRef tr;
-    if (!tile_of(groups, gtile, eh / (TN / 2), tr)) return;
+    if (!tile_of(groups, gtile, glight, eh / (TN / 2), tr)) return;
     const int base = tr.base, nrows = tr.nrows;
     const int h0 = tr.y * (TN / 2);
     const uint8_t *ex = table + (size_t)tr.e * lay.expert_bytes;
@@ -443,10 +464,11 @@ __global__ __launch_bounds__(GT, 3) void k_down_mfma(const uint8_t *__restrict__
                                                      const _Float16 *__restrict__ hdq,
                                                      const int *__restrict__ groups,
                                                      const int *__restrict__ gtile,
+                                                     const int *__restrict__ glight,
                                                      float *__restrict__ tmp, int d, int eh) {
     __shared__ DownLds L;
     TileRef tr;
-    if (!tile_of(groups, gtile, d / TN, tr)) return;
+    if (!tile_of(groups, gtile, glight, d / TN, tr)) return;
     const int base = tr.base, nrows = tr.nrows;
     const int n0 = tr.y * TN;
     const uint8_t *ex = table + (size_t)tr.e * lay.expert_bytes;
@@ -517,9 +539,10 @@ bool gemm_path_fits(const mhip_dims *s) {
 
 int gemm_max_tiles(int A, int E) { return (A + TM - 1) / TM + (A < E ? A : E); }
 
-// Workgroups for ny weight-row tiles: every XCD's share can hold all row tiles.
+// Workgroups for ny weight-row tiles: every XCD's heavy and light shares
+// (ceil(H / 8) + ceil(L / 8) <= ceil((H + L) / 8) + 1 row tiles) fit.
 static unsigned gemm_grid(int A, int E, int ny) {
-    const int share = (gemm_max_tiles(A, E) + NXCD - 1) / NXCD;
+    const int share = (gemm_max_tiles(A, E) + NXCD - 1) / NXCD + 1;
     return (unsigned)(NXCD * share * ny);
 }
 
@@ -531,7 +554,7 @@ int launch_gateup_mfma(hipStream_t st, const mhip_dims *s, const mhip_layout *la
     const unsigned grid = gemm_grid(A, s->n_experts, eh / (TN / 2));
     k_gateup_mfma<<<grid, GT, 0, st>>>((const uint8_t *)d_table_layer, *lay,
                                        (const _Float16 *)sc->xdq, sc->xsb, sc->groups,
-                                       sc->gtile, sc->perm, (_Float16 *)sc->hdq, d, eh,
+                                       sc->gtile, sc->glight, sc->perm, (_Float16 *)sc->hdq, d, eh,
                                        s->n_active, A);
     return (int)hipGetLastError();
 }
@@ -541,8 +564,8 @@ int launch_down_mfma(hipStream_t st, const mhip_dims *s, const mhip_layout *lay,
     const int d = s->dim, eh = s->expert_hidden;
     const unsigned grid = gemm_grid(A, s->n_experts, d / TN);
     k_down_mfma<<<grid, GT, 0, st>>>((const uint8_t *)d_table_layer, *lay,
-                                     (const _Float16 *)sc->hdq, sc->groups, sc->gtile, sc->tmp,
-                                     d, eh);
+                                     (const _Float16 *)sc->hdq, sc->groups, sc->gtile, sc->glight,
+                                     sc->tmp, d, eh);
     return (int)hipGetLastError();
 }
 

@@ -504,8 +504,9 @@ __global__ __launch_bounds__(256, 2) void k_router_logits_wide(const float *__re
 //   k_disp_count    per-chunk expert counts           -> hist[e][chunk]
 //   k_disp_scan     per expert, exclusive scan over the chunks; counts
 //   k_disp_scatter  offsets, the list of non-empty experts as (expert,
-//                   begin, end) groups and gtile[g], the number of tm-row
-//                   tiles before group g (gtile[n_groups] = all tiles); then
+//                   begin, end) groups, gtile[g], the number of tm-row
+//                   tiles before group g (gtile[n_groups] = all tiles), and
+//                   glight[g], the light tiles among them; then
 //                   each chunk in order, 64 assignments per step: the rank
 //                   of a lane among the step's lanes with the same expert
 //                   comes from one ballot per bit of the expert index.
@@ -591,49 +592,59 @@ __global__ __launch_bounds__(64 * DWG) void k_disp_count(const int *__restrict__
 }
 
 // The dispatch tables (counts, offsets[E+1], the list of non-empty experts as
-// (expert, begin, end) groups and gtile[g], the number of tm-row tiles before
-// group g) from parallel scans: every thread of the workgroup calls
-// (blockDim >= 256, E <= 256); thread x < E owns expert x. Three exclusive
-// scans over the experts (rows, non-empty experts, tiles) give each
-// expert's offset, its group number and its first tile. off[E] (LDS)
-// receives the offsets; with write_tables the global tables are written too.
-// sc: 12 ints of LDS.
+// (expert, begin, end) groups, gtile[g], the number of tm-row tiles before
+// group g, and glight[g], the number of light tiles before group g) from
+// parallel scans: every thread of the workgroup calls (blockDim >= 256,
+// E <= 256); thread x < E owns expert x. A group's tiles are tm rows each
+// but its last, which holds the remaining rows and is light when those are at
+// most tm / 2. Four exclusive scans over the experts (rows, non-empty
+// experts, tiles, light tiles) give each expert's offset, its group number,
+// its first tile and its light tiles before it. off[E] (LDS) receives the
+// offsets; with write_tables the global tables are written too.
+// sc: 16 ints of LDS.
 __device__ void disp_tables(int E, const int *tot, int *off, int *sc, bool write_tables,
-                            int *counts, int *offsets, int *groups, int *gtile, int tm) {
+                            int *counts, int *offsets, int *groups, int *gtile, int *glight,
+                            int tm) {
     const int x = threadIdx.x, lane = x & 63, w = x >> 6;
     const bool in = x < E;
     const int n = in ? tot[x] : 0;
     const int ne = n > 0 ? 1 : 0, nt = (n + tm - 1) / tm;
-    int a = n, b = ne, c = nt;
+    const int nl = n % tm != 0 && n % tm <= tm / 2 ? 1 : 0;
+    int a = n, b = ne, c = nt, l = nl;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const int ua = __shfl_up(a, o), ub = __shfl_up(b, o), uc = __shfl_up(c, o);
+        const int ua = __shfl_up(a, o), ub = __shfl_up(b, o), uc = __shfl_up(c, o),
+                  ul = __shfl_up(l, o);
         if (lane >= o) {
             a += ua;
             b += ub;
             c += uc;
+            l += ul;
         }
     }
     if (w < 4 && lane == 63) {
         sc[w] = a;
         sc[4 + w] = b;
         sc[8 + w] = c;
+        sc[12 + w] = l;
     }
     __syncthreads();
-    int pa = 0, pb = 0, pc = 0, ta = 0, tb = 0, tc = 0;
+    int pa = 0, pb = 0, pc = 0, pl = 0, ta = 0, tb = 0, tc = 0, tl = 0;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         if (k < w) {
             pa += sc[k];
             pb += sc[4 + k];
             pc += sc[8 + k];
+            pl += sc[12 + k];
         }
         ta += sc[k];
         tb += sc[4 + k];
         tc += sc[8 + k];
+        tl += sc[12 + k];
     }
     if (in) {
-        const int ea = pa + a - n, eb = pb + b - ne, ec = pc + c - nt;
+        const int ea = pa + a - n, eb = pb + b - ne, ec = pc + c - nt, el = pl + l - nl;
         off[x] = ea;
         if (write_tables) {
             counts[x] = n;
@@ -643,6 +654,7 @@ __device__ void disp_tables(int E, const int *tot, int *off, int *sc, bool write
                 groups[2 + 3 * eb] = ea;
                 groups[3 + 3 * eb] = ea + n;
                 gtile[eb] = ec;
+                glight[eb] = el;
             }
         }
     }
@@ -650,6 +662,7 @@ __device__ void disp_tables(int E, const int *tot, int *off, int *sc, bool write
         offsets[E] = ta;
         groups[0] = tb;
         gtile[tb] = tc;
+        glight[tb] = tl;
     }
     __syncthreads();
 }
@@ -685,14 +698,15 @@ __global__ __launch_bounds__(256) void k_disp_scan(int nch, int *__restrict__ hi
 }
 
 // Every workgroup derives the experts' first positions from counts[];
-// workgroup 0 also writes offsets, groups and gtile.
+// workgroup 0 also writes offsets, groups, gtile and glight.
 __global__ __launch_bounds__(64 * DWG) void k_disp_scatter(const int *__restrict__ idx, int A,
                                                            int E, int nch, int bits,
                                                            const int *__restrict__ hist,
                                                            int *__restrict__ counts,
                                                            int *__restrict__ offsets,
                                                            int *__restrict__ groups,
-                                                           int *__restrict__ gtile, int tm,
+                                                           int *__restrict__ gtile,
+                                                           int *__restrict__ glight, int tm,
                                                            int *__restrict__ perm,
                                                            int *__restrict__ pos,
                                                            int *status) {
@@ -700,11 +714,11 @@ __global__ __launch_bounds__(64 * DWG) void k_disp_scatter(const int *__restrict
     int *base = lds_s;                 // [DWG][E]: next position of each expert
     int *tot = lds_s + DWG * E;        // [E]
     int *off = tot + E;                // [E]
-    int *sc = off + E;                 // [12]
+    int *sc = off + E;                 // [16]
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     for (int e = threadIdx.x; e < E; e += blockDim.x) tot[e] = counts[e];
     __syncthreads();
-    disp_tables(E, tot, off, sc, blockIdx.x == 0, counts, offsets, groups, gtile, tm);
+    disp_tables(E, tot, off, sc, blockIdx.x == 0, counts, offsets, groups, gtile, glight, tm);
     const int ch = blockIdx.x * DWG + w;
     if (ch >= nch) return;  // a whole wavefront: no workgroup barrier follows
     int *bs = base + w * E;
@@ -723,13 +737,14 @@ __global__ __launch_bounds__(64 * DSMALL) void k_disp_small(const int *__restric
                                                             int *__restrict__ perm,
                                                             int *__restrict__ pos,
                                                             int *__restrict__ groups,
-                                                            int *__restrict__ gtile, int tm,
+                                                            int *__restrict__ gtile,
+                                                            int *__restrict__ glight, int tm,
                                                             int *status) {
     extern __shared__ int lds_i[];
     int *hist = lds_i;                 // [DSMALL][E]
     int *tot = lds_i + DSMALL * E;     // [E]
     int *off = tot + E;                // [E]
-    int *sc = off + E;                 // [12]
+    int *sc = off + E;                 // [16]
     const int w = threadIdx.x >> 6;
     for (int i = threadIdx.x; i < DSMALL * E; i += blockDim.x) hist[i] = 0;
     __syncthreads();
@@ -745,7 +760,7 @@ __global__ __launch_bounds__(64 * DSMALL) void k_disp_small(const int *__restric
         tot[e] = run;
     }
     __syncthreads();
-    disp_tables(E, tot, off, sc, true, counts, offsets, groups, gtile, tm);
+    disp_tables(E, tot, off, sc, true, counts, offsets, groups, gtile, glight, tm);
     if (w < nch) {
         int *bs = hist + w * E;
         for (int e = threadIdx.x & 63; e < E; e += 64) bs[e] += off[e];
@@ -1046,6 +1061,7 @@ size_t mhip_scratch_bytes(const mhip_dims *s, int T) {
     n += align256(A * (d / QK) * 4);   // xsb
     n += align256(A * eh);             // hq
     n += align256(A * (eh / QK) * 4);  // hs
+    n += align256((E + 1) * 4);        // glight
     return n;
 }
 
@@ -1078,6 +1094,7 @@ int mhip_scratch_carve(const mhip_dims *s, int T, void *d_base, mhip_scratch *o)
     o->xsb = (float *)take(A * (d / QK) * 4);
     o->hq = (int8_t *)take(A * eh);
     o->hs = (float *)take(A * (eh / QK) * 4);
+    o->glight = (int *)take((E + 1) * 4);
     return 0;
 }
 
@@ -1162,15 +1179,15 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     int *dhist = (int *)sc->tmp;
     slot = mhip::stage_begin(c, MHIP_STAGE_DISPATCH);
     if (nch <= DSMALL) {
-        k_disp_small<<<1, 64 * DSMALL, (DSMALL * E + 2 * E + 12) * 4, st>>>(
+        k_disp_small<<<1, 64 * DSMALL, (DSMALL * E + 2 * E + 16) * 4, st>>>(
             sc->idx, A, E, nch, bits, sc->counts, sc->offsets, sc->perm, sc->pos, sc->groups,
-            sc->gtile, MHIP_GEMM_TM, sc->status);
+            sc->gtile, sc->glight, MHIP_GEMM_TM, sc->status);
     } else {
         k_disp_count<<<dgrid, 64 * DWG, DWG * E * 4, st>>>(sc->idx, A, E, nch, dhist, sc->status);
         k_disp_scan<<<E, 256, 0, st>>>(nch, dhist, sc->counts);
-        k_disp_scatter<<<dgrid, 64 * DWG, ((DWG + 2) * E + 12) * 4, st>>>(
+        k_disp_scatter<<<dgrid, 64 * DWG, ((DWG + 2) * E + 16) * 4, st>>>(
             sc->idx, A, E, nch, bits, dhist, sc->counts, sc->offsets, sc->groups, sc->gtile,
-            MHIP_GEMM_TM, sc->perm, sc->pos, sc->status);
+            sc->glight, MHIP_GEMM_TM, sc->perm, sc->pos, sc->status);
     }
     mhip::stage_end(c, slot);
     if (mhip::check_launch(c, "dispatch")) return -1;

@@ -302,6 +302,11 @@ def test_matrix_path_ragged_buckets(oracle, qwen_dims, qwen_moe):
     sizes = groups[3:3 + 3 * G:3] - groups[2:2 + 3 * G:3]
     assert sizes.sum() == T * qwen_dims.n_active and sizes.max() < 128
     assert np.array_equal(gtile[:G + 1], np.concatenate([[0], np.cumsum((sizes + 127) // 128)]))
+    # light tiles: a bucket's last tile when it holds at most 64 rows
+    glight = qwen_moe.d2h(sc.glight, E + 1, np.int32)
+    rem = sizes % 128
+    assert np.array_equal(glight[:G + 1],
+                          np.concatenate([[0], np.cumsum((rem != 0) & (rem <= 64))]))
     xo, io, wo, lo, _ = oracle_layer(oracle, qwen_moe, qwen_dims, 0, x, router,
                                     need=im.ravel().tolist())
     assert np.array_equal(im, io)
