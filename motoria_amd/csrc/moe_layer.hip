@@ -769,6 +769,23 @@ __global__ __launch_bounds__(64 * DSMALL) void k_disp_small(const int *__restric
     }
 }
 
+// Sequential fp32 sum of the n floats at p (LDS), in order. Sixteen values
+// are read before they are added, so the chain waits for the LDS once per
+// sixteen values rather than once per value.
+__device__ __forceinline__ float lds_seq_sum(const float *p, int n) {
+    float s = 0.0f;
+    int b = 0;
+    for (; b + 16 <= n; b += 16) {
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) v[j] = p[b + j];
+#pragma unroll
+        for (int j = 0; j < 16; j++) s = s + v[j];
+    }
+    for (; b < n; b++) s = s + p[b];
+    return s;
+}
+
 // ---- gate/up + SwiGLU --------------------------------------------------------
 
 // Float offset of k_gateup's staged codes in its LDS (16-byte aligned) and
@@ -791,7 +808,7 @@ inline size_t gateup_lds(int d, int R) { return (size_t)gateup_xq_off(d, R) * 4 
 // SwiGLU g/(1+expf(-g))*u (forward.c:190) produces h, written in bucketed
 // order.
 template <int PK>
-__global__ __launch_bounds__(NT) void k_gateup(const uint8_t *__restrict__ table, mhip_layout lay,
+__global__ __launch_bounds__(NT, 6) void k_gateup(const uint8_t *__restrict__ table, mhip_layout lay,
                                                const int8_t *__restrict__ xq,
                                                const float *__restrict__ xs,
                                                const int *__restrict__ groups,
@@ -858,10 +875,7 @@ __global__ __launch_bounds__(NT) void k_gateup(const uint8_t *__restrict__ table
         }
         __syncthreads();
         for (int c = threadIdx.x; c < ntok * 2 * R; c += NT) {
-            const float *row = terms + c * ld;
-            float s = 0.0f;
-            for (int b = 0; b < nb; b++) s = s + row[b];
-            gu[c] = s;
+            gu[c] = lds_seq_sum(terms + c * ld, nb);
         }
         __syncthreads();
         for (int c = threadIdx.x; c < ntok * R; c += NT) {
@@ -977,10 +991,7 @@ __global__ __launch_bounds__(NT) void k_down(const uint8_t *__restrict__ table, 
         __syncthreads();
         for (int c = threadIdx.x; c < ntok * R; c += NT) {
             const int tb = c / R, r = c % R;
-            const float *row = terms + c * ld;
-            float s = 0.0f;
-            for (int b = 0; b < nbh; b++) s = s + row[b];
-            tmp[(size_t)(base + tb) * d + rc * R + r] = s;
+            tmp[(size_t)(base + tb) * d + rc * R + r] = lds_seq_sum(terms + c * ld, nbh);
         }
         __syncthreads();
     }
@@ -1018,8 +1029,10 @@ __global__ __launch_bounds__(256) void k_combine(float *__restrict__ x,
 }
 
 // Rows per workgroup: the largest power of two <= 32 with 2R*nb <= PK*NT
-// pairs (gate/up), R*nbh <= PK*NT (down).
+// pairs (gate/up), R*nbh <= PKD*NT (down; three pairs per thread hold the
+// 32 x 24 pairs of the 768-wide down rows exactly).
 constexpr int PK = 4;
+constexpr int PKD = 3;
 
 int rows_gateup(int nb) {
     int r = 32;
@@ -1029,7 +1042,7 @@ int rows_gateup(int nb) {
 
 int rows_down(int nbh) {
     int r = 32;
-    while (r > 1 && r * nbh > PK * NT) r >>= 1;
+    while (r > 1 && r * nbh > PKD * NT) r >>= 1;
     return r;
 }
 
@@ -1224,7 +1237,7 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     slot = mhip::stage_begin(c, MHIP_STAGE_DOWN);
     const int nbq = A * nbh;
     k_quant_h<<<(nbq + 255) / 256, 256, 0, st>>>(sc->h, sc->hq, sc->hs, nbq);
-    k_down<PK><<<(unsigned)G * (d / Rd), NT, dsh2, st>>>((const uint8_t *)d_table_layer, *lay,
+    k_down<PKD><<<(unsigned)G * (d / Rd), NT, dsh2, st>>>((const uint8_t *)d_table_layer, *lay,
                                                          sc->hq, sc->hs, sc->groups, sc->tmp, d,
                                                          eh, Rd);
     mhip::stage_end(c, slot);
