@@ -403,13 +403,14 @@ size_t router_logits_lds(int C, int d) {
 // The same chains with the tokens across the lanes: a workgroup takes RW_T = 64
 // tokens (lane = token) and 4 CPL experts (wavefront w: experts CPL w ..
 // CPL w + CPL - 1), so every lane runs CPL chains over one token and every
-// router value is a wavefront-wide broadcast. xn (transposed, rows padded to
-// 65 floats so the transposing stores and the row reads are conflict-free)
-// and the router rows go through LDS in chunks of RW_I values of i,
-// double-buffered in LDS and 4 / CPL chunks ahead in registers. CPL trades
-// chains per lane against workgroups (CPL = 1 for a few tokens). Needs d % RW_I == 0
-// and E % (4 CPL) == 0.
-constexpr int RW_T = 64, RW_I = 64;
+// router value is a wavefront-wide broadcast. xn (token-major, rows padded to
+// RW_I + 4 floats so that eight lanes reading 16 bytes of their own rows hit
+// distinct banks) and the router values (wavefront-major) go through LDS in
+// chunks of RW_I values of i, double-buffered in LDS and 4 / CPL chunks ahead
+// in registers; each lane reads four values of i of both with 16-byte reads.
+// CPL trades chains per lane against workgroups (CPL = 1 for a few tokens).
+// Needs d % RW_I == 0 and E % (4 CPL) == 0.
+constexpr int RW_T = 64, RW_I = 64, RW_LD = RW_I + 4;
 
 template <int CPL>
 struct alignas(4 * CPL) RwVec {
@@ -426,8 +427,8 @@ __global__ __launch_bounds__(256, 2) void k_router_logits_wide(const float *__re
     // chunks in flight in registers: a chunk's compute shrinks with CPL, so
     // fewer chains per lane prefetch further ahead
     constexpr int NP = 4 / CPL;
-    __shared__ float Xs[2][RW_I][RW_T + 1];
-    __shared__ V Ws[2][RW_I][4];
+    __shared__ __align__(16) float Xs[2][RW_T][RW_LD];
+    __shared__ __align__(16) V Ws[2][4][RW_I];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t0 = blockIdx.x * RW_T, e0 = blockIdx.y * 4 * CPL;
@@ -447,12 +448,13 @@ __global__ __launch_bounds__(256, 2) void k_router_logits_wide(const float *__re
     auto lstore = [&](int sl, int b) {
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            Xs[b][16 * q + 4 * k + 0][tt] = xr[sl][k].x;
-            Xs[b][16 * q + 4 * k + 1][tt] = xr[sl][k].y;
-            Xs[b][16 * q + 4 * k + 2][tt] = xr[sl][k].z;
-            Xs[b][16 * q + 4 * k + 3][tt] = xr[sl][k].w;
+            float *dst = &Xs[b][tt][16 * q + 4 * k];
+            dst[0] = xr[sl][k].x;
+            dst[1] = xr[sl][k].y;
+            dst[2] = xr[sl][k].z;
+            dst[3] = xr[sl][k].w;
         }
-        Ws[b][tid >> 2][tid & 3] = wr[sl];
+        Ws[b][tid & 3][tid >> 2] = wr[sl];
     };
     float s[CPL];
 #pragma unroll
@@ -471,12 +473,17 @@ __global__ __launch_bounds__(256, 2) void k_router_logits_wide(const float *__re
             const int c = ch + u;
             if (c >= nch) break;
             const int b = c & 1;
-#pragma unroll 16
-            for (int ii = 0; ii < RW_I; ii++) {
-                const float x = Xs[b][ii][lane];
-                const V w = Ws[b][ii][wave];
+#pragma unroll 4
+            for (int ii = 0; ii < RW_I; ii += 4) {
+                const float4 x4 = *(const float4 *)&Xs[b][lane][ii];
+                const float x[4] = {x4.x, x4.y, x4.z, x4.w};
+                V w[4];
 #pragma unroll
-                for (int k = 0; k < CPL; k++) s[k] = s[k] + w.v[k] * x;
+                for (int j = 0; j < 4; j++) w[j] = Ws[b][wave][ii + j];
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+#pragma unroll
+                    for (int k = 0; k < CPL; k++) s[k] = s[k] + w[j].v[k] * x[j];
             }
             // buffer b ^ 1 was last read in chunk c - 1, before the barrier
             // that ended it; slot (u + 1) % NP then takes chunk c + 1 + NP
