@@ -329,6 +329,7 @@ static_assert(NGU * GU_R * GU_LD <= SCR && DROWS * DN_LD <= SCR && LPW * D <= SC
 struct Lds {
     alignas(16) float x[D];
     alignas(16) float xn[NB * XN_LD];  // 32-blocks XN_LD floats apart
+    alignas(16) float xt[NB * XN_LD];  // fl(x * w), w the norm weight, laid out as xn
     alignas(16) int8_t xq[D];
     alignas(16) float scr[SCR];
     // expert outputs gathered for the combine; apart from scr, because rows
@@ -346,7 +347,9 @@ struct Lds {
     float bias[E];
     uint64_t etab[32];            // expf table
     int rk[4][E];                 // partial ranks
-    double part[NWAVE];
+    double part[NGU];             // the gate/up waves' partial sums of squares
+    unsigned ptag[NGU];           // the layer tag once part[w] is set
+    unsigned invtag;              // the layer tag once inv is set
     int order[E];                 // expert of each rank (ranks 0..K used)
     float inv;
     float sum;
@@ -464,6 +467,9 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
     for (int i = tid; i < D; i += NT) sh.x[i] = a.x[i];
     if (tid < E) sh.bias[tid] = a.bias ? a.bias[tid] : 0.0f;
     if (tid < 32) sh.etab[tid] = mia_expf_tab[tid];
+    // no tag of this launch ((epoch << 8) | layer) has this value
+    if (tid == 0) sh.invtag = (a.epoch + 1u) << 8;
+    if (tid < NGU) sh.ptag[tid] = (a.epoch + 1u) << 8;
 
     for (int l = 0; l < a.L; l++) {
         // Per-thread addresses are recomputed in every layer rather than held
@@ -475,62 +481,83 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
         TRACE(0);
         TRACE_CLK(30);
         // ---- A: rmsnorm (certified), xn, Q8(xn), logits -----------------------------
+        // Wavefront 0 computes the scale inv while the down waves form their
+        // logits' products without it, from xt_i = fl(x_i * w_i) (w the norm
+        // weight): p~_i = fl(W_ei * xt_i). The reference's product
+        // p_i = fl(W_ei * fl(fl(x_i * inv) * w_i)) is inv * p~_i * (1 + eta_i)
+        // with |eta_i| <= (1+u)^3 / (1-u)^2 - 1 < 5.0001 u (u = 2^-24, no
+        // underflow), so once inv is known the sums of p~ scaled by inv bound
+        // the reference's chain.
+#pragma unroll
+        for (int k = 0; k < D / NT; k++) {
+            const int i = tid + NT * k;
+            sh.xt[(i / 32) * XN_LD + i % 32] = sh.x[i] * wn[k];
+        }
         __syncthreads();
         TRACE(14);
-        {
+        // down waves, uniform in the wave: sum p~, sum_k |prefix_k|, sum |p~|
+        double lgS = 0.0, lgA = 0.0, lgP = 0.0;
+        if (gu_wave) {
+            // partial sums of squares, one per gate/up wave; wavefront 0
+            // adds them and brackets the scale. Any summation order is within
+            // (n + log2 n) 2^-53 S of the reference's sequential double sum
+            // (all terms >= 0); S -/+ m brackets it, and when both ends give
+            // the same fp32 scale it is the reference's. Otherwise lane 0
+            // runs the sequential sum.
             double ss = 0.0;
 #pragma unroll
-            for (int k = 0; k < D / NT; k++) {
-                const double v = (double)sh.x[tid + NT * k];
+            for (int k = 0; k < D / (NGU * 64); k++) {
+                const double v = (double)sh.x[tid + NGU * 64 * k];
                 ss = ss + v * v;
             }
             ss = lane63_d(wave_scan_d(ss));
-            if (lane == 0) sh.part[wave] = ss;
-        }
-        __syncthreads();
-        float inv;
-        {
-            // Every thread brackets the scale itself (same partials, same
-            // order, same result). Any summation order is within
-            // (n + log2 n) 2^-53 S of the reference's sequential sum (all
-            // terms >= 0); S -/+ m brackets it.
-            double S = 0.0;
-            for (int k = 0; k < NWAVE; k++) S = S + sh.part[k];
-            const double m = S * ((double)(D + 64) * 0x1p-52);
-            const float lo = (float)(1.0 / sqrt((S + m) / D + (double)a.eps));
-            const float hi = (float)(1.0 / sqrt((S - m) / D + (double)a.eps));
-            inv = lo;
-            if ((a.flags & MHIP_FORCE_SEQ_RMS) || lo != hi) {   // the same branch in every thread
-                if (tid == 0) {
-                    double sq = 0.0;
-                    for (int i = 0; i < D; i++) sq = sq + (double)sh.x[i] * (double)sh.x[i];
-                    sh.inv = (float)(1.0 / sqrt(sq / D + (double)a.eps));
-                    if (blockIdx.x == 0) status_update(ws, ST_RMS, a.epoch, true, 0);
+            if (lane == 0) {
+                sh.part[wave] = ss;
+                __hip_atomic_store(&sh.ptag[wave], tag, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+            if (wave == 0) {
+                long sp = 0;
+                for (;;) {
+                    const unsigned t = lane < NGU ? __hip_atomic_load(&sh.ptag[lane], __ATOMIC_ACQUIRE,
+                                                                      __HIP_MEMORY_SCOPE_WORKGROUP)
+                                                  : tag;
+                    if (__ballot(t != tag) == 0) break;
+                    __builtin_amdgcn_s_sleep(1);
+                    if (++sp > SPIN) {
+                        if (lane == 0) status_update(ws, ST_ABORT, a.epoch, false, 2);
+                        break;
+                    }
                 }
-                __syncthreads();
-                inv = sh.inv;
+                double S = 0.0;
+                for (int k = 0; k < NGU; k++) S = S + sh.part[k];
+                // lane 0 takes the lower end of the bracket, lane 1 the upper
+                const double m = S * ((double)(D + 64) * 0x1p-52);
+                const float end = (float)(1.0 / sqrt((lane == 1 ? S - m : S + m) / D + (double)a.eps));
+                const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(end), 0));
+                const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(end), 1));
+                float iv = lo;
+                if ((a.flags & MHIP_FORCE_SEQ_RMS) || lo != hi) {   // uniform in the wave
+                    float sq_inv = 0.0f;
+                    if (lane == 0) {
+                        double sq = 0.0;
+                        for (int i = 0; i < D; i++) sq = sq + (double)sh.x[i] * (double)sh.x[i];
+                        sq_inv = (float)(1.0 / sqrt(sq / D + (double)a.eps));
+                        if (blockIdx.x == 0) status_update(ws, ST_RMS, a.epoch, true, 0);
+                    }
+                    iv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq_inv)));
+                }
+                if (lane == 0) {
+                    sh.inv = iv;
+                    sh.nanflag = 0;
+                    __hip_atomic_store(&sh.invtag, tag, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
             }
-            if (tid == 0) sh.nanflag = 0;
-        }
-        TRACE(15);
-        {
-#pragma unroll
-            for (int k = 0; k < D / NT; k++) {
-                const int i = tid + NT * k;
-                sh.xn[(i / 32) * XN_LD + i % 32] = (sh.x[i] * inv) * wn[k];
-            }
-        }
-        __syncthreads();
-        TRACE_BY(20, NGU * 64);
-        // Parallel logits with a bound. The reference's logit is the
-        // sequential fp32 chain over p_i = fl(W_ei * xn_i); S = sum p_i in
-        // double, and |chain - S| <= 2^-24 * sum_k |S_k| (S_k the prefix sums).
-        if (!gu_wave) {
-            // This lane's 32 products (the reference's, fp32), summed in
-            // four independent stretches of 8; the prefix sums of the
-            // second pass restart each stretch from its own offset, so no
-            // dependency chain is longer than 8 additions.
-            const float4 *xv4 = (const float4 *)&sh.xn[lane * XN_LD];
+        } else if (!gu_wave) {
+            // This lane's 32 products, summed in four independent stretches
+            // of 8; the prefix sums of the second pass restart each stretch
+            // from its own offset, so no dependency chain is longer than 8
+            // additions.
+            const float4 *xv4 = (const float4 *)&sh.xt[lane * XN_LD];
             float pr[32];
 #pragma unroll
             for (int k = 0; k < 8; k++) {
@@ -540,12 +567,18 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                 pr[4 * k + 2] = wv.z * xv.z;
                 pr[4 * k + 3] = wv.w * xv.w;
             }
+            // sum |p~| in fp32 (32 terms >= 0: within 32 u of the exact sum,
+            // covered by the factor applied to lgP below)
             double cs[4];
+            float ap = 0.0f;
 #pragma unroll
             for (int m = 0; m < 4; m++) {
                 cs[m] = 0.0;
 #pragma unroll
-                for (int j = 0; j < 8; j++) cs[m] = cs[m] + (double)pr[8 * m + j];
+                for (int j = 0; j < 8; j++) {
+                    cs[m] = cs[m] + (double)pr[8 * m + j];
+                    ap = ap + fabsf(pr[8 * m + j]);
+                }
             }
             const double tot = (cs[0] + cs[1]) + (cs[2] + cs[3]);
             const double incl = wave_scan_d(tot);
@@ -564,20 +597,55 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                     run[m] = run[m] + (double)pr[8 * m + j];
                     ab[m] = ab[m] + fabs(run[m]);
                 }
-            const double absum = (ab[0] + ab[1]) + (ab[2] + ab[3]);
-            const double S = lane63_d(incl);
-            const double A = lane63_d(wave_scan_d(absum));
+            lgS = lane63_d(incl);
+            lgA = lane63_d(wave_scan_d((ab[0] + ab[1]) + (ab[2] + ab[3])));
+            lgP = lane63_d(wave_scan_d((double)ap)) * (1.0 + 0x1p-16);
             TRACE_BY(22, NGU * 64);
-            if (lane == 0) {
-                // S goes out rounded to fp32 (|S - Sf| <= 2^-24 |Sf|, plus an
-                // absolute 2^-150 for subnormals); the bound grows by that and
-                // is rounded upwards to fp32 by the (1 + 2^-22) factor.
-                const int e = rank * LPW + wave - NGU;
-                const float Sf = (float)S;
-                const double B = A * 0x1p-24 * (1.0 + 0x1p-8) + 0x1p-24 * fabs((double)Sf) + 1e-30;
-                put_tagged<true>(&ws->lgs[xcd][e], Sf, tag);
-                put_tagged<true>(&ws->lgb[xcd][e], (float)(B * (1.0 + 0x1p-22)), tag);
+        }
+        // every wave takes inv from wavefront 0 (LDS, release / acquire);
+        // wavefront 0 never waits for another, so the wait ends
+        {
+            long sp = 0;
+            while (__hip_atomic_load(&sh.invtag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != tag) {
+                __builtin_amdgcn_s_sleep(1);
+                if (++sp > SPIN) {
+                    if (lane == 0) status_update(ws, ST_ABORT, a.epoch, false, 2);
+                    break;
+                }
             }
+        }
+        const float inv = sh.inv;
+        TRACE(15);
+        {
+#pragma unroll
+            for (int k = 0; k < D / NT; k++) {
+                const int i = tid + NT * k;
+                sh.xn[(i / 32) * XN_LD + i % 32] = (sh.x[i] * inv) * wn[k];
+            }
+        }
+        if (!gu_wave && lane == 0) {
+            // The logit S = inv * sum p~ (double) and its bound: the
+            // reference's chain L over p is within u (1 + 2^-8) sum_k |S_k|
+            // of the exact sum of p (S_k its prefix sums; the slack covers
+            // the chain's own drift and the double sums), sum_k |S_k| <=
+            // inv * lgA + D * Ep, and the exact sum of p is within
+            // Ep = 5.0001 u inv lgP of inv * lgS. S goes out rounded to fp32
+            // (|S - Sf| <= u |Sf|, 2^-52 |S| for the double product, 2^-100
+            // for subnormal products); the bound is rounded upwards to fp32
+            // by the (1 + 2^-22) factor.
+            const int e = rank * LPW + wave - NGU;
+            const double di = (double)inv;
+            const double S = di * lgS;
+            const float Sf = (float)S;
+            const double Ep = 5.0001 * 0x1p-24 * di * lgP;
+            const double B = 0x1p-24 * (1.0 + 0x1p-8) * (di * lgA + (double)D * Ep) + Ep +
+                             0x1p-24 * fabs((double)Sf) + 0x1p-52 * fabs(S) + 0x1p-100;
+            put_tagged<true>(&ws->lgs[xcd][e], Sf, tag);
+            put_tagged<true>(&ws->lgb[xcd][e], (float)(B * (1.0 + 0x1p-22)), tag);
+        }
+        __syncthreads();
+        TRACE_BY(20, NGU * 64);
+        if (!gu_wave) {
             // Q8(xn) for stage C, while the logits travel (quant.c:11-27 per
             // element): four lanes per 32-block, eight elements each, the
             // block maximum over the quad by DPP (order-free).

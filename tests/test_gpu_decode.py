@@ -160,3 +160,28 @@ def test_host_layer_one_token_uses_decode_launch(oracle, qwen_dims, moe):
         assert np.array_equal(w.view(np.uint32), wo[0].view(np.uint32)), "layer %d gate weights" % l
         assert np.array_equal(x[0].view(np.uint32), xo[0].view(np.uint32)), "layer %d output" % l
 
+
+
+def test_decode_routing_many_tokens(oracle, qwen_dims, moe):
+    """Certified routing over many inputs: 24 tokens through every layer of
+    the handle, one launch per layer, each layer's expert indices bit-equal
+    to the oracle's routing of the same input (rmsnorm, router product,
+    softmax, top-8), with the layer's output as the next layer's input."""
+    say("test_decode_routing_many_tokens")
+    d = qwen_dims
+    norm = np.ones(d.dim, np.float32)
+    routers = [oracle.synth_router(W.WEIGHT_SEED, l, d) for l in range(LAYERS)]
+    xs = oracle.synth_x(W.X_SEED + 101, 24, d.dim)
+    checked = 0
+    for t in range(xs.shape[0]):
+        x = xs[t]
+        for l in range(LAYERS):
+            xn = oracle.rmsnorm(x, norm, d.norm_eps)
+            lg = oracle.matvec(routers[l], 0, xn, d.n_experts, d.dim)
+            io, _, _ = oracle.route(lg, d.n_active)
+            xg, ig, _ = moe.decode(l, l + 1, x)
+            assert moe.decode_status()[0] == 0
+            assert np.array_equal(ig[0], io), "token %d layer %d: %s vs %s" % (t, l, ig[0], io)
+            checked += 1
+            x = np.asarray(xg, np.float32)
+    say("  %d layer routings bit-equal, status %s" % (checked, moe.decode_status()))
