@@ -351,8 +351,10 @@ __global__ __launch_bounds__(GT, 2) void k_gateup_mfma(
     const int *__restrict__ glight, const int *__restrict__ perm, _Float16 *__restrict__ hdq, int d,
     int eh, int K, int A) {
     __shared__ GateUpLds L;
+    __shared__ uint64_t etab[32];  // the expf table, for the SwiGLU lookups
     TileRef tr;
     if (!tile_of(groups, gtile, glight, eh / (TN / 2), tr)) return;
+    if (threadIdx.x < 32) etab[threadIdx.x] = mia_expf_tab[threadIdx.x];  // read after the k loop's barriers
     const int base = tr.base, nrows = tr.nrows;
     const int h0 = tr.y * (TN / 2);
     const uint8_t *ex = table + (size_t)tr.e * lay.expert_bytes;
@@ -414,7 +416,7 @@ __global__ __launch_bounds__(GT, 2) void k_gateup_mfma(
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const float gv = acc[i][j][r], uv = acc[i + 2][j][r];
-                hv[r] = (gv / (1.0f + mia_expf_glibc(-gv))) * uv;
+                hv[r] = (gv / (1.0f + mia_expf_glibc_tab(-gv, etab))) * uv;
             }
             *(f4v *)&L.o[16 * j + l16][(WN / 2) * wave + 16 * i + 4 * c] = hv;
         }
