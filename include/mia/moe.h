@@ -46,7 +46,7 @@ int mia_moe_open(mia_moe **out, const mia_moe_config *cfg, char *err, size_t err
 void mia_moe_close(mia_moe *m);
 const char *mia_moe_error(const mia_moe *m);
 
-/* Reference blob geometry for this shape (src/storage/mia_file.c:275-283,
+/* Reference blob geometry for this shape (src/storage/mia_file.c:98-101,
  * tools/internal/mia/format.go:160-163). */
 size_t mia_moe_blob_bytes(const mia_moe *m);
 size_t mia_moe_off_up(const mia_moe *m);
@@ -72,7 +72,9 @@ int mia_moe_synth(mia_moe *m, uint64_t seed);
 /* One layer, moe() semantics, in place on host x[T][dim]. Bit-equal to the
  * reference (below MHIP_GEMM_MIN_A assignments; within 1e-3 above). One
  * token (T = 1) runs as one launch of the persistent decode kernel with the
- * exact router where mhip_decode_supported allows it, else per stage. */
+ * exact router where mhip_decode_supported allows it, else per stage; a
+ * decode launch that aborts is rerun per stage (same bits). A failing call
+ * names the first layer that met an expert index out of range. */
 int mia_moe_layer(mia_moe *m, int layer, float *x, int T);
 /* As mia_moe_layer with an optional logit bias[E] (added after the router,
  * before the softmax) and optional outputs idx[T][K], w[T][K] and
@@ -93,7 +95,9 @@ int mia_moe_stack_dev(mia_moe *m, int l0, int l1, float *d_x, int T);
  * (host) is updated in place; idx/w ([l1-l0][K]) receive the routing when
  * not NULL; bias (E floats) applies to every layer when not NULL. Expert
  * indices are bit-equal to the reference; the output is within ~1e-6
- * relative of it (the gate weights come from the parallel router logits). */
+ * relative of it (the gate weights come from the parallel router logits).
+ * Should the launch abort, the layers are rerun per stage (bit-equal to the
+ * reference) and mia_moe_decode_status shows the aborted launch. */
 int mia_moe_decode(mia_moe *m, int l0, int l1, float *x, const float *bias, int *idx, float *w);
 /* Same on device memory, queued on the handle's stream; check
  * mia_moe_decode_status after the stream completes. */

@@ -137,11 +137,12 @@ typedef struct {
     float *tmp;       /* [T*K][d]  down output, bucketed order */
     int *status;      /* [4] device-side error/diagnostic words */
     void *xdq;        /* [T][d]    fp16: the Q8 codes of xn (matrix-core path) */
-    void *hdq;        /* [T*K][eh] fp16: d_h * q_h of Q8(h), bucketed (matrix-core path) */
+    void *hdq;        /* [T*K][eh] fp16: the Q8 codes of h, bucketed (matrix-core path) */
     int *gtile;       /* [E+1]     tiles of MHIP_GEMM_TM rows before each group */
     float *xsb;       /* [d/32][T*K] Q8 scales of xn per assignment, bucketed (matrix-core path) */
     int8_t *hq;       /* [T*K][eh] Q8 codes of h, bucketed (vector path) */
-    float *hs;        /* [T*K][eh/32] Q8 scales of h, bucketed (vector path) */
+    float *hs;        /* Q8 scales of h, bucketed: [T*K][eh/32] (vector path), or
+                         [eh/32][T*K] block-major (matrix-core path) */
     int *glight;      /* [E+1]     light tiles (at most MHIP_GEMM_TM/2 rows) before each group */
 } mhip_scratch;
 
@@ -157,6 +158,8 @@ int mhip_scratch_carve(const mhip_dims *s, int max_tokens, void *d_base,
 #define MHIP_FORCE_EXACT_ROUTER 2 /* decode stack: always the exact router chain */
 #define MHIP_DECODE_TRACE 4       /* decode stack: record stage timestamps */
 #define MHIP_EXACT_EXPERTS 8      /* layer: bit-exact expert products at every T */
+#define MHIP_DECODE_FORCE_ABORT 16 /* decode stack: report abort bit 4 and stop after the
+                                      start barrier (tests the callers' abort handling) */
 
 /*
  * One MoE layer (rmsnorm -> router/top-K -> dispatch -> gate/up+SwiGLU ->
@@ -168,12 +171,13 @@ int mhip_scratch_carve(const mhip_dims *s, int max_tokens, void *d_base,
  * Routing (indices, order, gate weights) is bit-equal to the reference at
  * every T. The expert products are bit-equal too for small batches; from
  * MHIP_GEMM_MIN_A assignments on (and when the shape allows: d a multiple of
- * 256, expert_hidden of 128) they run on the matrix cores: the gate/up block
- * dots stay exact and each block term is added with one fused multiply-add
- * (h within a few fp32 ulps of the reference's), the down product takes fp16
- * operands; the layer output stays within 1e-3 relative of the reference
- * (max|diff| / max|ref|, measured <= 5.5e-4 on the update). MHIP_EXACT_EXPERTS
- * keeps the bit-exact vector path at every T.
+ * 256, expert_hidden of 128) they run on the matrix cores: the gate/up and
+ * down block dots stay exact integers and each block term is added with one
+ * fused multiply-add, so h and the expert outputs are within a few fp32 ulps
+ * of the reference's and Q8(h) differs only in a code whose h lies that
+ * close to a rounding boundary; the layer output stays within 1e-3 relative
+ * of the reference (max|diff| / max|ref|). MHIP_EXACT_EXPERTS keeps the
+ * bit-exact vector path at every T.
  */
 #define MHIP_GEMM_MIN_A 2048
 int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
@@ -187,16 +191,19 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
  * expert_hidden 768) on a 256-CU MI355X. d_table/d_router ([L][E][d], each
  * layer in the decode layout of mhip_router_decode_layout)/
  * d_router_t ([L][d][E])/d_norm ([L][d]) start at the first layer; d_bias
- * (E floats, every layer) may be NULL; d_x[d] is updated in place. d_ws is a
+ * (E floats, every layer) may be NULL; d_x[d] is updated in place; L is at
+ * most MHIP_DECODE_MAX_LAYERS (-1 beyond, before any device work). d_ws is a
  * workspace of mhip_decode_ws_bytes() bytes (not shared by concurrent
  * launches). d_idx/d_w ([L][n_active]) receive the routing when non-NULL.
  * Expert indices are bit-equal to the reference (certified parallel router,
  * exact fallback); the gate weights come from the parallel logits, within
  * ~1e-6 relative of the reference's. After the stream completes,
  * mhip_decode_status reports [0] abort bits (1: workgroups not on the
- * expected XCDs, 2: a wait timed out; the output is then invalid),
+ * expected XCDs, 2: a wait timed out, 4: MHIP_DECODE_FORCE_ABORT; the
+ * output is then invalid),
  * [1] rmsnorm fallbacks, [2] layers routed by the exact fallback.
  */
+#define MHIP_DECODE_MAX_LAYERS 256 /* layers of one decode-stack launch */
 size_t mhip_decode_ws_bytes(void);
 /* 1 when mhip_decode_stack can run this shape on this device (the
  * Qwen3-30B-A3B expert shape, 2048/128/<=8/768, and one 512-thread workgroup

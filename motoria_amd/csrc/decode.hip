@@ -139,7 +139,9 @@ __device__ void status_update(DecodeWs *ws, int i, unsigned epoch, bool add, uns
         old = prev;
     }
 }
-// Abort bits: 1 = workgroup not on the expected XCD, 2 = a wait timed out.
+// Abort bits: 1 = workgroup not on the expected XCD, 2 = a wait timed out,
+// 4 = forced by the caller (MHIP_DECODE_FORCE_ABORT; every workgroup leaves
+// after the start barrier).
 __device__ __forceinline__ bool aborted(DecodeWs *ws, unsigned epoch) {
     return status_get(ws, ST_ABORT, epoch) != 0;
 }
@@ -424,6 +426,8 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
     // workspace was cleared).
     if (tid == 0) {
         if (xcc_id() != (unsigned)xcd) status_update(ws, ST_ABORT, a.epoch, false, 1);
+        if ((a.flags & MHIP_DECODE_FORCE_ABORT) && blockIdx.x == 0)
+            status_update(ws, ST_ABORT, a.epoch, false, 4);
         __builtin_amdgcn_s_waitcnt(0);
         __hip_atomic_fetch_add(&ws->gstart[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         wait_flag(ws, &ws->gstart[0], NWG * a.epoch, a.epoch);
@@ -1038,12 +1042,17 @@ int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
                       const void *d_table, const float *d_router, const float *d_router_t,
                       const float *d_norm, const float *d_bias, float *d_x, int L, void *d_ws,
                       int *d_idx, float *d_w, int flags) {
-    if (mhip::check_dims(c, s) || mhip::use_device(c)) return -1;
+    // Arguments first (no device call before they pass). Exchange tags hold
+    // the layer in 8 bits, so one launch covers at most 256 layers.
+    if (mhip::check_dims(c, s)) return -1;
+    if (L < 0 || L > MHIP_DECODE_MAX_LAYERS)
+        return mhip::fail(c, "decode stack: L=%d outside [0, %d]", L, MHIP_DECODE_MAX_LAYERS);
     if (!decode_shape_fits(s))
         return mhip::fail(c, "decode stack: shape %d/%d/%d/%d is not the supported "
                              "2048/128/<=8/768", s->dim, s->n_experts, s->n_active,
                           s->expert_hidden);
-    if (L <= 0) return L == 0 ? 0 : mhip::fail(c, "decode stack: L=%d", L);
+    if (L == 0) return 0;
+    if (mhip::use_device(c)) return -1;
     const int fits = decode_device_fits(c);
     if (fits < 0) return -1;
     if (!fits)

@@ -6,19 +6,17 @@
 //   k_gateup_mfma  h = SwiGLU(Wg x, Wu x), then Q8_0(h)   forward.c:186-192
 //   k_down_mfma    tmp = Wd Q8(h)                           forward.c:192-193
 //
-// gate/up: the operands are the Q8_0 codes themselves, as fp16 integers, so
+// Both products run on the Q8_0 codes themselves, as fp16 integers:
 // v_mfma_f32_16x16x32_f16 over one 32-value block gives the exact int32
 // block dot (every partial sum is an integer below 2^24). The reference's
 // block term ((float)acc * d_w) * d_x is added to the row sum in block order
 // by the vector ALUs (matmul.c:19-28) with one fused multiply-add: the term's
-// last rounding and the addition's become one, so h is the reference's to
-// within a few fp32 ulps (~1e-7 relative). Q8(h) then differs from the
-// reference's in the rare code whose h sits within that distance of a
-// rounding boundary (one code step moves an output by < 1e-4 relative).
-//
-// down takes the reference's dequantized values (d * q for the weights,
-// d_h * q_h for h) rounded to fp16 on the matrix cores with fp32
-// accumulation: ~1e-4 relative of the reference, within the path's 1e-3.
+// last rounding and the addition's become one, so every row sum is the
+// reference's to within a few fp32 ulps (~1e-7 relative). gate/up writes
+// Q8(h) as fp16 codes plus block-major scales, which down reads the same way
+// as gate/up reads Q8(xn); no operand is ever rounded to fp16. Q8(h) differs
+// from the reference's only in the rare code whose h sits within those few
+// ulps of a rounding boundary.
 //
 // Tiles: 256 weight rows x 128 assignments (rows of one expert's bucket),
 // one 32-value Q8_0 block of k per step. Wavefront w owns weight rows
@@ -50,15 +48,14 @@ constexpr int KB = 32;            // k per step: one Q8_0 block
 constexpr int WN = TN / 4;        // weight rows per wavefront (64)
 constexpr int MI = WN / 16;       // 16-row weight tiles per wavefront (4)
 constexpr int NJ = TM / 16;       // 16-row assignment tiles (8)
-constexpr int NS_GU = 4;          // ring stages: gate/up (two workgroups per CU)
-constexpr int NS_DN = 3;          // down (three workgroups per CU)
+constexpr int NS = 4;             // ring stages (two workgroups per CU)
 constexpr int OLD = TM + 4;       // gate/up epilogue tile row stride (floats): 128 columns + pad
 constexpr int DLD = WN + 4;       // down epilogue tile row stride: 64 columns + pad
 
 static_assert(TM == 128 && TN == 256 && GT == 256, "tiling");
 
 // One step of the ring.
-//   x:  assignment rows, 32 fp16 codes/values = 4 chunks of 16 bytes; chunk c
+//   x:  assignment rows, 32 fp16 codes = 4 chunks of 16 bytes; chunk c
 //       of row m sits at slot c ^ ((m >> 1) & 3), so the eight rows that
 //       eight consecutive lanes read at one chunk fall on distinct banks;
 //   w:  weight rows, 32 int8 codes = 2 halves of 16 bytes; half h of row n
@@ -215,15 +212,14 @@ __device__ __forceinline__ Pieces pieces() {
 // The k loop over nk steps (nk >= NS - 1). On return acc[i][j][r] holds
 //   C[64*wave + 16*i + 4*(lane/16) + r][16*j + lane%16]
 // (weight row, assignment row) for the assignment tiles j < NJA (the tiles
-// that hold rows of the bucket; the others are not computed). GATEUP: exact block dots, and the block
-// terms added with their scales; otherwise fp16 dequantized weights
-// (d_w * q) accumulated on the matrix cores.
-template <bool GATEUP, int NS, int NJA>
+// that hold rows of the bucket; the others are not computed): the exact
+// block dots, each block term added with its two scales in block order.
+template <int NJA>
 __device__ __forceinline__ void gemm_tile(Step *ring, const Src &src, int nk, f4v acc[MI][NJ]) {
     static_assert(NJA >= 1 && NJA <= NJ, "assignment tiles");
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    constexpr int NLOAD = GATEUP ? 6 : 5;  // global_load_lds per wavefront per step
+    constexpr int NLOAD = 6;  // global_load_lds per wavefront per step
     const unsigned ring0 = lds_addr(ring);
     const unsigned ox = (unsigned)offsetof(Step, x) + (2 * wave) * 1024;
     const unsigned ow = (unsigned)offsetof(Step, w) + (2 * wave) * 1024;
@@ -237,7 +233,7 @@ __device__ __forceinline__ void gemm_tile(Step *ring, const Src &src, int nk, f4
         dma16(st + ow, src.w0 + (size_t)k * KB);
         dma16(st + ow + 1024, src.w1 + (size_t)k * KB);
         dma4(st + osw, src.sw + (size_t)k * src.swstep);
-        if (GATEUP && lane < 32) dma4(st + osx, src.sx + (size_t)k * src.sxstep);
+        if (lane < 32) dma4(st + osx, src.sx + (size_t)k * src.sxstep);
     };
 #pragma unroll
     for (int s = 0; s < NS - 1; s++) issue(s);
@@ -260,60 +256,56 @@ __device__ __forceinline__ void gemm_tile(Step *ring, const Src &src, int nk, f4
             const int n = WN * wave + 16 * i + l16;
             const uint2 q = *(const uint2 *)&S.w[n][16 * wslot(n, c >> 1) + 8 * (c & 1)];
             av[i] = codes8(q.x, q.y);
-            if (GATEUP) {
-                s4[i] = *(const f4v *)&S.sw[WN * wave + 16 * i + 4 * c];
-            } else {
-                const _Float16 sc = (_Float16)S.sw[n];
-                const h8 s8 = {sc, sc, sc, sc, sc, sc, sc, sc};
-                av[i] = av[i] * s8;
-            }
+            s4[i] = *(const f4v *)&S.sw[WN * wave + 16 * i + 4 * c];
         }
-        if (GATEUP) {
-            // The block dots of assignment tile j + 1 are started before the
-            // terms of tile j are added, so the vector ALUs never wait for
-            // the product they consume.
-            const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};
-            // x scales of this lane's assignment rows 16 j + l16, j < 8
-            const f4v sxa = *(const f4v *)&S.sx[8 * l16], sxb = *(const f4v *)&S.sx[8 * l16 + 4];
-            f4v blk[2][MI];
-            {
-                const h8 bv = *(const h8 *)&S.x[l16][8 * xslot(l16, c)];
+        // The block dots of assignment tile j + 1 are started before the
+        // terms of tile j are added, so the vector ALUs never wait for the
+        // product they consume.
+        const f4v z = {0.0f, 0.0f, 0.0f, 0.0f};
+        // x scales of this lane's assignment rows 16 j + l16, j < 8
+        const f4v sxa = *(const f4v *)&S.sx[8 * l16], sxb = *(const f4v *)&S.sx[8 * l16 + 4];
+        f4v blk[2][MI];
+        {
+            const h8 bv = *(const h8 *)&S.x[l16][8 * xslot(l16, c)];
 #pragma unroll
-                for (int i = 0; i < MI; i++)
-                    blk[0][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv, z, 0, 0, 0);
-            }
-#pragma unroll
-            for (int j = 0; j < NJA; j++) {
-                if (j + 1 < NJA) {
-                    const int m1 = 16 * (j + 1) + l16;
-                    const h8 bv = *(const h8 *)&S.x[m1][8 * xslot(m1, c)];
-#pragma unroll
-                    for (int i = 0; i < MI; i++)
-                        blk[(j + 1) & 1][i] =
-                            __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv, z, 0, 0, 0);
-                }
-                const float sx = j < 4 ? sxa[j & 3] : sxb[j & 3];
-#pragma unroll
-                for (int i = 0; i < MI; i++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        acc[i][j][r] =
-                            __builtin_fmaf(blk[j & 1][i][r] * s4[i][r], sx, acc[i][j][r]);
-            }
+            for (int i = 0; i < MI; i++)
+                blk[0][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv, z, 0, 0, 0);
         }
-        if (!GATEUP) {
 #pragma unroll
-            for (int j = 0; j < NJA; j++) {
-                const int m = 16 * j + l16;
-                const h8 bv = *(const h8 *)&S.x[m][8 * xslot(m, c)];
+        for (int j = 0; j < NJA; j++) {
+            if (j + 1 < NJA) {
+                const int m1 = 16 * (j + 1) + l16;
+                const h8 bv = *(const h8 *)&S.x[m1][8 * xslot(m1, c)];
 #pragma unroll
                 for (int i = 0; i < MI; i++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv, acc[i][j], 0, 0, 0);
+                    blk[(j + 1) & 1][i] =
+                        __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv, z, 0, 0, 0);
             }
+            const float sx = j < 4 ? sxa[j & 3] : sxb[j & 3];
+#pragma unroll
+            for (int i = 0; i < MI; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    acc[i][j][r] = __builtin_fmaf(blk[j & 1][i][r] * s4[i][r], sx, acc[i][j][r]);
         }
     }
     wait_vm<0>();  // the reloads past the end
     __syncthreads();
+}
+
+// The assignment tiles that hold rows of the bucket (a bucket's last tile
+// may hold few rows).
+__device__ __forceinline__ void gemm_tile_rows(Step *ring, const Src &src, int nk, int nrows,
+                                               f4v acc[MI][NJ]) {
+    const int nj = (nrows + 15) / 16;
+    if (nj > 4)
+        gemm_tile<8>(ring, src, nk, acc);
+    else if (nj > 2)
+        gemm_tile<4>(ring, src, nk, acc);
+    else if (nj > 1)
+        gemm_tile<2>(ring, src, nk, acc);
+    else
+        gemm_tile<1>(ring, src, nk, acc);
 }
 
 // ---- x block scales in bucketed, block-major order --------------------------------
@@ -328,16 +320,16 @@ __global__ __launch_bounds__(256) void k_xs_bucket(const float *__restrict__ xs,
 }
 
 union alignas(16) GateUpLds {
-    Step ring[NS_GU];
+    Step ring[NS];
     float o[TM][OLD];  // epilogue: 128 assignment rows x 128 h columns
 };
 union alignas(16) DownLds {
-    Step ring[NS_DN];
+    Step ring[NS];
     float o[TM][DLD];  // epilogue: 128 assignment rows x 64 down rows
 };
-static_assert(sizeof(GateUpLds) == NS_GU * sizeof(Step) && sizeof(DownLds) == NS_DN * sizeof(Step),
+static_assert(sizeof(GateUpLds) == NS * sizeof(Step) && sizeof(DownLds) == NS * sizeof(Step),
               "epilogue tiles fit the rings");
-static_assert(3 * sizeof(DownLds) <= 160 * 1024, "three down workgroups per CU");
+static_assert(2 * sizeof(DownLds) <= 160 * 1024, "two workgroups per CU");
 
 // ---- gate/up + SwiGLU + Q8(h) ----------------------------------------------------
 //
@@ -348,8 +340,8 @@ static_assert(3 * sizeof(DownLds) <= 160 * 1024, "three down workgroups per CU")
 __global__ __launch_bounds__(GT, 2) void k_gateup_mfma(
     const uint8_t *__restrict__ table, mhip_layout lay, const _Float16 *__restrict__ xq16,
     const float *__restrict__ xsb, const int *__restrict__ groups, const int *__restrict__ gtile,
-    const int *__restrict__ glight, const int *__restrict__ perm, _Float16 *__restrict__ hdq, int d,
-    int eh, int K, int A) {
+    const int *__restrict__ glight, const int *__restrict__ perm, _Float16 *__restrict__ hq16,
+    float *__restrict__ hsb, int d, int eh, int K, int A) {
     __shared__ GateUpLds L;
     __shared__ uint64_t etab[32];  // the expf table, for the SwiGLU lookups
     TileRef tr;
@@ -395,16 +387,7 @@ __global__ __launch_bounds__(GT, 2) void k_gateup_mfma(
     for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = (f4v){0.0f, 0.0f, 0.0f, 0.0f};
-    // a bucket's last tile may hold few rows: only its assignment tiles run
-    const int nj = (nrows + 15) / 16;
-    if (nj > 4)
-        gemm_tile<true, NS_GU, 8>(L.ring, src, d / KB, acc);
-    else if (nj > 2)
-        gemm_tile<true, NS_GU, 4>(L.ring, src, d / KB, acc);
-    else if (nj > 1)
-        gemm_tile<true, NS_GU, 2>(L.ring, src, d / KB, acc);
-    else
-        gemm_tile<true, NS_GU, 1>(L.ring, src, d / KB, acc);
+    gemm_tile_rows(L.ring, src, d / KB, nrows, acc);
 
     // SwiGLU into the h tile (LDS, reused): row = assignment, column = h - h0
     const int c = lane >> 4, l16 = lane & 15;
@@ -422,8 +405,10 @@ __global__ __launch_bounds__(GT, 2) void k_gateup_mfma(
         }
     __syncthreads();
     {
-        // Q8_0 of 32-blocks of h (quant.c:11-27), stored dequantized: thread
-        // (m, b2) does blocks 2 b2 and 2 b2 + 1 of row m
+        // Q8_0 of 32-blocks of h (quant.c:11-27): the codes as fp16 integers
+        // (bucketed rows) and the scales block-major (hsb[block][row], the
+        // down kernel's x scales); thread (m, b2) does blocks 2 b2 and
+        // 2 b2 + 1 of row m
         const int m = tid >> 1, b2 = tid & 1;
         if (m < nrows) {
 #pragma unroll
@@ -446,10 +431,11 @@ __global__ __launch_bounds__(GT, 2) void k_gateup_mfma(
                 const float qi = dsc != 0.0f ? 1.0f / dsc : 0.0f;
                 h8 o[4];
 #pragma unroll
-                for (int k = 0; k < 32; k++) o[k >> 3][k & 7] = (_Float16)(roundf(v[k] * qi) * dsc);
-                h8 *dst = (h8 *)(hdq + (size_t)(base + m) * eh + h0 + 32 * blk);
+                for (int k = 0; k < 32; k++) o[k >> 3][k & 7] = (_Float16)roundf(v[k] * qi);
+                h8 *dst = (h8 *)(hq16 + (size_t)(base + m) * eh + h0 + 32 * blk);
 #pragma unroll
                 for (int k = 0; k < 4; k++) dst[k] = o[k];
+                hsb[(size_t)(h0 / KB + blk) * A + base + m] = dsc;
             }
         }
     }
@@ -458,16 +444,19 @@ __global__ __launch_bounds__(GT, 2) void k_gateup_mfma(
 // ---- down -----------------------------------------------------------------------------
 //
 // blockIdx.x = tile of assignment rows x 8 column tiles of 256 consecutive
-// down rows n0..n0+255. The x operand is the tile's Q8(h) (fp16, bucketed
-// order, contiguous). Results go out through LDS in two halves of 128
-// columns, so every assignment row is written as 512 contiguous bytes.
-__global__ __launch_bounds__(GT, 3) void k_down_mfma(const uint8_t *__restrict__ table,
+// down rows n0..n0+255. The x operand is the tile's Q8(h) (fp16 codes,
+// bucketed order, contiguous) with its block-major scales. Results go out
+// through LDS a wavefront's 64 columns at a time, so every assignment row is
+// written as 256 contiguous bytes.
+__global__ __launch_bounds__(GT, 2) void k_down_mfma(const uint8_t *__restrict__ table,
                                                      mhip_layout lay,
-                                                     const _Float16 *__restrict__ hdq,
+                                                     const _Float16 *__restrict__ hq16,
+                                                     const float *__restrict__ hsb,
                                                      const int *__restrict__ groups,
                                                      const int *__restrict__ gtile,
                                                      const int *__restrict__ glight,
-                                                     float *__restrict__ tmp, int d, int eh) {
+                                                     float *__restrict__ tmp, int d, int eh,
+                                                     int A) {
     __shared__ DownLds L;
     TileRef tr;
     if (!tile_of(groups, gtile, glight, d / TN, tr)) return;
@@ -479,15 +468,17 @@ __global__ __launch_bounds__(GT, 3) void k_down_mfma(const uint8_t *__restrict__
     Src src;
     {
         const Pieces p = pieces();
-        src.x0 = hdq + (size_t)(base + min(p.xr0, nrows - 1)) * eh + p.xc0 * 8;
-        src.x1 = hdq + (size_t)(base + min(p.xr1, nrows - 1)) * eh + p.xc1 * 8;
+        src.x0 = hq16 + (size_t)(base + min(p.xr0, nrows - 1)) * eh + p.xc0 * 8;
+        src.x1 = hq16 + (size_t)(base + min(p.xr1, nrows - 1)) * eh + p.xc1 * 8;
         const int8_t *dq = (const int8_t *)(ex + lay.down_q);
         src.w0 = dq + (size_t)(n0 + p.wr0) * eh + 16 * p.wh0;
         src.w1 = dq + (size_t)(n0 + p.wr1) * eh + 16 * p.wh1;
         src.sw = (const float *)(ex + lay.down_st) + n0 + WN * wave + lane;
         src.swstep = d;
-        src.sx = nullptr;
-        src.sxstep = 0;
+        // sx slot p = 32 wave + lane holds bucket row 16 (p % 8) + p / 8
+        const int ps = 32 * wave + (lane & 31);
+        src.sx = hsb + base + min(16 * (ps & 7) + (ps >> 3), nrows - 1);
+        src.sxstep = A;
     }
 
     f4v acc[MI][NJ];
@@ -495,15 +486,7 @@ __global__ __launch_bounds__(GT, 3) void k_down_mfma(const uint8_t *__restrict__
     for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = (f4v){0.0f, 0.0f, 0.0f, 0.0f};
-    const int nj = (nrows + 15) / 16;
-    if (nj > 4)
-        gemm_tile<false, NS_DN, 8>(L.ring, src, eh / KB, acc);
-    else if (nj > 2)
-        gemm_tile<false, NS_DN, 4>(L.ring, src, eh / KB, acc);
-    else if (nj > 1)
-        gemm_tile<false, NS_DN, 2>(L.ring, src, eh / KB, acc);
-    else
-        gemm_tile<false, NS_DN, 1>(L.ring, src, eh / KB, acc);
+    gemm_tile_rows(L.ring, src, eh / KB, nrows, acc);
 
     const int c = lane >> 4, l16 = lane & 15;
 #pragma unroll
@@ -535,8 +518,8 @@ namespace mhip {
 
 bool gemm_path_fits(const mhip_dims *s) {
     // whole tiles of weight rows, and enough k steps to fill the rings
-    return s->dim % TN == 0 && s->expert_hidden % (TN / 2) == 0 && s->dim / KB >= NS_GU - 1 &&
-           s->expert_hidden / KB >= NS_DN - 1;
+    return s->dim % TN == 0 && s->expert_hidden % (TN / 2) == 0 && s->dim / KB >= NS - 1 &&
+           s->expert_hidden / KB >= NS - 1;
 }
 
 int gemm_max_tiles(int A, int E) { return (A + TM - 1) / TM + (A < E ? A : E); }
@@ -556,8 +539,8 @@ int launch_gateup_mfma(hipStream_t st, const mhip_dims *s, const mhip_layout *la
     const unsigned grid = gemm_grid(A, s->n_experts, eh / (TN / 2));
     k_gateup_mfma<<<grid, GT, 0, st>>>((const uint8_t *)d_table_layer, *lay,
                                        (const _Float16 *)sc->xdq, sc->xsb, sc->groups,
-                                       sc->gtile, sc->glight, sc->perm, (_Float16 *)sc->hdq, d, eh,
-                                       s->n_active, A);
+                                       sc->gtile, sc->glight, sc->perm, (_Float16 *)sc->hdq,
+                                       sc->hs, d, eh, s->n_active, A);
     return (int)hipGetLastError();
 }
 
@@ -566,8 +549,8 @@ int launch_down_mfma(hipStream_t st, const mhip_dims *s, const mhip_layout *lay,
     const int d = s->dim, eh = s->expert_hidden;
     const unsigned grid = gemm_grid(A, s->n_experts, d / TN);
     k_down_mfma<<<grid, GT, 0, st>>>((const uint8_t *)d_table_layer, *lay,
-                                     (const _Float16 *)sc->hdq, sc->groups, sc->gtile, sc->glight,
-                                     sc->tmp, d, eh);
+                                     (const _Float16 *)sc->hdq, sc->hs, sc->groups, sc->gtile,
+                                     sc->glight, sc->tmp, d, eh, A);
     return (int)hipGetLastError();
 }
 

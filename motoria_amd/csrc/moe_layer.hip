@@ -15,9 +15,13 @@
 // run in block order, and sums the reference takes in double are either
 // reproduced exactly or certified (see k_rmsnorm_q8). For large batches the
 // gate/up and down stages switch to the matrix-core kernels of moe_gemm.hip
-// (exact block dots with a fused block term for gate/up, fp16 operands for
-// down; the layer within 1e-3 of the reference); routing and dispatch stay
-// bit-exact.
+// (exact block dots, each block term added with one fused multiply-add; the
+// layer within 1e-3 of the reference); routing and dispatch stay bit-exact.
+//
+// Status words (sc->status, cleared by the host per call): [0] bit 0 = an
+// expert index out of range; [1] rmsnorm sums that took the sequential path;
+// [2] 1 + the ordinal (since the clear) of the first layer launch that met a
+// bad index; [3] layer launches completed since the clear.
 #include "mhip_internal.h"
 
 namespace {
@@ -518,7 +522,8 @@ __global__ __launch_bounds__(256, 2) void k_router_logits_wide(const float *__re
 //                   of a lane among the step's lanes with the same expert
 //                   comes from one ballot per bit of the expert index.
 // Up to DSMALL chunks, one workgroup does all three (k_disp_small).
-// status[0] |= 1 on a bad index (the assignment is then counted as expert 0).
+// status[0] |= 1 on a bad index (the assignment is then counted as expert 0),
+// and status[2] names the first layer launch that met one.
 constexpr int DCH = 256;               // assignments per chunk (4 steps of 64)
 constexpr int DWG = 4;                 // chunks (wavefronts) per workgroup
 
@@ -535,6 +540,7 @@ __device__ __forceinline__ int disp_key(const int *idx, int a, int A, int E, int
     const int e = idx[a];
     if (e < 0 || e >= E) {
         atomicOr(&status[0], 1);
+        atomicCAS(&status[2], 0, status[3] + 1);
         return 0;
     }
     return e;
@@ -1007,13 +1013,16 @@ __global__ __launch_bounds__(NT) void k_down(const uint8_t *__restrict__ table, 
 // ---- combine -------------------------------------------------------------------
 // x_i = x_i + w_j * tmp_j,i for j = 0..K-1 in top-K order (forward.c:194).
 // Four consecutive elements per thread (d % 4 == 0); the K rows of a token
-// are requested before the ordered sum consumes them.
+// are requested before the ordered sum consumes them. One thread counts the
+// layer launch in status[3].
 __global__ __launch_bounds__(256) void k_combine(float *__restrict__ x,
                                                  const float *__restrict__ w,
                                                  const int *__restrict__ pos,
-                                                 const float *__restrict__ tmp, int d, int K) {
+                                                 const float *__restrict__ tmp, int d, int K,
+                                                 int *__restrict__ status) {
     const int t = blockIdx.y;
     const int i = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
+    if (t == 0 && i == 0) status[3] += 1;
     if (i >= d) return;
     float4 *xp = (float4 *)(x + (size_t)t * d + i);
     float4 v = *xp;
@@ -1223,7 +1232,7 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
         if (mhip::check(c, (hipError_t)e, "down_mfma launch")) return -1;
         dim3 cg(mhip::blocks_for(d, 1024), T);
         slot = mhip::stage_begin(c, MHIP_STAGE_COMBINE);
-        k_combine<<<cg, 256, 0, st>>>(d_x, sc->w, sc->pos, sc->tmp, d, K);
+        k_combine<<<cg, 256, 0, st>>>(d_x, sc->w, sc->pos, sc->tmp, d, K, sc->status);
         mhip::stage_end(c, slot);
         return mhip::check_launch(c, "combine");
     }
@@ -1252,7 +1261,7 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
 
     dim3 cg(mhip::blocks_for(d, 1024), T);
     slot = mhip::stage_begin(c, MHIP_STAGE_COMBINE);
-    k_combine<<<cg, 256, 0, st>>>(d_x, sc->w, sc->pos, sc->tmp, d, K);
+    k_combine<<<cg, 256, 0, st>>>(d_x, sc->w, sc->pos, sc->tmp, d, K, sc->status);
     mhip::stage_end(c, slot);
     return mhip::check_launch(c, "combine");
 }

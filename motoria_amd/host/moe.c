@@ -42,6 +42,7 @@ static int fail(mia_moe *m, const char *fmt, ...) {
 }
 
 static int gpu_fail(mia_moe *m) { return fail(m, "%s", mhip_error(m->gpu)); }
+static int check_status(mia_moe *m, int l0);
 
 static size_t align_up(size_t n, size_t a) { return (n + a - 1) / a * a; }
 
@@ -226,13 +227,22 @@ static int run_layer(mia_moe *m, int layer, float *d_x, int T, const float *d_bi
     return 0;
 }
 
+/* The device status words describe the last public layer or stack call:
+ * cleared (fill kernel) before its first launch. */
+static int clear_status(mia_moe *m) {
+    if (mhip_zero(m->gpu, m->sc.status, 16)) return gpu_fail(m);
+    return 0;
+}
+
 int mia_moe_layer_dev(mia_moe *m, int layer, float *d_x, int T, const float *d_bias) {
+    if (clear_status(m)) return -1;
     return run_layer(m, layer, d_x, T, d_bias);
 }
 
 int mia_moe_stack_dev(mia_moe *m, int l0, int l1, float *d_x, int T) {
     if (l0 < 0 || l1 > m->n_layers || l0 > l1)
         return fail(m, "layer range [%d, %d) outside [0, %d)", l0, l1, m->n_layers);
+    if (clear_status(m)) return -1;
     for (int l = l0; l < l1; l++)
         if (run_layer(m, l, d_x, T, NULL)) return -1;
     return 0;
@@ -262,6 +272,20 @@ int mia_moe_decode_trace(mia_moe *m, unsigned long long *out) {
     return 0;
 }
 
+/* Layers [l0, l1) of one token per stage on m->d_x (the bit-exact path),
+ * each layer's routing copied to the decode routing arrays. */
+static int decode_per_stage(mia_moe *m, int l0, int l1, const float *d_bias) {
+    const size_t K = (size_t)m->dims.n_active;
+    if (clear_status(m)) return -1;
+    for (int l = l0; l < l1; l++) {
+        if (run_layer(m, l, m->d_x, 1, d_bias)) return -1;
+        if (mhip_d2d(m->gpu, m->d_didx + l * K, m->sc.idx, K * 4) ||
+            mhip_d2d(m->gpu, m->d_dw + l * K, m->sc.w, K * 4))
+            return gpu_fail(m);
+    }
+    return check_status(m, l0);
+}
+
 int mia_moe_decode(mia_moe *m, int l0, int l1, float *x, const float *bias, int *idx, float *w) {
     const size_t d = (size_t)m->dims.dim, E = (size_t)m->dims.n_experts,
                  K = (size_t)m->dims.n_active;
@@ -270,8 +294,15 @@ int mia_moe_decode(mia_moe *m, int l0, int l1, float *x, const float *bias, int 
     if (mia_moe_decode_dev(m, l0, l1, m->d_x, bias ? m->d_bias : NULL)) return -1;
     int st[4];
     if (mhip_sync(m->gpu) || mhip_decode_status(m->gpu, m->d_dws, st)) return gpu_fail(m);
-    if (st[0]) return fail(m, "decode stack aborted (status %d: %s)", st[0],
-                           (st[0] & 1) ? "workgroups not on the expected XCDs" : "a wait timed out");
+    if (st[0]) {
+        /* The launch aborted (a wait timed out, workgroups not placed as it
+         * needs, or a forced abort) and left d_x invalid; x (host) is
+         * untouched: run the layers per stage instead. mia_moe_decode_status
+         * still shows the aborted launch. */
+        if (mhip_h2d(m->gpu, m->d_x, x, d * 4) ||
+            decode_per_stage(m, l0, l1, bias ? m->d_bias : NULL))
+            return -1;
+    }
     if (mhip_d2h(m->gpu, x, m->d_x, d * 4) ||
         (idx && mhip_d2h(m->gpu, idx, m->d_didx + l0 * K, (size_t)(l1 - l0) * K * 4)) ||
         (w && mhip_d2h(m->gpu, w, m->d_dw + l0 * K, (size_t)(l1 - l0) * K * 4)))
@@ -284,10 +315,14 @@ int mia_moe_status(mia_moe *m, int status[4]) {
     return 0;
 }
 
-static int check_status(mia_moe *m) {
+/* Fails when the last call's layers met an expert index out of range,
+ * naming the first such layer (l0 = the call's first layer). */
+static int check_status(mia_moe *m, int l0) {
     int st[4];
     if (mia_moe_status(m, st)) return -1;
-    if (st[0] & 1) return fail(m, "router produced an expert index out of range");
+    if (st[0] & 1)
+        return fail(m, "router produced an expert index out of range (layer %d)",
+                    l0 + (st[2] > 0 ? st[2] - 1 : 0));
     return 0;
 }
 
@@ -295,7 +330,8 @@ static int check_status(mia_moe *m) {
  * with the exact router (bit-equal to the reference, like the per-stage
  * path, and several times faster at T = 1). x and the routing travel through
  * the pinned staging buffer with queued copies, so the call waits for the
- * device once (in the status read). */
+ * device once (in the status read). Returns 1 (x untouched) when the launch
+ * aborted: the caller then runs the layer per stage. */
 static int decode_one_layer(mia_moe *m, int layer, float *x, const float *bias, int *idx,
                             float *w) {
     const size_t d = (size_t)m->dims.dim, E = (size_t)m->dims.n_experts,
@@ -321,8 +357,7 @@ static int decode_one_layer(mia_moe *m, int layer, float *x, const float *bias, 
     int st[4];
     /* the status read waits for the stream, copies above included */
     if (mhip_decode_status(m->gpu, m->d_dws, st)) return gpu_fail(m);
-    if (st[0]) return fail(m, "decode launch aborted (status %d: %s)", st[0],
-                           (st[0] & 1) ? "workgroups not on the expected XCDs" : "a wait timed out");
+    if (st[0]) return 1;
     memcpy(x, hy, d * 4);
     if (idx) memcpy(idx, hi, K * 4);
     if (w) memcpy(w, hw, K * 4);
@@ -337,10 +372,18 @@ int mia_moe_layer_ex(mia_moe *m, int layer, float *x, int T, const float *bias, 
     if (T == 1 && !logits && !(m->flags & MHIP_EXACT_EXPERTS)) {
         const int ok = mhip_decode_supported(m->gpu, &m->dims);
         if (ok < 0) return gpu_fail(m);
-        if (ok) return decode_one_layer(m, layer, x, bias, idx, w);
+        if (ok) {
+            const int rc = decode_one_layer(m, layer, x, bias, idx, w);
+            if (rc <= 0) return rc;
+            /* the launch aborted (a wait timed out, or workgroups were not
+             * placed as it needs): x is untouched, and the per-stage path
+             * below gives the same bits (mia_moe_decode_status still
+             * shows the aborted launch) */
+        }
     }
     const size_t d = (size_t)m->dims.dim, E = (size_t)m->dims.n_experts,
                  K = (size_t)m->dims.n_active;
+    if (clear_status(m)) return -1;
     if (mhip_h2d(m->gpu, m->d_x, x, (size_t)T * d * 4)) return gpu_fail(m);
     if (bias && mhip_h2d(m->gpu, m->d_bias, bias, E * 4)) return gpu_fail(m);
     if (run_layer(m, layer, m->d_x, T, bias ? m->d_bias : NULL)) return -1;
@@ -349,7 +392,7 @@ int mia_moe_layer_ex(mia_moe *m, int layer, float *x, int T, const float *bias, 
         (w && mhip_d2h(m->gpu, w, m->sc.w, (size_t)T * K * 4)) ||
         (logits && mhip_d2h(m->gpu, logits, m->sc.logits, (size_t)T * E * 4)))
         return gpu_fail(m);
-    return check_status(m);
+    return check_status(m, layer);
 }
 
 int mia_moe_layer(mia_moe *m, int layer, float *x, int T) {
@@ -364,5 +407,5 @@ int mia_moe_stack(mia_moe *m, int l0, int l1, float *x, int T) {
     if (mhip_h2d(m->gpu, m->d_x, x, (size_t)T * d * 4)) return gpu_fail(m);
     if (mia_moe_stack_dev(m, l0, l1, m->d_x, T)) return -1;
     if (mhip_d2h(m->gpu, x, m->d_x, (size_t)T * d * 4)) return gpu_fail(m);
-    return check_status(m);
+    return check_status(m, l0);
 }

@@ -63,6 +63,10 @@ def lib():
         L.orc_moe_layer.argtypes = [ctypes.POINTER(Dims), _i, _p, _p, _p, _p, _p,
                                     _p, _p, _p, _p, _i]
         L.orc_moe_stack.argtypes = [ctypes.POINTER(Dims), _i, _i, _p, _p, _p, _p, _i]
+        L.orc_moe_layer_bucketed.argtypes = [ctypes.POINTER(Dims), _i, _p, _p, _p, _p, _p,
+                                             _p, _p, _p, _i]
+        L.orc_route_tokens.argtypes = [ctypes.POINTER(Dims), _i, _p, _p, _p, _p, _p, _p, _p,
+                                       _i]
         L.orc_route.argtypes = [_p, _i, _i, _i, _p, _p]
         L.orc_dispatch.argtypes = [_p, _i, _i, _i, _p, _p, _p, _p]
         L.orc_synth_x.argtypes = [_u64, _i, _i, _p]
@@ -208,6 +212,45 @@ def moe_layer(d, x, ffn_norm, router, blobs, bias=None, nthreads=1):
     if rc != 0:
         raise RuntimeError("orc_moe_layer failed (%d)" % rc)
     return x, idx, w, logits, xn
+
+
+def moe_layer_bucketed(d, x, ffn_norm, router, blobs, bias=None, nthreads=1):
+    """The same layer as moe_layer (same bits) computed expert by expert, for
+    large T. Returns (x_out, idx, w, logits)."""
+    x = np.array(x, dtype=np.float32, order="C", ndmin=2)
+    T = x.shape[0]
+    idx = np.zeros((T, d.n_active), dtype=np.int32)
+    w = np.zeros((T, d.n_active), dtype=np.float32)
+    logits = np.zeros((T, d.n_experts), dtype=np.float32)
+    ptrs = _blob_ptrs(blobs, d.n_experts)
+    bias = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    rc = lib().orc_moe_layer_bucketed(ctypes.byref(d), T, _ptr(x),
+                                      _ptr(np.ascontiguousarray(ffn_norm, dtype=np.float32)),
+                                      _ptr(np.ascontiguousarray(router, dtype=np.float32)),
+                                      _ptr(bias), ptrs, _ptr(idx), _ptr(w), _ptr(logits),
+                                      nthreads)
+    if rc != 0:
+        raise RuntimeError("orc_moe_layer_bucketed failed (%d)" % rc)
+    return x, idx, w, logits
+
+
+def route_tokens(d, x, ffn_norm, router, bias=None, nthreads=1):
+    """Routing only (rmsnorm, router chains, softmax, top-K, gate weights) of
+    every token of x[T][dim]: the layer without its experts. Returns
+    (idx, w, logits)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    idx = np.zeros((T, d.n_active), dtype=np.int32)
+    w = np.zeros((T, d.n_active), dtype=np.float32)
+    logits = np.zeros((T, d.n_experts), dtype=np.float32)
+    bias = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    rc = lib().orc_route_tokens(ctypes.byref(d), T, _ptr(x),
+                                _ptr(np.ascontiguousarray(ffn_norm, dtype=np.float32)),
+                                _ptr(np.ascontiguousarray(router, dtype=np.float32)),
+                                _ptr(bias), _ptr(idx), _ptr(w), _ptr(logits), nthreads)
+    if rc != 0:
+        raise RuntimeError("orc_route_tokens failed (%d)" % rc)
+    return idx, w, logits
 
 
 def moe_stack(d, x, ffn_norm, router, blobs, nthreads=1):

@@ -64,19 +64,43 @@ static float dot_q8(const orc_block_q8 *a, const orc_block_q8 *b, int nb) {
     return s;
 }
 
-/* src/tensor/matmul.c:66-87,91-106 on x86: quantize x once (Q8), then the
- * scalar row loop. The Apple-only GCD row split does not change any bits. */
-void orc_matvec(float *out, const void *w, int wtype, const float *x,
-                orc_block_q8 *xq, int rows, int cols) {
+/* Rows [r0, r1) of the scalar row loop (src/tensor/matmul.c:66-81). */
+static void rows_kernel(float *out, const void *w, int wtype, const float *x,
+                        const orc_block_q8 *xq, int r0, int r1, int cols) {
     if (wtype == ORC_F32) {
         const float *wf = (const float *)w;
-        for (int r = 0; r < rows; r++) out[r] = dot_f32(wf + (size_t)r * cols, x, cols);
+        for (int r = r0; r < r1; r++) out[r] = dot_f32(wf + (size_t)r * cols, x, cols);
         return;
     }
-    orc_quantize_row_q8(x, xq, cols);
     const int nb = cols / ORC_QK;
     const orc_block_q8 *wq = (const orc_block_q8 *)w;
-    for (int r = 0; r < rows; r++) out[r] = dot_q8(wq + (size_t)r * nb, xq, nb);
+    for (int r = r0; r < r1; r++) out[r] = dot_q8(wq + (size_t)r * nb, xq, nb);
+}
+
+/* src/tensor/matmul.c:89-106: quantize x once (Q8), then the row loop; with
+ * nthreads > 1, chunks of 64 rows spread over threads when the matrix is
+ * large enough (the reference's GCD split on Apple, CHUNK_ROWS = 64,
+ * PARALLEL_MIN_WORK = 65536). Each row is one sequential dot either way, so
+ * the split changes no bits. */
+static void matvec_mt(float *out, const void *w, int wtype, const float *x,
+                      orc_block_q8 *xq, int rows, int cols, int nthreads) {
+    if (wtype == ORC_Q8_0) orc_quantize_row_q8(x, xq, cols);
+    if (nthreads > 1 && (long)rows * cols >= 65536 && rows > 64) {
+        const int chunks = (rows + 63) / 64;
+#pragma omp parallel for num_threads(nthreads) schedule(dynamic, 1)
+        for (int c = 0; c < chunks; c++) {
+            const int r0 = c * 64, r1 = r0 + 64 < rows ? r0 + 64 : rows;
+            rows_kernel(out, w, wtype, x, xq, r0, r1, cols);
+        }
+        return;
+    }
+    rows_kernel(out, w, wtype, x, xq, 0, rows, cols);
+}
+
+/* src/tensor/matmul.c:91-106 on x86 (one thread). */
+void orc_matvec(float *out, const void *w, int wtype, const float *x,
+                orc_block_q8 *xq, int rows, int cols) {
+    matvec_mt(out, w, wtype, x, xq, rows, cols, 1);
 }
 
 /* src/model/forward.c:75-81: sum of squares in double, in order. */
@@ -150,7 +174,7 @@ static int moe_token(const orc_dims *s, float *x, const float *ffn_norm,
                      const float *router, const float *bias,
                      const unsigned char *const *blobs, int *idx_out,
                      float *w_out, float *logits_out, float *xn_out,
-                     float *scratch, orc_block_q8 *xq) {
+                     float *scratch, orc_block_q8 *xq, int row_threads) {
     const int d = s->dim, E = s->n_experts, K = s->n_active, eh = s->expert_hidden;
     int idx[64];
     float w[64];
@@ -159,7 +183,7 @@ static int moe_token(const orc_dims *s, float *x, const float *ffn_norm,
           *tmp = up + eh;
 
     orc_rmsnorm(xn, x, ffn_norm, d, s->norm_eps);
-    orc_matvec(prob, router, ORC_F32, xn, NULL, E, d);
+    matvec_mt(prob, router, ORC_F32, xn, NULL, E, d, row_threads);
     if (bias)
         for (int e = 0; e < E; e++) prob[e] = prob[e] + bias[e];
     if (logits_out) memcpy(logits_out, prob, sizeof(float) * (size_t)E);
@@ -172,13 +196,13 @@ static int moe_token(const orc_dims *s, float *x, const float *ffn_norm,
     for (int j = 0; j < K; j++) {
         const unsigned char *blob = blobs[idx[j]];
         if (!blob) return -1;
-        orc_matvec(gate, blob, ORC_Q8_0, xn, xq, eh, d);
-        orc_matvec(up, blob + off_up, ORC_Q8_0, xn, xq, eh, d);
+        matvec_mt(gate, blob, ORC_Q8_0, xn, xq, eh, d, row_threads);
+        matvec_mt(up, blob + off_up, ORC_Q8_0, xn, xq, eh, d, row_threads);
         for (int i = 0; i < eh; i++) {
             float g = gate[i];
             gate[i] = (g / (1.0f + expf(-g))) * up[i];
         }
-        orc_matvec(tmp, blob + off_down, ORC_Q8_0, gate, xq, d, eh);
+        matvec_mt(tmp, blob + off_down, ORC_Q8_0, gate, xq, d, eh, row_threads);
         for (int i = 0; i < d; i++) x[i] = x[i] + w[j] * tmp[i];
     }
     return 0;
@@ -195,9 +219,13 @@ int orc_moe_layer(const orc_dims *s, int T, float *x, const float *ffn_norm,
     const int d = s->dim, E = s->n_experts, K = s->n_active;
     const int maxd = d > s->expert_hidden ? d : s->expert_hidden;
     int rc = 0;
+    if (nthreads < 1) nthreads = 1;
+    /* One token: threads over 64-row chunks of each matrix. */
+    const int row_threads = T == 1 ? nthreads : 1;
+    if (T == 1) nthreads = 1;
     /* Tokens are independent (the reference steps them one at a time), so
      * threads over tokens change no bits. */
-#pragma omp parallel num_threads(nthreads > 0 ? nthreads : 1) reduction(| : rc)
+#pragma omp parallel num_threads(nthreads) reduction(| : rc)
     {
         float *scratch = malloc(sizeof(float) * (size_t)scratch_floats(s));
         orc_block_q8 *xq = malloc(sizeof(orc_block_q8) * (size_t)(maxd / ORC_QK));
@@ -208,7 +236,7 @@ int orc_moe_layer(const orc_dims *s, int T, float *x, const float *ffn_norm,
             if (moe_token(s, x + (size_t)t * d, ffn_norm, router, bias, blobs,
                           idx ? idx + (size_t)t * K : NULL, w ? w + (size_t)t * K : NULL,
                           logits ? logits + (size_t)t * E : NULL,
-                          xn ? xn + (size_t)t * d : NULL, scratch, xq))
+                          xn ? xn + (size_t)t * d : NULL, scratch, xq, row_threads))
                 rc |= 1;
         }
         free(scratch);
@@ -229,6 +257,263 @@ int orc_moe_stack(const orc_dims *s, int L, int T, float *x,
         if (rc) return rc;
     }
     return 0;
+}
+
+/* ---- expert-bucketed restatement of the same layer (a checker for large T) ----
+ *
+ * orc_moe_layer_bucketed computes, for every (token, weight row), the same
+ * sequential chain as dot_q8 and every other value in the same order as
+ * moe_token; only the loop nest differs: tokens are grouped by expert (the
+ * stable bucketing of orc_dispatch) and each weight row meets 16 tokens of
+ * its bucket at once. The block dot is accumulated in float: every partial
+ * sum of 32 products of two int8 codes is an integer below 2^24, so it is
+ * exact in any order and equals (float) of the int32 dot. Pinned bit-equal to
+ * orc_moe_layer by tests/test_oracle.py. */
+typedef float orc_v16 __attribute__((vector_size(64)));
+
+/* out[r * ostride + t] for the four consecutive Q8_0 weight rows w (nb
+ * blocks each) against tokens t < n of a bucket held transposed:
+ * xf[(32 k + i) * tp + t] = code i of block k of token t (as float; zero for
+ * t >= n), xs[k * tp + t] its scale; tp is a multiple of 16. */
+__attribute__((target_clones("avx512f", "avx2", "default")))
+static void rows4_bucket(const orc_block_q8 *w, int nb, const float *xf, const float *xs,
+                         int tp, int n, float *out, int ostride) {
+    for (int t0 = 0; t0 < n; t0 += 16) {
+        orc_v16 s0 = {0}, s1 = {0}, s2 = {0}, s3 = {0};
+        for (int k = 0; k < nb; k++) {
+            orc_v16 a0 = {0}, a1 = {0}, a2 = {0}, a3 = {0};
+            const float *xk = xf + (size_t)k * ORC_QK * tp + t0;
+            const orc_block_q8 *w0 = w + k, *w1 = w + nb + k, *w2 = w + 2 * nb + k,
+                               *w3 = w + 3 * nb + k;
+            for (int i = 0; i < ORC_QK; i++) {
+                orc_v16 xv;
+                memcpy(&xv, xk + (size_t)i * tp, sizeof xv);
+                a0 = a0 + (float)w0->q[i] * xv;
+                a1 = a1 + (float)w1->q[i] * xv;
+                a2 = a2 + (float)w2->q[i] * xv;
+                a3 = a3 + (float)w3->q[i] * xv;
+            }
+            orc_v16 sv;
+            memcpy(&sv, xs + (size_t)k * tp + t0, sizeof sv);
+            s0 = s0 + (a0 * w0->d) * sv;
+            s1 = s1 + (a1 * w1->d) * sv;
+            s2 = s2 + (a2 * w2->d) * sv;
+            s3 = s3 + (a3 * w3->d) * sv;
+        }
+        for (int t = 0; t < 16 && t0 + t < n; t++) {
+            out[t0 + t] = s0[t];
+            out[(size_t)ostride + t0 + t] = s1[t];
+            out[2 * (size_t)ostride + t0 + t] = s2[t];
+            out[3 * (size_t)ostride + t0 + t] = s3[t];
+        }
+    }
+}
+
+/* Q8_0 (quant.c:11-27) of the 32-values blocks of column t of v[rows][tp]
+ * (rows a multiple of 32), in place: v receives the codes as floats, sc[k *
+ * tp + t] the block scales. */
+static void quant_column(float *v, float *sc, int rows, int tp, int t) {
+    float blk[ORC_QK];
+    orc_block_q8 q;
+    for (int k = 0; k < rows / ORC_QK; k++) {
+        for (int i = 0; i < ORC_QK; i++) blk[i] = v[(size_t)(k * ORC_QK + i) * tp + t];
+        orc_quantize_row_q8(blk, &q, ORC_QK);
+        for (int i = 0; i < ORC_QK; i++) v[(size_t)(k * ORC_QK + i) * tp + t] = (float)q.q[i];
+        sc[(size_t)k * tp + t] = q.d;
+    }
+}
+
+/* rmsnorm, router chains (+bias), softmax/top-K/gate weights of T tokens
+ * (forward.c:75-81,175-181); xn[T][d] receives the rmsnorm output. The E
+ * chains of a token advance together over the transposed router, each in the
+ * reference's order (a rounded product, then a rounded add). */
+static int route_phase(const orc_dims *s, int T, const float *x, const float *ffn_norm,
+                       const float *router, const float *bias, float *xn, int *idx, float *w,
+                       float *logits_out, int nthreads) {
+    const int d = s->dim, E = s->n_experts, K = s->n_active;
+    int rc = 0;
+    float *wt = malloc(sizeof(float) * (size_t)d * E);
+    if (!wt) return -1;
+#pragma omp parallel for num_threads(nthreads) schedule(static)
+    for (int i = 0; i < d; i++)
+        for (int e = 0; e < E; e++) wt[(size_t)i * E + e] = router[(size_t)e * d + i];
+#pragma omp parallel num_threads(nthreads) reduction(| : rc)
+    {
+        float *lg = malloc(sizeof(float) * (size_t)E);
+        if (!lg) rc |= 1;
+#pragma omp for schedule(static)
+        for (int t = 0; t < T; t++) {
+            if (!lg) continue;
+            float *xt = xn + (size_t)t * d;
+            orc_rmsnorm(xt, x + (size_t)t * d, ffn_norm, d, s->norm_eps);
+            for (int e = 0; e < E; e++) lg[e] = 0.0f;
+            for (int i = 0; i < d; i++) {
+                const float xv = xt[i];
+                const float *wr = wt + (size_t)i * E;
+                for (int e = 0; e < E; e++) lg[e] = lg[e] + wr[e] * xv;
+            }
+            if (bias)
+                for (int e = 0; e < E; e++) lg[e] = lg[e] + bias[e];
+            if (logits_out) memcpy(logits_out + (size_t)t * E, lg, sizeof(float) * (size_t)E);
+            orc_route(lg, E, K, s->norm_topk, idx + (size_t)t * K, w + (size_t)t * K);
+        }
+        free(lg);
+    }
+    free(wt);
+    return rc ? -1 : 0;
+}
+
+int orc_route_tokens(const orc_dims *s, int T, const float *x, const float *ffn_norm,
+                     const float *router, const float *bias, int *idx, float *w,
+                     float *logits, int nthreads) {
+    if (s->n_active > 64 || T < 0) return -1;
+    if (T == 0) return 0;
+    float *xn = malloc(sizeof(float) * (size_t)T * s->dim);
+    if (!xn) return -1;
+    const int rc = route_phase(s, T, x, ffn_norm, router, bias, xn, idx, w, logits,
+                               nthreads < 1 ? 1 : nthreads);
+    free(xn);
+    return rc;
+}
+
+int orc_moe_layer_bucketed(const orc_dims *s, int T, float *x, const float *ffn_norm,
+                           const float *router, const float *bias,
+                           const unsigned char *const *blobs, int *idx_out, float *w_out,
+                           float *logits_out, int nthreads) {
+    const int d = s->dim, E = s->n_experts, K = s->n_active, eh = s->expert_hidden;
+    const int nb = d / ORC_QK, A = T * K;
+    if (K > 64 || d % ORC_QK || eh % ORC_QK || T < 0) return -1;
+    if (T == 0) return 0;
+    if (nthreads < 1) nthreads = 1;
+    const size_t off_up = orc_off_up(s), off_down = orc_off_down(s);
+    int rc = 0;
+    float *xn = malloc(sizeof(float) * (size_t)T * d);
+    int *idx = malloc(sizeof(int) * (size_t)A);
+    float *w = malloc(sizeof(float) * (size_t)A);
+    int *counts = malloc(sizeof(int) * (size_t)E), *offsets = malloc(sizeof(int) * (size_t)(E + 1));
+    int *perm = malloc(sizeof(int) * (size_t)A), *pos = malloc(sizeof(int) * (size_t)A);
+    size_t *boff = malloc(sizeof(size_t) * (size_t)(E + 1));
+    int *tps = malloc(sizeof(int) * (size_t)E);
+    float *xf = NULL, *xs = NULL, *gu = NULL, *hs = NULL, *tmp = NULL;
+    if (!xn || !idx || !w || !counts || !offsets || !perm || !pos || !boff || !tps) {
+        rc = -1;
+        goto out;
+    }
+    rc = route_phase(s, T, x, ffn_norm, router, bias, xn, idx, w, logits_out, nthreads);
+    if (rc || orc_dispatch(idx, T, K, E, counts, offsets, perm, pos)) {
+        rc = -1;
+        goto out;
+    }
+    if (idx_out) memcpy(idx_out, idx, sizeof(int) * (size_t)A);
+    if (w_out) memcpy(w_out, w, sizeof(float) * (size_t)A);
+    boff[0] = 0;
+    for (int e = 0; e < E; e++) {
+        if (counts[e] && !blobs[e]) rc = -1; /* a cache miss whose load failed */
+        tps[e] = (counts[e] + 15) / 16 * 16;
+        boff[e + 1] = boff[e] + (size_t)tps[e];
+    }
+    if (rc) goto out;
+    const size_t cols = boff[E];
+    xf = calloc((size_t)d * cols, sizeof(float));
+    xs = calloc((size_t)nb * cols, sizeof(float));
+    gu = calloc((size_t)2 * eh * cols, sizeof(float));
+    hs = calloc((size_t)(eh / ORC_QK) * cols, sizeof(float));
+    tmp = calloc((size_t)d * cols, sizeof(float));
+    if (!xf || !xs || !gu || !hs || !tmp) {
+        rc = -1;
+        goto out;
+    }
+    /* each bucket's Q8(xn) rows, transposed; bucket e's columns start at
+     * boff[e] of a d x cols array, so a bucket's column stride is cols */
+#pragma omp parallel num_threads(nthreads)
+    {
+        orc_block_q8 *q = malloc(sizeof(orc_block_q8) * (size_t)nb);
+#pragma omp for schedule(dynamic, 1)
+        for (int e = 0; e < E; e++) {
+            if (!q) continue;
+            for (int a = 0; a < counts[e]; a++) {
+                const int t = perm[offsets[e] + a] / K;
+                orc_quantize_row_q8(xn + (size_t)t * d, q, d);
+                const size_t c = boff[e] + (size_t)a;
+                for (int k = 0; k < nb; k++) {
+                    xs[(size_t)k * cols + c] = q[k].d;
+                    for (int i = 0; i < ORC_QK; i++)
+                        xf[(size_t)(k * ORC_QK + i) * cols + c] = (float)q[k].q[i];
+                }
+            }
+        }
+        if (!q) rc = -1;
+        free(q);
+    }
+    if (rc) goto out;
+    /* gate/up rows (gate in gu[0..eh), up in gu[eh..2eh)), 32 rows per task */
+    {
+        const int chunks = 2 * eh / 32;
+#pragma omp parallel for num_threads(nthreads) schedule(dynamic, 1) collapse(2)
+        for (int e = 0; e < E; e++)
+            for (int c = 0; c < chunks; c++) {
+                if (!counts[e]) continue;
+                const int r0 = c * 32, mat = r0 / eh, rr = r0 % eh;
+                const orc_block_q8 *wm =
+                    (const orc_block_q8 *)(blobs[e] + (mat ? off_up : 0)) + (size_t)rr * nb;
+                for (int r = 0; r < 32; r += 4)
+                    rows4_bucket(wm + (size_t)r * nb, nb, xf + boff[e], xs + boff[e], (int)cols,
+                                 counts[e], gu + (size_t)(r0 + r) * cols + boff[e], (int)cols);
+            }
+    }
+    /* SwiGLU (forward.c:189-191), then Q8(h) per assignment: the codes
+     * replace h in gu[0..eh) */
+#pragma omp parallel for num_threads(nthreads) schedule(dynamic, 16)
+    for (int a = 0; a < A; a++) {
+        const int e = idx[perm[a]];
+        const int c = (int)boff[e] + (a - offsets[e]);
+        for (int r = 0; r < eh; r++) {
+            const float g = gu[(size_t)r * cols + c];
+            gu[(size_t)r * cols + c] = (g / (1.0f + expf(-g))) * gu[(size_t)(eh + r) * cols + c];
+        }
+        quant_column(gu, hs, eh, (int)cols, c);
+    }
+    /* down rows, 32 per task */
+    {
+        const int chunks = d / 32, nbh = eh / ORC_QK;
+#pragma omp parallel for num_threads(nthreads) schedule(dynamic, 1) collapse(2)
+        for (int e = 0; e < E; e++)
+            for (int c = 0; c < chunks; c++) {
+                if (!counts[e]) continue;
+                const orc_block_q8 *wm = (const orc_block_q8 *)(blobs[e] + off_down) +
+                                         (size_t)c * 32 * nbh;
+                for (int r = 0; r < 32; r += 4)
+                    rows4_bucket(wm + (size_t)r * nbh, nbh, gu + boff[e], hs + boff[e],
+                                 (int)cols, counts[e],
+                                 tmp + (size_t)(c * 32 + r) * cols + boff[e], (int)cols);
+            }
+    }
+    /* combine (forward.c:194): x_i = x_i + w_j * tmp_j,i, j in top-K order */
+#pragma omp parallel for num_threads(nthreads) schedule(static)
+    for (int t = 0; t < T; t++)
+        for (int j = 0; j < K; j++) {
+            const int a = pos[t * K + j], e = idx[t * K + j];
+            const size_t c = boff[e] + (size_t)(a - offsets[e]);
+            const float wj = w[t * K + j];
+            float *xt = x + (size_t)t * d;
+            for (int i = 0; i < d; i++) xt[i] = xt[i] + wj * tmp[(size_t)i * cols + c];
+        }
+out:
+    free(xn);
+    free(idx);
+    free(w);
+    free(counts);
+    free(offsets);
+    free(perm);
+    free(pos);
+    free(boff);
+    free(tps);
+    free(xf);
+    free(xs);
+    free(gu);
+    free(hs);
+    free(tmp);
+    return rc;
 }
 
 int orc_dispatch(const int *idx, int T, int K, int E, int *counts,

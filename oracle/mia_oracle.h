@@ -20,7 +20,8 @@
  *   orc_rmsnorm          unit-RMS invariant (tools/internal/ref/ref_test.go:18-28);
  *                        bit-equal to oracle/_ref inside the layer.
  *   orc_softmax/top_k    known answers (ref_test.go:30-56), tie rule, brute force.
- *   orc_moe_token        bit-equal to oracle/_ref (real moe()) on golden vectors.
+ *   orc_moe_layer        bit-equal to oracle/_ref (real moe()) on golden vectors.
+ *   orc_moe_layer_bucketed  bit-equal to orc_moe_layer (loop nest only differs).
  *   orc_dispatch         brute-force stable sort; permutation invariants.
  */
 #include <stddef.h>
@@ -69,7 +70,9 @@ size_t orc_blob_bytes(const orc_dims *s);
  * call then fails like a cache miss whose load failed). bias may be NULL.
  * Optional outputs (NULL to skip): idx[T][K], w[T][K], logits[T][E] (after
  * the bias), xn[T][dim]. Returns 0, or -1 (K > 64 or a missing expert).
- * nthreads > 1 spreads tokens over OpenMP threads (same bits).
+ * nthreads > 1 spreads tokens over OpenMP threads, or, for one token, the
+ * 64-row chunks of every matrix (the reference's CHUNK_ROWS split; same
+ * bits).
  */
 int orc_moe_layer(const orc_dims *s, int T, float *x, const float *ffn_norm,
                   const float *router, const float *bias,
@@ -81,6 +84,21 @@ int orc_moe_layer(const orc_dims *s, int T, float *x, const float *ffn_norm,
 int orc_moe_stack(const orc_dims *s, int L, int T, float *x,
                   const float *ffn_norm, const float *router,
                   const unsigned char *const *blobs, int nthreads);
+
+/* The same layer as orc_moe_layer (same bits), computed expert by expert:
+ * tokens bucketed by expert, 16 tokens per weight-row pass (for large T).
+ * Optional outputs idx[T][K], w[T][K], logits[T][E]. Returns 0 or -1. */
+int orc_moe_layer_bucketed(const orc_dims *s, int T, float *x, const float *ffn_norm,
+                           const float *router, const float *bias,
+                           const unsigned char *const *blobs, int *idx, float *w,
+                           float *logits, int nthreads);
+
+/* Routing only (rmsnorm, router chains + bias, softmax, top-K, gate weights)
+ * of T tokens, the first half of orc_moe_layer (same bits). Outputs
+ * idx[T][K], w[T][K], logits[T][E] (after the bias; may be NULL). */
+int orc_route_tokens(const orc_dims *s, int T, const float *x, const float *ffn_norm,
+                     const float *router, const float *bias, int *idx, float *w,
+                     float *logits, int nthreads);
 
 /* Stable counting sort of the T*K assignments (t, j) by expert idx[t][j],
  * t-major then j. counts[E], offsets[E+1], perm[T*K] = t*K + j in bucketed

@@ -68,7 +68,7 @@ int ref_moe_layer(int dim, int n_experts, int n_active, int expert_hidden,
     layer.ffn_norm = ffn_norm;
     layer.router = router;
     f.layers = &layer;
-    /* src/storage/mia_file.c:275-278 */
+    /* src/storage/mia_file.c:98-101 */
     size_t mat = (size_t)expert_hidden * mia_row_bytes(MIA_Q8_0, dim);
     f.off_up = (mat + 63) / 64 * 64;
     f.off_down = 2 * f.off_up;

@@ -87,3 +87,17 @@ def test_no_oracle_in_product():
             if f.endswith((".py", ".c", ".h", ".hip")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert "import oracle" not in text and "mia_oracle" not in text, f
+
+
+def test_decode_stack_rejects_more_than_256_layers_before_any_device_call():
+    """Exchange tags hold the layer in 8 bits: one decode launch covers at
+    most 256 layers, and the argument check comes before any device call (so
+    it runs here without a GPU and without a context)."""
+    d = M.Dims(2048, 128, 8, 768, 1, 1e-6)
+    lay = M.Layout()
+    L = M.lib()
+    assert L.mhip_layout_of(ctypes.byref(d), ctypes.byref(lay)) == 0
+    for bad in (M.DECODE_MAX_LAYERS + 1, 1000, -1):
+        rc = L.mhip_decode_stack(None, ctypes.byref(d), ctypes.byref(lay), None, None, None,
+                                 None, None, None, bad, None, None, None, 0)
+        assert rc == -1

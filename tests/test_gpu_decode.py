@@ -5,6 +5,7 @@ within the north-star tolerance (max|diff| / max|ref| <= 1e-3; the kernel's
 gate weights come from the parallel router logits, so ~1e-6 is expected).
 With the exact router forced, the output must be bit-equal to the oracle.
 """
+import ctypes
 import sys
 
 import numpy as np
@@ -185,3 +186,53 @@ def test_decode_routing_many_tokens(oracle, qwen_dims, moe):
             checked += 1
             x = np.asarray(xg, np.float32)
     say("  %d layer routings bit-equal, status %s" % (checked, moe.decode_status()))
+
+
+def test_aborted_launch_falls_back_per_stage(oracle, qwen_dims, moe):
+    """A decode launch that aborts (here forced from the host: every
+    workgroup leaves after the start barrier, MHIP_DECODE_FORCE_ABORT) leaves
+    the host x untouched, and both host entry points rerun the layers per
+    stage: the one-token layer call and the multi-layer decode return the
+    oracle's bits, while the decode status still shows the aborted launch."""
+    say("test_aborted_launch_falls_back_per_stage")
+    d = qwen_dims
+    K = d.n_active
+    moe.set_flags(M.MHIP_DECODE_FORCE_ABORT)
+    try:
+        x0 = oracle.synth_x(W.X_SEED + 31, 1, d.dim)
+        x = x0.copy()
+        idx = np.zeros(K, np.int32)
+        w = np.zeros(K, np.float32)
+        rc = M.lib().mia_moe_layer_ex(moe.h, 2, x.ctypes.data, 1, None, idx.ctypes.data,
+                                      w.ctypes.data, None)
+        assert rc == 0, M.lib().mia_moe_error(moe.h).decode()
+        assert moe.decode_status()[0] == 4, "the decode launch was not the aborted one"
+        xo, io, wo, _, _ = run_oracle_layer(oracle, moe, d, 2, x0[0])
+        assert np.array_equal(idx, io[0])
+        assert np.array_equal(w.view(np.uint32), wo[0].view(np.uint32))
+        assert np.array_equal(x[0].view(np.uint32), xo[0].view(np.uint32))
+
+        xg, ig, wg = moe.decode(0, 3, x0[0])
+        assert moe.decode_status()[0] == 4
+        x = x0[0]
+        for l in range(3):
+            xo, io, wo, _, _ = run_oracle_layer(oracle, moe, d, l, x)
+            assert np.array_equal(ig[l], io[0]), "layer %d indices" % l
+            assert np.array_equal(wg[l].view(np.uint32), wo[0].view(np.uint32)), "layer %d w" % l
+            x = xo[0]
+        assert np.array_equal(xg.view(np.uint32), x.view(np.uint32))
+    finally:
+        moe.set_flags(0)
+    xg, _, _ = moe.decode(0, 1, x0[0])  # the next launch runs normally
+    assert moe.decode_status()[0] == 0
+
+
+def test_decode_rejects_more_than_256_layers(qwen_dims, moe):
+    say("test_decode_rejects_more_than_256_layers")
+    L = M.lib()
+    lay = M.Layout()
+    assert L.mhip_layout_of(ctypes.byref(moe.dims), ctypes.byref(lay)) == 0
+    rc = L.mhip_decode_stack(moe.gpu, ctypes.byref(moe.dims), ctypes.byref(lay), None, None,
+                             None, None, None, None, M.DECODE_MAX_LAYERS + 1, None, None, None, 0)
+    assert rc == -1
+    assert b"outside [0, 256]" in L.mhip_error(moe.gpu)

@@ -234,54 +234,47 @@ def test_layer_skewed_2048(oracle, qwen_dims, qwen_moe):
     assert 0.35 < share4 < 0.5 and 20 <= zero <= 40
 
 
-def _routing_and_sample(oracle, d, T, seed, bias=None, nsample=96):
-    """One matrix-core layer at T tokens on a fresh one-layer handle: every
-    token's logits, expert indices and gate weights bit-equal to the oracle's
-    (rmsnorm, router chain and routing per token), and the layer output of a
-    seeded sample of tokens within TOL (the oracle's layer is per token, so
-    the sample checks the full-size launch)."""
+def _every_token(oracle, d, T, seed, bias=None):
+    """One matrix-core layer at T tokens on a fresh one-layer handle with a
+    non-unit ffn_norm: every token's logits, expert indices and gate weights
+    bit-equal to the oracle's, and the layer output of every token within
+    TOL (the oracle's expert-bucketed layer, same bits as its per-token one)."""
     moe = M.Moe(n_layers=1, max_tokens=T, device=0, **W.SHAPE)
     try:
         moe.synth(W.WEIGHT_SEED)
+        router = oracle.synth_router(W.WEIGHT_SEED, 0, d)
+        norm = (1.0 + 0.1 * np.random.default_rng(77).standard_normal(d.dim)).astype(np.float32)
+        moe.set_layer(0, norm, router)
         moe.sync()
         x = oracle.synth_x(seed, T, d.dim)
-        router = oracle.synth_router(W.WEIGHT_SEED, 0, d)
         xm, im, wm, lm = _gpu_layer(moe, 0, x, bias, 0)
-        norm = np.ones(d.dim, np.float32)
-        for t in range(T):
-            xn = oracle.rmsnorm(x[t], norm, d.norm_eps)
-            lo = oracle.matvec(router, 0, xn, d.n_experts, d.dim)
-            if bias is not None:
-                lo = (lo + bias).astype(np.float32)
-            io, wo, _ = oracle.route(lo, d.n_active, d.norm_topk)
-            assert np.array_equal(bits(lm[t]), bits(lo)), "token %d logits" % t
-            assert np.array_equal(im[t], io), "token %d expert indices" % t
-            assert np.array_equal(bits(wm[t]), bits(wo)), "token %d gate weights" % t
-        sample = np.sort(np.random.default_rng(5).choice(T, nsample, replace=False))
-        xs = x[sample]
-        xo, io, _, _, _ = oracle_layer(oracle, moe, d, 0, xs, router, bias=bias,
-                                       need=im[sample].ravel().tolist())
-        assert np.array_equal(im[sample], io)
-        e_delta, e_out = rel_err(xm[sample] - xs, xo - xs), rel_err(xm[sample], xo)
-        say("  sample of %d: rel err update %.3e, output %.3e" % (nsample, e_delta, e_out))
+        blobs = [None] * d.n_experts
+        for e in sorted(set(im.ravel().tolist())):
+            blobs[e] = moe.read_expert(0, e)
+        xo, io, wo, lo = oracle.moe_layer_bucketed(d, x, norm, router, blobs, bias=bias,
+                                                   nthreads=NTHREADS)
+        assert_bits(lm, lo, "logits")
+        assert np.array_equal(im, io), "expert indices"
+        assert_bits(wm, wo, "gate weights")
+        e_delta, e_out = rel_err(xm - x, xo - x), rel_err(xm, xo)
+        say("  all %d tokens: rel err update %.3e, output %.3e" % (T, e_delta, e_out))
         assert e_delta <= TOL and e_out <= TOL
     finally:
         moe.close()
 
 
-def test_layer_prefill_4096_routing_and_sample(oracle, qwen_dims):
+def test_layer_prefill_4096_every_token(oracle, qwen_dims):
     """T=4096, the prefill benchmark shape (matrix-core experts, four router
     chains per lane)."""
-    say("test_layer_prefill_4096_routing_and_sample")
-    _routing_and_sample(oracle, qwen_dims, 4096, W.X_SEED + 11)
+    say("test_layer_prefill_4096_every_token")
+    _every_token(oracle, qwen_dims, 4096, W.X_SEED + 11)
 
 
 def test_layer_ragged_2111_with_bias(oracle, qwen_dims):
     """T=2111: the last 64-token router group and the last bucket tiles are
     partial, four router chains per lane, with the skewed logit bias."""
     say("test_layer_ragged_2111_with_bias")
-    _routing_and_sample(oracle, qwen_dims, 2111, W.X_SEED + 13,
-                        bias=W.zipf_bias(qwen_dims.n_experts), nsample=64)
+    _every_token(oracle, qwen_dims, 2111, W.X_SEED + 13, bias=W.zipf_bias(qwen_dims.n_experts))
 
 
 def test_matrix_path_ragged_buckets(oracle, qwen_dims, qwen_moe):
@@ -335,13 +328,13 @@ def test_forced_sequential_rmsnorm_same_bits(oracle, qwen_dims, qwen_moe):
     say("test_forced_sequential_rmsnorm_same_bits")
     x = oracle.synth_x(W.X_SEED + 2, 16, qwen_dims.dim)
     a = qwen_moe.layer(0, x)
-    before = qwen_moe.status()[1]
     qwen_moe.set_flags(M.MHIP_FORCE_SEQ_RMS)
     try:
         b = qwen_moe.layer(0, x)
     finally:
         qwen_moe.set_flags(0)
-    assert qwen_moe.status()[1] - before >= 16
+    st = qwen_moe.status()  # the status words describe the last call
+    assert st[1] == 16 and st[3] == 1, st
     for u, v in zip(a, b):
         assert np.array_equal(np.asarray(u).view(np.uint32), np.asarray(v).view(np.uint32))
 

@@ -187,3 +187,104 @@ def test_synthetic_blob_layout(oracle, tiny_dims):
     # padding past the down matrix stays zero
     end = oracle.off_down(d) + d.dim * (d.expert_hidden // 32 * 36)
     assert not b[end:].any()
+
+
+# ---- the bucketed layer, routing only, and the 64-row-chunk split ---------------
+
+MID = dict(dim=512, n_experts=16, n_active=4, expert_hidden=256, norm_topk=1, norm_eps=1e-6)
+
+
+def _weights(oracle, d, seed, sigma_norm=0.1):
+    blobs = [oracle.synth_expert_blob(seed, 0, e, d) for e in range(d.n_experts)]
+    router = (oracle.synth_router(seed, 0, d) * np.float32(10.0)).astype(np.float32)
+    rng = np.random.default_rng(seed)
+    norm = (1.0 + sigma_norm * rng.standard_normal(d.dim)).astype(np.float32)
+    return blobs, router, norm
+
+
+def _same_bits(a, b):
+    return np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
+
+
+@pytest.mark.parametrize("shape,T,with_bias", [("tiny", 64, False), ("tiny", 1, True),
+                                               ("mid", 97, True), ("mid8", 40, False)])
+def test_bucketed_layer_is_bit_equal(oracle, shape, T, with_bias):
+    kw = {"tiny": oracle.TINY, "mid": MID, "mid8": dict(MID, n_experts=64, n_active=8)}[shape]
+    d = oracle.dims(**kw)
+    blobs, router, norm = _weights(oracle, d, 21)
+    x = oracle.synth_x(22, T, d.dim)
+    bias = (np.random.default_rng(2).standard_normal(d.n_experts)).astype(np.float32) \
+        if with_bias else None
+    xa, ia, wa, la, _ = oracle.moe_layer(d, x, norm, router, blobs, bias=bias)
+    xb, ib, wb, lb = oracle.moe_layer_bucketed(d, x, norm, router, blobs, bias=bias, nthreads=4)
+    assert np.array_equal(ia, ib)
+    assert _same_bits(wa, wb) and _same_bits(la, lb)
+    assert _same_bits(xa, xb)
+    ir, wr, lr = oracle.route_tokens(d, x, norm, router, bias=bias, nthreads=3)
+    assert np.array_equal(ia, ir) and _same_bits(wa, wr) and _same_bits(la, lr)
+
+
+def test_bucketed_layer_missing_expert_fails(oracle):
+    d = oracle.dims(**oracle.TINY)
+    blobs, router, norm = _weights(oracle, d, 5)
+    x = oracle.synth_x(4, 8, d.dim)
+    _, idx, _, _, _ = oracle.moe_layer(d, x, norm, router, blobs)
+    blobs[int(idx[0, 0])] = None
+    with pytest.raises(RuntimeError):
+        oracle.moe_layer_bucketed(d, x, norm, router, blobs)
+
+
+def test_row_chunk_threads_do_not_change_bits(oracle):
+    """One token with nthreads > 1 splits every large matrix into 64-row
+    chunks over threads (the reference's CHUNK_ROWS split): same bits."""
+    d = oracle.dims(**MID)
+    blobs, router, norm = _weights(oracle, d, 31)
+    x = oracle.synth_x(32, 1, d.dim)
+    a = oracle.moe_layer(d, x, norm, router, blobs, nthreads=1)
+    b = oracle.moe_layer(d, x, norm, router, blobs, nthreads=4)
+    for u, v in zip(a, b):
+        assert _same_bits(u, v)
+
+
+# ---- where the logit bias enters (added after the router product, before the
+# softmax; the hook the skewed workload adds to forward.c:175-176) --------------
+
+def test_bias_is_added_to_the_router_logits(oracle):
+    d = oracle.dims(**MID)
+    blobs, router, norm = _weights(oracle, d, 41)
+    x = oracle.synth_x(42, 8, d.dim)
+    bias = np.random.default_rng(3).standard_normal(d.n_experts).astype(np.float32)
+    _, _, _, l0, _ = oracle.moe_layer(d, x, norm, router, blobs)
+    _, _, _, l1, _ = oracle.moe_layer(d, x, norm, router, blobs, bias=bias)
+    assert _same_bits(l1, (l0 + bias).astype(np.float32))  # one fp32 add per logit
+
+
+def test_dominant_bias_forces_rank_zero(oracle):
+    d = oracle.dims(**MID)
+    blobs, router, norm = _weights(oracle, d, 43)
+    x = oracle.synth_x(44, 16, d.dim)
+    for e in (0, 7, d.n_experts - 1):
+        bias = np.zeros(d.n_experts, np.float32)
+        bias[e] = 100.0
+        _, idx, w, _, _ = oracle.moe_layer(d, x, norm, router, blobs, bias=bias)
+        assert np.all(idx[:, 0] == e)
+        # the other experts' softmax mass underflows next to e^100: w_0 = 1
+        assert np.all(w[:, 0] == np.float32(1.0))
+
+
+def test_constant_bias_keeps_the_ranking(oracle):
+    d = oracle.dims(**MID)
+    blobs, router, norm = _weights(oracle, d, 45)
+    x = oracle.synth_x(46, 32, d.dim)
+    _, i0, w0, l0, _ = oracle.moe_layer(d, x, norm, router, blobs)
+    for c in (-3.0, 0.5, 7.0):
+        _, i1, w1, _, _ = oracle.moe_layer(d, x, norm, router, blobs,
+                                           bias=np.full(d.n_experts, c, np.float32))
+        # a constant shift moves every logit by one rounding at most: the
+        # ranking is unchanged wherever its gaps exceed that rounding
+        srt = np.sort(l0, axis=1)[:, ::-1]
+        gap = np.min(np.abs(np.diff(srt[:, :d.n_active + 1], axis=1)), axis=1)
+        clear = gap > 4 * np.spacing(np.float32(abs(c) + np.max(np.abs(l0))))
+        assert clear.sum() >= 28
+        assert np.array_equal(i0[clear], i1[clear])
+        assert np.max(np.abs(w0 - w1)) < 1e-5
