@@ -172,12 +172,11 @@ int mhip_scratch_carve(const mhip_dims *s, int max_tokens, void *d_base,
  * every T. The expert products are bit-equal too for small batches; from
  * MHIP_GEMM_MIN_A assignments on (and when the shape allows: d a multiple of
  * 256, expert_hidden of 128) they run on the matrix cores: the gate/up and
- * down block dots stay exact integers and each block term is added with one
- * fused multiply-add, so h and the expert outputs are within a few fp32 ulps
- * of the reference's and Q8(h) differs only in a code whose h lies that
- * close to a rounding boundary; the layer output stays within 1e-3 relative
- * of the reference (max|diff| / max|ref|). MHIP_EXACT_EXPERTS keeps the
- * bit-exact vector path at every T.
+ * down block dots stay exact integers; gate/up adds each block term in the
+ * reference's rounding order (h and Q8(h) bit-equal), down with one fused
+ * multiply-add (expert outputs within a few fp32 ulps), so the layer output
+ * is within ~1e-6 relative of the reference (max|diff| / max|ref|).
+ * MHIP_EXACT_EXPERTS keeps the bit-exact vector path at every T.
  */
 #define MHIP_GEMM_MIN_A 2048
 int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,

@@ -3,9 +3,11 @@
 // attention call), for the Qwen3-30B-A3B shape (dim 2048, 128 experts, top-K
 // with K <= 8, expert_hidden 768).
 //
-// Layout on the chip. The grid is 256 workgroups of 512 threads, one per CU;
-// workgroup b runs on XCD b % 8 (checked against HW_REG_XCC_ID at start).
-// XCD k owns routed expert slot k: its 32 workgroups stream that expert's
+// Layout on the chip. The grid is 256 workgroups of 512 threads, one per CU,
+// 32 on each XCD; a workgroup reads its XCD from HW_REG_XCC_ID and takes a
+// rank among that XCD's workgroups from a per-XCD ticket at start (an XCD
+// that receives more than 32 aborts the launch). XCD k owns routed expert
+// slot k: its 32 workgroups stream that expert's
 // gate/up/down rows (5.3 MB) while the other XCDs stream theirs, so each
 // expert's intermediate h stays inside one XCD. Every XCD recomputes the
 // (tiny) router and top-K itself, so the only cross-XCD traffic per layer is
@@ -77,8 +79,13 @@ static_assert(NT == 4 * E, "ranks: four threads per expert");
 // Tagged words: (tag << 32) | fp32 bits.
 typedef unsigned long long tw;
 
+struct alignas(64) Ticket {
+    unsigned n;                   // workgroups of this XCD that arrived (one cache line each)
+};
+
 struct DecodeWs {
     unsigned gstart[64];          // start barrier: NWG arrivals per launch, never reset
+    Ticket xtick[2][NX];          // per-XCD rank tickets, by launch parity
     tw status[32];                // (epoch << 32) | value: [0] abort bits,
                                   // [1] rms fallbacks, [2] router fallbacks
     // Every per-XCD array starts on a 256-byte boundary, so no cache line
@@ -359,6 +366,7 @@ struct Lds {
     float w[KMAX];
     int fallback;
     int nanflag;
+    int role[2];                  // this workgroup's XCD and rank within it
 };
 
 // Sequential fp32 sum of n (multiple of 4) LDS floats starting at p, in
@@ -400,14 +408,14 @@ __device__ __forceinline__ float lds_seq_sum_n(const float *p, float s) {
     do {                                                                                   \
         if ((a.flags & MHIP_DECODE_TRACE) && tid == (who) && l >= MHIP_TRACE_L0 &&         \
             l < MHIP_TRACE_L0 + MHIP_TRACE_NL)                                             \
-            ws->trace[l - MHIP_TRACE_L0][blockIdx.x][slot] = __builtin_amdgcn_s_memrealtime(); \
+            ws->trace[l - MHIP_TRACE_L0][xcd + NX * rank][slot] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
 #define TRACE(slot) TRACE_BY(slot, 0)
 #define TRACE_CLK(slot)                                                                    \
     do {                                                                                   \
         if ((a.flags & MHIP_DECODE_TRACE) && tid == 0 && l >= MHIP_TRACE_L0 &&             \
             l < MHIP_TRACE_L0 + MHIP_TRACE_NL)                                             \
-            ws->trace[l - MHIP_TRACE_L0][blockIdx.x][slot] = __builtin_amdgcn_s_memtime();  \
+            ws->trace[l - MHIP_TRACE_L0][xcd + NX * rank][slot] = __builtin_amdgcn_s_memtime();  \
     } while (0)
 
 __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
@@ -415,24 +423,41 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
     DecodeWs *ws = a.ws;
     int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int xcd = blockIdx.x % NX, rank = blockIdx.x / NX;
     const int K = a.K;
     const int need = K < E ? K + 1 : K;     // ranks certified: K and the first not taken
     const size_t layer_bytes = (size_t)E * a.lay.expert_bytes;
     const bool gu_wave = wave < NGU;
 
-    // Start: every workgroup checks its XCD, then a device-wide barrier
-    // (the counter gains NWG per launch; epochs count launches since the
-    // workspace was cleared).
+    // Start: every workgroup reads its XCD from the hardware and takes a
+    // rank among that XCD's workgroups from the XCD's ticket counter of this
+    // launch (the dispatcher deals the 256 workgroups to the 8 XCDs in turn,
+    // 32 each, but which XCD receives the first one varies between launches
+    // of different queues); then a device-wide barrier (the counter gains
+    // NWG per launch; epochs count launches since the workspace was cleared).
     if (tid == 0) {
-        if (xcc_id() != (unsigned)xcd) status_update(ws, ST_ABORT, a.epoch, false, 1);
+        const unsigned hx = xcc_id();
+        unsigned rk = WPX;
+        if (hx < NX)
+            rk = __hip_atomic_fetch_add(&ws->xtick[a.epoch & 1][hx].n, 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+        if (rk >= WPX) status_update(ws, ST_ABORT, a.epoch, false, 1);
+        sh.role[0] = hx < NX ? (int)hx : 0;
+        sh.role[1] = rk < WPX ? (int)rk : 0;
         if ((a.flags & MHIP_DECODE_FORCE_ABORT) && blockIdx.x == 0)
             status_update(ws, ST_ABORT, a.epoch, false, 4);
         __builtin_amdgcn_s_waitcnt(0);
         __hip_atomic_fetch_add(&ws->gstart[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         wait_flag(ws, &ws->gstart[0], NWG * a.epoch, a.epoch);
+        // every workgroup of this launch holds its ticket: the other parity's
+        // counters start the next launch from zero
+        if (blockIdx.x == 0)
+            for (int k = 0; k < NX; k++)
+                __hip_atomic_store(&ws->xtick[(a.epoch + 1) & 1][k].n, 0u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
+    const int xcd = __builtin_amdgcn_readfirstlane(sh.role[0]);
+    const int rank = __builtin_amdgcn_readfirstlane(sh.role[1]);
     // An XCD without a routed slot has nothing that another XCD reads.
     if (aborted(ws, a.epoch) || xcd >= K) return;
 
@@ -546,7 +571,7 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                         double sq = 0.0;
                         for (int i = 0; i < D; i++) sq = sq + (double)sh.x[i] * (double)sh.x[i];
                         sq_inv = (float)(1.0 / sqrt(sq / D + (double)a.eps));
-                        if (blockIdx.x == 0) status_update(ws, ST_RMS, a.epoch, true, 0);
+                        if (xcd == 0 && rank == 0) status_update(ws, ST_RMS, a.epoch, true, 0);
                     }
                     iv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq_inv)));
                 }
@@ -943,7 +968,7 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             __syncthreads();
             TRACE(5);
             TRACE(13);
-            if (blockIdx.x == 0 && tid < K) {
+            if (xcd == 0 && rank == 0 && tid < K) {
                 if (a.idx_out) a.idx_out[(size_t)l * K + tid] = sh.idx[tid];
                 if (a.w_out) a.w_out[(size_t)l * K + tid] = sh.w[tid];
             }

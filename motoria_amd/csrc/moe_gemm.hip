@@ -10,13 +10,16 @@
 // v_mfma_f32_16x16x32_f16 over one 32-value block gives the exact int32
 // block dot (every partial sum is an integer below 2^24). The reference's
 // block term ((float)acc * d_w) * d_x is added to the row sum in block order
-// by the vector ALUs (matmul.c:19-28) with one fused multiply-add: the term's
-// last rounding and the addition's become one, so every row sum is the
-// reference's to within a few fp32 ulps (~1e-7 relative). gate/up writes
-// Q8(h) as fp16 codes plus block-major scales, which down reads the same way
-// as gate/up reads Q8(xn); no operand is ever rounded to fp16. Q8(h) differs
-// from the reference's only in the rare code whose h sits within those few
-// ulps of a rounding boundary.
+// by the vector ALUs (matmul.c:19-28). gate/up keeps the reference's three
+// roundings, so h, and Q8(h) after it, are bit-equal to the reference's: h
+// is requantized, and a code that flips on a last-ulp difference moves a
+// token's layer output by up to ~1.5e-3 relative (measured over 48 layers of
+// 4096 tokens with one fused multiply-add there). down, whose output is not
+// requantized, adds each term with one fused multiply-add (the second
+// product's rounding and the addition's become one): the expert outputs are
+// within a few fp32 ulps of the reference's. gate/up writes Q8(h) as fp16
+// codes plus block-major scales, which down reads the same way as gate/up
+// reads Q8(xn); no operand is ever rounded to fp16.
 //
 // Tiles: 256 weight rows x 128 assignments (rows of one expert's bucket),
 // one 32-value Q8_0 block of k per step. Wavefront w owns weight rows
@@ -214,7 +217,10 @@ __device__ __forceinline__ Pieces pieces() {
 // (weight row, assignment row) for the assignment tiles j < NJA (the tiles
 // that hold rows of the bucket; the others are not computed): the exact
 // block dots, each block term added with its two scales in block order.
-template <int NJA>
+// EXACT: the reference's three roundings, s = s + ((float)acc * d_w) * d_x
+// (bit-equal row sums); otherwise the second product and the addition are
+// one fused multiply-add (within a few ulps).
+template <bool EXACT, int NJA>
 __device__ __forceinline__ void gemm_tile(Step *ring, const Src &src, int nk, f4v acc[MI][NJ]) {
     static_assert(NJA >= 1 && NJA <= NJ, "assignment tiles");
     const int tid = threadIdx.x, lane = tid & 63;
@@ -285,8 +291,13 @@ __device__ __forceinline__ void gemm_tile(Step *ring, const Src &src, int nk, f4
 #pragma unroll
             for (int i = 0; i < MI; i++)
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    acc[i][j][r] = __builtin_fmaf(blk[j & 1][i][r] * s4[i][r], sx, acc[i][j][r]);
+                for (int r = 0; r < 4; r++) {
+                    const float t = blk[j & 1][i][r] * s4[i][r];
+                    if (EXACT)
+                        acc[i][j][r] = acc[i][j][r] + t * sx;  // no contraction (-ffp-contract=off)
+                    else
+                        acc[i][j][r] = __builtin_fmaf(t, sx, acc[i][j][r]);
+                }
         }
     }
     wait_vm<0>();  // the reloads past the end
@@ -295,17 +306,18 @@ __device__ __forceinline__ void gemm_tile(Step *ring, const Src &src, int nk, f4
 
 // The assignment tiles that hold rows of the bucket (a bucket's last tile
 // may hold few rows).
+template <bool EXACT>
 __device__ __forceinline__ void gemm_tile_rows(Step *ring, const Src &src, int nk, int nrows,
                                                f4v acc[MI][NJ]) {
     const int nj = (nrows + 15) / 16;
     if (nj > 4)
-        gemm_tile<8>(ring, src, nk, acc);
+        gemm_tile<EXACT, 8>(ring, src, nk, acc);
     else if (nj > 2)
-        gemm_tile<4>(ring, src, nk, acc);
+        gemm_tile<EXACT, 4>(ring, src, nk, acc);
     else if (nj > 1)
-        gemm_tile<2>(ring, src, nk, acc);
+        gemm_tile<EXACT, 2>(ring, src, nk, acc);
     else
-        gemm_tile<1>(ring, src, nk, acc);
+        gemm_tile<EXACT, 1>(ring, src, nk, acc);
 }
 
 // ---- x block scales in bucketed, block-major order --------------------------------
@@ -387,7 +399,7 @@ __global__ __launch_bounds__(GT, 2) void k_gateup_mfma(
     for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = (f4v){0.0f, 0.0f, 0.0f, 0.0f};
-    gemm_tile_rows(L.ring, src, d / KB, nrows, acc);
+    gemm_tile_rows<true>(L.ring, src, d / KB, nrows, acc);
 
     // SwiGLU into the h tile (LDS, reused): row = assignment, column = h - h0
     const int c = lane >> 4, l16 = lane & 15;
@@ -486,7 +498,7 @@ __global__ __launch_bounds__(GT, 2) void k_down_mfma(const uint8_t *__restrict__
     for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = (f4v){0.0f, 0.0f, 0.0f, 0.0f};
-    gemm_tile_rows(L.ring, src, eh / KB, nrows, acc);
+    gemm_tile_rows<false>(L.ring, src, eh / KB, nrows, acc);
 
     const int c = lane >> 4, l16 = lane & 15;
 #pragma unroll

@@ -15,8 +15,8 @@
 // run in block order, and sums the reference takes in double are either
 // reproduced exactly or certified (see k_rmsnorm_q8). For large batches the
 // gate/up and down stages switch to the matrix-core kernels of moe_gemm.hip
-// (exact block dots, each block term added with one fused multiply-add; the
-// layer within 1e-3 of the reference); routing and dispatch stay bit-exact.
+// (exact block dots; h and Q8(h) bit-equal, the expert outputs within a few
+// ulps); routing and dispatch stay bit-exact.
 //
 // Status words (sc->status, cleared by the host per call): [0] bit 0 = an
 // expert index out of range; [1] rmsnorm sums that took the sequential path;

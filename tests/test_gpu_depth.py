@@ -6,9 +6,10 @@ decode kernel's prefetch of the next layer's norm are all exercised.
 
 - decode48 (one token, the persistent decode kernel): teacher-forced, one
   launch per layer on the oracle's own input, expert indices bit-equal and
-  the update within TOL; then one 48-layer launch compared end to end, where
-  a routing difference may only start at a near-tie of the oracle's gate
-  probabilities (the two paths' inputs differ by rounding there).
+  the update within TOL; then one 48-layer launch audited on its own
+  trajectory (every layer's routing bit-equal to the oracle's on the same
+  input, every update within TOL), with the oracle's free-running chain
+  reported beside it.
 - batch64x48 (64 tokens, the vector kernels): every layer bit-equal to the
   oracle, each on the previous layer's output, and the one-call 48-layer
   stack bit-equal to the oracle's stack.
@@ -34,7 +35,6 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-3
 L = 48
 NTHREADS = min(16, os.cpu_count() or 1)
-NEAR_TIE = 1e-4  # relative gap of the oracle's probabilities that rounding of the input can cross
 
 
 def say(*a):
@@ -118,44 +118,45 @@ def test_decode48_teacher_forced(oracle, qwen_dims, deep):
 
 
 def test_decode48_one_launch_divergence_audit(oracle, qwen_dims, deep):
+    """One 48-layer launch from x0, audited layer by layer on its own
+    trajectory: the input of layer l is the output of a launch of layers
+    [0, l) from x0 (the kernel is deterministic: the 48-layer launch is
+    repeated and compared bit for bit). At every layer the oracle, given that
+    same input, must route exactly as the launch did and produce the update
+    within TOL. The oracle's free-running chain from x0 is compared too: where
+    its routing first departs from the launch's, the departure must come from
+    the input (the two chains' inputs differ there, by the rounding the gate
+    weights add per layer, amplified by Q8 code flips), which the first check
+    already proves: on the launch's own input the routing is the oracle's."""
     say("test_decode48_one_launch_divergence_audit")
     moe, norms, routers = deep
     d = qwen_dims
-    K = d.n_active
     for seed in (W.X_SEED + 5, W.X_SEED + 6):
         x0 = oracle.synth_x(seed, 1, d.dim)[0]
         xg, ig, _ = moe.decode(0, L, x0)
-        st = moe.decode_status()
-        assert st[0] == 0, st
-        x = x0
-        diverged = None
+        assert moe.decode_status()[0] == 0
+        xg2, ig2, _ = moe.decode(0, L, x0)
+        assert np.array_equal(bits(xg), bits(xg2)) and np.array_equal(ig, ig2), "not deterministic"
+        xin = [x0] + [moe.decode(0, l, x0)[0] for l in range(1, L)] + [xg]
+        worst = 0.0
         for l in range(L):
-            xo, io, _, lo = oracle_layer(oracle, d, moe, norms, routers, l, x)
-            if not np.array_equal(ig[l], io[0]):
-                diverged = l
-                # the oracle's gate probabilities at this layer: every expert
-                # that differs must sit at a near-tie of the ordering
-                p = oracle.softmax(lo[0])
-                top = np.sort(p)[::-1]
-                kth = top[K - 1]
-                for e in set(ig[l].tolist()) ^ set(io[0].tolist()):
-                    assert abs(p[e] - kth) <= NEAR_TIE * kth, \
-                        "layer %d: expert %d differs away from a near-tie" % (l, e)
-                if set(ig[l].tolist()) == set(io[0].tolist()):
-                    # same set, different order: the swapped pair is a near-tie
-                    for j in range(K):
-                        if ig[l][j] != io[0][j]:
-                            a, b = p[ig[l][j]], p[io[0][j]]
-                            assert abs(a - b) <= NEAR_TIE * max(a, b), "layer %d order" % l
-                break
+            xo, io, _, _ = oracle_layer(oracle, d, moe, norms, routers, l, xin[l])
+            assert np.array_equal(ig[l], io[0]), "layer %d: routing of the launch's own input" % l
+            e = rel(xin[l + 1] - xin[l], xo[0] - xin[l])
+            worst = max(worst, e)
+            assert e <= TOL, "layer %d: update rel err %.2e" % (l, e)
+        # the oracle's free-running chain
+        x, first = x0, None
+        for l in range(L):
+            xo, io, _, _ = oracle_layer(oracle, d, moe, norms, routers, l, x)
+            if first is None and not np.array_equal(ig[l], io[0]):
+                first = (l, rel(xin[l], x))
             x = xo[0]
-        if diverged is None:
-            e = rel(xg - x0, x - x0)
-            say("  seed %d: 48 layers routed identically, end-to-end update rel err %.2e"
-                % (seed, e))
-            assert e <= TOL and rel(xg, x) <= TOL
-        else:
-            say("  seed %d: routing first differs at layer %d, at a near-tie" % (seed, diverged))
+        say("  seed %d: every layer of the launch routed as the oracle routes its input, worst "
+            "update rel err %.2e; free-running oracle chain: %s, end-to-end rel diff %.2e"
+            % (seed, worst, "same routing at all 48 layers" if first is None else
+               "routing departs at layer %d where the inputs differ by %.1e" % first,
+               rel(xg, x)))
 
 
 # ---- batch64x48 -------------------------------------------------------------------
