@@ -213,6 +213,25 @@ int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
                       const void *d_table, const float *d_router, const float *d_router_t,
                       const float *d_norm, const float *d_bias, float *d_x, int L,
                       void *d_ws, int *d_idx, float *d_w, int flags);
+/*
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). mhip_decode_stack without the workspace argument: the
+ * workspace is a device-resident array of the library, one per GPU, of
+ * mhip_decode_ws_bytes() bytes (0.95 MiB, held until the process ends; its
+ * address is taken once per device when a context is opened). The call
+ * queues the launch and, when d_status (device int[4]) is not NULL, a copy
+ * of this launch's status words ([0] abort bits, [1] rmsnorm fallbacks,
+ * [2] exact-router layers, [3] 0) into it; it allocates nothing. L is at most
+ * MHIP_DECODE_MAX_LAYERS (-1 beyond). Every call on one GPU shares that
+ * GPU's workspace: calls that overlap on one GPU (two streams, two threads)
+ * race; calls in stream order do not.
+ */
+int mhip_decode_stack_noalloc(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
+                              const void *d_table, const float *d_router,
+                              const float *d_router_t, const float *d_norm, const float *d_bias,
+                              float *d_x, int L, int *d_idx, float *d_w, int *d_status,
+                              int flags);
 int mhip_decode_status(mhip_ctx *c, const void *d_ws, int status[4]);
 /* With MHIP_DECODE_TRACE set: the 100 MHz real-time counter read by thread 0
  * of each of the 256 workgroups at up to MHIP_TRACE_SLOTS stage boundaries

@@ -97,6 +97,8 @@ SIGNATURES = {
     "mhip_decode_supported": (_i, [_p, ctypes.POINTER(Dims)]),
     "mhip_decode_stack": (_i, [_p, ctypes.POINTER(Dims), ctypes.POINTER(Layout), _p, _p, _p, _p,
                                _p, _p, _i, _p, _p, _p, _i]),
+    "mhip_decode_stack_noalloc": (_i, [_p, ctypes.POINTER(Dims), ctypes.POINTER(Layout), _p, _p,
+                                       _p, _p, _p, _p, _i, _p, _p, _p, _i]),
     "mhip_decode_status": (_i, [_p, _p, ctypes.POINTER(_i)]),
     "mhip_decode_trace": (_i, [_p, _p, _p]),
     "mhip_quantize_q8": (_i, [_p, _p, _p, _i]),

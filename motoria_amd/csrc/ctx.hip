@@ -117,6 +117,7 @@ int mhip_open(mhip_ctx **out, int device, char *err, size_t errlen) {
                               "hipStreamCreate");
     for (int i = 0; i < 16 && !rc; i++)
         rc = mhip::check(c, hipEventCreate(&c->marks[i]), "hipEventCreate");
+    if (!rc) rc = mhip::decode_noalloc_setup(c);
     if (rc) {
         if (err && errlen) snprintf(err, errlen, "%s", c->err);
         mhip_close(c);

@@ -119,6 +119,18 @@ struct DecodeArgs {
     unsigned epoch;               // tag of this launch (bits 8..31 of every tag)
 };
 
+// The allocation-free entry point's workspace (the array `scratch` below):
+// its size, and per device the address of that device's copy and the epoch
+// of the last launch that used it (shared by every context of the device;
+// calls that overlap on one GPU race, like two launches on one workspace).
+constexpr size_t STATIC_WS_BYTES = (sizeof(DecodeWs) + 255) / 256 * 256;
+constexpr int MAX_DEVICES = 64;
+struct StaticWs {
+    void *ptr;       // device address of this device's copy (0 until set up)
+    unsigned epoch;  // launches since it was last cleared
+};
+StaticWs g_static_ws[MAX_DEVICES];
+
 __device__ __forceinline__ unsigned xcc_id() {
     return __builtin_amdgcn_s_getreg((20) | (0 << 6) | ((4 - 1) << 11));
 }
@@ -1051,24 +1063,12 @@ bool decode_shape_fits(const mhip_dims *s) {
            s->n_active <= KMAX;
 }
 
-}  // namespace
+// ---- host side --------------------------------------------------------------------
 
-extern "C" {
-
-size_t mhip_decode_ws_bytes(void) { return (sizeof(DecodeWs) + 255) / 256 * 256; }
-
-int mhip_decode_supported(mhip_ctx *c, const mhip_dims *s) {
-    if (mhip::check_dims(c, s) || mhip::use_device(c)) return -1;
-    if (!decode_shape_fits(s)) return 0;
-    return decode_device_fits(c);
-}
-
-int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
-                      const void *d_table, const float *d_router, const float *d_router_t,
-                      const float *d_norm, const float *d_bias, float *d_x, int L, void *d_ws,
-                      int *d_idx, float *d_w, int flags) {
-    // Arguments first (no device call before they pass). Exchange tags hold
-    // the layer in 8 bits, so one launch covers at most 256 layers.
+// Argument checks shared by both entry points (no device call before they
+// pass): 1 to launch, 0 for nothing to do (L = 0), -1 on an error. Exchange
+// tags hold the layer in 8 bits, so one launch covers at most 256 layers.
+int check_decode_args(mhip_ctx *c, const mhip_dims *s, int L) {
     if (mhip::check_dims(c, s)) return -1;
     if (L < 0 || L > MHIP_DECODE_MAX_LAYERS)
         return mhip::fail(c, "decode stack: L=%d outside [0, %d]", L, MHIP_DECODE_MAX_LAYERS);
@@ -1084,18 +1084,35 @@ int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
         return mhip::fail(c, "decode stack needs %d CUs with one %d-thread workgroup each "
                              "(device has %d CUs, occupancy %d)", NWG, NT, c->decode_cus,
                           c->decode_occ);
-    if ((uintptr_t)d_ws % 256)
-        return mhip::fail(c, "decode stack: workspace %p is not 256-byte aligned", d_ws);
-    DecodeWs *ws = (DecodeWs *)d_ws;
-    // Exchanged words and status words are tagged with the launch's epoch,
-    // so stale words of earlier launches never match, and the start counter
-    // grows by NWG per launch: nothing is cleared between launches. A
-    // workspace this context has not used last (or an epoch about to leave
-    // its 24 bits) is cleared whole first (fill kernel, no memset).
-    if (ws != c->decode_ws || c->decode_epoch >= (1u << 24) - 1) {
+    return 1;
+}
+
+// The status words of the launch tagged `epoch`, copied to status[4]
+// (status[3] = 0) for callers that read them later from device memory.
+__global__ void k_decode_status_out(const DecodeWs *ws, unsigned epoch, int *status) {
+    const int i = threadIdx.x;
+    if (i < 3) {
+        const tw v = __hip_atomic_load(&ws->status[i], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        status[i] = (unsigned)(v >> 32) == epoch ? (int)(unsigned)v : 0;
+    } else if (i == 3) {
+        status[3] = 0;
+    }
+}
+
+// One launch of the decode kernel on workspace ws, whose launches are
+// counted by *epoch. Exchanged words and status words are tagged with the
+// launch's epoch, so stale words of earlier launches never match, and the
+// start counter grows by NWG per launch: nothing is cleared between launches.
+// The workspace is cleared whole first (fill kernel, no memset) when `fresh`
+// or when the epoch is about to leave its 24 bits. Queues no allocation.
+int launch_decode(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay, const void *d_table,
+                  const float *d_router, const float *d_router_t, const float *d_norm,
+                  const float *d_bias, float *d_x, int L, DecodeWs *ws, unsigned *epoch,
+                  bool fresh, int *d_idx, float *d_w, int *d_status, int flags) {
+    if (fresh || *epoch >= (1u << 24) - 1) {
         if (mhip_zero(c, ws, offsetof(DecodeWs, trace))) return -1;
-        c->decode_ws = ws;
-        c->decode_epoch = 0;
+        *epoch = 0;
     }
     if ((flags & MHIP_DECODE_TRACE) && mhip_zero(c, ws->trace, sizeof(ws->trace))) return -1;
     DecodeArgs a;
@@ -1114,17 +1131,94 @@ int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     a.norm_topk = s->norm_topk;
     a.flags = flags;
     a.eps = s->norm_eps;
-    a.epoch = ++c->decode_epoch;
+    a.epoch = ++*epoch;
     // An ordinary launch: one 512-thread workgroup fits each of the 256 CUs
-    // (checked above), so on an otherwise idle device all of them are
+    // (checked before), so on an otherwise idle device all of them are
     // resident at once. Should one not be, the start barrier times out and
     // the launch reports abort bit 2 instead of waiting for ever.
     int slot = mhip::stage_begin(c, MHIP_STAGE_DECODE);
     k_decode_stack<<<NWG, NT, 0, c->stream>>>(a);
     const hipError_t e = hipGetLastError();
     mhip::stage_end(c, slot);
-    if (e != hipSuccess) c->decode_epoch--;   // nothing arrived at the start counter
-    return mhip::check(c, e, "decode stack launch");
+    if (e != hipSuccess) {
+        --*epoch;  // nothing arrived at the start counter
+        return mhip::check(c, e, "decode stack launch");
+    }
+    if (d_status) {
+        k_decode_status_out<<<1, 64, 0, c->stream>>>(ws, a.epoch, d_status);
+        return mhip::check_launch(c, "decode status copy");
+    }
+    return 0;
+}
+
+}  // namespace
+
+// Workspace of mhip_decode_stack_noalloc: a device-resident array of the
+// library, one copy per GPU (each device holds its own instance at its own
+// address until the process ends). Host code never uses this name as an
+// address: the address of a device's copy comes from hipGetSymbolAddress,
+// taken once per device at context set-up (decode_noalloc_setup).
+static __device__ __align__(256) unsigned char scratch[STATIC_WS_BYTES];
+
+namespace mhip {
+
+int decode_noalloc_setup(mhip_ctx *c) {
+    if (c->device < 0 || c->device >= MAX_DEVICES) return 0;  // the entry point then refuses
+    StaticWs &st = g_static_ws[c->device];
+    if (st.ptr) return 0;
+    void *ptr = nullptr;
+    if (check(c, hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)),
+              "hipGetSymbolAddress (decode workspace)"))
+        return -1;
+    if (!ptr || (uintptr_t)ptr % 256) return fail(c, "decode workspace symbol at %p", ptr);
+    // cleared once here; afterwards the launches' epochs keep it consistent
+    if (mhip_zero(c, ptr, STATIC_WS_BYTES) || mhip_sync(c)) return -1;
+    st.ptr = ptr;
+    st.epoch = 0;
+    return 0;
+}
+
+}  // namespace mhip
+
+extern "C" {
+
+size_t mhip_decode_ws_bytes(void) { return (sizeof(DecodeWs) + 255) / 256 * 256; }
+
+int mhip_decode_supported(mhip_ctx *c, const mhip_dims *s) {
+    if (mhip::check_dims(c, s) || mhip::use_device(c)) return -1;
+    if (!decode_shape_fits(s)) return 0;
+    return decode_device_fits(c);
+}
+
+int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
+                      const void *d_table, const float *d_router, const float *d_router_t,
+                      const float *d_norm, const float *d_bias, float *d_x, int L, void *d_ws,
+                      int *d_idx, float *d_w, int flags) {
+    const int ok = check_decode_args(c, s, L);
+    if (ok <= 0) return ok;
+    if ((uintptr_t)d_ws % 256)
+        return mhip::fail(c, "decode stack: workspace %p is not 256-byte aligned", d_ws);
+    DecodeWs *ws = (DecodeWs *)d_ws;
+    // A workspace this context has not used last starts from a cleared one.
+    const int rc = launch_decode(c, s, lay, d_table, d_router, d_router_t, d_norm, d_bias, d_x,
+                                 L, ws, &c->decode_epoch, ws != c->decode_ws, d_idx, d_w,
+                                 nullptr, flags);
+    if (rc == 0) c->decode_ws = ws;
+    return rc;
+}
+
+int mhip_decode_stack_noalloc(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
+                              const void *d_table, const float *d_router,
+                              const float *d_router_t, const float *d_norm, const float *d_bias,
+                              float *d_x, int L, int *d_idx, float *d_w, int *d_status,
+                              int flags) {
+    const int ok = check_decode_args(c, s, L);
+    if (ok <= 0) return ok;
+    StaticWs *st = c->device < MAX_DEVICES ? &g_static_ws[c->device] : nullptr;
+    if (!st || !st->ptr)
+        return mhip::fail(c, "no-alloc decode: device %d has no set-up workspace", c->device);
+    return launch_decode(c, s, lay, d_table, d_router, d_router_t, d_norm, d_bias, d_x, L,
+                         (DecodeWs *)st->ptr, &st->epoch, false, d_idx, d_w, d_status, flags);
 }
 
 int mhip_decode_status(mhip_ctx *c, const void *d_ws, int status[4]) {

@@ -47,6 +47,10 @@ inline unsigned blocks_for(size_t n, unsigned per) {
     return (unsigned)((n + per - 1) / per);
 }
 
+// Once per device (at context set-up, that device current): the device
+// address of the allocation-free decode workspace (decode.hip).
+int decode_noalloc_setup(mhip_ctx *c);
+
 // Matrix-core expert products (moe_gemm.hip).
 bool gemm_path_fits(const mhip_dims *s);
 int gemm_max_tiles(int A, int E);
