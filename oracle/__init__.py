@@ -40,12 +40,24 @@ def dims(**kw):
     return Dims(**kw)
 
 
-def lib():
+def select(variant):
+    """Which build the wrappers below call: "default" (oracle/liboracle.so,
+    gcc -O3 -ffp-contract=off) or "native" (oracle/_native/liboracle.so, the
+    same with -march=native, built by `make -C oracle native` on the host
+    that runs it)."""
+    global _LIB
+    _LIB = None
+    lib(variant)
+
+
+def lib(variant=None):
     global _LIB
     if _LIB is None:
-        path = os.path.join(_HERE, "liboracle.so")
+        name = os.path.join("_native", "liboracle.so") if variant == "native" else "liboracle.so"
+        path = os.path.join(_HERE, name)
         if not os.path.exists(path):
-            raise RuntimeError("oracle/liboracle.so is not built (make -C oracle)")
+            raise RuntimeError("oracle/%s is not built (make -C oracle%s)"
+                               % (name, " native" if variant == "native" else ""))
         L = ctypes.CDLL(path)
         L.orc_row_bytes.restype = ctypes.c_size_t
         L.orc_row_bytes.argtypes = [_i, _i]

@@ -220,9 +220,19 @@ int orc_moe_layer(const orc_dims *s, int T, float *x, const float *ffn_norm,
     const int maxd = d > s->expert_hidden ? d : s->expert_hidden;
     int rc = 0;
     if (nthreads < 1) nthreads = 1;
-    /* One token: threads over 64-row chunks of each matrix. */
-    const int row_threads = T == 1 ? nthreads : 1;
-    if (T == 1) nthreads = 1;
+    if (T == 1 && nthreads > 1) {
+        /* One token: threads over 64-row chunks of each matrix, each chunk
+         * loop a top-level parallel region (the pool's threads are reused). */
+        float *scratch = malloc(sizeof(float) * (size_t)scratch_floats(s));
+        orc_block_q8 *xq = malloc(sizeof(orc_block_q8) * (size_t)(maxd / ORC_QK));
+        if (!scratch || !xq ||
+            moe_token(s, x, ffn_norm, router, bias, blobs, idx, w, logits, xn, scratch, xq,
+                      nthreads))
+            rc = 1;
+        free(scratch);
+        free(xq);
+        return rc ? -1 : 0;
+    }
     /* Tokens are independent (the reference steps them one at a time), so
      * threads over tokens change no bits. */
 #pragma omp parallel num_threads(nthreads) reduction(| : rc)
@@ -236,7 +246,7 @@ int orc_moe_layer(const orc_dims *s, int T, float *x, const float *ffn_norm,
             if (moe_token(s, x + (size_t)t * d, ffn_norm, router, bias, blobs,
                           idx ? idx + (size_t)t * K : NULL, w ? w + (size_t)t * K : NULL,
                           logits ? logits + (size_t)t * E : NULL,
-                          xn ? xn + (size_t)t * d : NULL, scratch, xq, row_threads))
+                          xn ? xn + (size_t)t * d : NULL, scratch, xq, 1))
                 rc |= 1;
         }
         free(scratch);

@@ -288,3 +288,30 @@ def test_constant_bias_keeps_the_ranking(oracle):
         assert clear.sum() >= 28
         assert np.array_equal(i0[clear], i1[clear])
         assert np.max(np.abs(w0 - w1)) < 1e-5
+
+
+def test_native_build_gives_the_same_bits(oracle):
+    """The -march=native build of the oracle (the best-case CPU baseline) is
+    the same arithmetic: -ffp-contract=off keeps every product rounded."""
+    import subprocess
+    import os
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run(["make", "-s", "-C", os.path.join(root, "oracle"), "native"],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        pytest.skip("native oracle build failed: %s" % r.stderr[-200:])
+    d = oracle.dims(**MID)
+    blobs, router, norm = _weights(oracle, d, 51)
+    x = oracle.synth_x(52, 24, d.dim)
+    a = oracle.moe_layer(d, x, norm, router, blobs)
+    b1 = oracle.moe_layer(d, x[:1], norm, router, blobs, nthreads=4)
+    try:
+        oracle.select("native")
+        b = oracle.moe_layer(d, x, norm, router, blobs)
+        c1 = oracle.moe_layer(d, x[:1], norm, router, blobs, nthreads=4)
+    finally:
+        oracle.select("default")
+    for u, v in zip(a, b):
+        assert _same_bits(u, v)
+    for u, v in zip(b1, c1):
+        assert _same_bits(u, v)
