@@ -69,6 +69,38 @@ int mia_moe_set_layer(mia_moe *m, int layer, const float *ffn_norm, const float 
  * and routers ~ N(0, 0.02), ffn_norm = 1. */
 int mia_moe_synth(mia_moe *m, uint64_t seed);
 
+/* ---- .mia model files --------------------------------------------------
+ * The header of a .mia file (the reference's mia_header,
+ * include/mia/mia_file.h:10-21: 112 bytes, little-endian) and the expert
+ * blob offsets derived from it (src/storage/mia_file.c:98-101). */
+typedef struct {
+    uint32_t version, wtype, dim, n_layers, n_heads, n_kv_heads, head_dim, vocab;
+    uint32_t n_experts, n_active, expert_hidden, norm_topk;
+    float rope_theta, norm_eps;
+    uint64_t dense_offset, dense_size;
+    uint64_t experts_offset, expert_blob_size;
+    uint64_t tok_offset, tok_size;
+    uint64_t off_up, off_down; /* up and down matrices inside a blob */
+} mia_file_info;
+
+/* Reads and checks a .mia file's header: magic "MIA1", version 1, the
+ * reference reader's shape rules (src/storage/mia_file.c:53-61), the dense
+ * section laid out as the converter's NewLayout (tools/internal/mia/
+ * format.go:129-165; the walk must end at dense_size), gate/up/down fitting
+ * the blob, and a file long enough for every expert blob. 0, or -1 with the
+ * reason in err. Reads no tensor. */
+int mia_file_probe(const char *path, mia_file_info *info, char *err, size_t errlen);
+/* File offsets of layer `layer`'s ffn_norm[dim] and router[E][dim] (fp32)
+ * in a probed file. 0, or -1 for a layer out of range. */
+int mia_file_layer_offsets(const mia_file_info *info, int layer, uint64_t *ffn_norm,
+                           uint64_t *router);
+/* Fills the handle from a .mia file: every layer's ffn_norm and router
+ * (mia_moe_set_layer) and every (layer, expert) blob into the HBM table,
+ * bit-identical to filling it through the loader port with the reference's
+ * mia_file_read_expert. The file's shape, norm settings and Q8_0 weight type
+ * must be the handle's. */
+int mia_moe_load_file(mia_moe *m, const char *path);
+
 /* One layer, moe() semantics, in place on host x[T][dim]. Bit-equal to the
  * reference (below MHIP_GEMM_MIN_A assignments; within 1e-3 above). One
  * token (T = 1) runs as one launch of the persistent decode kernel with the

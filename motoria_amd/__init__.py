@@ -56,6 +56,33 @@ class Scratch(ctypes.Structure):
                                   "hdq", "gtile", "xsb", "hq", "hs", "glight")]
 
 
+class FileInfo(ctypes.Structure):
+    """mia_file_info (include/mia/moe.h): a .mia header and blob offsets."""
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "version", "wtype", "dim", "n_layers", "n_heads", "n_kv_heads", "head_dim", "vocab",
+        "n_experts", "n_active", "expert_hidden", "norm_topk")] + [
+        ("rope_theta", _f), ("norm_eps", _f)] + [(n, ctypes.c_uint64) for n in (
+            "dense_offset", "dense_size", "experts_offset", "expert_blob_size", "tok_offset",
+            "tok_size", "off_up", "off_down")]
+
+
+def file_probe(path):
+    """mia_file_probe: (FileInfo, None) or (None, error message)."""
+    info = FileInfo()
+    err = ctypes.create_string_buffer(512)
+    if lib().mia_file_probe(path.encode(), ctypes.byref(info), err, 512) != 0:
+        return None, err.value.decode()
+    return info, None
+
+
+def file_layer_offsets(info, layer):
+    fn, rt = ctypes.c_uint64(), ctypes.c_uint64()
+    if lib().mia_file_layer_offsets(ctypes.byref(info), layer, ctypes.byref(fn),
+                                    ctypes.byref(rt)) != 0:
+        raise ValueError("layer %d out of range" % layer)
+    return fn.value, rt.value
+
+
 # Every function the library exports, with its ctypes signature. tests check
 # this list against the declarations in include/.
 SIGNATURES = {
@@ -110,6 +137,9 @@ SIGNATURES = {
     "mia_dequantize_row": (None, [_i, _p, _p, _i]),
     "mia_matvec": (None, [_p, _p, _i, _p, _p, _i, _i]),
     "mia_matvec_scalar": (None, [_p, _p, _i, _p, _p, _i, _i]),
+    # include/mia/matvec_cache.h
+    "mia_matvec_register": (_i, [_p, _i, _i, _i]),
+    "mia_matvec_unregister": (_i, [_p]),
     # include/mia/moe.h
     "mia_moe_open": (_i, [ctypes.POINTER(_p), ctypes.POINTER(MoeConfig), ctypes.c_char_p, _sz]),
     "mia_moe_close": (None, [_p]),
@@ -127,6 +157,11 @@ SIGNATURES = {
     "mia_moe_stack": (_i, [_p, _i, _i, _p, _i]),
     "mia_moe_layer_dev": (_i, [_p, _i, _p, _i, _p]),
     "mia_moe_stack_dev": (_i, [_p, _i, _i, _p, _i]),
+    "mia_file_probe": (_i, [ctypes.c_char_p, ctypes.POINTER(FileInfo), ctypes.c_char_p, _sz]),
+    "mia_file_layer_offsets": (_i, [ctypes.POINTER(FileInfo), _i,
+                                    ctypes.POINTER(ctypes.c_uint64),
+                                    ctypes.POINTER(ctypes.c_uint64)]),
+    "mia_moe_load_file": (_i, [_p, ctypes.c_char_p]),
     "mia_moe_decode": (_i, [_p, _i, _i, _p, _p, _p, _p]),
     "mia_moe_decode_dev": (_i, [_p, _i, _i, _p, _p]),
     "mia_moe_decode_status": (_i, [_p, ctypes.POINTER(_i)]),
@@ -230,6 +265,10 @@ class Moe:
         """loader_fn(layer, expert, dst_ptr) -> int, the storage port."""
         cb = LOADER(lambda ctx, l, e, dst: loader_fn(l, e, dst))
         self._check(lib().mia_moe_load_experts(self.h, cb, None), "mia_moe_load_experts")
+
+    def load_file(self, path):
+        """Fill the handle from a .mia file (mia_moe_load_file)."""
+        self._check(lib().mia_moe_load_file(self.h, path.encode()), "mia_moe_load_file")
 
     def read_expert(self, layer, expert):
         out = np.zeros(self.blob_bytes, dtype=np.uint8)

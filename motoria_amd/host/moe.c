@@ -9,7 +9,10 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "moe_internal.h"
+
 struct mia_moe {
+    mia_moe_config cfg; /* as opened */
     mhip_ctx *gpu;
     mhip_dims dims;
     mhip_layout lay;
@@ -42,6 +45,16 @@ static int fail(mia_moe *m, const char *fmt, ...) {
 }
 
 static int gpu_fail(mia_moe *m) { return fail(m, "%s", mhip_error(m->gpu)); }
+
+int mia_moe_fail(mia_moe *m, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(m->err, sizeof(m->err), fmt, ap);
+    va_end(ap);
+    return -1;
+}
+void *mia_moe_table(mia_moe *m) { return m->d_table; }
+const mia_moe_config *mia_moe_cfg(const mia_moe *m) { return &m->cfg; }
 static int check_status(mia_moe *m, int l0);
 
 static size_t align_up(size_t n, size_t a) { return (n + a - 1) / a * a; }
@@ -84,6 +97,7 @@ int mia_moe_open(mia_moe **out, const mia_moe_config *cfg, char *err, size_t err
         if (err && errlen) snprintf(err, errlen, "out of host memory");
         return -1;
     }
+    m->cfg = *cfg;
     m->dims.dim = cfg->dim;
     m->dims.n_experts = cfg->n_experts;
     m->dims.n_active = cfg->n_active;

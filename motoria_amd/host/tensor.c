@@ -3,19 +3,31 @@
  * with their host-pointer interface, executed by the HIP kernels of
  * include/mia_hip.h on a lazily opened context of device 0 (or
  * $MIA_DEVICE). The functions return void in the reference interface, so a
- * GPU failure is reported on stderr and aborts.
+ * GPU failure is reported on stderr and aborts. Matrices registered with
+ * mia_matvec_register (include/mia/matvec_cache.h) stay in HBM.
  */
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
 #include "mia/matmul.h"
+#include "mia/matvec_cache.h"
 #include "mia/quant.h"
 #include "mia_hip.h"
 
 static mhip_ctx *g_ctx;
 static void *g_buf[4];
 static size_t g_cap[4];
+
+/* Registered (device-resident) matrices, keyed by host pointer. */
+typedef struct {
+    const void *w;
+    mia_wtype t;
+    int rows, cols;
+    void *d_w;
+} resident;
+static resident *g_res;
+static int g_nres, g_capres;
 
 static void die(const char *what) {
     fprintf(stderr, "motoria: %s: %s\n", what, g_ctx ? mhip_error(g_ctx) : "no GPU context");
@@ -79,6 +91,44 @@ void mia_dequantize_row(mia_wtype t, const void *src, float *dst, int n) {
         die("dequantize_row");
 }
 
+static int find_resident(const void *w) {
+    for (int i = 0; i < g_nres; i++)
+        if (g_res[i].w == w) return i;
+    return -1;
+}
+
+int mia_matvec_register(const void *w, mia_wtype t, int rows, int cols) {
+    if (!w || rows <= 0 || cols <= 0 || (t != MIA_F32 && t != MIA_Q8_0) ||
+        (t == MIA_Q8_0 && cols % MIA_QK))
+        return -1;
+    mia_matvec_unregister(w);
+    if (g_nres == g_capres) {
+        const int cap = g_capres ? 2 * g_capres : 16;
+        resident *r = realloc(g_res, sizeof(resident) * (size_t)cap);
+        if (!r) return -1;
+        g_res = r;
+        g_capres = cap;
+    }
+    mhip_ctx *c = ctx();
+    const size_t wb = (size_t)rows * mia_row_bytes(t, cols);
+    void *d = mhip_malloc(c, wb);
+    if (!d) return -1;
+    if (mhip_h2d(c, d, w, wb)) {
+        mhip_free(c, d);
+        return -1;
+    }
+    g_res[g_nres++] = (resident){w, t, rows, cols, d};
+    return 0;
+}
+
+int mia_matvec_unregister(const void *w) {
+    const int i = find_resident(w);
+    if (i < 0) return -1;
+    mhip_free(ctx(), g_res[i].d_w);
+    g_res[i] = g_res[--g_nres];
+    return 0;
+}
+
 void mia_matvec(float *out, const void *w, mia_wtype t, const float *x, mia_block_q8 *xq,
                 int rows, int cols) {
     if (rows <= 0) return;
@@ -86,11 +136,14 @@ void mia_matvec(float *out, const void *w, mia_wtype t, const float *x, mia_bloc
     const size_t wb = (size_t)rows * mia_row_bytes(t, cols);
     const size_t xb = (size_t)cols * sizeof(float);
     const size_t qb = t == MIA_Q8_0 ? (size_t)(cols / MIA_QK) * sizeof(mia_block_q8) : 0;
-    void *dw = buf(0, wb);
+    /* a registered matrix of this type and shape is read from HBM */
+    const int r = find_resident(w);
+    const int hit = r >= 0 && g_res[r].t == t && g_res[r].rows == rows && g_res[r].cols == cols;
+    void *dw = hit ? g_res[r].d_w : buf(0, wb);
     float *dx = buf(1, xb ? xb : 4);
     void *dq = buf(2, qb ? qb : 4);
     float *dout = buf(3, (size_t)rows * sizeof(float));
-    if (mhip_h2d(c, dw, w, wb) || mhip_h2d(c, dx, x, xb) ||
+    if ((!hit && mhip_h2d(c, dw, w, wb)) || mhip_h2d(c, dx, x, xb) ||
         mhip_matvec(c, dout, dw, (int)t, dx, dq, rows, cols) ||
         mhip_d2h(c, out, dout, (size_t)rows * sizeof(float)) ||
         (qb && xq && mhip_d2h(c, xq, dq, qb)))

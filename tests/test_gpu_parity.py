@@ -129,6 +129,37 @@ def test_quantize_and_matvec_bit_exact(oracle):
         assert_bits(deq, oracle.dequantize_row_q8(wq[: cols // 32 * 36], cols), "dequantize")
 
 
+def test_matvec_registered_weights(oracle):
+    """A registered matrix is read from its HBM copy: bit-equal results;
+    another shape at the same pointer is not served from the copy; after
+    unregistering, the host bytes are read again."""
+    say("test_matvec_registered_weights")
+    L = M.lib()
+    rows, cols = 1024, 512
+    u = _xorshift_uniform(rows * cols + cols, state=0x2468ACE)
+    w = (u[: rows * cols] * 2.0).astype(np.float32)
+    x = u[rows * cols:].copy()
+    wq = oracle.quantize_row_q8(w)
+    out = np.zeros(rows, np.float32)
+    assert L.mia_matvec_register(wq.ctypes.data, 1, rows, cols) == 0
+    assert L.mia_matvec_register(w.ctypes.data, 0, rows, cols) == 0
+    for _ in range(2):
+        L.mia_matvec(out.ctypes.data, wq.ctypes.data, 1, x.ctypes.data, None, rows, cols)
+        assert_bits(out, oracle.matvec(wq, 1, x, rows, cols), "registered q8")
+        L.mia_matvec(out.ctypes.data, w.ctypes.data, 0, x.ctypes.data, None, rows, cols)
+        assert_bits(out, oracle.matvec(w, 0, x, rows, cols), "registered f32")
+    half = np.zeros(rows // 2, np.float32)
+    L.mia_matvec(half.ctypes.data, wq.ctypes.data, 1, x.ctypes.data, None, rows // 2, cols)
+    assert_bits(half, oracle.matvec(wq, 1, x, rows // 2, cols), "other shape, same pointer")
+    assert L.mia_matvec_unregister(wq.ctypes.data) == 0
+    assert L.mia_matvec_unregister(wq.ctypes.data) == -1
+    assert L.mia_matvec_unregister(w.ctypes.data) == 0
+    wq[4:36] = oracle.quantize_row_q8(np.ones(32, np.float32))[4:]  # new codes in row 0
+    L.mia_matvec(out.ctypes.data, wq.ctypes.data, 1, x.ctypes.data, None, rows, cols)
+    assert_bits(out, oracle.matvec(wq, 1, x, rows, cols), "after unregistering")
+    assert L.mia_matvec_register(wq.ctypes.data, 1, rows, 33) == -1  # cols % 32
+
+
 # ---- expert table ------------------------------------------------------------------
 
 def test_table_synth_matches_host_generator(oracle, qwen_dims, qwen_moe):
