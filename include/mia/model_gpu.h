@@ -1,0 +1,65 @@
+#ifndef MIA_MODEL_GPU_H
+#define MIA_MODEL_GPU_H
+/*
+ * The reference engine's model step, mia_model_step (include/mia/model.h:21-23
+ * and src/model/forward.c:199-217 of the reference), with every tensor in
+ * HBM on one GPU: the token's embedding, then per layer the attention block
+ * (forward.c:118-165, KV cache in HBM) and the MoE FFN (the HBM expert table
+ * of include/mia/moe.h), then the final rmsnorm and the output head. Only
+ * the logits cross PCIe. Q8_0 models.
+ *
+ * Conventions follow the reference engine: C99, 0/-1 (or NULL) returns with
+ * the reason in mia_gpu_model_error, rich error text at open time, one host
+ * thread per handle.
+ */
+#include <stddef.h>
+#include <stdint.h>
+
+#include "mia/moe.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mia_gpu_model mia_gpu_model;
+
+/* Opens a .mia file (mia_file_probe's checks), uploads its dense section,
+ * expert table, norms and routers to device `device`, and sizes the KV cache
+ * for max_seq positions. */
+int mia_gpu_model_open(mia_gpu_model **out, const char *path, int max_seq, int device,
+                       char *err, size_t errlen);
+/* No counterpart in the reference: a model of the given shape (the
+ * mia_file_info header fields; wtype Q8_0) with seeded synthetic weights
+ * generated in HBM (matrices ~ N(0, 0.02) quantized to Q8_0, norms 1, the
+ * MoE handle's mia_moe_synth), for benchmarks at shapes whose files would
+ * not fit a test's disk. */
+int mia_gpu_model_synth(mia_gpu_model **out, const mia_file_info *shape, int max_seq,
+                        int device, uint64_t seed, char *err, size_t errlen);
+void mia_gpu_model_close(mia_gpu_model *m);
+const char *mia_gpu_model_error(const mia_gpu_model *m);
+int mia_gpu_model_vocab(const mia_gpu_model *m);
+
+/* Feeds `token` at position `pos` (sequential from 0) and returns the
+ * vocabulary logits (owned by the handle, valid until the next call), or
+ * NULL when pos is outside [0, max_seq) or token outside [0, vocab), or on a
+ * device error. */
+const float *mia_gpu_model_step(mia_gpu_model *m, int token, int pos);
+
+/* Flags of the MoE layers (include/mia_hip.h), as mia_moe_set_flags:
+ * MHIP_FORCE_EXACT_ROUTER (the default): the one-layer launch of the decode
+ * kernel with the reference's sequential router chains; logits bit-equal to
+ * the reference's. 0: the same launch with the certified parallel router
+ * (expert indices bit-equal, gate weights within ~1e-6 relative; through the
+ * requantizations of later layers the logits then move by whole Q8 steps,
+ * ~5e-4 of max|logit| each, up to ~1e-2 in all). MHIP_EXACT_EXPERTS: the
+ * per-stage kernels (bit-equal, no decode launch). MHIP_DECODE_FORCE_ABORT:
+ * every decode launch aborts and the step reruns per stage (a test of that
+ * fallback). */
+void mia_gpu_model_set_flags(mia_gpu_model *m, int flags);
+/* Decode launches of the last step that aborted (rerun per stage). */
+int mia_gpu_model_aborts(const mia_gpu_model *m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

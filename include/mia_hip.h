@@ -243,6 +243,35 @@ int mhip_decode_status(mhip_ctx *c, const void *d_ws, int status[4]);
 #define MHIP_TRACE_SLOTS 32
 int mhip_decode_trace(mhip_ctx *c, const void *d_ws, unsigned long long *out);
 
+/* ---- attention and output head of one token (decode) ---------------------
+ * src/model/forward.c:118-165 and :214-215 of the reference, bit-equal to its
+ * x86 build. Dense weights are device copies of the .mia file's tensors:
+ * wq [n_heads*head_dim][dim], wk/wv [n_kv_heads*head_dim][dim],
+ * wo [dim][n_heads*head_dim], output [vocab][dim] in 36-byte Q8_0 blocks;
+ * attn_norm/output_norm [dim], q_norm/k_norm [head_dim] fp32. */
+typedef struct {
+    int dim, n_heads, n_kv_heads, head_dim; /* head_dim even, <= 256; dim, heads*head_dim <= 8192 */
+    float norm_eps;
+} mhip_attn_dims;
+
+size_t mhip_attention_scratch_bytes(const mhip_attn_dims *s, int max_seq);
+/* Attention of the token at `pos` for one layer, in place on d_x[dim]
+ * (x += Wo attention(rmsnorm(x))). d_kc/d_vc: this layer's K and V cache,
+ * [max_seq][n_kv_heads*head_dim] fp32; row pos is written, rows < pos read.
+ * d_rope: [max_seq][head_dim/2][2] doubles, cos and sin of
+ * pos * theta^(-2i/head_dim) as the host libm gives them (the reference's
+ * angles, forward.c:84-93). d_scratch: mhip_attention_scratch_bytes(). */
+int mhip_attention(mhip_ctx *c, const mhip_attn_dims *s, const float *d_attn_norm,
+                   const void *d_wq, const void *d_wk, const void *d_wv, const void *d_wo,
+                   const float *d_q_norm, const float *d_k_norm, const double *d_rope,
+                   float *d_kc, float *d_vc, int pos, int max_seq, float *d_x,
+                   void *d_scratch, int flags);
+/* logits[vocab] = output Q8(rmsnorm(x, output_norm)) (forward.c:214-215);
+ * d_scratch as for mhip_attention. */
+int mhip_output_head(mhip_ctx *c, const mhip_attn_dims *s, const float *d_output_norm,
+                     const void *d_output, int vocab, const float *d_x, float *d_logits,
+                     void *d_scratch, int flags);
+
 /* ---- reference tensor ops on device pointers ---------------------------- */
 /* Q8_0 blocks in the reference's 36-byte format. */
 int mhip_quantize_q8(mhip_ctx *c, const float *d_x, void *d_blocks, int n);

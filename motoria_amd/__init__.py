@@ -56,6 +56,11 @@ class Scratch(ctypes.Structure):
                                   "hdq", "gtile", "xsb", "hq", "hs", "glight")]
 
 
+class AttnDims(ctypes.Structure):
+    _fields_ = [("dim", _i), ("n_heads", _i), ("n_kv_heads", _i), ("head_dim", _i),
+                ("norm_eps", _f)]
+
+
 class FileInfo(ctypes.Structure):
     """mia_file_info (include/mia/moe.h): a .mia header and blob offsets."""
     _fields_ = [(n, ctypes.c_uint32) for n in (
@@ -128,6 +133,10 @@ SIGNATURES = {
                                        _p, _p, _p, _p, _i, _p, _p, _p, _i]),
     "mhip_decode_status": (_i, [_p, _p, ctypes.POINTER(_i)]),
     "mhip_decode_trace": (_i, [_p, _p, _p]),
+    "mhip_attention_scratch_bytes": (_sz, [ctypes.POINTER(AttnDims), _i]),
+    "mhip_attention": (_i, [_p, ctypes.POINTER(AttnDims), _p, _p, _p, _p, _p, _p, _p, _p, _p,
+                            _p, _i, _i, _p, _p, _i]),
+    "mhip_output_head": (_i, [_p, ctypes.POINTER(AttnDims), _p, _p, _i, _p, _p, _p, _i]),
     "mhip_quantize_q8": (_i, [_p, _p, _p, _i]),
     "mhip_dequantize_q8": (_i, [_p, _p, _p, _i]),
     "mhip_matvec": (_i, [_p, _p, _p, _i, _p, _p, _i, _i]),
@@ -170,6 +179,17 @@ SIGNATURES = {
     "mia_moe_scratch": (ctypes.POINTER(Scratch), [_p]),
     "mia_moe_set_flags": (None, [_p, _i]),
     "mia_moe_status": (_i, [_p, ctypes.POINTER(_i)]),
+    # include/mia/model_gpu.h
+    "mia_gpu_model_open": (_i, [ctypes.POINTER(_p), ctypes.c_char_p, _i, _i, ctypes.c_char_p,
+                                _sz]),
+    "mia_gpu_model_synth": (_i, [ctypes.POINTER(_p), ctypes.POINTER(FileInfo), _i, _i, _u64,
+                                 ctypes.c_char_p, _sz]),
+    "mia_gpu_model_close": (None, [_p]),
+    "mia_gpu_model_error": (ctypes.c_char_p, [_p]),
+    "mia_gpu_model_vocab": (_i, [_p]),
+    "mia_gpu_model_step": (ctypes.POINTER(_f), [_p, _i, _i]),
+    "mia_gpu_model_set_flags": (None, [_p, _i]),
+    "mia_gpu_model_aborts": (_i, [_p]),
 }
 
 # The storage port type (include/mia/expert_cache.h).
@@ -443,3 +463,54 @@ class Gpu:
         out = np.zeros(shape, dtype=dtype)
         self.check(lib().mhip_d2h(self.h, _ptr(out), p, out.nbytes), "d2h")
         return out
+
+
+class GpuModel:
+    """mia_gpu_model (include/mia/model_gpu.h): the whole model step of a
+    Q8_0 .mia file on one GPU."""
+
+    def __init__(self, path, max_seq, device=0, flags=MHIP_FORCE_EXACT_ROUTER, synth=None):
+        """Opens the .mia file at `path`, or (path None) generates the model
+        of shape `synth` = (dict of header fields, seed) in HBM."""
+        h = _p()
+        err = ctypes.create_string_buffer(512)
+        if path is None:
+            cfg, seed = synth
+            info = FileInfo(version=1, wtype=1, **{k: v for k, v in cfg.items()
+                                                   if k in dict(FileInfo._fields_)})
+            rc = lib().mia_gpu_model_synth(ctypes.byref(h), ctypes.byref(info), max_seq, device,
+                                           seed, err, 512)
+        else:
+            rc = lib().mia_gpu_model_open(ctypes.byref(h), path.encode(), max_seq, device, err,
+                                          512)
+        if rc != 0:
+            raise RuntimeError("mia_gpu_model_open: " + err.value.decode())
+        self.h = h
+        self.vocab = lib().mia_gpu_model_vocab(h)
+        self.set_flags(flags)
+
+    def close(self):
+        if self.h:
+            lib().mia_gpu_model_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_flags(self, flags):
+        lib().mia_gpu_model_set_flags(self.h, flags)
+
+    def aborts(self):
+        """Decode launches of the last step that aborted (rerun per stage)."""
+        return lib().mia_gpu_model_aborts(self.h)
+
+    def step(self, token, pos):
+        """Logits (a copy) of `token` at `pos`."""
+        r = lib().mia_gpu_model_step(self.h, token, pos)
+        if not r:
+            raise RuntimeError("mia_gpu_model_step: " +
+                               lib().mia_gpu_model_error(self.h).decode())
+        return np.ctypeslib.as_array(r, shape=(self.vocab,)).copy()

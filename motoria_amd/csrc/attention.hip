@@ -1,0 +1,291 @@
+// Attention of one token (decode) for the Qwen3-MoE model on one MI355X:
+// src/model/forward.c:118-165 of the reference, every value in the
+// reference's operation order (bit-equal to its x86 build):
+//
+//   rmsnorm(x, attn_norm) -> Q8(xn)                       forward.c:123
+//   q, k, v = Wq, Wk, Wv Q8(xn)   (k_rows_q8)             forward.c:124-126
+//   per head: rmsnorm(q_h / k_h) and NeoX RoPE, then the
+//   K and V rows appended to the cache (k_qk_rope)        forward.c:127-139
+//   scores, softmax and the weighted sum of V per head
+//   (k_attn_scores, k_attn_mix)                           forward.c:141-163
+//   x += Wo Q8(att)   (k_quant_rows, k_rows_q8)           forward.c:164-165
+//
+// and the output head (forward.c:214-215) with the same row kernel. Weights
+// stay in the .mia file's 36-byte Q8_0 blocks. RoPE's angles come from a
+// table the host fills with its libm (the reference computes them in
+// double with pow/cos/sin per call), so the rotations are the reference's.
+#include "mhip_internal.h"
+
+namespace {
+
+constexpr int QK = mhip::QK;
+constexpr int MAXNB = 256;  // blocks per row the row kernel holds (dims up to 8192)
+
+// out[r] = (resid ? resid[r] : 0) + the reference's Q8 dot of weight row r
+// (36-byte blocks) with the activation's codes xq[nb*32] and scales xs[nb]
+// (src/tensor/matmul.c:19-28): one wavefront per row, lane b computes the
+// block terms of blocks b, b + 64, ..., then lane 0 adds them in block order.
+__global__ __launch_bounds__(256) void k_rows_q8(const uint8_t *__restrict__ w, int rows, int nb,
+                                                 const int8_t *__restrict__ xq,
+                                                 const float *__restrict__ xs,
+                                                 const float *resid, float *out) {
+    __shared__ float terms[4][MAXNB];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + wave;
+    if (r >= rows) return;
+    const uint8_t *wr = w + (size_t)r * nb * 36;
+    for (int b = lane; b < nb; b += 64) {
+        const uint32_t *blk = (const uint32_t *)(wr + (size_t)b * 36);
+        const float dw = __uint_as_float(blk[0]);
+        const int4 w0 = make_int4((int)blk[1], (int)blk[2], (int)blk[3], (int)blk[4]);
+        const int4 w1 = make_int4((int)blk[5], (int)blk[6], (int)blk[7], (int)blk[8]);
+        const int4 *xv = (const int4 *)(xq + (size_t)b * QK);
+        terms[wave][b] = mhip_dev::block_term(mhip_dev::dot32_i8(w0, w1, xv[0], xv[1]), dw, xs[b]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane == 0) {
+        float s = 0.0f;
+        for (int b = 0; b < nb; b++) s = s + terms[wave][b];
+        out[r] = resid ? resid[r] + s : s;
+    }
+}
+
+// Q8_0 of a row of n values into codes and scales (src/tensor/quant.c:11-27),
+// one thread per 32-block.
+__global__ __launch_bounds__(256) void k_quant_rows(const float *__restrict__ x, int nb,
+                                                    int8_t *__restrict__ q,
+                                                    float *__restrict__ s) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nb) return;
+    const float *v = x + (size_t)b * QK;
+    float amax = 0.0f;
+    for (int i = 0; i < QK; i++) {
+        const float a = fabsf(v[i]);
+        amax = a > amax ? a : amax;
+    }
+    const float d = amax / 127.0f;
+    const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+    for (int i = 0; i < QK; i++) q[(size_t)b * QK + i] = (int8_t)roundf(v[i] * inv);
+    s[b] = d;
+}
+
+// forward.c:127-139 and the cache append. Wavefront h < nh: query head h;
+// nh <= h < nh + nkv: key head h - nh; then value heads, copied. A head's
+// rmsnorm sums squares in double in index order (forward.c:75-81, one lane),
+// then NeoX RoPE rotates element i with i + hd/2 by the angle of
+// rope[pos][i] (cos, sin in double), each result rounded to float once.
+__global__ __launch_bounds__(256) void k_qk_rope(float *__restrict__ q, const float *__restrict__ k,
+                                                 const float *__restrict__ v,
+                                                 const float *__restrict__ q_norm,
+                                                 const float *__restrict__ k_norm,
+                                                 const double *__restrict__ rope, int pos, int nh,
+                                                 int nkv, int hd, float eps,
+                                                 float *__restrict__ kc_row,
+                                                 float *__restrict__ vc_row) {
+    __shared__ float hv[4][256];
+    __shared__ float inv_sh[4];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int h = blockIdx.x * 4 + wave;
+    if (h >= nh + 2 * nkv) return;
+    if (h >= nh + nkv) {  // value head: the cache row as computed
+        const int j = h - nh - nkv;
+        for (int i = lane; i < hd; i += 64) vc_row[j * hd + i] = v[j * hd + i];
+        return;
+    }
+    const bool isq = h < nh;
+    const float *src = isq ? q + (size_t)h * hd : k + (size_t)(h - nh) * hd;
+    const float *w = isq ? q_norm : k_norm;
+    float *row = hv[wave];
+    for (int i = lane; i < hd; i += 64) row[i] = src[i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane == 0) {
+        double ss = 0.0;
+        for (int i = 0; i < hd; i++) ss = ss + (double)row[i] * (double)row[i];
+        inv_sh[wave] = (float)(1.0 / sqrt(ss / hd + (double)eps));
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float inv = inv_sh[wave];
+    const int half = hd / 2;
+    const double *rp = rope + (size_t)pos * half * 2;
+    float *dst = isq ? q + (size_t)h * hd : kc_row + (size_t)(h - nh) * hd;
+    for (int i = lane; i < half; i += 64) {
+        const float x0 = (row[i] * inv) * w[i];
+        const float x1 = (row[i + half] * inv) * w[i + half];
+        const double c = rp[2 * i], s = rp[2 * i + 1];
+        dst[i] = (float)((double)x0 * c - (double)x1 * s);
+        dst[i + half] = (float)((double)x0 * s + (double)x1 * c);
+    }
+}
+
+// forward.c:143-149: score[h][t] = (sequential fp32 dot of q_h and the
+// cached k_t of its key head) * scale, one thread per (head, position).
+__global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q,
+                                                     const float *__restrict__ kc, int n, int nh,
+                                                     int group, int hd, int kvd, float scale,
+                                                     float *__restrict__ scores, int ld) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= nh * n) return;
+    const int h = idx / n, t = idx % n;
+    const float *qh = q + (size_t)h * hd;
+    const float *kt = kc + (size_t)t * kvd + (size_t)(h / group) * hd;
+    float dot = 0.0f;
+    for (int i = 0; i < hd; i++) dot = dot + qh[i] * kt[i];
+    scores[(size_t)h * ld + t] = dot * scale;
+}
+
+// forward.c:150-162 for head blockIdx.x: softmax of the n scores (first
+// maximum, the restated glibc expf, sequential sum, division), then
+// att[h][i] = sum over t of p_t * v_t[i] in position order, one thread per i.
+__global__ __launch_bounds__(256) void k_attn_mix(float *__restrict__ scores, int ld, int n,
+                                                  const float *__restrict__ vc, int group, int hd,
+                                                  int kvd, float *__restrict__ att) {
+    __shared__ float red[256];
+    __shared__ float sum_sh;
+    __shared__ uint64_t etab[32];
+    const int h = blockIdx.x, tid = threadIdx.x;
+    float *s = scores + (size_t)h * ld;
+    if (tid < 32) etab[tid] = mia_expf_tab[tid];
+    float mx = -__builtin_inff();
+    for (int t = tid; t < n; t += 256) mx = fmaxf(mx, s[t]);
+    red[tid] = mx;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) red[tid] = fmaxf(red[tid], red[tid + o]);
+        __syncthreads();
+    }
+    // the reference's running maximum picks the first maximum; every
+    // maximum has the same value, and NaN scores stay NaN either way
+    mx = red[0];
+    for (int t = tid; t < n; t += 256) s[t] = mia_expf_glibc_tab(s[t] - mx, etab);
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+        for (int t = 0; t < n; t++) sum = sum + s[t];
+        sum_sh = sum;
+    }
+    __syncthreads();
+    const float sum = sum_sh;
+    for (int t = tid; t < n; t += 256) s[t] = s[t] / sum;
+    __syncthreads();
+    if (tid < hd) {
+        const float *vt = vc + (size_t)(h / group) * hd + tid;
+        float o = 0.0f;
+        for (int t = 0; t < n; t++) o = o + s[t] * vt[(size_t)t * kvd];
+        att[(size_t)h * hd + tid] = o;
+    }
+}
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+struct AttnScratch {
+    float *xn, *xs, *q, *k, *v, *att, *atts, *scores;
+    int8_t *xq, *attq;
+    int *status;
+};
+
+AttnScratch carve(const mhip_attn_dims *s, int max_seq, void *base) {
+    const size_t d = s->dim, qd = (size_t)s->n_heads * s->head_dim,
+                 kvd = (size_t)s->n_kv_heads * s->head_dim;
+    uint8_t *p = (uint8_t *)base;
+    auto take = [&](size_t bytes) {
+        void *r = p;
+        p += align256(bytes);
+        return r;
+    };
+    AttnScratch a;
+    a.xn = (float *)take(d * 4);
+    a.xq = (int8_t *)take(d);
+    a.xs = (float *)take(d / QK * 4);
+    a.q = (float *)take(qd * 4);
+    a.k = (float *)take(kvd * 4);
+    a.v = (float *)take(kvd * 4);
+    a.att = (float *)take(qd * 4);
+    a.attq = (int8_t *)take(qd);
+    a.atts = (float *)take(qd / QK * 4);
+    a.scores = (float *)take((size_t)s->n_heads * max_seq * 4);
+    a.status = (int *)take(16);
+    return a;
+}
+
+int check_attn(mhip_ctx *c, const mhip_attn_dims *s, int max_seq) {
+    if (!s) return mhip::fail(c, "null attention dims");
+    const int qd = s->n_heads * s->head_dim;
+    if (s->dim <= 0 || s->dim % QK || s->dim / QK > MAXNB || s->n_heads <= 0 ||
+        s->n_kv_heads <= 0 || s->n_heads % s->n_kv_heads || s->head_dim <= 0 ||
+        s->head_dim % 2 || s->head_dim > 256 || qd % QK || qd / QK > MAXNB)
+        return mhip::fail(c, "attention shape dim=%d heads=%d/%d head_dim=%d not supported",
+                          s->dim, s->n_heads, s->n_kv_heads, s->head_dim);
+    if (max_seq <= 0) return mhip::fail(c, "max_seq=%d", max_seq);
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mhip_attention_scratch_bytes(const mhip_attn_dims *s, int max_seq) {
+    const size_t d = s->dim, qd = (size_t)s->n_heads * s->head_dim,
+                 kvd = (size_t)s->n_kv_heads * s->head_dim;
+    return align256(d * 4) + align256(d) + align256(d / QK * 4) + align256(qd * 4) +
+           2 * align256(kvd * 4) + align256(qd * 4) + align256(qd) + align256(qd / QK * 4) +
+           align256((size_t)s->n_heads * max_seq * 4) + align256(16);
+}
+
+int mhip_attention(mhip_ctx *c, const mhip_attn_dims *s, const float *d_attn_norm,
+                   const void *d_wq, const void *d_wk, const void *d_wv, const void *d_wo,
+                   const float *d_q_norm, const float *d_k_norm, const double *d_rope,
+                   float *d_kc, float *d_vc, int pos, int max_seq, float *d_x,
+                   void *d_scratch, int flags) {
+    if (check_attn(c, s, max_seq)) return -1;
+    if (pos < 0 || pos >= max_seq)
+        return mhip::fail(c, "attention: pos=%d outside [0, max_seq=%d)", pos, max_seq);
+    if (mhip::use_device(c)) return -1;
+    const int d = s->dim, nh = s->n_heads, nkv = s->n_kv_heads, hd = s->head_dim;
+    const int qd = nh * hd, kvd = nkv * hd, n = pos + 1;
+    AttnScratch a = carve(s, max_seq, d_scratch);
+    hipStream_t st = c->stream;
+    mhip::launch_rmsnorm_q8(st, d_x, d_attn_norm, a.xn, a.xq, a.xs, 1, d, s->norm_eps,
+                            (flags & MHIP_FORCE_SEQ_RMS) ? 1 : 0, a.status);
+    const int nb = d / QK;
+    k_rows_q8<<<mhip::blocks_for(qd, 4), 256, 0, st>>>((const uint8_t *)d_wq, qd, nb, a.xq, a.xs,
+                                                        nullptr, a.q);
+    k_rows_q8<<<mhip::blocks_for(kvd, 4), 256, 0, st>>>((const uint8_t *)d_wk, kvd, nb, a.xq,
+                                                         a.xs, nullptr, a.k);
+    k_rows_q8<<<mhip::blocks_for(kvd, 4), 256, 0, st>>>((const uint8_t *)d_wv, kvd, nb, a.xq,
+                                                         a.xs, nullptr, a.v);
+    if (mhip::check_launch(c, "attention qkv")) return -1;
+    k_qk_rope<<<mhip::blocks_for(nh + 2 * nkv, 4), 256, 0, st>>>(
+        a.q, a.k, a.v, d_q_norm, d_k_norm, d_rope, pos, nh, nkv, hd, s->norm_eps,
+        d_kc + (size_t)pos * kvd, d_vc + (size_t)pos * kvd);
+    const float scale = 1.0f / sqrtf((float)hd);
+    k_attn_scores<<<mhip::blocks_for((size_t)nh * n, 256), 256, 0, st>>>(
+        a.q, d_kc, n, nh, nh / nkv, hd, kvd, scale, a.scores, max_seq);
+    k_attn_mix<<<nh, 256, 0, st>>>(a.scores, max_seq, n, d_vc, nh / nkv, hd, kvd, a.att);
+    k_quant_rows<<<mhip::blocks_for(qd / QK, 256), 256, 0, st>>>(a.att, qd / QK, a.attq, a.atts);
+    k_rows_q8<<<mhip::blocks_for(d, 4), 256, 0, st>>>((const uint8_t *)d_wo, d, qd / QK, a.attq,
+                                                       a.atts, d_x, d_x);
+    return mhip::check_launch(c, "attention");
+}
+
+int mhip_output_head(mhip_ctx *c, const mhip_attn_dims *s, const float *d_output_norm,
+                     const void *d_output, int vocab, const float *d_x, float *d_logits,
+                     void *d_scratch, int flags) {
+    if (check_attn(c, s, 1)) return -1;
+    if (vocab <= 0) return mhip::fail(c, "output head: vocab=%d", vocab);
+    if (mhip::use_device(c)) return -1;
+    AttnScratch a = carve(s, 1, d_scratch);
+    const int d = s->dim;
+    mhip::launch_rmsnorm_q8(c->stream, d_x, d_output_norm, a.xn, a.xq, a.xs, 1, d, s->norm_eps,
+                            (flags & MHIP_FORCE_SEQ_RMS) ? 1 : 0, a.status);
+    k_rows_q8<<<mhip::blocks_for(vocab, 4), 256, 0, c->stream>>>(
+        (const uint8_t *)d_output, vocab, d / QK, a.xq, a.xs, nullptr, d_logits);
+    return mhip::check_launch(c, "output head");
+}
+
+}  // extern "C"

@@ -51,6 +51,11 @@ inline unsigned blocks_for(size_t n, unsigned per) {
 // address of the allocation-free decode workspace (decode.hip).
 int decode_noalloc_setup(mhip_ctx *c);
 
+// rmsnorm + Q8_0 of T rows of d values (the certified sum of moe_layer.hip;
+// status[1] counts rows that took the sequential sum). Queues one launch.
+void launch_rmsnorm_q8(hipStream_t st, const float *x, const float *w, float *xn, int8_t *xq,
+                       float *xs, int T, int d, float eps, int force_seq, int *status);
+
 // Matrix-core expert products (moe_gemm.hip).
 bool gemm_path_fits(const mhip_dims *s);
 int gemm_max_tiles(int A, int E);

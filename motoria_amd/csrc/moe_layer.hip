@@ -1064,6 +1064,19 @@ int rows_down(int nbh) {
 
 }  // namespace
 
+namespace mhip {
+
+void launch_rmsnorm_q8(hipStream_t st, const float *x, const float *w, float *xn, int8_t *xq,
+                       float *xs, int T, int d, float eps, int force_seq, int *status) {
+    if (d == RN_D)
+        k_rmsnorm_q8_w<<<(T + 3) / 4, 256, 0, st>>>(x, w, xn, xq, xs, nullptr, T, eps, force_seq,
+                                                    status);
+    else
+        k_rmsnorm_q8<<<T, NT, 0, st>>>(x, w, xn, xq, xs, nullptr, d, eps, force_seq, status);
+}
+
+}  // namespace mhip
+
 extern "C" {
 
 size_t mhip_scratch_bytes(const mhip_dims *s, int T) {

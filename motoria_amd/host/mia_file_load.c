@@ -74,31 +74,32 @@ static uint64_t tensor_bytes(uint32_t wtype, uint64_t rows, uint64_t cols, int q
     return rows * cols * 4;
 }
 
-/* The dense walk: offset (from dense_offset) of layer l's ffn_norm and
- * router, and the end of the section. One cursor, each tensor aligned to 64
- * bytes, in NewLayout's order. */
-static uint64_t dense_walk(const mia_file_info *h, int want_layer, uint64_t *ffn_norm,
-                           uint64_t *router) {
+uint64_t mia_dense_walk(const mia_file_info *h, int want_layer, mia_layer_offsets *lo,
+                        uint64_t *token_embd, uint64_t *output_norm, uint64_t *output) {
     const uint64_t d = h->dim, hd = h->head_dim, V = h->vocab;
     const uint64_t qd = (uint64_t)h->n_heads * hd, kvd = (uint64_t)h->n_kv_heads * hd;
     uint64_t off = 0;
-#define TAKE(rows, cols, q) (off = align_up64(off + tensor_bytes(h->wtype, rows, cols, q), TENSOR_ALIGN))
-    TAKE(V, d, 1); /* token_embd */
+    /* records the cursor in *dst, then steps over one tensor (64-byte aligned) */
+#define TAKE(dst, rows, cols, q)                                                              \
+    do {                                                                                      \
+        if (dst) *(dst) = off;                                                                \
+        off = align_up64(off + tensor_bytes(h->wtype, rows, cols, q), TENSOR_ALIGN);          \
+    } while (0)
+    TAKE(token_embd, V, d, 1);
     for (uint32_t l = 0; l < h->n_layers; l++) {
-        TAKE(1, d, 0);     /* attn_norm */
-        TAKE(qd, d, 1);    /* wq */
-        TAKE(kvd, d, 1);   /* wk */
-        TAKE(kvd, d, 1);   /* wv */
-        TAKE(d, qd, 1);    /* wo */
-        TAKE(1, hd, 0);    /* q_norm */
-        TAKE(1, hd, 0);    /* k_norm */
-        if ((int)l == want_layer) *ffn_norm = off;
-        TAKE(1, d, 0);     /* ffn_norm */
-        if ((int)l == want_layer) *router = off;
-        TAKE(h->n_experts, d, 0); /* router */
+        mia_layer_offsets *L = lo && (int)l == want_layer ? lo : NULL;
+        TAKE(L ? &L->attn_norm : NULL, 1, d, 0);
+        TAKE(L ? &L->wq : NULL, qd, d, 1);
+        TAKE(L ? &L->wk : NULL, kvd, d, 1);
+        TAKE(L ? &L->wv : NULL, kvd, d, 1);
+        TAKE(L ? &L->wo : NULL, d, qd, 1);
+        TAKE(L ? &L->q_norm : NULL, 1, hd, 0);
+        TAKE(L ? &L->k_norm : NULL, 1, hd, 0);
+        TAKE(L ? &L->ffn_norm : NULL, 1, d, 0);
+        TAKE(L ? &L->router : NULL, h->n_experts, d, 0);
     }
-    TAKE(1, d, 0); /* output_norm */
-    TAKE(V, d, 1); /* output */
+    TAKE(output_norm, 1, d, 0);
+    TAKE(output, V, d, 1);
 #undef TAKE
     return off;
 }
@@ -144,8 +145,7 @@ int mia_file_probe(const char *path, mia_file_info *h, char *err, size_t errlen)
     if (h->dim == 0 || h->n_layers == 0 || h->n_experts == 0 || h->n_active == 0 ||
         h->expert_hidden == 0)
         return perr(err, errlen, "%s: empty MoE shape", path);
-    uint64_t fn = 0, rt = 0;
-    const uint64_t end = dense_walk(h, -1, &fn, &rt);
+    const uint64_t end = mia_dense_walk(h, -1, NULL, NULL, NULL, NULL);
     if (end != h->dense_size)
         return perr(err, errlen, "%s: dense layout mismatch (%llu vs %llu)", path,
                     (unsigned long long)end, (unsigned long long)h->dense_size);
@@ -169,9 +169,10 @@ int mia_file_probe(const char *path, mia_file_info *h, char *err, size_t errlen)
 int mia_file_layer_offsets(const mia_file_info *h, int layer, uint64_t *ffn_norm,
                            uint64_t *router) {
     if (layer < 0 || (uint32_t)layer >= h->n_layers) return -1;
-    dense_walk(h, layer, ffn_norm, router);
-    *ffn_norm += h->dense_offset;
-    *router += h->dense_offset;
+    mia_layer_offsets lo;
+    mia_dense_walk(h, layer, &lo, NULL, NULL, NULL);
+    *ffn_norm = h->dense_offset + lo.ffn_norm;
+    *router = h->dense_offset + lo.router;
     return 0;
 }
 

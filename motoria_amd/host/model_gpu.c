@@ -1,0 +1,356 @@
+/*
+ * mia_model_step on one GPU (include/mia/model_gpu.h): the token's
+ * embedding, n_layers x (attention, MoE), final rmsnorm and output head, all
+ * on device memory (src/model/forward.c:199-217 of the reference).
+ *
+ * The .mia file's dense section is uploaded as it is laid out (36-byte
+ * Q8_0 blocks, fp32 vectors), so each tensor's device address is the
+ * dense walk's offset. The MoE layers run the one-layer launch of the
+ * persistent decode kernel where the shape allows it (the exact router in
+ * exact mode), else the per-stage kernels, which are bit-exact. Each decode
+ * launch reports its status into a per-layer slot; should one abort, the
+ * step restores x from the copy taken before that layer's MoE and reruns
+ * from there per stage (the KV rows of the later layers are rewritten).
+ */
+#define _FILE_OFFSET_BITS 64
+#define _POSIX_C_SOURCE 200809L
+#include "mia/model_gpu.h"
+
+#include <errno.h>
+#include <fcntl.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+#include "moe_internal.h"
+
+struct mia_gpu_model {
+    mia_file_info info;
+    mia_moe *moe;
+    mhip_ctx *gpu;
+    mia_moe_tensors mt;
+    mhip_attn_dims ad;
+    int max_seq, flags, decode_ok, aborts;
+    unsigned char *d_dense;
+    mia_layer_offsets *lo;   /* [L] */
+    uint64_t off_embd, off_onorm, off_out;
+    float *d_kc, *d_vc;      /* [L][max_seq][kvd] */
+    double *d_rope;          /* [max_seq][head_dim/2][2] */
+    void *d_scratch;
+    float *d_x;              /* [dim] residual */
+    float *d_xsave;          /* [L][dim] x before each layer's MoE */
+    int *d_status;           /* [L][4] decode status per layer */
+    float *d_logits;         /* [vocab] */
+    float *h_logits;         /* pinned [vocab] */
+    int *h_status;           /* pinned [L][4] */
+    char err[512];
+};
+
+static int mfail(mia_gpu_model *m, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(m->err, sizeof(m->err), fmt, ap);
+    va_end(ap);
+    return -1;
+}
+
+const char *mia_gpu_model_error(const mia_gpu_model *m) { return m ? m->err : "null handle"; }
+int mia_gpu_model_vocab(const mia_gpu_model *m) { return (int)m->info.vocab; }
+void mia_gpu_model_set_flags(mia_gpu_model *m, int flags) { m->flags = flags; }
+int mia_gpu_model_aborts(const mia_gpu_model *m) { return m->aborts; }
+
+void mia_gpu_model_close(mia_gpu_model *m) {
+    if (!m) return;
+    if (m->gpu) {
+        mhip_sync(m->gpu);
+        mhip_free(m->gpu, m->d_dense);
+        mhip_free(m->gpu, m->d_kc);
+        mhip_free(m->gpu, m->d_vc);
+        mhip_free(m->gpu, m->d_rope);
+        mhip_free(m->gpu, m->d_scratch);
+        mhip_free(m->gpu, m->d_x);
+        mhip_free(m->gpu, m->d_xsave);
+        mhip_free(m->gpu, m->d_status);
+        mhip_free(m->gpu, m->d_logits);
+        mhip_host_free(m->gpu, m->h_logits);
+        mhip_host_free(m->gpu, m->h_status);
+    }
+    mia_moe_close(m->moe);
+    free(m->lo);
+    free(m);
+}
+
+/* The dense section, read through pinned staging in 64 MiB pieces. */
+static int upload_dense(mia_gpu_model *m, const char *path) {
+    const int fd = open(path, O_RDONLY);
+    if (fd < 0) return mfail(m, "open %s: %s", path, strerror(errno));
+    const size_t chunk = (size_t)64 << 20;
+    unsigned char *h = mhip_host_malloc(m->gpu, chunk);
+    int rc = h ? 0 : mfail(m, "pinned staging: %s", mhip_error(m->gpu));
+    for (uint64_t done = 0; !rc && done < m->info.dense_size;) {
+        const size_t n = m->info.dense_size - done < chunk ? (size_t)(m->info.dense_size - done)
+                                                           : chunk;
+        size_t got = 0;
+        while (got < n) {
+            const ssize_t r = pread(fd, h + got, n - got, (off_t)(m->info.dense_offset + done + got));
+            if (r < 0 && errno == EINTR) continue;
+            if (r <= 0) break;
+            got += (size_t)r;
+        }
+        if (got != n)
+            rc = mfail(m, "%s: reading the dense section", path);
+        else if (mhip_h2d(m->gpu, m->d_dense + done, h, n))
+            rc = mfail(m, "%s", mhip_error(m->gpu));
+        done += n;
+    }
+    if (h) mhip_host_free(m->gpu, h);
+    close(fd);
+    return rc;
+}
+
+/* Opens the MoE handle and allocates and fills everything but the weights
+ * for the shape in m->info. */
+static int setup(mia_gpu_model *m, int max_seq, int device) {
+    const mia_file_info *h = &m->info;
+    char e2[256];
+    if (h->wtype != MIA_Q8_0)
+        return mfail(m, "weight type %u; the GPU model runs Q8_0 models", h->wtype);
+    if (max_seq < 1) return mfail(m, "max_seq=%d", max_seq);
+    mia_moe_config c = {(int)h->dim, (int)h->n_layers, (int)h->n_experts, (int)h->n_active,
+                        (int)h->expert_hidden, (int)h->norm_topk, h->norm_eps, 1, device};
+    if (mia_moe_open(&m->moe, &c, e2, sizeof e2)) return mfail(m, "%s", e2);
+    m->gpu = mia_moe_gpu(m->moe);
+    m->max_seq = max_seq;
+    m->flags = MHIP_FORCE_EXACT_ROUTER;
+    mia_moe_get_tensors(m->moe, &m->mt);
+    m->ad = (mhip_attn_dims){(int)h->dim, (int)h->n_heads, (int)h->n_kv_heads, (int)h->head_dim,
+                             h->norm_eps};
+    const int ok = mhip_decode_supported(m->gpu, &m->mt.dims);
+    if (ok < 0) return mfail(m, "%s", mhip_error(m->gpu));
+    m->decode_ok = ok > 0;
+    const size_t L = h->n_layers, kvd = (size_t)h->n_kv_heads * h->head_dim;
+    const size_t half = h->head_dim / 2, ws = mhip_attention_scratch_bytes(&m->ad, max_seq);
+    m->lo = calloc(L, sizeof(*m->lo));
+    for (size_t l = 0; m->lo && l < L; l++)
+        mia_dense_walk(h, (int)l, &m->lo[l], &m->off_embd, &m->off_onorm, &m->off_out);
+    m->d_dense = mhip_malloc(m->gpu, (size_t)h->dense_size);
+    m->d_kc = mhip_malloc(m->gpu, L * max_seq * kvd * 4);
+    m->d_vc = mhip_malloc(m->gpu, L * max_seq * kvd * 4);
+    m->d_rope = mhip_malloc(m->gpu, (size_t)max_seq * half * 2 * 8);
+    m->d_scratch = mhip_malloc(m->gpu, ws);
+    m->d_x = mhip_malloc(m->gpu, (size_t)h->dim * 4);
+    m->d_xsave = mhip_malloc(m->gpu, L * h->dim * 4);
+    m->d_status = mhip_malloc(m->gpu, L * 16);
+    m->d_logits = mhip_malloc(m->gpu, (size_t)h->vocab * 4);
+    m->h_logits = mhip_host_malloc(m->gpu, (size_t)h->vocab * 4);
+    m->h_status = mhip_host_malloc(m->gpu, L * 16);
+    if (!m->lo || !m->d_dense || !m->d_kc || !m->d_vc || !m->d_rope || !m->d_scratch ||
+        !m->d_x || !m->d_xsave || !m->d_status || !m->d_logits || !m->h_logits || !m->h_status)
+        return mfail(m, "device memory: %s", mhip_error(m->gpu));
+    /* RoPE angles as the reference computes them (forward.c:86-89) */
+    double *t = malloc((size_t)max_seq * half * 2 * 8);
+    if (!t) return mfail(m, "out of host memory");
+    for (size_t p = 0; p < (size_t)max_seq; p++)
+        for (size_t i = 0; i < half; i++) {
+            const double freq = pow((double)h->rope_theta, -2.0 * (double)i / h->head_dim);
+            const double a = (double)p * freq;
+            t[(p * half + i) * 2] = cos(a);
+            t[(p * half + i) * 2 + 1] = sin(a);
+        }
+    const int rc = mhip_h2d(m->gpu, m->d_rope, t, (size_t)max_seq * half * 2 * 8) ||
+                   mhip_zero(m->gpu, m->d_kc, L * max_seq * kvd * 4) ||
+                   mhip_zero(m->gpu, m->d_vc, L * max_seq * kvd * 4) ||
+                   mhip_zero(m->gpu, m->d_scratch, ws) || mhip_sync(m->gpu);
+    free(t);
+    return rc ? mfail(m, "%s", mhip_error(m->gpu)) : 0;
+}
+
+static int finish(mia_gpu_model *m, int rc, mia_gpu_model **out, char *err, size_t errlen) {
+    if (rc) {
+        if (err && errlen) snprintf(err, errlen, "%s", m->err);
+        mia_gpu_model_close(m);
+        return -1;
+    }
+    *out = m;
+    return 0;
+}
+
+int mia_gpu_model_open(mia_gpu_model **out, const char *path, int max_seq, int device,
+                       char *err, size_t errlen) {
+    *out = NULL;
+    mia_gpu_model *m = calloc(1, sizeof(*m));
+    if (!m) {
+        if (err && errlen) snprintf(err, errlen, "out of host memory");
+        return -1;
+    }
+    char e2[256];
+    int rc = mia_file_probe(path, &m->info, e2, sizeof e2) ? mfail(m, "%s", e2) : 0;
+    if (!rc) rc = setup(m, max_seq, device);
+    if (!rc && mia_moe_load_file(m->moe, path)) rc = mfail(m, "%s", mia_moe_error(m->moe));
+    if (!rc) rc = upload_dense(m, path);
+    return finish(m, rc, out, err, errlen);
+}
+
+/* Q8_0 matrix [rows][cols] at d_dense + off from N(0, 0.02) values. */
+static int synth_q8(mia_gpu_model *m, float *tmp, uint64_t off, size_t rows, size_t cols,
+                    uint64_t seed, uint64_t stream) {
+    const size_t n = rows * cols;
+    if (mhip_synth_f32(m->gpu, tmp, n, seed, stream, 0.02) ||
+        mhip_quantize_q8(m->gpu, tmp, m->d_dense + off, (int)n))
+        return mfail(m, "%s", mhip_error(m->gpu));
+    return 0;
+}
+
+int mia_gpu_model_synth(mia_gpu_model **out, const mia_file_info *shape, int max_seq,
+                        int device, uint64_t seed, char *err, size_t errlen) {
+    *out = NULL;
+    mia_gpu_model *m = calloc(1, sizeof(*m));
+    if (!m) {
+        if (err && errlen) snprintf(err, errlen, "out of host memory");
+        return -1;
+    }
+    mia_file_info *h = &m->info;
+    *h = *shape;
+    h->dense_offset = 0;
+    h->dense_size = mia_dense_walk(h, -1, NULL, NULL, NULL, NULL);
+    int rc = 0;
+    if (!h->dim || h->dim % MIA_QK || !h->n_layers || !h->n_heads || !h->n_kv_heads ||
+        h->n_heads % h->n_kv_heads || !h->head_dim || h->head_dim % 2 || !h->vocab ||
+        !h->n_experts || !h->n_active || h->n_active > h->n_experts || !h->expert_hidden ||
+        h->expert_hidden % MIA_QK || ((uint64_t)h->n_heads * h->head_dim) % MIA_QK)
+        rc = mfail(m, "unsupported model shape");
+    if (!rc) rc = setup(m, max_seq, device);
+    if (!rc && mia_moe_synth(m->moe, seed)) rc = mfail(m, "%s", mia_moe_error(m->moe));
+    const uint64_t d = h->dim, qd = (uint64_t)h->n_heads * h->head_dim,
+                   kvd = (uint64_t)h->n_kv_heads * h->head_dim;
+    const uint64_t big = (uint64_t)h->vocab * d > qd * d ? (uint64_t)h->vocab * d : qd * d;
+    float *tmp = rc ? NULL : mhip_malloc(m->gpu, big * 4);
+    if (!rc && !tmp) rc = mfail(m, "device memory: %s", mhip_error(m->gpu));
+    if (!rc) rc = synth_q8(m, tmp, m->off_embd, h->vocab, d, seed, 1);
+    for (uint32_t l = 0; !rc && l < h->n_layers; l++) {
+        const mia_layer_offsets *o = &m->lo[l];
+        const uint64_t st = 16 + 8 * (uint64_t)l;
+        rc = synth_q8(m, tmp, o->wq, qd, d, seed, st) ||
+             synth_q8(m, tmp, o->wk, kvd, d, seed, st + 1) ||
+             synth_q8(m, tmp, o->wv, kvd, d, seed, st + 2) ||
+             synth_q8(m, tmp, o->wo, d, qd, seed, st + 3);
+        if (!rc &&
+            (mhip_fill_f32(m->gpu, (float *)(m->d_dense + o->attn_norm), d, 1.0f) ||
+             mhip_fill_f32(m->gpu, (float *)(m->d_dense + o->q_norm), h->head_dim, 1.0f) ||
+             mhip_fill_f32(m->gpu, (float *)(m->d_dense + o->k_norm), h->head_dim, 1.0f) ||
+             mhip_fill_f32(m->gpu, (float *)(m->d_dense + o->ffn_norm), d, 1.0f) ||
+             mhip_synth_f32(m->gpu, (float *)(m->d_dense + o->router), (size_t)h->n_experts * d,
+                            seed, st + 4, 0.02)))
+            rc = mfail(m, "%s", mhip_error(m->gpu));
+    }
+    if (!rc) rc = synth_q8(m, tmp, m->off_out, h->vocab, d, seed, 2);
+    if (!rc && (mhip_fill_f32(m->gpu, (float *)(m->d_dense + m->off_onorm), d, 1.0f) ||
+                mhip_sync(m->gpu)))
+        rc = mfail(m, "%s", mhip_error(m->gpu));
+    if (tmp) mhip_free(m->gpu, tmp);
+    return finish(m, rc, out, err, errlen);
+}
+
+/* Queues the attention of layer l at pos. */
+static int attention(mia_gpu_model *m, int l, int pos) {
+    const size_t kvd = (size_t)m->info.n_kv_heads * m->info.head_dim;
+    const mia_layer_offsets *o = &m->lo[l];
+    const unsigned char *b = m->d_dense;
+    float *kc = m->d_kc + (size_t)l * m->max_seq * kvd, *vc = m->d_vc + (size_t)l * m->max_seq * kvd;
+    if (mhip_attention(m->gpu, &m->ad, (const float *)(b + o->attn_norm), b + o->wq, b + o->wk,
+                       b + o->wv, b + o->wo, (const float *)(b + o->q_norm),
+                       (const float *)(b + o->k_norm), m->d_rope, kc, vc, pos, m->max_seq, m->d_x,
+                       m->d_scratch, 0))
+        return mfail(m, "%s", mhip_error(m->gpu));
+    return 0;
+}
+
+/* Queues the MoE of layer l on d_x: one decode launch reporting into its
+ * status slot, or (per_stage, or no decode launch for this shape) the
+ * per-stage kernels. */
+static int moe(mia_gpu_model *m, int l, int per_stage) {
+    if (per_stage || !m->decode_ok || (m->flags & MHIP_EXACT_EXPERTS)) {
+        if (mia_moe_layer_dev(m->moe, l, m->d_x, 1, NULL))
+            return mfail(m, "%s", mia_moe_error(m->moe));
+        return 0;
+    }
+    const mia_moe_tensors *t = &m->mt;
+    const size_t d = (size_t)t->dims.dim, E = (size_t)t->dims.n_experts;
+    if (mhip_decode_stack_noalloc(m->gpu, &t->dims, &t->lay,
+                                  (const unsigned char *)t->table +
+                                      (size_t)l * E * t->lay.expert_bytes,
+                                  t->router_dl + (size_t)l * E * d, t->router_t + (size_t)l * E * d,
+                                  t->norm + (size_t)l * d, NULL, m->d_x, 1, NULL, NULL,
+                                  m->d_status + 4 * l,
+                                  m->flags & (MHIP_FORCE_EXACT_ROUTER | MHIP_DECODE_FORCE_ABORT)))
+        return mfail(m, "%s", mhip_error(m->gpu));
+    return 0;
+}
+
+/* Queues the final rmsnorm, the output head and the logits' copy to host
+ * (forward.c:214-215). */
+static int head(mia_gpu_model *m) {
+    const mia_file_info *h = &m->info;
+    if (mhip_output_head(m->gpu, &m->ad, (const float *)(m->d_dense + m->off_onorm),
+                         m->d_dense + m->off_out, (int)h->vocab, m->d_x, m->d_logits,
+                         m->d_scratch, 0) ||
+        mhip_d2h_async(m->gpu, m->h_logits, m->d_logits, (size_t)h->vocab * 4))
+        return mfail(m, "%s", mhip_error(m->gpu));
+    return 0;
+}
+
+const float *mia_gpu_model_step(mia_gpu_model *m, int token, int pos) {
+    const mia_file_info *h = &m->info;
+    const int L = (int)h->n_layers, d = (int)h->dim;
+    if (pos < 0 || pos >= m->max_seq || token < 0 || token >= (int)h->vocab) {
+        mfail(m, "token %d at position %d outside [0, %u) x [0, %d)", token, pos, h->vocab,
+              m->max_seq);
+        return NULL;
+    }
+    const int decode = m->decode_ok && !(m->flags & MHIP_EXACT_EXPERTS);
+    /* forward.c:205-208: the embedding row, dequantized */
+    const size_t row = (size_t)(d / MIA_QK) * 36;
+    if (mhip_dequantize_q8(m->gpu, m->d_dense + m->off_embd + (size_t)token * row, m->d_x, d)) {
+        mfail(m, "%s", mhip_error(m->gpu));
+        return NULL;
+    }
+    for (int l = 0; l < L; l++) {
+        if (attention(m, l, pos) ||
+            (decode && mhip_d2d(m->gpu, m->d_xsave + (size_t)l * d, m->d_x, (size_t)d * 4)) ||
+            moe(m, l, 0))
+            return NULL;
+    }
+    /* the head is queued before the decode launches' status is known: one
+     * wait per step; an abort (rare) reruns from the first aborted layer */
+    if (head(m)) return NULL;
+    if ((decode && mhip_d2h_async(m->gpu, m->h_status, m->d_status, (size_t)L * 16)) ||
+        mhip_sync(m->gpu)) {
+        mfail(m, "%s", mhip_error(m->gpu));
+        return NULL;
+    }
+    m->aborts = 0;
+    int first = -1;
+    for (int l = 0; decode && l < L; l++)
+        if (m->h_status[4 * l]) {
+            m->aborts++;
+            if (first < 0) first = l;
+        }
+    if (first >= 0) {
+        if (mhip_d2d(m->gpu, m->d_x, m->d_xsave + (size_t)first * d, (size_t)d * 4)) {
+            mfail(m, "%s", mhip_error(m->gpu));
+            return NULL;
+        }
+        if (moe(m, first, 1)) return NULL;
+        for (int l = first + 1; l < L; l++)
+            if (attention(m, l, pos) || moe(m, l, 1)) return NULL;
+        if (head(m)) return NULL;
+        if (mhip_sync(m->gpu)) {
+            mfail(m, "%s", mhip_error(m->gpu));
+            return NULL;
+        }
+    }
+    return m->h_logits;
+}

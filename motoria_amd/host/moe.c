@@ -54,6 +54,14 @@ int mia_moe_fail(mia_moe *m, const char *fmt, ...) {
     return -1;
 }
 void *mia_moe_table(mia_moe *m) { return m->d_table; }
+void mia_moe_get_tensors(const mia_moe *m, mia_moe_tensors *t) {
+    t->table = m->d_table;
+    t->router_dl = m->d_router_dl;
+    t->router_t = m->d_router_t;
+    t->norm = m->d_norm;
+    t->lay = m->lay;
+    t->dims = m->dims;
+}
 const mia_moe_config *mia_moe_cfg(const mia_moe *m) { return &m->cfg; }
 static int check_status(mia_moe *m, int l0);
 

@@ -50,6 +50,14 @@ def select(variant):
     lib(variant)
 
 
+class Model(ctypes.Structure):
+    """orc_model (mia_oracle.h): the tensors of a whole model."""
+    _fields_ = [("moe", Dims), ("n_layers", _i), ("n_heads", _i), ("n_kv_heads", _i),
+                ("head_dim", _i), ("vocab", _i), ("wtype", _i), ("rope_theta", _f)] + [
+        (n, _p) for n in ("token_embd", "output", "output_norm", "attn_norm", "q_norm",
+                          "k_norm", "ffn_norm", "router", "wq", "wk", "wv", "wo", "blobs")]
+
+
 def lib(variant=None):
     global _LIB
     if _LIB is None:
@@ -77,6 +85,8 @@ def lib(variant=None):
         L.orc_moe_stack.argtypes = [ctypes.POINTER(Dims), _i, _i, _p, _p, _p, _p, _i]
         L.orc_moe_layer_bucketed.argtypes = [ctypes.POINTER(Dims), _i, _p, _p, _p, _p, _p,
                                              _p, _p, _p, _i]
+        L.orc_model_step.argtypes = [ctypes.POINTER(Model), _p, _p, _i, _i, _i, _p, _p, _i]
+        L.orc_rope_row.argtypes = [_p, _i, _i, _f]
         L.orc_route_tokens.argtypes = [ctypes.POINTER(Dims), _i, _p, _p, _p, _p, _p, _p, _p,
                                        _i]
         L.orc_route.argtypes = [_p, _i, _i, _i, _p, _p]
@@ -263,6 +273,44 @@ def route_tokens(d, x, ffn_norm, router, bias=None, nthreads=1):
     if rc != 0:
         raise RuntimeError("orc_route_tokens failed (%d)" % rc)
     return idx, w, logits
+
+
+def model_step(model, kc, vc, max_seq, token, pos, nthreads=1):
+    """orc_model_step: logits[vocab] of the token at pos (kc/vc: the KV
+    cache, [L][max_seq][kv_dim] float32, updated in place), and the residual
+    after the last layer."""
+    logits = np.zeros(model.vocab, np.float32)
+    x = np.zeros(model.moe.dim, np.float32)
+    rc = lib().orc_model_step(ctypes.byref(model), _ptr(kc), _ptr(vc), max_seq, token, pos,
+                              _ptr(logits), _ptr(x), nthreads)
+    if rc != 0:
+        raise RuntimeError("orc_model_step failed (%d)" % rc)
+    return logits, x
+
+
+def rope_row(x, pos, theta):
+    x = np.array(x, dtype=np.float32)
+    lib().orc_rope_row(_ptr(x), x.size, pos, theta)
+    return x
+
+
+def ref_model_logits(path, tokens, max_seq, n_slots):
+    """The reference's own mia_model_step over a .mia file (oracle/_ref):
+    logits[len(tokens)][vocab]."""
+    import struct
+    with open(path, "rb") as f:
+        vocab = struct.unpack("<I", f.read(36)[32:36])[0]
+    toks = np.ascontiguousarray(tokens, dtype=np.int32)
+    out = np.zeros((toks.size, vocab), np.float32)
+    err = ctypes.create_string_buffer(256)
+    R = ref()
+    R.ref_model_logits.argtypes = [ctypes.c_char_p, _i, _i, _i, _p, _p, ctypes.c_char_p,
+                                   ctypes.c_size_t]
+    rc = R.ref_model_logits(path.encode(), max_seq, n_slots, toks.size, _ptr(toks), _ptr(out),
+                            err, 256)
+    if rc != 0:
+        raise RuntimeError("ref_model_logits failed (%d): %s" % (rc, err.value.decode()))
+    return out
 
 
 def moe_stack(d, x, ffn_norm, router, blobs, nthreads=1):

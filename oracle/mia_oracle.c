@@ -526,6 +526,133 @@ out:
     return rc;
 }
 
+/* ---- one whole model step (src/model/forward.c:118-165,199-217) ---------- */
+
+/* forward.c:84-93: NeoX rotary embedding (element i pairs with i + hd/2),
+ * angles and rotation in double, each element rounded to float once. */
+static void orc_rope(float *x, int hd, int pos, float theta) {
+    const int half = hd / 2;
+    for (int i = 0; i < half; i++) {
+        const double freq = pow((double)theta, -2.0 * i / hd);
+        const double a = pos * freq, c = cos(a), sn = sin(a);
+        const float x0 = x[i], x1 = x[i + half];
+        x[i] = (float)(x0 * c - x1 * sn);
+        x[i + half] = (float)(x0 * sn + x1 * c);
+    }
+}
+
+void orc_rope_row(float *x, int hd, int pos, float theta) { orc_rope(x, hd, pos, theta); }
+
+/* forward.c:118-165: attention of the token at `pos` for layer l, in place
+ * on x; the layer's K and V rows are written to kc/vc[pos]. */
+static int orc_attention(const orc_model *m, int l, int pos, float *x, float *kc, float *vc) {
+    const int d = m->moe.dim, hd = m->head_dim, nh = m->n_heads, nkv = m->n_kv_heads;
+    const int qd = nh * hd, kvd = nkv * hd;
+    const float eps = m->moe.norm_eps;
+    const int maxd = d > qd ? d : qd;
+    float *xn = malloc(sizeof(float) * (size_t)d), *q = malloc(sizeof(float) * (size_t)qd);
+    float *k = malloc(sizeof(float) * (size_t)kvd), *v = malloc(sizeof(float) * (size_t)kvd);
+    float *att = malloc(sizeof(float) * (size_t)qd), *tmp = malloc(sizeof(float) * (size_t)d);
+    float *scores = malloc(sizeof(float) * (size_t)(pos + 1));
+    orc_block_q8 *xq = malloc(sizeof(orc_block_q8) * (size_t)(maxd / ORC_QK));
+    int rc = 0;
+    if (!xn || !q || !k || !v || !att || !tmp || !scores || !xq) {
+        rc = -1;
+        goto out;
+    }
+    orc_rmsnorm(xn, x, m->attn_norm[l], d, eps);
+    orc_matvec(q, m->wq[l], m->wtype, xn, xq, qd, d);
+    orc_matvec(k, m->wk[l], m->wtype, xn, xq, kvd, d);
+    orc_matvec(v, m->wv[l], m->wtype, xn, xq, kvd, d);
+    for (int h = 0; h < nh; h++) {
+        orc_rmsnorm(q + h * hd, q + h * hd, m->q_norm[l], hd, eps);
+        orc_rope(q + h * hd, hd, pos, m->rope_theta);
+    }
+    for (int h = 0; h < nkv; h++) {
+        orc_rmsnorm(k + h * hd, k + h * hd, m->k_norm[l], hd, eps);
+        orc_rope(k + h * hd, hd, pos, m->rope_theta);
+    }
+    memcpy(kc + (size_t)pos * kvd, k, sizeof(float) * (size_t)kvd);
+    memcpy(vc + (size_t)pos * kvd, v, sizeof(float) * (size_t)kvd);
+    const int group = nh / nkv;
+    const float scale = 1.0f / sqrtf((float)hd);
+    for (int h = 0; h < nh; h++) {
+        const float *qh = q + h * hd;
+        const int kvh = h / group;
+        for (int t = 0; t <= pos; t++) {
+            const float *kt = kc + (size_t)t * kvd + kvh * hd;
+            float dot = 0.0f;
+            for (int i = 0; i < hd; i++) dot = dot + qh[i] * kt[i];
+            scores[t] = dot * scale;
+        }
+        orc_softmax(scores, pos + 1);
+        float *o = att + h * hd;
+        for (int i = 0; i < hd; i++) o[i] = 0.0f;
+        for (int t = 0; t <= pos; t++) {
+            const float *vt = vc + (size_t)t * kvd + kvh * hd;
+            for (int i = 0; i < hd; i++) o[i] = o[i] + scores[t] * vt[i];
+        }
+    }
+    orc_matvec(tmp, m->wo[l], m->wtype, att, xq, d, qd);
+    for (int i = 0; i < d; i++) x[i] = x[i] + tmp[i];
+out:
+    free(xn);
+    free(q);
+    free(k);
+    free(v);
+    free(att);
+    free(tmp);
+    free(scores);
+    free(xq);
+    return rc;
+}
+
+int orc_model_step(const orc_model *m, float *kc, float *vc, int max_seq, int token, int pos,
+                   float *logits, float *x_out, int nthreads) {
+    const int d = m->moe.dim, E = m->moe.n_experts, V = m->vocab;
+    const int kvd = m->n_kv_heads * m->head_dim;
+    if (pos < 0 || pos >= max_seq || token < 0 || token >= V || m->wtype != ORC_Q8_0) return -1;
+    const int maxd = d > m->moe.expert_hidden ? d : m->moe.expert_hidden;
+    float *x = malloc(sizeof(float) * (size_t)d), *xn = malloc(sizeof(float) * (size_t)d);
+    float *scratch = malloc(sizeof(float) * (size_t)scratch_floats(&m->moe));
+    orc_block_q8 *xq = malloc(sizeof(orc_block_q8) * (size_t)(maxd / ORC_QK));
+    int rc = 0;
+    if (!x || !xn || !scratch || !xq) {
+        rc = -1;
+        goto out;
+    }
+    /* forward.c:205-208: the token's embedding row, dequantized */
+    orc_dequantize_row(m->wtype,
+                       (const unsigned char *)m->token_embd +
+                           (size_t)token * orc_row_bytes(m->wtype, d),
+                       x, d);
+    for (int l = 0; l < m->n_layers && !rc; l++) {
+        const size_t off = (size_t)l * max_seq * kvd;
+        rc = orc_attention(m, l, pos, x, kc + off, vc + off);
+        if (!rc)
+            rc = moe_token(&m->moe, x, m->ffn_norm[l], m->router[l], NULL,
+                           m->blobs + (size_t)l * E, NULL, NULL, NULL, NULL, scratch, xq,
+                           nthreads);
+    }
+    if (rc) goto out;
+    if (x_out) memcpy(x_out, x, sizeof(float) * (size_t)d);
+    /* forward.c:214-215: final norm and output head */
+    orc_rmsnorm(xn, x, m->output_norm, d, m->moe.norm_eps);
+    float *hq = malloc(sizeof(orc_block_q8) * (size_t)(d / ORC_QK));
+    if (!hq) {
+        rc = -1;
+        goto out;
+    }
+    matvec_mt(logits, m->output, m->wtype, xn, (orc_block_q8 *)hq, V, d, nthreads);
+    free(hq);
+out:
+    free(x);
+    free(xn);
+    free(scratch);
+    free(xq);
+    return rc;
+}
+
 int orc_dispatch(const int *idx, int T, int K, int E, int *counts,
                  int *offsets, int *perm, int *pos) {
     const int A = T * K;

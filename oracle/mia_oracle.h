@@ -22,6 +22,9 @@
  *   orc_softmax/top_k    known answers (ref_test.go:30-56), tie rule, brute force.
  *   orc_moe_layer        bit-equal to oracle/_ref (real moe()) on golden vectors.
  *   orc_moe_layer_bucketed  bit-equal to orc_moe_layer (loop nest only differs).
+ *   orc_model_step       bit-equal to oracle/_ref's mia_model_step (golden
+ *                        logits of tests/golden/model_*.npz); RoPE against
+ *                        its closed form (a rotation preserves norms).
  *   orc_dispatch         brute-force stable sort; permutation invariants.
  */
 #include <stddef.h>
@@ -99,6 +102,34 @@ int orc_moe_layer_bucketed(const orc_dims *s, int T, float *x, const float *ffn_
 int orc_route_tokens(const orc_dims *s, int T, const float *x, const float *ffn_norm,
                      const float *router, const float *bias, int *idx, float *w,
                      float *logits, int nthreads);
+
+/* A whole model (the tensors a .mia file holds, src/model/forward.c). */
+typedef struct {
+    orc_dims moe;                        /* dim and the MoE shape, norm_eps */
+    int n_layers, n_heads, n_kv_heads, head_dim, vocab, wtype;
+    float rope_theta;
+    const void *token_embd, *output;     /* [vocab][dim] in wtype */
+    const float *output_norm;            /* [dim] */
+    const float *const *attn_norm;       /* [L] -> [dim] */
+    const float *const *q_norm;          /* [L] -> [head_dim] */
+    const float *const *k_norm;          /* [L] -> [head_dim] */
+    const float *const *ffn_norm;        /* [L] -> [dim] */
+    const float *const *router;          /* [L] -> [E][dim] */
+    const void *const *wq, *const *wk, *const *wv, *const *wo; /* [L], in wtype */
+    const unsigned char *const *blobs;   /* [L * E] expert blobs (Q8_0) */
+} orc_model;
+
+/* mia_model_step (src/model/forward.c:199-217) for the token at `pos`:
+ * embedding, n_layers x (attention, MoE), final rmsnorm and output head into
+ * logits[vocab]. kc/vc: the caller's KV cache, [L][max_seq][n_kv_heads *
+ * head_dim] floats, positions < pos already filled by earlier steps.
+ * x_out (optional) receives the residual after the last layer. nthreads
+ * spreads 64-row chunks of the large matrices over threads (same bits).
+ * Q8_0 models only. Returns 0 or -1. */
+int orc_model_step(const orc_model *m, float *kc, float *vc, int max_seq, int token, int pos,
+                   float *logits, float *x_out, int nthreads);
+/* forward.c:84-93 on one head row, in place (exposed for tests). */
+void orc_rope_row(float *x, int hd, int pos, float theta);
 
 /* Stable counting sort of the T*K assignments (t, j) by expert idx[t][j],
  * t-major then j. counts[E], offsets[E+1], perm[T*K] = t*K + j in bucketed

@@ -117,3 +117,42 @@ int ref_moe_layer(int dim, int n_experts, int n_active, int expert_hidden,
     }
     return 0;
 }
+
+/*
+ * The reference's whole-model step on a .mia file, in the manner of
+ * src/app/dump.c: mia_file_open (src/storage/mia_file.c), an expert cache of
+ * n_slots slots over mia_file_read_expert, mia_model_init and
+ * mia_model_step (src/model/forward.c:199-217) for tokens[0..n) at positions
+ * 0..n-1. logits[n][vocab]. Returns 0, or the failing step's position + 1
+ * (or a negative code when opening failed; err receives the reason).
+ */
+int ref_model_logits(const char *path, int max_seq, int n_slots, int n, const int *tokens,
+                     float *logits, char *err, size_t errlen) {
+    mia_file f;
+    if (mia_file_open(&f, path, err, errlen) != 0) return -1;
+    mia_expert_cache cache;
+    if (mia_cache_init(&cache, (int)f.h.n_layers, (int)f.h.n_experts, f.h.expert_blob_size,
+                       n_slots, mia_file_read_expert, &f) != 0) {
+        mia_file_close(&f);
+        return -2;
+    }
+    mia_model m;
+    if (mia_model_init(&m, &f, &cache, max_seq) != 0) {
+        mia_cache_free(&cache);
+        mia_file_close(&f);
+        return -3;
+    }
+    int rc = 0;
+    for (int p = 0; p < n; p++) {
+        const float *lg = mia_model_step(&m, tokens[p], p);
+        if (!lg) {
+            rc = p + 1;
+            break;
+        }
+        memcpy(logits + (size_t)p * f.h.vocab, lg, sizeof(float) * f.h.vocab);
+    }
+    mia_model_free(&m);
+    mia_cache_free(&cache);
+    mia_file_close(&f);
+    return rc;
+}

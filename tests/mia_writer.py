@@ -102,6 +102,48 @@ def write(path, cfg, wtype, dense, expert_blob, tokenizer=b""):
 encode_q8 = None  # set by the caller: float32 values -> Q8_0 bytes (per 32-value block)
 
 
+def synthetic(O, path, cfg, wtype=Q8_0, seed=7):
+    """A synthetic model file: dense tensors ~ N(0, 0.02) from numpy's
+    seeded generator (norms 1 + 0.1 N(0, 1); routers N(0, 0.16) so routing is
+    decisive), Q8_0 matrices quantized with the oracle's quantizer, experts
+    from the synthetic generator (Q8_0 files) or fp32 normals (F32 files).
+    O is the oracle module. Returns the layout of `write`."""
+    global encode_q8
+    encode_q8 = O.quantize_row_q8
+    rng = np.random.default_rng(seed)
+    d = O.dims(dim=cfg["dim"], n_experts=cfg["n_experts"], n_active=cfg["n_active"],
+               expert_hidden=cfg["expert_hidden"], norm_topk=cfg["norm_topk"],
+               norm_eps=cfg["norm_eps"])
+
+    def dense(name, rows, cols):
+        if "norm" in name:
+            return 1.0 + 0.1 * rng.standard_normal(rows * cols)
+        if name.endswith("router"):
+            return 0.4 * rng.standard_normal(rows * cols)
+        return 0.02 * rng.standard_normal(rows * cols)
+
+    _, _, up, down, blob = layout(cfg, wtype)
+
+    def expert(l, e):
+        if wtype == Q8_0:
+            return O.synth_expert_blob(seed + l, l, e, d)
+        b = np.zeros(blob, np.uint8)
+        eh, dim = cfg["expert_hidden"], cfg["dim"]
+        for off, n in ((0, eh * dim), (up, eh * dim), (down, dim * eh)):
+            b[off:off + 4 * n] = (0.02 * rng.standard_normal(n)).astype(np.float32).view(np.uint8)
+        return b
+
+    return write(path, cfg, wtype, dense, expert, tokenizer=b"tok")
+
+
+# A model with the attention shape of Qwen3-30B-A3B (dim 2048, 32 query and 4
+# key/value heads of 128) and a smaller MoE and vocabulary, for model-step
+# tests that run on the CPU.
+MINI_QWEN = dict(dim=2048, n_layers=2, n_heads=32, n_kv_heads=4, head_dim=128, vocab=64,
+                 n_experts=16, n_active=4, expert_hidden=768, norm_topk=1, rope_theta=1e6,
+                 norm_eps=1e-6)
+
+
 def read_dense(path, lay, name):
     """A dense fp32 tensor back from the file (vectors and routers)."""
     _, rows, cols, quant, off = lay["entries"][name]
@@ -115,3 +157,50 @@ def read_blob(path, lay, cfg, layer, expert):
     with open(path, "rb") as f:
         f.seek(lay["experts_offset"] + (layer * cfg["n_experts"] + expert) * lay["blob"])
         return np.frombuffer(f.read(lay["blob"]), dtype=np.uint8)
+
+
+class FileModel:
+    """An oracle.Model over the bytes of a .mia file written by `write`
+    (Q8_0), with the pointer arrays it needs kept alive."""
+
+    def __init__(self, O, path, cfg):
+        import ctypes
+        self.data = np.fromfile(path, dtype=np.uint8)
+        entries, _, _, _, blob = layout(cfg, Q8_0)
+        entries = {e[0]: e for e in entries}
+        base = self.data.ctypes.data
+        experts_offset = align(HEADER_REGION + layout(cfg, Q8_0)[1], EXPERT_ALIGN)
+        L, E = cfg["n_layers"], cfg["n_experts"]
+
+        def ptr(name):
+            return base + HEADER_REGION + entries[name][4]
+
+        def arr(names):
+            a = (ctypes.c_void_p * len(names))(*[ptr(n) for n in names])
+            self.keep.append(a)
+            return ctypes.cast(a, ctypes.c_void_p)
+
+        self.keep = []
+        m = O.Model()
+        m.moe = O.dims(dim=cfg["dim"], n_experts=E, n_active=cfg["n_active"],
+                       expert_hidden=cfg["expert_hidden"], norm_topk=cfg["norm_topk"],
+                       norm_eps=cfg["norm_eps"])
+        m.n_layers, m.n_heads, m.n_kv_heads = L, cfg["n_heads"], cfg["n_kv_heads"]
+        m.head_dim, m.vocab, m.wtype, m.rope_theta = (cfg["head_dim"], cfg["vocab"], Q8_0,
+                                                      cfg["rope_theta"])
+        m.token_embd, m.output, m.output_norm = ptr("token_embd"), ptr("output"), ptr("output_norm")
+        for field, suffix in (("attn_norm", "attn_norm"), ("q_norm", "q_norm"), ("k_norm", "k_norm"),
+                              ("ffn_norm", "ffn_norm"), ("router", "router"), ("wq", "wq"),
+                              ("wk", "wk"), ("wv", "wv"), ("wo", "wo")):
+            setattr(m, field, arr(["blk.%d.%s" % (l, suffix) for l in range(L)]))
+        blobs = (ctypes.c_void_p * (L * E))(
+            *[base + experts_offset + i * blob for i in range(L * E)])
+        self.keep.append(blobs)
+        m.blobs = ctypes.cast(blobs, ctypes.c_void_p)
+        self.model = m
+        self.cfg = cfg
+
+    def kv_cache(self, max_seq):
+        c = self.cfg
+        n = c["n_layers"] * max_seq * c["n_kv_heads"] * c["head_dim"]
+        return np.zeros(n, np.float32), np.zeros(n, np.float32)

@@ -62,3 +62,48 @@ def test_layer_golden(oracle, name, shape_key, wseed, xseed, T):
     assert np.array_equal(idx, g["idx"])
     for got, key in [(xn, "xn"), (logits, "logits"), (w, "w"), (xo, "x_out")]:
         assert np.array_equal(bits(got), bits(g[key])), key
+
+
+# ---- whole-model step (tests/golden/make_golden_model.py) -------------------------
+
+@pytest.mark.parametrize("name", ["model_tiny", "model_mini_qwen"])
+def test_model_step_golden(oracle, tmp_path, name):
+    """orc_model_step (embedding, attention with RoPE and the KV cache, MoE,
+    output head) bit-equal to the reference's own mia_model_step logits, on
+    the .mia file the test writer regenerates from the fixture's seed."""
+    import hashlib
+    import json
+    import mia_writer as MW
+
+    g = load(name)
+    spec = json.load(open(os.path.join(GOLDEN, "MANIFEST_model.json")))[name]
+    path = str(tmp_path / (name + ".mia"))
+    MW.synthetic(oracle, path, spec["cfg"], MW.Q8_0, int(g["seed"]))
+    assert hashlib.sha256(open(path, "rb").read()).hexdigest() == str(g["file_sha256"]), \
+        "the writer no longer reproduces the fixture's file"
+    fm = MW.FileModel(oracle, path, spec["cfg"])
+    max_seq = int(g["max_seq"])
+    kc, vc = fm.kv_cache(max_seq)
+    want = g["logits_bits"]
+    for p, tok in enumerate(g["tokens"].tolist()):
+        lg, _ = oracle.model_step(fm.model, kc, vc, max_seq, tok, p, nthreads=4)
+        assert np.array_equal(lg.view(np.uint32), want[p]), "position %d" % p
+
+
+def test_rope_known_answers(oracle):
+    """forward.c:84-93: position 0 is the identity; otherwise element i and
+    i + hd/2 rotate by pos * theta^(-2i/hd) (closed form in double, to one
+    float rounding), which keeps each pair's norm."""
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(128).astype(np.float32)
+    assert np.array_equal(oracle.rope_row(x, 0, 1e6).view(np.uint32), x.view(np.uint32))
+    for pos in (1, 7, 1000):
+        y = oracle.rope_row(x, pos, 1e6)
+        i = np.arange(64)
+        a = pos * np.power(1e6, -2.0 * i / 128)
+        x0, x1 = x[:64].astype(np.float64), x[64:].astype(np.float64)
+        want0 = (x0 * np.cos(a) - x1 * np.sin(a)).astype(np.float32)
+        want1 = (x0 * np.sin(a) + x1 * np.cos(a)).astype(np.float32)
+        ulp = np.spacing(np.abs(np.concatenate([want0, want1])))
+        assert np.all(np.abs(y - np.concatenate([want0, want1])) <= ulp)
+        assert np.allclose(y[:64] ** 2 + y[64:] ** 2, x[:64] ** 2 + x[64:] ** 2, rtol=1e-5)

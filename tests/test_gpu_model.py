@@ -1,0 +1,189 @@
+"""The whole model step on the GPU (mia_gpu_model, include/mia/model_gpu.h).
+
+Embedding, attention with RoPE and the KV cache in HBM, the MoE FFN, final
+rmsnorm and output head (src/model/forward.c:199-217 of the reference) over
+.mia files written by tests/mia_writer.py:
+
+- the golden models: logits bit-equal to the reference's own mia_model_step
+  (tests/golden/model_*.npz, made from oracle/_ref);
+- a long context on the tiny model: bit-equal to the oracle's model step at
+  every position up to 300;
+- two layers of the Qwen3-30B-A3B shape (attention 32/4 heads of 128, MoE
+  128 x 768, top-8) with a 1000-token vocabulary: bit-equal to the oracle
+  with the exact router (and after forced aborts of every decode launch,
+  which rerun per stage); with the certified router (gate weights within
+  ~1e-6 relative) the later layers' Q8 requantizations turn that into whole
+  quantization steps, ~5e-4 of max|logit| each: max|diff| / max|ref| <= 2e-2,
+  and the same top token wherever the reference's top-two margin exceeds
+  twice that;
+- the full Qwen3-30B-A3B shape (48 layers, vocabulary 151936) generated in
+  HBM: the decode-kernel step bit-equal to the per-stage step.
+"""
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import motoria_amd as M
+import mia_writer as MW
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TOL_CERT = 2e-2
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("name", ["model_tiny", "model_mini_qwen"])
+def test_model_golden(oracle, tmp_path, name):
+    say("test_model_golden", name)
+    g = np.load(os.path.join(GOLDEN, name + ".npz"))
+    spec = json.load(open(os.path.join(GOLDEN, "MANIFEST_model.json")))[name]
+    path = str(tmp_path / (name + ".mia"))
+    MW.synthetic(oracle, path, spec["cfg"], MW.Q8_0, int(g["seed"]))
+    assert hashlib.sha256(open(path, "rb").read()).hexdigest() == str(g["file_sha256"])
+    for flags in (M.MHIP_FORCE_EXACT_ROUTER, M.MHIP_EXACT_EXPERTS):
+        m = M.GpuModel(path, int(g["max_seq"]), flags=flags)
+        try:
+            for p, tok in enumerate(g["tokens"].tolist()):
+                got = m.step(tok, p)
+                assert np.array_equal(bits(got), g["logits_bits"][p]), \
+                    "%s flags=%d position %d" % (name, flags, p)
+        finally:
+            m.close()
+        say("  flags=%d: %d positions bit-equal to the reference" % (flags, len(g["tokens"])))
+
+
+def test_model_tiny_long_context_and_bounds(oracle, tmp_path):
+    say("test_model_tiny_long_context_and_bounds")
+    path = str(tmp_path / "tiny.mia")
+    MW.synthetic(oracle, path, MW.TINY, MW.Q8_0, 21)
+    fm = MW.FileModel(oracle, path, MW.TINY)
+    max_seq, n = 320, 300
+    kc, vc = fm.kv_cache(max_seq)
+    toks = np.random.default_rng(5).integers(0, MW.TINY["vocab"], n).tolist()
+    m = M.GpuModel(path, max_seq)
+    try:
+        for p, tok in enumerate(toks):
+            want, _ = oracle.model_step(fm.model, kc, vc, max_seq, tok, p, nthreads=4)
+            assert np.array_equal(bits(m.step(tok, p)), bits(want)), "position %d" % p
+        say("  %d positions bit-equal to the oracle" % n)
+        for tok, pos in ((0, max_seq), (0, -1), (MW.TINY["vocab"], 0), (-1, 0)):
+            with pytest.raises(RuntimeError, match="outside"):
+                m.step(tok, pos)
+        # the handle still works after the rejected calls
+        want, _ = oracle.model_step(fm.model, kc, vc, max_seq, 7, n, nthreads=4)
+        assert np.array_equal(bits(m.step(7, n)), bits(want))
+    finally:
+        m.close()
+    with pytest.raises(RuntimeError, match="max_seq"):
+        M.GpuModel(path, 0)
+    with pytest.raises(RuntimeError, match="open"):
+        M.GpuModel(str(tmp_path / "absent.mia"), 4)
+    f32 = str(tmp_path / "f32.mia")
+    MW.synthetic(oracle, f32, MW.TINY, MW.F32, 21)
+    with pytest.raises(RuntimeError, match="Q8_0"):
+        M.GpuModel(f32, 4)
+
+
+QWEN2 = dict(dim=2048, n_layers=2, n_heads=32, n_kv_heads=4, head_dim=128, vocab=1000,
+             n_experts=128, n_active=8, expert_hidden=768, norm_topk=1, rope_theta=1e6,
+             norm_eps=1e-6)
+QWEN_TOKENS = 24
+
+
+@pytest.fixture(scope="module")
+def qwen_model(oracle, tmp_path_factory):
+    """A two-layer Qwen3-30B-A3B-shaped file and the oracle's logits of
+    QWEN_TOKENS seeded tokens."""
+    path = str(tmp_path_factory.mktemp("qwen") / "qwen2.mia")
+    say("write the two-layer Qwen-shaped file")
+    MW.synthetic(oracle, path, QWEN2, MW.Q8_0, 31)
+    fm = MW.FileModel(oracle, path, QWEN2)
+    kc, vc = fm.kv_cache(QWEN_TOKENS)
+    toks = np.random.default_rng(8).integers(0, QWEN2["vocab"], QWEN_TOKENS).tolist()
+    want = np.stack([oracle.model_step(fm.model, kc, vc, QWEN_TOKENS, t, p, nthreads=8)[0]
+                     for p, t in enumerate(toks)])
+    del fm
+    return path, toks, want
+
+
+@pytest.mark.parametrize("flags,aborts", [
+    (M.MHIP_FORCE_EXACT_ROUTER, 0),
+    (M.MHIP_FORCE_EXACT_ROUTER | M.MHIP_DECODE_FORCE_ABORT, 2),
+    (M.MHIP_EXACT_EXPERTS, 0),
+])
+def test_model_qwen_shape_bit_exact(qwen_model, flags, aborts):
+    say("test_model_qwen_shape_bit_exact flags=%d" % flags)
+    path, toks, want = qwen_model
+    m = M.GpuModel(path, QWEN_TOKENS, flags=flags)
+    try:
+        for p, tok in enumerate(toks):
+            got = m.step(tok, p)
+            assert m.aborts() == aborts
+            assert np.array_equal(bits(got), bits(want[p])), "position %d" % p
+    finally:
+        m.close()
+    say("  %d positions bit-equal to the oracle" % len(toks))
+
+
+def check_certified(got, want, where):
+    err = float(np.max(np.abs(got.astype(np.float64) - want)) / np.max(np.abs(want)))
+    assert err <= TOL_CERT, "%s: rel err %.3g" % (where, err)
+    top2 = np.sort(want)[-2:]
+    if top2[1] - top2[0] > 2 * TOL_CERT * np.max(np.abs(want)):
+        assert int(np.argmax(got)) == int(np.argmax(want)), where
+    return err
+
+
+def test_model_qwen_shape_certified(qwen_model):
+    say("test_model_qwen_shape_certified")
+    path, toks, want = qwen_model
+    m = M.GpuModel(path, QWEN_TOKENS, flags=0)
+    worst = 0.0
+    try:
+        for p, tok in enumerate(toks):
+            got = m.step(tok, p)
+            assert m.aborts() == 0
+            worst = max(worst, check_certified(got, want[p], "position %d" % p))
+    finally:
+        m.close()
+    say("  worst rel err %.3g over %d positions" % (worst, len(toks)))
+
+
+QWEN_FULL = dict(dim=2048, n_layers=48, n_heads=32, n_kv_heads=4, head_dim=128, vocab=151936,
+                 n_experts=128, n_active=8, expert_hidden=768, norm_topk=1, rope_theta=1e6,
+                 norm_eps=1e-6)
+
+
+def test_model_full_shape_decode_equals_per_stage():
+    say("test_model_full_shape_decode_equals_per_stage")
+    n = 6
+    a = M.GpuModel(None, 64, synth=(QWEN_FULL, 5))
+    b = M.GpuModel(None, 64, flags=M.MHIP_EXACT_EXPERTS, synth=(QWEN_FULL, 5))
+    c = M.GpuModel(None, 64, flags=0, synth=(QWEN_FULL, 5))
+    try:
+        toks = np.random.default_rng(3).integers(0, QWEN_FULL["vocab"], n).tolist()
+        worst = 0.0
+        for p, tok in enumerate(toks):
+            la, lb, lc = a.step(tok, p), b.step(tok, p), c.step(tok, p)
+            assert a.aborts() == 0 and c.aborts() == 0
+            assert np.all(np.isfinite(la))
+            assert np.array_equal(bits(la), bits(lb)), "position %d" % p
+            worst = max(worst, check_certified(lc, lb.astype(np.float64), "position %d" % p))
+        say("  %d positions: decode step == per-stage step; certified worst %.3g" % (n, worst))
+    finally:
+        a.close()
+        b.close()
+        c.close()

@@ -26,34 +26,7 @@ def say(*a):
 
 
 def make_file(oracle, path, cfg, wtype=MW.Q8_0, seed=7):
-    """A synthetic model: dense tensors ~ N(0, 0.02) (norms 1 + 0.1 N(0, 1),
-    routers scaled so routing is decisive), experts from the synthetic
-    generator (Q8_0) or fp32 normals (F32 files)."""
-    MW.encode_q8 = oracle.quantize_row_q8
-    rng = np.random.default_rng(seed)
-    d = oracle.dims(dim=cfg["dim"], n_experts=cfg["n_experts"], n_active=cfg["n_active"],
-                    expert_hidden=cfg["expert_hidden"], norm_topk=cfg["norm_topk"],
-                    norm_eps=cfg["norm_eps"])
-
-    def dense(name, rows, cols):
-        if "norm" in name:
-            return 1.0 + 0.1 * rng.standard_normal(rows * cols)
-        if name.endswith("router"):
-            return 0.4 * rng.standard_normal(rows * cols)
-        return 0.02 * rng.standard_normal(rows * cols)
-
-    _, _, up, down, blob = MW.layout(cfg, wtype)
-
-    def expert(l, e):
-        if wtype == MW.Q8_0:
-            return oracle.synth_expert_blob(seed + l, l, e, d)
-        b = np.zeros(blob, np.uint8)
-        eh, dim = cfg["expert_hidden"], cfg["dim"]
-        for off, n in ((0, eh * dim), (up, eh * dim), (down, dim * eh)):
-            b[off:off + 4 * n] = (0.02 * rng.standard_normal(n)).astype(np.float32).view(np.uint8)
-        return b
-
-    return MW.write(path, cfg, wtype, dense, expert, tokenizer=b"tok")
+    return MW.synthetic(oracle, path, cfg, wtype, seed)
 
 
 @pytest.fixture(scope="module")
