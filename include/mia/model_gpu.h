@@ -45,6 +45,12 @@ int mia_gpu_model_vocab(const mia_gpu_model *m);
  * device error. */
 const float *mia_gpu_model_step(mia_gpu_model *m, int token, int pos);
 
+/* The step followed by the token sampler on the device logits
+ * (mhip_sample, src/tokenizer/sampler.c:33-66 of the reference; s->n must
+ * be the vocabulary size): returns the picked token id, or -1. Only the id
+ * crosses PCIe; s->rng advances as mia_sample's would. */
+int mia_gpu_model_step_sample(mia_gpu_model *m, int token, int pos, mhip_sampler *s);
+
 /* Flags of the MoE layers (include/mia_hip.h), as mia_moe_set_flags:
  * MHIP_FORCE_EXACT_ROUTER (the default): the one-layer launch of the decode
  * kernel with the reference's sequential router chains; logits bit-equal to

@@ -272,6 +272,30 @@ int mhip_output_head(mhip_ctx *c, const mhip_attn_dims *s, const float *d_output
                      const void *d_output, int vocab, const float *d_x, float *d_logits,
                      void *d_scratch, int flags);
 
+/* ---- token sampler on device logits -------------------------------------
+ * src/tokenizer/sampler.c of the reference: mhip_sampler is mia_sampler
+ * (include/mia/sampler.h:11-16) without its host buffer; init as
+ * mia_sampler_init (sampler.c:6-14: top_p outside (0, 1] becomes 1, seed 0
+ * the default state). mhip_sample is mia_sample (sampler.c:33-66) on
+ * d_logits[n] (left unchanged): the picked token id goes to *d_token
+ * (device int) and s->rng advances as the reference's does (once per call
+ * with temperature > 0). Same picks as the reference; candidates of equal
+ * probability in ascending index (glibc's merge-sort qsort). Where the
+ * reference reads outside its buffer (no candidate: NaN logits, or a
+ * cutoff above every probability) the greedy token is picked. */
+#define MHIP_SAMPLE_MAX_N (1 << 21)
+typedef struct {
+    float temperature, top_p;
+    int n;
+    uint64_t rng;
+} mhip_sampler;
+void mhip_sampler_init(mhip_sampler *s, float temperature, float top_p, int n, uint64_t seed);
+/* Device scratch of mhip_sample for n logits (0 when n is outside
+ * [1, MHIP_SAMPLE_MAX_N]). */
+size_t mhip_sample_scratch_bytes(int n);
+int mhip_sample(mhip_ctx *c, mhip_sampler *s, const float *d_logits, void *d_scratch,
+                int *d_token);
+
 /* ---- reference tensor ops on device pointers ---------------------------- */
 /* Q8_0 blocks in the reference's 36-byte format. */
 int mhip_quantize_q8(mhip_ctx *c, const float *d_x, void *d_blocks, int n);

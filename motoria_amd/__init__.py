@@ -61,6 +61,11 @@ class AttnDims(ctypes.Structure):
                 ("norm_eps", _f)]
 
 
+class Sampler(ctypes.Structure):
+    """mhip_sampler (include/mia_hip.h)."""
+    _fields_ = [("temperature", _f), ("top_p", _f), ("n", _i), ("rng", _u64)]
+
+
 class FileInfo(ctypes.Structure):
     """mia_file_info (include/mia/moe.h): a .mia header and blob offsets."""
     _fields_ = [(n, ctypes.c_uint32) for n in (
@@ -137,6 +142,9 @@ SIGNATURES = {
     "mhip_attention": (_i, [_p, ctypes.POINTER(AttnDims), _p, _p, _p, _p, _p, _p, _p, _p, _p,
                             _p, _i, _i, _p, _p, _i]),
     "mhip_output_head": (_i, [_p, ctypes.POINTER(AttnDims), _p, _p, _i, _p, _p, _p, _i]),
+    "mhip_sampler_init": (None, [ctypes.POINTER(Sampler), _f, _f, _i, _u64]),
+    "mhip_sample_scratch_bytes": (_sz, [_i]),
+    "mhip_sample": (_i, [_p, ctypes.POINTER(Sampler), _p, _p, _p]),
     "mhip_quantize_q8": (_i, [_p, _p, _p, _i]),
     "mhip_dequantize_q8": (_i, [_p, _p, _p, _i]),
     "mhip_matvec": (_i, [_p, _p, _p, _i, _p, _p, _i, _i]),
@@ -188,6 +196,7 @@ SIGNATURES = {
     "mia_gpu_model_error": (ctypes.c_char_p, [_p]),
     "mia_gpu_model_vocab": (_i, [_p]),
     "mia_gpu_model_step": (ctypes.POINTER(_f), [_p, _i, _i]),
+    "mia_gpu_model_step_sample": (_i, [_p, _i, _i, ctypes.POINTER(Sampler)]),
     "mia_gpu_model_set_flags": (None, [_p, _i]),
     "mia_gpu_model_aborts": (_i, [_p]),
 }
@@ -507,6 +516,15 @@ class GpuModel:
         """Decode launches of the last step that aborted (rerun per stage)."""
         return lib().mia_gpu_model_aborts(self.h)
 
+    def step_sample(self, token, pos, sampler):
+        """The next token picked on the device (sampler: a Sampler over the
+        vocabulary, its rng advanced in place)."""
+        r = lib().mia_gpu_model_step_sample(self.h, token, pos, ctypes.byref(sampler))
+        if r < 0:
+            raise RuntimeError("mia_gpu_model_step_sample: " +
+                               lib().mia_gpu_model_error(self.h).decode())
+        return r
+
     def step(self, token, pos):
         """Logits (a copy) of `token` at `pos`."""
         r = lib().mia_gpu_model_step(self.h, token, pos)
@@ -514,3 +532,16 @@ class GpuModel:
             raise RuntimeError("mia_gpu_model_step: " +
                                lib().mia_gpu_model_error(self.h).decode())
         return np.ctypeslib.as_array(r, shape=(self.vocab,)).copy()
+
+
+def sampler(temperature, top_p, n, seed):
+    """mhip_sampler_init."""
+    s = Sampler()
+    lib().mhip_sampler_init(ctypes.byref(s), temperature, top_p, n, seed)
+    return s
+
+
+def sample_dev(gpu, s, d_logits, d_scratch, d_token):
+    """mhip_sample on a Gpu context (queued; read d_token after a sync)."""
+    gpu.check(lib().mhip_sample(gpu.h, ctypes.byref(s), d_logits, d_scratch, d_token),
+              "mhip_sample")

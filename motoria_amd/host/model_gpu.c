@@ -44,6 +44,8 @@ struct mia_gpu_model {
     float *d_xsave;          /* [L][dim] x before each layer's MoE */
     int *d_status;           /* [L][4] decode status per layer */
     float *d_logits;         /* [vocab] */
+    void *d_sample;          /* mhip_sample scratch for vocab logits */
+    int *d_token, *h_token;  /* the sampled token (device, pinned) */
     float *h_logits;         /* pinned [vocab] */
     int *h_status;           /* pinned [L][4] */
     char err[512];
@@ -75,6 +77,9 @@ void mia_gpu_model_close(mia_gpu_model *m) {
         mhip_free(m->gpu, m->d_xsave);
         mhip_free(m->gpu, m->d_status);
         mhip_free(m->gpu, m->d_logits);
+        mhip_free(m->gpu, m->d_sample);
+        mhip_free(m->gpu, m->d_token);
+        mhip_host_free(m->gpu, m->h_token);
         mhip_host_free(m->gpu, m->h_logits);
         mhip_host_free(m->gpu, m->h_status);
     }
@@ -147,8 +152,14 @@ static int setup(mia_gpu_model *m, int max_seq, int device) {
     m->d_logits = mhip_malloc(m->gpu, (size_t)h->vocab * 4);
     m->h_logits = mhip_host_malloc(m->gpu, (size_t)h->vocab * 4);
     m->h_status = mhip_host_malloc(m->gpu, L * 16);
+    const size_t sb = mhip_sample_scratch_bytes((int)h->vocab);
+    if (!sb) return mfail(m, "vocabulary of %u tokens: no sampler for it", h->vocab);
+    m->d_sample = mhip_malloc(m->gpu, sb);
+    m->d_token = mhip_malloc(m->gpu, sizeof(int));
+    m->h_token = mhip_host_malloc(m->gpu, sizeof(int));
     if (!m->lo || !m->d_dense || !m->d_kc || !m->d_vc || !m->d_rope || !m->d_scratch ||
-        !m->d_x || !m->d_xsave || !m->d_status || !m->d_logits || !m->h_logits || !m->h_status)
+        !m->d_x || !m->d_xsave || !m->d_status || !m->d_logits || !m->h_logits ||
+        !m->h_status || !m->d_sample || !m->d_token || !m->h_token)
         return mfail(m, "device memory: %s", mhip_error(m->gpu));
     /* RoPE angles as the reference computes them (forward.c:86-89) */
     double *t = malloc((size_t)max_seq * half * 2 * 8);
@@ -290,47 +301,58 @@ static int moe(mia_gpu_model *m, int l, int per_stage) {
     return 0;
 }
 
-/* Queues the final rmsnorm, the output head and the logits' copy to host
- * (forward.c:214-215). */
-static int head(mia_gpu_model *m) {
+/* What follows the last layer: the final rmsnorm and the output head
+ * (forward.c:214-215), then either the logits' copy to host or the sampler
+ * on the device logits and the token's copy. */
+typedef struct {
+    mhip_sampler *s; /* NULL: copy the logits */
+    uint64_t rng;    /* s->rng before the step (a rerun draws again from it) */
+} step_tail;
+
+static int tail(mia_gpu_model *m, step_tail *t) {
     const mia_file_info *h = &m->info;
     if (mhip_output_head(m->gpu, &m->ad, (const float *)(m->d_dense + m->off_onorm),
                          m->d_dense + m->off_out, (int)h->vocab, m->d_x, m->d_logits,
-                         m->d_scratch, 0) ||
-        mhip_d2h_async(m->gpu, m->h_logits, m->d_logits, (size_t)h->vocab * 4))
+                         m->d_scratch, 0))
+        return mfail(m, "%s", mhip_error(m->gpu));
+    if (!t->s) {
+        if (mhip_d2h_async(m->gpu, m->h_logits, m->d_logits, (size_t)h->vocab * 4))
+            return mfail(m, "%s", mhip_error(m->gpu));
+        return 0;
+    }
+    t->s->rng = t->rng;
+    if (mhip_sample(m->gpu, t->s, m->d_logits, m->d_sample, m->d_token) ||
+        mhip_d2h_async(m->gpu, m->h_token, m->d_token, sizeof(int)))
         return mfail(m, "%s", mhip_error(m->gpu));
     return 0;
 }
 
-const float *mia_gpu_model_step(mia_gpu_model *m, int token, int pos) {
+/* One step, then the tail; 0 or -1. */
+static int run_step(mia_gpu_model *m, int token, int pos, step_tail *t) {
     const mia_file_info *h = &m->info;
     const int L = (int)h->n_layers, d = (int)h->dim;
-    if (pos < 0 || pos >= m->max_seq || token < 0 || token >= (int)h->vocab) {
-        mfail(m, "token %d at position %d outside [0, %u) x [0, %d)", token, pos, h->vocab,
-              m->max_seq);
-        return NULL;
-    }
+    if (pos < 0 || pos >= m->max_seq || token < 0 || token >= (int)h->vocab)
+        return mfail(m, "token %d at position %d outside [0, %u) x [0, %d)", token, pos, h->vocab,
+                     m->max_seq);
+    if (t->s && t->s->n != (int)h->vocab)
+        return mfail(m, "sampler over %d logits, the vocabulary has %u", t->s->n, h->vocab);
     const int decode = m->decode_ok && !(m->flags & MHIP_EXACT_EXPERTS);
     /* forward.c:205-208: the embedding row, dequantized */
     const size_t row = (size_t)(d / MIA_QK) * 36;
-    if (mhip_dequantize_q8(m->gpu, m->d_dense + m->off_embd + (size_t)token * row, m->d_x, d)) {
-        mfail(m, "%s", mhip_error(m->gpu));
-        return NULL;
-    }
+    if (mhip_dequantize_q8(m->gpu, m->d_dense + m->off_embd + (size_t)token * row, m->d_x, d))
+        return mfail(m, "%s", mhip_error(m->gpu));
     for (int l = 0; l < L; l++) {
         if (attention(m, l, pos) ||
             (decode && mhip_d2d(m->gpu, m->d_xsave + (size_t)l * d, m->d_x, (size_t)d * 4)) ||
             moe(m, l, 0))
-            return NULL;
+            return -1;
     }
-    /* the head is queued before the decode launches' status is known: one
+    /* the tail is queued before the decode launches' status is known: one
      * wait per step; an abort (rare) reruns from the first aborted layer */
-    if (head(m)) return NULL;
+    if (tail(m, t)) return -1;
     if ((decode && mhip_d2h_async(m->gpu, m->h_status, m->d_status, (size_t)L * 16)) ||
-        mhip_sync(m->gpu)) {
-        mfail(m, "%s", mhip_error(m->gpu));
-        return NULL;
-    }
+        mhip_sync(m->gpu))
+        return mfail(m, "%s", mhip_error(m->gpu));
     m->aborts = 0;
     int first = -1;
     for (int l = 0; decode && l < L; l++)
@@ -338,19 +360,28 @@ const float *mia_gpu_model_step(mia_gpu_model *m, int token, int pos) {
             m->aborts++;
             if (first < 0) first = l;
         }
-    if (first >= 0) {
-        if (mhip_d2d(m->gpu, m->d_x, m->d_xsave + (size_t)first * d, (size_t)d * 4)) {
-            mfail(m, "%s", mhip_error(m->gpu));
-            return NULL;
-        }
-        if (moe(m, first, 1)) return NULL;
-        for (int l = first + 1; l < L; l++)
-            if (attention(m, l, pos) || moe(m, l, 1)) return NULL;
-        if (head(m)) return NULL;
-        if (mhip_sync(m->gpu)) {
-            mfail(m, "%s", mhip_error(m->gpu));
-            return NULL;
-        }
+    if (first < 0) return 0;
+    if (mhip_d2d(m->gpu, m->d_x, m->d_xsave + (size_t)first * d, (size_t)d * 4))
+        return mfail(m, "%s", mhip_error(m->gpu));
+    if (moe(m, first, 1)) return -1;
+    for (int l = first + 1; l < L; l++)
+        if (attention(m, l, pos) || moe(m, l, 1)) return -1;
+    if (tail(m, t)) return -1;
+    if (mhip_sync(m->gpu)) return mfail(m, "%s", mhip_error(m->gpu));
+    return 0;
+}
+
+const float *mia_gpu_model_step(mia_gpu_model *m, int token, int pos) {
+    step_tail t = {NULL, 0};
+    return run_step(m, token, pos, &t) ? NULL : m->h_logits;
+}
+
+int mia_gpu_model_step_sample(mia_gpu_model *m, int token, int pos, mhip_sampler *s) {
+    if (!s) return mfail(m, "null sampler");
+    step_tail t = {s, s->rng};
+    if (run_step(m, token, pos, &t)) {
+        s->rng = t.rng;
+        return -1;
     }
-    return m->h_logits;
+    return *m->h_token;
 }

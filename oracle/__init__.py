@@ -50,6 +50,11 @@ def select(variant):
     lib(variant)
 
 
+class Sampler(ctypes.Structure):
+    """orc_sampler (mia_oracle.h)."""
+    _fields_ = [("temperature", _f), ("top_p", _f), ("n", _i), ("rng", _u64)]
+
+
 class Model(ctypes.Structure):
     """orc_model (mia_oracle.h): the tensors of a whole model."""
     _fields_ = [("moe", Dims), ("n_layers", _i), ("n_heads", _i), ("n_kv_heads", _i),
@@ -87,6 +92,10 @@ def lib(variant=None):
                                              _p, _p, _p, _i]
         L.orc_model_step.argtypes = [ctypes.POINTER(Model), _p, _p, _i, _i, _i, _p, _p, _i]
         L.orc_rope_row.argtypes = [_p, _i, _i, _f]
+        L.orc_sampler_init.argtypes = [ctypes.POINTER(Sampler), _f, _f, _i, _u64]
+        L.orc_sampler_rand01.restype = _f
+        L.orc_sampler_rand01.argtypes = [ctypes.POINTER(Sampler)]
+        L.orc_sample.argtypes = [ctypes.POINTER(Sampler), _p]
         L.orc_route_tokens.argtypes = [ctypes.POINTER(Dims), _i, _p, _p, _p, _p, _p, _p, _p,
                                        _i]
         L.orc_route.argtypes = [_p, _i, _i, _i, _p, _p]
@@ -359,3 +368,23 @@ def ref_moe_layer(d, x, ffn_norm, router, blobs):
     if rc != 0:
         raise RuntimeError("ref_moe_layer failed (%d)" % rc)
     return x, idx_loaded, idx, w, logits, xn
+
+
+def sample(logits, temperature, top_p, seed, draws):
+    """orc_sample: `draws` tokens from one sampler state over the same
+    logits (float32[n])."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    s = Sampler()
+    lib().orc_sampler_init(ctypes.byref(s), temperature, top_p, lg.size, seed)
+    return [lib().orc_sample(ctypes.byref(s), _ptr(lg)) for _ in range(draws)]
+
+
+def ref_sample(logits, temperature, top_p, seed, draws):
+    """The reference's own mia_sample (oracle/_ref), as `sample`."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    out = np.zeros(draws, np.int32)
+    R = ref()
+    R.ref_sample.argtypes = [_p, _i, _f, _f, _u64, _i, _p]
+    if R.ref_sample(_ptr(lg), lg.size, temperature, top_p, seed, draws, _ptr(out)) != 0:
+        raise RuntimeError("ref_sample failed")
+    return out.tolist()

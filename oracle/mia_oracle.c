@@ -710,3 +710,94 @@ void orc_synth_expert_blob(uint64_t seed, int layer, int expert,
         }
     }
 }
+
+/* ---- token sampler (src/tokenizer/sampler.c) ------------------------------------ */
+
+void orc_sampler_init(orc_sampler *s, float temperature, float top_p, int n, uint64_t seed) {
+    s->temperature = temperature;
+    s->top_p = (top_p > 0.0f && top_p <= 1.0f) ? top_p : 1.0f;
+    s->n = n;
+    s->rng = seed ? seed : 0x2545F4914F6CDD1DULL;
+}
+
+/* xorshift64* (shifts 12, 25, 27; multiplier 2685821657736338717), the top
+ * 24 bits of the product over 2^24 */
+float orc_sampler_rand01(orc_sampler *s) {
+    uint64_t x = s->rng;
+    x ^= x >> 12;
+    x ^= x << 25;
+    x ^= x >> 27;
+    s->rng = x;
+    return (float)((x * 0x2545F4914F6CDD1DULL) >> 40) / 16777216.0f;
+}
+
+typedef struct {
+    float p;
+    int i;
+} orc_cand;
+
+static int cand_order(const void *a, const void *b) {
+    const orc_cand *x = a, *y = b;
+    if (x->p != y->p) return x->p > y->p ? -1 : 1;
+    return (x->i > y->i) - (x->i < y->i);
+}
+
+int orc_sample(orc_sampler *s, const float *logits) {
+    const int n = s->n;
+    int best = 0;
+    for (int i = 1; i < n; i++)
+        if (logits[i] > logits[best]) best = i;
+    if (s->temperature <= 0.0f) return best;
+    float *e = malloc(sizeof(float) * (size_t)n);
+    orc_cand *c = malloc(sizeof(orc_cand) * (size_t)n);
+    if (!e || !c) {
+        free(e);
+        free(c);
+        return -1;
+    }
+    /* :42-44: e_i = expf((l_i - max) / T), summed in index order */
+    const float mx = logits[best];
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) {
+        e[i] = expf((logits[i] - mx) / s->temperature);
+        sum = sum + e[i];
+    }
+    /* :46-51: candidates p >= (1 - top_p) / (n - 1) */
+    const float cutoff = (1.0f - s->top_p) / (float)(n > 1 ? n - 1 : 1);
+    int m = 0;
+    for (int i = 0; i < n; i++) {
+        const float p = e[i] / sum;
+        if (p >= cutoff) {
+            c[m].p = p;
+            c[m].i = i;
+            m++;
+        }
+    }
+    /* :53-66: the shortest prefix whose running sum reaches top_p; r in
+     * [0, cum); the first candidate whose running sum exceeds r. The draw
+     * is taken even with no candidate (the state advances as the
+     * reference's does). */
+    if (m > 0) qsort(c, (size_t)m, sizeof(orc_cand), cand_order);
+    float cum = 0.0f;
+    int last = m - 1;
+    for (int i = 0; i < m; i++) {
+        cum = cum + c[i].p;
+        if (cum >= s->top_p) {
+            last = i;
+            break;
+        }
+    }
+    const float r = orc_sampler_rand01(s) * cum;
+    int tok = m > 0 ? c[last].i : best;
+    float acc = 0.0f;
+    for (int i = 0; i <= last; i++) {
+        acc = acc + c[i].p;
+        if (r < acc) {
+            tok = c[i].i;
+            break;
+        }
+    }
+    free(e);
+    free(c);
+    return tok;
+}

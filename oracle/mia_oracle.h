@@ -131,6 +131,24 @@ int orc_model_step(const orc_model *m, float *kc, float *vc, int max_seq, int to
 /* forward.c:84-93 on one head row, in place (exposed for tests). */
 void orc_rope_row(float *x, int hd, int pos, float theta);
 
+/* The token sampler (src/tokenizer/sampler.c). init: top_p outside (0, 1]
+ * becomes 1, seed 0 the default state (:6-14). */
+typedef struct {
+    float temperature, top_p;
+    int n;
+    uint64_t rng;
+} orc_sampler;
+void orc_sampler_init(orc_sampler *s, float temperature, float top_p, int n, uint64_t seed);
+/* xorshift64* step and its 24-bit float in [0, 1) (:20-25). */
+float orc_sampler_rand01(orc_sampler *s);
+/* mia_sample (:33-66) on logits[n] (not modified): greedy when temperature
+ * <= 0, else the nucleus draw; candidates in descending probability, equal
+ * probabilities in ascending index (the order the reference's qsort gives
+ * with glibc's merge sort). An empty candidate list (logits with NaN, or a
+ * cutoff above every probability), where the reference reads outside its
+ * buffer, returns the greedy token. */
+int orc_sample(orc_sampler *s, const float *logits);
+
 /* Stable counting sort of the T*K assignments (t, j) by expert idx[t][j],
  * t-major then j. counts[E], offsets[E+1], perm[T*K] = t*K + j in bucketed
  * order, pos[t*K + j] = its position in perm. Returns 0 or -1 (bad index). */

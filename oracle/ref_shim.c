@@ -156,3 +156,28 @@ int ref_model_logits(const char *path, int max_seq, int n_slots, int n, const in
     mia_file_close(&f);
     return rc;
 }
+
+/*
+ * The reference's own sampler (src/tokenizer/sampler.c): `draws` calls of
+ * mia_sample on fresh copies of logits[n] (it overwrites them) with one
+ * sampler state, the picked tokens into out[draws].
+ */
+#include "mia/sampler.h"
+
+int ref_sample(const float *logits, int n, float temperature, float top_p, uint64_t seed,
+               int draws, int *out) {
+    mia_sampler s;
+    if (mia_sampler_init(&s, temperature, top_p, n, seed) != 0) return -1;
+    float *work = malloc(sizeof(float) * (size_t)n);
+    if (!work) {
+        mia_sampler_free(&s);
+        return -1;
+    }
+    for (int d = 0; d < draws; d++) {
+        memcpy(work, logits, sizeof(float) * (size_t)n);
+        out[d] = mia_sample(&s, work);
+    }
+    free(work);
+    mia_sampler_free(&s);
+    return 0;
+}

@@ -107,3 +107,69 @@ def test_rope_known_answers(oracle):
         ulp = np.spacing(np.abs(np.concatenate([want0, want1])))
         assert np.all(np.abs(y - np.concatenate([want0, want1])) <= ulp)
         assert np.allclose(y[:64] ** 2 + y[64:] ** 2, x[:64] ** 2 + x[64:] ** 2, rtol=1e-5)
+
+
+# ---- token sampler (tests/golden/make_golden_sampler.py) --------------------------
+
+def sampler_cases(oracle):
+    """(name, logits, temperature, top_p, seed, draws, tokens) of every case
+    in tests/golden/sampler.npz."""
+    import json
+    g = load("sampler")
+    out = []
+    for c in json.loads(str(g["manifest"])):
+        if "logit_seed" in c:
+            lg = (np.float32(c["scale"]) * oracle.synth_x(c["logit_seed"], 1, c["n"])[0])
+            lg = lg.astype(np.float32)
+        else:
+            lg = g["logits_" + c["name"]]
+        out.append((c["name"], lg, c["t"], c["p"], c["seed"], c["draws"],
+                    g["tokens_" + c["name"]].tolist()))
+    return out
+
+
+def test_sampler_golden(oracle):
+    """orc_sample picks the reference's own tokens (src/tokenizer/sampler.c:
+    33-66), including the reference's unit tests (tests/test_sampler.c:4-32:
+    greedy argmax, a tiny top_p keeps only the best, two equal logits both
+    drawn > 850 times in 2000)."""
+    for name, lg, t, p, seed, draws, want in sampler_cases(oracle):
+        assert oracle.sample(lg, t, p, seed, draws) == want, name
+    cases = {c[0]: c for c in sampler_cases(oracle)}
+    assert cases["greedy_argmax"][6] == [1]
+    assert set(cases["tiny_top_p"][6]) == {1}
+    pair = cases["equal_pair"][6]
+    assert pair.count(0) > 850 and pair.count(1) > 850
+
+
+def test_sampler_rand01_is_xorshift64star(oracle):
+    """The draw is the top 24 bits of xorshift64* (Vigna's published
+    generator: x ^= x >> 12, x ^= x << 25, x ^= x >> 27, output x times
+    2685821657736338717 mod 2^64), computed here with Python integers."""
+    import ctypes
+    s = oracle.Sampler()
+    oracle.lib().orc_sampler_init(ctypes.byref(s), 1.0, 1.0, 10, 12345)
+    x, M = 12345, (1 << 64) - 1
+    for _ in range(1000):
+        x ^= x >> 12
+        x ^= (x << 25) & M
+        x ^= x >> 27
+        want = ((x * 2685821657736338717) & M) >> 40
+        assert oracle.lib().orc_sampler_rand01(ctypes.byref(s)) == np.float32(want / 16777216.0)
+    oracle.lib().orc_sampler_init(ctypes.byref(s), 1.0, 1.0, 10, 0)
+    assert s.rng == 0x2545F4914F6CDD1D
+
+
+def test_sampler_greedy_brute_force(oracle):
+    """Greedy is the first maximum; NaN never wins except at index 0 (the
+    reference's strict comparison, sampler.c:34-37), checked against numpy."""
+    rng = np.random.default_rng(4)
+    for n in (1, 2, 7, 100, 4096):
+        for _ in range(20):
+            lg = np.round(rng.standard_normal(n) * 3).astype(np.float32)
+            if n > 3 and rng.random() < 0.5:
+                lg[rng.integers(1, n, 3)] = np.nan
+            want = int(np.nanargmax(lg)) if not np.all(np.isnan(lg[1:])) or n == 1 else 0
+            if np.isnan(lg[0]):
+                want = 0
+            assert oracle.sample(lg, 0.0, 1.0, 1, 1) == [want]
