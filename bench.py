@@ -353,6 +353,81 @@ def measure(wl_name, steps, warmup, multi_kernel=False):
     return res, moe
 
 
+QWEN_MODEL = dict(dim=2048, n_layers=48, n_heads=32, n_kv_heads=4, head_dim=128,
+                  vocab=151936, n_experts=128, n_active=8, expert_hidden=768, norm_topk=1,
+                  rope_theta=1e6, norm_eps=1e-6)
+
+
+def model_token_bytes(c, pos):
+    """Algorithmic HBM bytes of one whole-model step at position pos: every
+    dense matrix of the step read once in Q8_0 (QKV, O per layer, the output
+    head, one embedding row), the touched experts and router of every layer,
+    the K/V cache rows 0..pos of every layer, x in and out per layer."""
+    d, L = c["dim"], c["n_layers"]
+    qd, kvd = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
+    row = lambda cols: cols // 32 * 36
+    attn = (qd + 2 * kvd) * row(d) + d * row(qd) + 2 * (pos + 1) * kvd * 4 + 2 * kvd * 4
+    moe = c["n_active"] * 5308416 + c["n_experts"] * d * 4
+    return L * (attn + moe + 4 * d * 4) + row(d) + c["vocab"] * row(d) + c["vocab"] * 4
+
+
+def model_decode(steps, warmup):
+    """Tokens/s of the whole model step (mia_gpu_model_step: embedding,
+    attention with the KV cache, MoE, output head; logits bit-equal to the
+    reference) at the full Qwen3-30B-A3B shape, weights generated in HBM,
+    tokens fed back greedily on the device (mia_gpu_model_step_sample)."""
+    out = {}
+    for name, flags in (("exact", M.MHIP_FORCE_EXACT_ROUTER), ("certified", 0)):
+        m = M.GpuModel(None, warmup + steps + 1, flags=flags, synth=(QWEN_MODEL, 5))
+        s = M.sampler(0.0, 1.0, QWEN_MODEL["vocab"], 1)
+        tok = 1
+        for p in range(warmup):
+            tok = m.step_sample(tok, p, s)
+        t0 = time.perf_counter()
+        for p in range(warmup, warmup + steps):
+            tok = m.step_sample(tok, p, s)
+        dt = time.perf_counter() - t0
+        m.close()
+        nbytes = sum(model_token_bytes(QWEN_MODEL, p) for p in range(warmup, warmup + steps))
+        out[name] = {"tokens_per_s": steps / dt, "ms_per_token": dt / steps * 1e3,
+                     "achieved_gbs": nbytes / dt / 1e9,
+                     "frac": nbytes / dt / 1e9 / HBM_PEAK_GBS}
+        log("model step (%s router): %.3f ms/token, %.1f tokens/s"
+            % (name, dt / steps * 1e3, steps / dt))
+    out["workload"] = ("whole model step at the Qwen3-30B-A3B shape (48 layers, 32/4 heads of "
+                       "128, vocabulary 151936), positions %d..%d, greedy tokens picked on the "
+                       "device; host clock around the steps" % (warmup, warmup + steps - 1))
+    out["bytes_per_token"] = model_token_bytes(QWEN_MODEL, warmup)
+    return out
+
+
+def sampler_timing(draws=50):
+    """Microseconds per mhip_sample over vocabulary-sized logits (N(0, 3)):
+    greedy, and temperature/top-p draws (the two fp32 running sums of the
+    reference's sampler are sequential chains)."""
+    n = QWEN_MODEL["vocab"]
+    g = M.Gpu(0)
+    lg = (3.0 * np.random.default_rng(0).standard_normal(n)).astype(np.float32)
+    d_l, d_t = g.upload(lg), g.malloc(4)
+    d_s = g.malloc(M.lib().mhip_sample_scratch_bytes(n))
+    out = {}
+    for t, p in ((0.0, 1.0), (0.8, 0.95), (1.0, 1.0)):
+        s = M.sampler(t, p, n, 5)
+        for _ in range(3):
+            M.sample_dev(g, s, d_l, d_s, d_t)
+        g.check(M.lib().mhip_sync(g.h), "sync")
+        t0 = time.perf_counter()
+        for _ in range(draws):
+            M.sample_dev(g, s, d_l, d_s, d_t)
+        g.check(M.lib().mhip_sync(g.h), "sync")
+        out["T=%g top_p=%g" % (t, p)] = (time.perf_counter() - t0) / draws * 1e6
+    for p_ in (d_l, d_t, d_s):
+        g.free(p_)
+    g.close()
+    log("sampler (us per draw over %d logits): %s" % (n, out))
+    return {"logits": n, "us_per_draw": out}
+
+
 def copy_calibration():
     """Three 256 MiB device-to-device copies through the library
     (mhip_d2d): the known-size kernel that scales the FETCH_SIZE and
@@ -380,6 +455,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the T=4096 layer measured beside the default workload")
+    ap.add_argument("--no-model", action="store_true",
+                    help="skip the whole-model step measured beside the default workload")
+    ap.add_argument("--only-model", action="store_true",
+                    help="only the whole-model step and the sampler timing")
     ap.add_argument("--cpu-layers", type=int, default=4)
     ap.add_argument("--cpu-tokens", type=int, default=512)
     ap.add_argument("--multi-kernel", action="store_true",
@@ -399,6 +478,10 @@ def main():
         sys.exit(1)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.only_model:
+        print(json.dumps({"model_decode": model_decode(args.steps, args.warmup),
+                          "sampler": sampler_timing()}))
         return
 
     res, moe = measure(args.workload, args.steps, args.warmup, args.multi_kernel)
@@ -420,6 +503,11 @@ def main():
         prefill = dict(pres["roofline"], workload="prefill4096: " + pres["wl"]["doc"],
                        layer_ms=pres["ms_step"], tokens_per_s=pres["tokens_per_s"],
                        intensity=pres["intensity"])
+
+    model = None
+    if args.workload == "decode48" and not args.no_model:
+        model = model_decode(32, 4)
+        model["sampler"] = sampler_timing()
 
     out = {
         "metric": METRIC,
@@ -452,6 +540,7 @@ def main():
                  "one launch per stage, expert products on the matrix cores" if matrix else
                  "one launch per stage"),
         "roofline_prefill4096": prefill,
+        "model_decode": model,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
