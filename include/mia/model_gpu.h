@@ -45,6 +45,20 @@ int mia_gpu_model_vocab(const mia_gpu_model *m);
  * device error. */
 const float *mia_gpu_model_step(mia_gpu_model *m, int token, int pos);
 
+/* The step without the output head: the KV cache of every layer gains the
+ * token's row, no logits are formed (a prompt position whose logits nobody
+ * reads, src/app/serve.c:91-106). 0 or -1. */
+int mia_gpu_model_feed(mia_gpu_model *m, int token, int pos);
+
+/* The token sampler (mhip_sample) on the logits of the last
+ * mia_gpu_model_step / _step_sample call, left on the device: the picked
+ * id, or -1 (also when the last call was a feed or failed). */
+int mia_gpu_model_sample(mia_gpu_model *m, mhip_sampler *s);
+
+/* The model's header fields (mia_file_probe's view of the file, or the
+ * shape mia_gpu_model_synth was given). */
+const mia_file_info *mia_gpu_model_info(const mia_gpu_model *m);
+
 /* The step followed by the token sampler on the device logits
  * (mhip_sample, src/tokenizer/sampler.c:33-66 of the reference; s->n must
  * be the vocabulary size): returns the picked token id, or -1. Only the id

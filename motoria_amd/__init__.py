@@ -197,8 +197,21 @@ SIGNATURES = {
     "mia_gpu_model_vocab": (_i, [_p]),
     "mia_gpu_model_step": (ctypes.POINTER(_f), [_p, _i, _i]),
     "mia_gpu_model_step_sample": (_i, [_p, _i, _i, ctypes.POINTER(Sampler)]),
+    "mia_gpu_model_feed": (_i, [_p, _i, _i]),
+    "mia_gpu_model_sample": (_i, [_p, ctypes.POINTER(Sampler)]),
+    "mia_gpu_model_info": (ctypes.POINTER(FileInfo), [_p]),
     "mia_gpu_model_set_flags": (None, [_p, _i]),
     "mia_gpu_model_aborts": (_i, [_p]),
+    # include/mia/serve.h
+    "mia_bpe_open": (_i, [ctypes.POINTER(_p), _p, _sz]),
+    "mia_bpe_close": (None, [_p]),
+    "mia_bpe_encode": (_i, [_p, ctypes.c_char_p, _p, _i]),
+    "mia_bpe_piece": (ctypes.POINTER(ctypes.c_ubyte), [_p, _i, ctypes.POINTER(_i)]),
+    "mia_bpe_is_stop": (_i, [_p, _i]),
+    "mia_bpe_vocab": (_i, [_p]),
+    "mia_bpe_im_start": (_i, [_p]),
+    "mia_chat_turn_text": (_p, [ctypes.c_char_p, _i, _i]),
+    "mia_serve": (_i, [ctypes.c_char_p, _i, _u64, _i, _p, _p]),
 }
 
 # The storage port type (include/mia/expert_cache.h).
@@ -525,6 +538,20 @@ class GpuModel:
                                lib().mia_gpu_model_error(self.h).decode())
         return r
 
+    def feed(self, token, pos):
+        """A prompt step without the output head."""
+        if lib().mia_gpu_model_feed(self.h, token, pos) != 0:
+            raise RuntimeError("mia_gpu_model_feed: " +
+                               lib().mia_gpu_model_error(self.h).decode())
+
+    def sample(self, sampler):
+        """The sampler on the last step's device logits."""
+        r = lib().mia_gpu_model_sample(self.h, ctypes.byref(sampler))
+        if r < 0:
+            raise RuntimeError("mia_gpu_model_sample: " +
+                               lib().mia_gpu_model_error(self.h).decode())
+        return r
+
     def step(self, token, pos):
         """Logits (a copy) of `token` at `pos`."""
         r = lib().mia_gpu_model_step(self.h, token, pos)
@@ -545,3 +572,61 @@ def sample_dev(gpu, s, d_logits, d_scratch, d_token):
     """mhip_sample on a Gpu context (queued; read d_token after a sync)."""
     gpu.check(lib().mhip_sample(gpu.h, ctypes.byref(s), d_logits, d_scratch, d_token),
               "mhip_sample")
+
+
+SERVE_PATH = os.path.join(_HERE, "mia-serve")
+
+
+class Bpe:
+    """mia_bpe (include/mia/serve.h): the MTK1 tokenizer of a .mia file."""
+
+    def __init__(self, blob):
+        self._blob = bytes(blob)
+        h = _p()
+        if lib().mia_bpe_open(ctypes.byref(h), self._blob, len(self._blob)) != 0:
+            raise ValueError("not a valid MTK1 blob")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().mia_bpe_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def encode(self, text, max_ids=1 << 16):
+        """Ids of `text` (str or UTF-8 bytes), or None when more than max_ids
+        would be needed."""
+        raw = text.encode() if isinstance(text, str) else text
+        out = np.zeros(max(max_ids, 1), np.int32)
+        n = lib().mia_bpe_encode(self.h, raw, out.ctypes.data, max_ids)
+        return None if n < 0 else out[:n].tolist()
+
+    def piece(self, i):
+        n = _i()
+        p = lib().mia_bpe_piece(self.h, i, ctypes.byref(n))
+        return ctypes.string_at(p, n.value)
+
+    def is_stop(self, i):
+        return bool(lib().mia_bpe_is_stop(self.h, i))
+
+    def vocab(self):
+        return lib().mia_bpe_vocab(self.h)
+
+    def im_start(self):
+        return lib().mia_bpe_im_start(self.h)
+
+
+def chat_turn_text(user, think, continuing):
+    """mia_chat_turn_text (freed here)."""
+    p = lib().mia_chat_turn_text(user.encode(), think, continuing)
+    if not p:
+        raise MemoryError("mia_chat_turn_text")
+    try:
+        return ctypes.string_at(p).decode()
+    finally:
+        ctypes.CDLL(None).free(ctypes.c_void_p(p))

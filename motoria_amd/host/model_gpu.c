@@ -34,6 +34,7 @@ struct mia_gpu_model {
     mia_moe_tensors mt;
     mhip_attn_dims ad;
     int max_seq, flags, decode_ok, aborts;
+    int logits_ok; /* d_logits holds the last step's logits */
     unsigned char *d_dense;
     mia_layer_offsets *lo;   /* [L] */
     uint64_t off_embd, off_onorm, off_out;
@@ -307,10 +308,12 @@ static int moe(mia_gpu_model *m, int l, int per_stage) {
 typedef struct {
     mhip_sampler *s; /* NULL: copy the logits */
     uint64_t rng;    /* s->rng before the step (a rerun draws again from it) */
+    int no_head;     /* a prompt position whose logits nobody reads */
 } step_tail;
 
 static int tail(mia_gpu_model *m, step_tail *t) {
     const mia_file_info *h = &m->info;
+    if (t->no_head) return 0;
     if (mhip_output_head(m->gpu, &m->ad, (const float *)(m->d_dense + m->off_onorm),
                          m->d_dense + m->off_out, (int)h->vocab, m->d_x, m->d_logits,
                          m->d_scratch, 0))
@@ -330,6 +333,7 @@ static int tail(mia_gpu_model *m, step_tail *t) {
 /* One step, then the tail; 0 or -1. */
 static int run_step(mia_gpu_model *m, int token, int pos, step_tail *t) {
     const mia_file_info *h = &m->info;
+    m->logits_ok = 0;
     const int L = (int)h->n_layers, d = (int)h->dim;
     if (pos < 0 || pos >= m->max_seq || token < 0 || token >= (int)h->vocab)
         return mfail(m, "token %d at position %d outside [0, %u) x [0, %d)", token, pos, h->vocab,
@@ -360,7 +364,10 @@ static int run_step(mia_gpu_model *m, int token, int pos, step_tail *t) {
             m->aborts++;
             if (first < 0) first = l;
         }
-    if (first < 0) return 0;
+    if (first < 0) {
+        m->logits_ok = !t->no_head;
+        return 0;
+    }
     if (mhip_d2d(m->gpu, m->d_x, m->d_xsave + (size_t)first * d, (size_t)d * 4))
         return mfail(m, "%s", mhip_error(m->gpu));
     if (moe(m, first, 1)) return -1;
@@ -368,17 +375,36 @@ static int run_step(mia_gpu_model *m, int token, int pos, step_tail *t) {
         if (attention(m, l, pos) || moe(m, l, 1)) return -1;
     if (tail(m, t)) return -1;
     if (mhip_sync(m->gpu)) return mfail(m, "%s", mhip_error(m->gpu));
+    m->logits_ok = !t->no_head;
     return 0;
 }
 
 const float *mia_gpu_model_step(mia_gpu_model *m, int token, int pos) {
-    step_tail t = {NULL, 0};
+    step_tail t = {NULL, 0, 0};
     return run_step(m, token, pos, &t) ? NULL : m->h_logits;
 }
 
+int mia_gpu_model_feed(mia_gpu_model *m, int token, int pos) {
+    step_tail t = {NULL, 0, 1};
+    return run_step(m, token, pos, &t);
+}
+
+int mia_gpu_model_sample(mia_gpu_model *m, mhip_sampler *s) {
+    if (!s) return mfail(m, "null sampler");
+    if (!m->logits_ok) return mfail(m, "no logits: the last call was not a step");
+    if (s->n != (int)m->info.vocab)
+        return mfail(m, "sampler over %d logits, the vocabulary has %u", s->n, m->info.vocab);
+    if (mhip_sample(m->gpu, s, m->d_logits, m->d_sample, m->d_token) ||
+        mhip_d2h_async(m->gpu, m->h_token, m->d_token, sizeof(int)) || mhip_sync(m->gpu))
+        return mfail(m, "%s", mhip_error(m->gpu));
+    return *m->h_token;
+}
+
+const mia_file_info *mia_gpu_model_info(const mia_gpu_model *m) { return &m->info; }
+
 int mia_gpu_model_step_sample(mia_gpu_model *m, int token, int pos, mhip_sampler *s) {
     if (!s) return mfail(m, "null sampler");
-    step_tail t = {s, s->rng};
+    step_tail t = {s, s->rng, 0};
     if (run_step(m, token, pos, &t)) {
         s->rng = t.rng;
         return -1;

@@ -181,3 +181,19 @@ int ref_sample(const float *logits, int n, float temperature, float top_p, uint6
     mia_sampler_free(&s);
     return 0;
 }
+
+/*
+ * The reference's own tokenizer (src/tokenizer/bpe.c) and chat template
+ * (src/model/runtime.c:84-95): ids of `text` under the MTK1 blob, or -1
+ * (load failure: -2).
+ */
+#include "mia/tokenizer.h"
+
+int ref_tok_encode(const unsigned char *blob, size_t n, const char *text, int *out, int max) {
+    mia_tokenizer t;
+    if (mia_tok_load(&t, blob, n) != 0) return -2;
+    const int r = mia_tok_encode(&t, text, out, max);
+    mia_tok_free(&t);
+    return r;
+}
+

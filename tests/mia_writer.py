@@ -102,7 +102,7 @@ def write(path, cfg, wtype, dense, expert_blob, tokenizer=b""):
 encode_q8 = None  # set by the caller: float32 values -> Q8_0 bytes (per 32-value block)
 
 
-def synthetic(O, path, cfg, wtype=Q8_0, seed=7):
+def synthetic(O, path, cfg, wtype=Q8_0, seed=7, tokenizer=b"tok"):
     """A synthetic model file: dense tensors ~ N(0, 0.02) from numpy's
     seeded generator (norms 1 + 0.1 N(0, 1); routers N(0, 0.16) so routing is
     decisive), Q8_0 matrices quantized with the oracle's quantizer, experts
@@ -133,7 +133,7 @@ def synthetic(O, path, cfg, wtype=Q8_0, seed=7):
             b[off:off + 4 * n] = (0.02 * rng.standard_normal(n)).astype(np.float32).view(np.uint8)
         return b
 
-    return write(path, cfg, wtype, dense, expert, tokenizer=b"tok")
+    return write(path, cfg, wtype, dense, expert, tokenizer=tokenizer)
 
 
 # A model with the attention shape of Qwen3-30B-A3B (dim 2048, 32 query and 4
@@ -204,3 +204,72 @@ class FileModel:
         c = self.cfg
         n = c["n_layers"] * max_seq * c["n_kv_heads"] * c["head_dim"]
         return np.zeros(n, np.float32), np.zeros(n, np.float32)
+
+
+# ---- MTK1 tokenizer blobs (the reader's format, src/tokenizer/bpe.c:35-95) --------
+
+NO_ID = 0xFFFFFFFF
+
+
+def mtk1_blob(pieces, merges=(), specials=(), eos=None, im_start=None, im_end=None):
+    """pieces: byte strings (id = index); merges: (a, b, result) in rank
+    order; specials: ids matched literally before pre-tokenization; eos /
+    im_start / im_end: ids or None."""
+    opt = lambda v: NO_ID if v is None else v  # noqa: E731
+    out = [b"MTK1", struct.pack("<6I", len(pieces), len(merges), len(specials), opt(eos),
+                                opt(im_start), opt(im_end))]
+    for p in pieces:
+        out.append(struct.pack("<H", len(p)) + p)
+    for a, b, r in merges:
+        out.append(struct.pack("<3I", a, b, r))
+    for s in specials:
+        out.append(struct.pack("<I", s))
+    return b"".join(out)
+
+
+def chat_tokenizer():
+    """The reference's serve test vocabulary (tools/e2e/serve_test.go:16-33):
+    ids 0..91 are '!'..'|', 92 space, 93 newline, 94 <|im_start|>,
+    95 <|im_end|>; no merges."""
+    pieces = [bytes([33 + i]) for i in range(92)] + [b" ", b"\n", b"<|im_start|>",
+                                                     b"<|im_end|>"]
+    return mtk1_blob(pieces, specials=(94, 95), im_start=94, im_end=95)
+
+
+def trained_tokenizer(corpus, n_merges, seed=0):
+    """A byte-level BPE vocabulary: the 256 bytes in a seeded order, then
+    n_merges merges trained greedily on `corpus` (most frequent adjacent
+    pair, ties to the smaller pair), plus three specials; a duplicate merge
+    pair and a duplicate single-byte piece exercise the reader's
+    first-wins rules."""
+    import random
+    rnd = random.Random(seed)
+    order = list(range(256))
+    rnd.shuffle(order)
+    pieces = [bytes([b]) for b in order]
+    byte_id = {b: i for i, b in enumerate(order)}
+    words = [[byte_id[c] for c in w.encode()] for w in corpus.split(" ") if w]
+    merges = []
+    for _ in range(n_merges):
+        counts = {}
+        for w in words:
+            for x, y in zip(w, w[1:]):
+                counts[(x, y)] = counts.get((x, y), 0) + 1
+        if not counts:
+            break
+        pair = min(counts, key=lambda k: (-counts[k], k))
+        new = len(pieces)
+        pieces.append(pieces[pair[0]] + pieces[pair[1]])
+        merges.append((pair[0], pair[1], new))
+        for w in words:
+            i = 0
+            while i + 1 < len(w):
+                if (w[i], w[i + 1]) == pair:
+                    w[i:i + 2] = [new]
+                i += 1
+    merges.append((merges[0][0], merges[0][1], merges[-1][2]))  # duplicate pair: rank 0 wins
+    pieces.append(pieces[0])                                     # duplicate byte: first id wins
+    base = len(pieces)
+    pieces += [b"<|endoftext|>", b"<|im_start|>", b"<|im_end|>"]
+    return mtk1_blob(pieces, merges, specials=(base, base + 1, base + 2), eos=base,
+                     im_start=base + 1, im_end=base + 2), len(pieces)

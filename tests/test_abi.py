@@ -9,7 +9,8 @@ import motoria_amd as M
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADERS = ["include/mia_hip.h", "include/mia/quant.h", "include/mia/matmul.h",
-           "include/mia/matvec_cache.h", "include/mia/moe.h", "include/mia/model_gpu.h"]
+           "include/mia/matvec_cache.h", "include/mia/moe.h", "include/mia/model_gpu.h",
+           "include/mia/serve.h"]
 
 
 def declared_functions():
