@@ -213,10 +213,12 @@ def gateup_bytes_matrix(n_touched, T, shape):
     return w + T * d * 2 + T * K * (d // 32) * 4 + T * K * eh * 2 + T * K * (eh // 32) * 4
 
 
-def measure(wl_name, steps, warmup, multi_kernel=False):
+def measure(wl_name, steps, warmup, multi_kernel=False, graph=True):
     """Times `steps` steps of one workload on a fresh handle (weights and x
     generated in HBM first). Returns (result dict, handle); the caller
-    closes the handle."""
+    closes the handle. A multi-kernel stack without a bias runs as one HIP
+    graph replay per step (graph=True), its dominant kernel then timed in a
+    separate eager pass."""
     wl = W.WORKLOADS[wl_name]
     shape = dict(W.SHAPE)
     L, T = wl["layers"], wl["tokens"]
@@ -238,8 +240,9 @@ def measure(wl_name, steps, warmup, multi_kernel=False):
     moe.synth_f32(d_x0, T * d, W.X_SEED, 1 << 40, 1.0)
 
     persistent = T == 1 and not multi_kernel
+    graphed = graph and not persistent and d_bias is None
 
-    def step():
+    def step(eager=False):
         if persistent:
             # decode: each step takes the previous step's output as its
             # token (K experts per layer whatever x is, so the bytes per step
@@ -247,7 +250,9 @@ def measure(wl_name, steps, warmup, multi_kernel=False):
             moe.decode_dev(0, L, d_x, d_bias)
             return
         M.lib().mhip_d2d(moe.gpu, d_x, d_x0, nbytes)
-        if d_bias is None:
+        if graphed and not eager:
+            moe.stack_graph(0, L, d_x, T)
+        elif d_bias is None:
             moe.stack_dev(0, L, d_x, T)
         else:
             for l in range(L):
@@ -269,7 +274,7 @@ def measure(wl_name, steps, warmup, multi_kernel=False):
     # the dominant kernel, so the two region events time it (launch gaps
     # included); per-launch events would add their own gaps to the step.
     dom = "decode" if persistent else "gateup"
-    moe.stage_timing([] if persistent else [dom], max_launches=L * steps + 16)
+    moe.stage_timing([] if persistent or graphed else [dom], max_launches=L * steps + 16)
     moe.sync()
     t0 = time.perf_counter()
     moe.mark(0)
@@ -279,13 +284,19 @@ def measure(wl_name, steps, warmup, multi_kernel=False):
     moe.sync()
     t1 = time.perf_counter()
     ev_ms = moe.elapsed_ms(0, 1)
+    if graphed:
+        # the dominant kernel's launches, bracketed by events in eager steps
+        moe.stage_timing([dom], max_launches=L * steps + 16)
+        for _ in range(steps):
+            step(eager=True)
+        moe.sync()
     stage = {dom: (ev_ms, steps) if persistent else moe.stage_time(dom)}
     dstat = moe.decode_status() if persistent else None
     # Untimed diagnostic pass: every stage bracketed by events.
     diag_steps = min(steps, 5)
     moe.stage_timing(M.STAGES, max_launches=len(M.STAGES) * L * diag_steps + 16)
     for _ in range(diag_steps):
-        step()
+        step(eager=True)
     moe.sync()
     diag = {st: moe.stage_time(st) for st in M.STAGES}
     moe.stage_timing([], 0)
@@ -348,7 +359,7 @@ def measure(wl_name, steps, warmup, multi_kernel=False):
         "warmup": warmup, "ms_step": ms_step, "tokens_per_s": tokens_per_s,
         "step_bytes": step_bytes, "step_ops": step_ops, "hbm_gbs": hbm_gbs,
         "intensity": ai, "touched": touched, "roofline": roof, "persistent": persistent,
-        "matrix": matrix,
+        "matrix": matrix, "graphed": graphed,
     }
     return res, moe
 
@@ -464,6 +475,8 @@ def main():
     ap.add_argument("--multi-kernel", action="store_true",
                     help="batch-1 workloads: one launch per stage instead of the "
                          "persistent decode kernel")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="multi-kernel stacks: eager launches instead of one HIP graph per step")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three 256 MiB device copies (counter calibration)")
     args = ap.parse_args()
@@ -484,7 +497,8 @@ def main():
                           "sampler": sampler_timing()}))
         return
 
-    res, moe = measure(args.workload, args.steps, args.warmup, args.multi_kernel)
+    res, moe = measure(args.workload, args.steps, args.warmup, args.multi_kernel,
+                       graph=not args.no_graph)
     wl, shape, persistent, matrix = res["wl"], res["shape"], res["persistent"], res["matrix"]
     cpu = None
     if not args.no_cpu:
@@ -537,8 +551,9 @@ def main():
                 "intensity_op_per_byte": res["intensity"]},
         "roofline": res["roofline"],
         "path": ("persistent decode kernel" if persistent else
-                 "one launch per stage, expert products on the matrix cores" if matrix else
-                 "one launch per stage"),
+                 ("one launch per stage, expert products on the matrix cores" if matrix else
+                  "one launch per stage") + ("; the stack replayed as one HIP graph per step"
+                                             if res["graphed"] else "")),
         "roofline_prefill4096": prefill,
         "model_decode": model,
         "cpu_baseline": cpu,

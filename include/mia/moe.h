@@ -121,6 +121,12 @@ int mia_moe_stack(mia_moe *m, int l0, int l1, float *x, int T);
  * queued on the handle's stream and returns before it completes. */
 int mia_moe_layer_dev(mia_moe *m, int layer, float *d_x, int T, const float *d_bias);
 int mia_moe_stack_dev(mia_moe *m, int l0, int l1, float *d_x, int T);
+/* mia_moe_stack_dev as one HIP graph (no counterpart in the reference): the
+ * first call records the stack's launches (kernel nodes only) and every call
+ * replays them as one submission; a call with other arguments (or after
+ * mia_moe_set_flags) records again. The recording holds d_x: replays read
+ * and write that buffer. Results are bit-identical to mia_moe_stack_dev's. */
+int mia_moe_stack_graph(mia_moe *m, int l0, int l1, float *d_x, int T);
 
 /* Decode of one token through layers [l0, l1) in a single persistent launch
  * (the Qwen3-30B-A3B shape on a 256-CU MI355X; mhip_decode_stack). x[dim]

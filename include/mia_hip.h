@@ -256,7 +256,8 @@ typedef struct {
 
 size_t mhip_attention_scratch_bytes(const mhip_attn_dims *s, int max_seq);
 /* Attention of the token at `pos` for one layer, in place on d_x[dim]
- * (x += Wo attention(rmsnorm(x))). d_kc/d_vc: this layer's K and V cache,
+ * (x += Wo attention(rmsnorm(x))); d_x_copy, when not NULL, receives the
+ * new x too. d_kc/d_vc: this layer's K and V cache,
  * [max_seq][n_kv_heads*head_dim] fp32; row pos is written, rows < pos read.
  * d_rope: [max_seq][head_dim/2][2] doubles, cos and sin of
  * pos * theta^(-2i/head_dim) as the host libm gives them (the reference's
@@ -265,12 +266,28 @@ int mhip_attention(mhip_ctx *c, const mhip_attn_dims *s, const float *d_attn_nor
                    const void *d_wq, const void *d_wk, const void *d_wv, const void *d_wo,
                    const float *d_q_norm, const float *d_k_norm, const double *d_rope,
                    float *d_kc, float *d_vc, int pos, int max_seq, float *d_x,
-                   void *d_scratch, int flags);
+                   float *d_x_copy, void *d_scratch, int flags);
 /* logits[vocab] = output Q8(rmsnorm(x, output_norm)) (forward.c:214-215);
  * d_scratch as for mhip_attention. */
 int mhip_output_head(mhip_ctx *c, const mhip_attn_dims *s, const float *d_output_norm,
                      const void *d_output, int vocab, const float *d_x, float *d_logits,
                      void *d_scratch, int flags);
+
+/* ---- HIP graphs -----------------------------------------------------------
+ * No counterpart in the reference. The launches queued on a context between
+ * mhip_graph_begin and mhip_graph_end are recorded (not run) into a graph,
+ * which mhip_graph_launch replays on the context's stream as one
+ * submission. Only kernel launches and device-to-device copies may be
+ * queued meanwhile (the library's clears are fill kernels; stage-timing
+ * events are skipped while capturing); a call that waits for the device
+ * fails the capture. The graph replays the recorded arguments: the same
+ * pointers, shapes and flags. mhip_graph_end(c, NULL) ends a capture and
+ * drops it (also after an error inside it). */
+typedef struct mhip_graph mhip_graph;
+int mhip_graph_begin(mhip_ctx *c);
+int mhip_graph_end(mhip_ctx *c, mhip_graph **out);
+int mhip_graph_launch(mhip_ctx *c, mhip_graph *g);
+void mhip_graph_destroy(mhip_graph *g);
 
 /* ---- token sampler on device logits -------------------------------------
  * src/tokenizer/sampler.c of the reference: mhip_sampler is mia_sampler

@@ -140,8 +140,12 @@ SIGNATURES = {
     "mhip_decode_trace": (_i, [_p, _p, _p]),
     "mhip_attention_scratch_bytes": (_sz, [ctypes.POINTER(AttnDims), _i]),
     "mhip_attention": (_i, [_p, ctypes.POINTER(AttnDims), _p, _p, _p, _p, _p, _p, _p, _p, _p,
-                            _p, _i, _i, _p, _p, _i]),
+                            _p, _i, _i, _p, _p, _p, _i]),
     "mhip_output_head": (_i, [_p, ctypes.POINTER(AttnDims), _p, _p, _i, _p, _p, _p, _i]),
+    "mhip_graph_begin": (_i, [_p]),
+    "mhip_graph_end": (_i, [_p, ctypes.POINTER(_p)]),
+    "mhip_graph_launch": (_i, [_p, _p]),
+    "mhip_graph_destroy": (None, [_p]),
     "mhip_sampler_init": (None, [ctypes.POINTER(Sampler), _f, _f, _i, _u64]),
     "mhip_sample_scratch_bytes": (_sz, [_i]),
     "mhip_sample": (_i, [_p, ctypes.POINTER(Sampler), _p, _p, _p]),
@@ -174,6 +178,7 @@ SIGNATURES = {
     "mia_moe_stack": (_i, [_p, _i, _i, _p, _i]),
     "mia_moe_layer_dev": (_i, [_p, _i, _p, _i, _p]),
     "mia_moe_stack_dev": (_i, [_p, _i, _i, _p, _i]),
+    "mia_moe_stack_graph": (_i, [_p, _i, _i, _p, _i]),
     "mia_file_probe": (_i, [ctypes.c_char_p, ctypes.POINTER(FileInfo), ctypes.c_char_p, _sz]),
     "mia_file_layer_offsets": (_i, [ctypes.POINTER(FileInfo), _i,
                                     ctypes.POINTER(ctypes.c_uint64),
@@ -357,6 +362,9 @@ class Moe:
 
     def stack_dev(self, l0, l1, d_x, T):
         self._check(lib().mia_moe_stack_dev(self.h, l0, l1, d_x, T), "mia_moe_stack_dev")
+
+    def stack_graph(self, l0, l1, d_x, T):
+        self._check(lib().mia_moe_stack_graph(self.h, l0, l1, d_x, T), "mia_moe_stack_graph")
 
     def decode(self, l0, l1, x, bias=None):
         """One token through layers [l0, l1) in one persistent launch.

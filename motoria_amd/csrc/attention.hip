@@ -25,15 +25,24 @@ constexpr int MAXNB = 256;  // blocks per row the row kernel holds (dims up to 8
 // (36-byte blocks) with the activation's codes xq[nb*32] and scales xs[nb]
 // (src/tensor/matmul.c:19-28): one wavefront per row, lane b computes the
 // block terms of blocks b, b + 64, ..., then lane 0 adds them in block order.
-__global__ __launch_bounds__(256) void k_rows_q8(const uint8_t *__restrict__ w, int rows, int nb,
-                                                 const int8_t *__restrict__ xq,
-                                                 const float *__restrict__ xs,
-                                                 const float *resid, float *out) {
+// Up to three matrices in one launch (rows of segment k: [r0[k], r0[k+1]),
+// weights w[k], output out[k]); copy, when set, receives out[0] too.
+struct RowSegs {
+    const uint8_t *w[3];
+    float *out[3];
+    int r0[4];
+};
+
+__global__ __launch_bounds__(256) void k_rows_q8(RowSegs sg, int nb, const int8_t *__restrict__ xq,
+                                                 const float *__restrict__ xs, const float *resid,
+                                                 float *copy) {
     __shared__ float terms[4][MAXNB];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r = blockIdx.x * 4 + wave;
-    if (r >= rows) return;
-    const uint8_t *wr = w + (size_t)r * nb * 36;
+    const int row = blockIdx.x * 4 + wave;
+    if (row >= sg.r0[3]) return;
+    const int k = row >= sg.r0[1] ? (row >= sg.r0[2] ? 2 : 1) : 0;
+    const int r = row - sg.r0[k];
+    const uint8_t *wr = sg.w[k] + (size_t)r * nb * 36;
     for (int b = lane; b < nb; b += 64) {
         const uint32_t *blk = (const uint32_t *)(wr + (size_t)b * 36);
         const float dw = __uint_as_float(blk[0]);
@@ -48,8 +57,15 @@ __global__ __launch_bounds__(256) void k_rows_q8(const uint8_t *__restrict__ w, 
     if (lane == 0) {
         float s = 0.0f;
         for (int b = 0; b < nb; b++) s = s + terms[wave][b];
-        out[r] = resid ? resid[r] + s : s;
+        const float o = resid ? resid[r] + s : s;
+        sg.out[k][r] = o;
+        if (copy && k == 0) copy[r] = o;
     }
+}
+
+RowSegs one_seg(const void *w, float *out, int rows) {
+    RowSegs g = {{(const uint8_t *)w, nullptr, nullptr}, {out, nullptr, nullptr}, {0, rows, rows, rows}};
+    return g;
 }
 
 // Q8_0 of a row of n values into codes and scales (src/tensor/quant.c:11-27),
@@ -181,6 +197,117 @@ __global__ __launch_bounds__(256) void k_attn_mix(float *__restrict__ scores, in
     }
 }
 
+// One query head per workgroup, the whole of forward.c:127-163 for it:
+// the head's rmsnorm and RoPE of q and of its key head's k (every head of a
+// group recomputes that k; the group's first head appends k and v to the
+// cache), the scores of positions 0..pos against the cache (position pos
+// from the fresh k), softmax, the position-ordered mix, and Q8 of the
+// head's att values (head_dim % 32 == 0: its blocks lie inside the head).
+// The arithmetic of k_qk_rope, k_attn_scores, k_attn_mix and k_quant_rows,
+// in the same order. LDS: q, k, the scores [max_seq] after them.
+__device__ __forceinline__ void head_norm_rope(const float *src, const float *w, const double *rp,
+                                               int hd, float eps, float *dst, float *tmp,
+                                               float *inv_sh) {
+    const int tid = threadIdx.x;
+    for (int i = tid; i < hd; i += blockDim.x) tmp[i] = src[i];
+    __syncthreads();
+    if (tid == 0) {
+        double ss = 0.0;
+        for (int i = 0; i < hd; i++) ss = ss + (double)tmp[i] * (double)tmp[i];
+        *inv_sh = (float)(1.0 / sqrt(ss / hd + (double)eps));
+    }
+    __syncthreads();
+    const float inv = *inv_sh;
+    const int half = hd / 2;
+    for (int i = tid; i < half; i += blockDim.x) {
+        const float x0 = (tmp[i] * inv) * w[i];
+        const float x1 = (tmp[i + half] * inv) * w[i + half];
+        const double c = rp[2 * i], sn = rp[2 * i + 1];
+        dst[i] = (float)((double)x0 * c - (double)x1 * sn);
+        dst[i + half] = (float)((double)x0 * sn + (double)x1 * c);
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void k_attn_head(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    const float *__restrict__ q_norm, const float *__restrict__ k_norm,
+    const double *__restrict__ rope, int pos, int nh, int nkv, int hd, float eps, float scale,
+    float *__restrict__ kc, float *__restrict__ vc, int8_t *__restrict__ attq,
+    float *__restrict__ atts) {
+    extern __shared__ float lds[];
+    __shared__ float red[256];
+    __shared__ float inv_sh, sum_sh;
+    __shared__ uint64_t etab[32];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int group = nh / nkv, g = h / group, kvd = nkv * hd, n = pos + 1;
+    float *qs = lds, *ks = lds + hd, *tmp = lds + 2 * hd, *sc = lds + 3 * hd;
+    if (tid < 32) etab[tid] = mia_expf_tab[tid];
+    const double *rp = rope + (size_t)pos * (hd / 2) * 2;
+    head_norm_rope(q + (size_t)h * hd, q_norm, rp, hd, eps, qs, tmp, &inv_sh);
+    head_norm_rope(k + (size_t)g * hd, k_norm, rp, hd, eps, ks, tmp, &inv_sh);
+    if (h % group == 0)
+        for (int i = tid; i < hd; i += blockDim.x) {
+            kc[(size_t)pos * kvd + (size_t)g * hd + i] = ks[i];
+            vc[(size_t)pos * kvd + (size_t)g * hd + i] = v[(size_t)g * hd + i];
+        }
+    // scores (forward.c:143-149): sequential fp32 dots, one position per thread
+    for (int t = tid; t < n; t += blockDim.x) {
+        const float *kt = t == pos ? ks : kc + (size_t)t * kvd + (size_t)g * hd;
+        float dot = 0.0f;
+        for (int i = 0; i < hd; i += 4) {
+            const float4 k4 = *(const float4 *)(kt + i);
+            dot = dot + qs[i] * k4.x;
+            dot = dot + qs[i + 1] * k4.y;
+            dot = dot + qs[i + 2] * k4.z;
+            dot = dot + qs[i + 3] * k4.w;
+        }
+        sc[t] = dot * scale;
+    }
+    __syncthreads();
+    // softmax (forward.c:150-156): the maximum (order-free), the restated
+    // expf, the sequential sum, the division
+    float mx = -__builtin_inff();
+    for (int t = tid; t < n; t += blockDim.x) mx = fmaxf(mx, sc[t]);
+    red[tid] = mx;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) red[tid] = fmaxf(red[tid], red[tid + o]);
+        __syncthreads();
+    }
+    mx = red[0];
+    for (int t = tid; t < n; t += blockDim.x) sc[t] = mia_expf_glibc_tab(sc[t] - mx, etab);
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+        for (int t = 0; t < n; t++) sum = sum + sc[t];
+        sum_sh = sum;
+    }
+    __syncthreads();
+    const float sum = sum_sh;
+    for (int t = tid; t < n; t += blockDim.x) sc[t] = sc[t] / sum;
+    __syncthreads();
+    // mix (forward.c:157-162), then Q8 of the head's att (quant.c:11-27)
+    float o = 0.0f;
+    if (tid < hd) {
+        const float *vt = vc + (size_t)g * hd + tid;
+        for (int t = 0; t < pos; t++) o = o + sc[t] * vt[(size_t)t * kvd];
+        o = o + sc[pos] * v[(size_t)g * hd + tid];
+        // the block's maximum by a 32-lane butterfly (order-free; from 0,
+        // a NaN never wins, as in the sequential loop)
+        float am = fmaxf(0.0f, fabsf(o));
+#pragma unroll
+        for (int m = 16; m >= 1; m >>= 1) am = fmaxf(am, __shfl_xor(am, m, 32));
+        const float d = am / 127.0f;
+        const float qi = d != 0.0f ? 1.0f / d : 0.0f;
+        attq[(size_t)h * hd + tid] = (int8_t)roundf(o * qi);
+        if ((lane & 31) == 0) atts[((size_t)h * hd + tid) / QK] = d;
+    }
+}
+
+constexpr size_t HEAD_LDS_MAX = 150 * 1024;  // dynamic LDS of k_attn_head
+size_t head_lds(int hd, int max_seq) { return ((size_t)3 * hd + (size_t)max_seq) * sizeof(float); }
+
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
 struct AttnScratch {
@@ -241,7 +368,7 @@ int mhip_attention(mhip_ctx *c, const mhip_attn_dims *s, const float *d_attn_nor
                    const void *d_wq, const void *d_wk, const void *d_wv, const void *d_wo,
                    const float *d_q_norm, const float *d_k_norm, const double *d_rope,
                    float *d_kc, float *d_vc, int pos, int max_seq, float *d_x,
-                   void *d_scratch, int flags) {
+                   float *d_x_copy, void *d_scratch, int flags) {
     if (check_attn(c, s, max_seq)) return -1;
     if (pos < 0 || pos >= max_seq)
         return mhip::fail(c, "attention: pos=%d outside [0, max_seq=%d)", pos, max_seq);
@@ -253,23 +380,38 @@ int mhip_attention(mhip_ctx *c, const mhip_attn_dims *s, const float *d_attn_nor
     mhip::launch_rmsnorm_q8(st, d_x, d_attn_norm, a.xn, a.xq, a.xs, 1, d, s->norm_eps,
                             (flags & MHIP_FORCE_SEQ_RMS) ? 1 : 0, a.status);
     const int nb = d / QK;
-    k_rows_q8<<<mhip::blocks_for(qd, 4), 256, 0, st>>>((const uint8_t *)d_wq, qd, nb, a.xq, a.xs,
-                                                        nullptr, a.q);
-    k_rows_q8<<<mhip::blocks_for(kvd, 4), 256, 0, st>>>((const uint8_t *)d_wk, kvd, nb, a.xq,
-                                                         a.xs, nullptr, a.k);
-    k_rows_q8<<<mhip::blocks_for(kvd, 4), 256, 0, st>>>((const uint8_t *)d_wv, kvd, nb, a.xq,
-                                                         a.xs, nullptr, a.v);
+    RowSegs qkv = {{(const uint8_t *)d_wq, (const uint8_t *)d_wk, (const uint8_t *)d_wv},
+                   {a.q, a.k, a.v},
+                   {0, qd, qd + kvd, qd + 2 * kvd}};
+    k_rows_q8<<<mhip::blocks_for(qd + 2 * kvd, 4), 256, 0, st>>>(qkv, nb, a.xq, a.xs, nullptr,
+                                                                  nullptr);
     if (mhip::check_launch(c, "attention qkv")) return -1;
-    k_qk_rope<<<mhip::blocks_for(nh + 2 * nkv, 4), 256, 0, st>>>(
-        a.q, a.k, a.v, d_q_norm, d_k_norm, d_rope, pos, nh, nkv, hd, s->norm_eps,
-        d_kc + (size_t)pos * kvd, d_vc + (size_t)pos * kvd);
     const float scale = 1.0f / sqrtf((float)hd);
-    k_attn_scores<<<mhip::blocks_for((size_t)nh * n, 256), 256, 0, st>>>(
-        a.q, d_kc, n, nh, nh / nkv, hd, kvd, scale, a.scores, max_seq);
-    k_attn_mix<<<nh, 256, 0, st>>>(a.scores, max_seq, n, d_vc, nh / nkv, hd, kvd, a.att);
-    k_quant_rows<<<mhip::blocks_for(qd / QK, 256), 256, 0, st>>>(a.att, qd / QK, a.attq, a.atts);
-    k_rows_q8<<<mhip::blocks_for(d, 4), 256, 0, st>>>((const uint8_t *)d_wo, d, qd / QK, a.attq,
-                                                       a.atts, d_x, d_x);
+    const size_t hl = head_lds(hd, max_seq);
+    if (hd % QK == 0 && hl <= HEAD_LDS_MAX) {
+        static int lds_set[64];  // per device ordinal (contexts of one device share it)
+        if (c->device >= 0 && c->device < 64 && !lds_set[c->device]) {
+            if (mhip::check(c, hipFuncSetAttribute((const void *)k_attn_head,
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   (int)HEAD_LDS_MAX),
+                            "attention LDS attribute"))
+                return -1;
+            lds_set[c->device] = 1;
+        }
+        k_attn_head<<<nh, 256, hl, st>>>(a.q, a.k, a.v, d_q_norm, d_k_norm, d_rope, pos, nh, nkv,
+                                         hd, s->norm_eps, scale, d_kc, d_vc, a.attq, a.atts);
+    } else {
+        k_qk_rope<<<mhip::blocks_for(nh + 2 * nkv, 4), 256, 0, st>>>(
+            a.q, a.k, a.v, d_q_norm, d_k_norm, d_rope, pos, nh, nkv, hd, s->norm_eps,
+            d_kc + (size_t)pos * kvd, d_vc + (size_t)pos * kvd);
+        k_attn_scores<<<mhip::blocks_for((size_t)nh * n, 256), 256, 0, st>>>(
+            a.q, d_kc, n, nh, nh / nkv, hd, kvd, scale, a.scores, max_seq);
+        k_attn_mix<<<nh, 256, 0, st>>>(a.scores, max_seq, n, d_vc, nh / nkv, hd, kvd, a.att);
+        k_quant_rows<<<mhip::blocks_for(qd / QK, 256), 256, 0, st>>>(a.att, qd / QK, a.attq,
+                                                                      a.atts);
+    }
+    k_rows_q8<<<mhip::blocks_for(d, 4), 256, 0, st>>>(one_seg(d_wo, d_x, d), qd / QK, a.attq,
+                                                       a.atts, d_x, d_x_copy);
     return mhip::check_launch(c, "attention");
 }
 
@@ -284,7 +426,7 @@ int mhip_output_head(mhip_ctx *c, const mhip_attn_dims *s, const float *d_output
     mhip::launch_rmsnorm_q8(c->stream, d_x, d_output_norm, a.xn, a.xq, a.xs, 1, d, s->norm_eps,
                             (flags & MHIP_FORCE_SEQ_RMS) ? 1 : 0, a.status);
     k_rows_q8<<<mhip::blocks_for(vocab, 4), 256, 0, c->stream>>>(
-        (const uint8_t *)d_output, vocab, d / QK, a.xq, a.xs, nullptr, d_logits);
+        one_seg(d_output, d_logits, vocab), d / QK, a.xq, a.xs, nullptr, nullptr);
     return mhip::check_launch(c, "output head");
 }
 

@@ -44,7 +44,7 @@ int check_dims(mhip_ctx *c, const mhip_dims *s) {
 }
 
 int stage_begin(mhip_ctx *c, int stage) {
-    if (!(c->st_mask & (1u << stage)) || c->st_n >= c->st_cap) return -1;
+    if (c->capturing || !(c->st_mask & (1u << stage)) || c->st_n >= c->st_cap) return -1;
     const int slot = c->st_n++;
     c->st_stage[slot] = stage;
     (void)hipEventRecord(c->st_ev[2 * slot], c->stream);
@@ -280,6 +280,69 @@ int mhip_elapsed(mhip_ctx *c, int slot0, int slot1, float *ms) {
     if (mhip::check(c, hipEventSynchronize(c->marks[slot1]), "hipEventSynchronize")) return -1;
     return mhip::check(c, hipEventElapsedTime(ms, c->marks[slot0], c->marks[slot1]),
                        "hipEventElapsedTime");
+}
+
+}  // extern "C"
+
+// ---- HIP graphs ---------------------------------------------------------------
+
+struct mhip_graph {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+extern "C" {
+
+int mhip_graph_begin(mhip_ctx *c) {
+    if (c->capturing) return mhip::fail(c, "a capture is already open on this context");
+    if (mhip::use_device(c)) return -1;
+    if (mhip::check(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal),
+                    "hipStreamBeginCapture"))
+        return -1;
+    c->capturing = 1;
+    return 0;
+}
+
+int mhip_graph_end(mhip_ctx *c, mhip_graph **out) {
+    if (out) *out = nullptr;
+    if (!c->capturing) return mhip::fail(c, "no capture is open on this context");
+    c->capturing = 0;
+    hipGraph_t g = nullptr;
+    if (mhip::check(c, hipStreamEndCapture(c->stream, &g), "hipStreamEndCapture")) {
+        if (g) (void)hipGraphDestroy(g);
+        return -1;
+    }
+    if (!out) {  // the caller abandons the capture
+        (void)hipGraphDestroy(g);
+        return 0;
+    }
+    mhip_graph *r = (mhip_graph *)calloc(1, sizeof(mhip_graph));
+    if (!r) {
+        (void)hipGraphDestroy(g);
+        return mhip::fail(c, "out of host memory");
+    }
+    r->graph = g;
+    if (mhip::check(c, hipGraphInstantiate(&r->exec, g, nullptr, nullptr, 0),
+                    "hipGraphInstantiate")) {
+        (void)hipGraphDestroy(g);
+        free(r);
+        return -1;
+    }
+    *out = r;
+    return 0;
+}
+
+int mhip_graph_launch(mhip_ctx *c, mhip_graph *g) {
+    if (!g) return mhip::fail(c, "null graph");
+    if (mhip::use_device(c)) return -1;
+    return mhip::check(c, hipGraphLaunch(g->exec, c->stream), "hipGraphLaunch");
+}
+
+void mhip_graph_destroy(mhip_graph *g) {
+    if (!g) return;
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    free(g);
 }
 
 }  // extern "C"

@@ -22,6 +22,7 @@ struct mhip_ctx {
     const void *decode_ws;  // workspace those tags were written to
     int decode_checked;           // 0 unknown, 1 the decode launch fits the device, 2 it does not
     int decode_cus, decode_occ;   // the CU count and occupancy that check found
+    int capturing;                // between mhip_graph_begin and mhip_graph_end
     char err[512];
 };
 

@@ -431,6 +431,7 @@ __global__ __launch_bounds__(256, 2) void k_router_logits_wide(const float *__re
     // chunks in flight in registers: a chunk's compute shrinks with CPL, so
     // fewer chains per lane prefetch further ahead
     constexpr int NP = 4 / CPL;
+    constexpr int BI = 32;  // one chain per lane: values of i read from LDS per batch
     __shared__ __align__(16) float Xs[2][RW_T][RW_LD];
     __shared__ __align__(16) V Ws[2][4][RW_I];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -477,17 +478,39 @@ __global__ __launch_bounds__(256, 2) void k_router_logits_wide(const float *__re
             const int c = ch + u;
             if (c >= nch) break;
             const int b = c & 1;
+            if constexpr (CPL == 1) {
+                // one chain per lane: BI values of i at a time, all their LDS
+                // reads first (one wait), then the additions back to back
+#pragma unroll
+                for (int ii = 0; ii < RW_I; ii += BI) {
+                    float x[BI];
+                    V w[BI];
+#pragma unroll
+                    for (int j = 0; j < BI; j += 4) {
+                        const float4 x4 = *(const float4 *)&Xs[b][lane][ii + j];
+                        x[j] = x4.x;
+                        x[j + 1] = x4.y;
+                        x[j + 2] = x4.z;
+                        x[j + 3] = x4.w;
+                    }
+#pragma unroll
+                    for (int j = 0; j < BI; j++) w[j] = Ws[b][wave][ii + j];
+#pragma unroll
+                    for (int j = 0; j < BI; j++) s[0] = s[0] + w[j].v[0] * x[j];
+                }
+            } else {
 #pragma unroll 4
-            for (int ii = 0; ii < RW_I; ii += 4) {
-                const float4 x4 = *(const float4 *)&Xs[b][lane][ii];
-                const float x[4] = {x4.x, x4.y, x4.z, x4.w};
-                V w[4];
+                for (int ii = 0; ii < RW_I; ii += 4) {
+                    const float4 x4 = *(const float4 *)&Xs[b][lane][ii];
+                    const float x[4] = {x4.x, x4.y, x4.z, x4.w};
+                    V w[4];
 #pragma unroll
-                for (int j = 0; j < 4; j++) w[j] = Ws[b][wave][ii + j];
+                    for (int j = 0; j < 4; j++) w[j] = Ws[b][wave][ii + j];
 #pragma unroll
-                for (int j = 0; j < 4; j++)
+                    for (int j = 0; j < 4; j++)
 #pragma unroll
-                    for (int k = 0; k < CPL; k++) s[k] = s[k] + w[j].v[k] * x[j];
+                        for (int k = 0; k < CPL; k++) s[k] = s[k] + w[j].v[k] * x[j];
+                }
             }
             // buffer b ^ 1 was last read in chunk c - 1, before the barrier
             // that ended it; slot (u + 1) % NP then takes chunk c + 1 + NP

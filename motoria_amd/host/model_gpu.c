@@ -266,8 +266,9 @@ int mia_gpu_model_synth(mia_gpu_model **out, const mia_file_info *shape, int max
     return finish(m, rc, out, err, errlen);
 }
 
-/* Queues the attention of layer l at pos. */
-static int attention(mia_gpu_model *m, int l, int pos) {
+/* Queues the attention of layer l at pos (and, with save, the copy of the
+ * new x that an aborted MoE launch of the layer restarts from). */
+static int attention(mia_gpu_model *m, int l, int pos, int save) {
     const size_t kvd = (size_t)m->info.n_kv_heads * m->info.head_dim;
     const mia_layer_offsets *o = &m->lo[l];
     const unsigned char *b = m->d_dense;
@@ -275,7 +276,7 @@ static int attention(mia_gpu_model *m, int l, int pos) {
     if (mhip_attention(m->gpu, &m->ad, (const float *)(b + o->attn_norm), b + o->wq, b + o->wk,
                        b + o->wv, b + o->wo, (const float *)(b + o->q_norm),
                        (const float *)(b + o->k_norm), m->d_rope, kc, vc, pos, m->max_seq, m->d_x,
-                       m->d_scratch, 0))
+                       save ? m->d_xsave + (size_t)l * m->info.dim : NULL, m->d_scratch, 0))
         return mfail(m, "%s", mhip_error(m->gpu));
     return 0;
 }
@@ -346,9 +347,7 @@ static int run_step(mia_gpu_model *m, int token, int pos, step_tail *t) {
     if (mhip_dequantize_q8(m->gpu, m->d_dense + m->off_embd + (size_t)token * row, m->d_x, d))
         return mfail(m, "%s", mhip_error(m->gpu));
     for (int l = 0; l < L; l++) {
-        if (attention(m, l, pos) ||
-            (decode && mhip_d2d(m->gpu, m->d_xsave + (size_t)l * d, m->d_x, (size_t)d * 4)) ||
-            moe(m, l, 0))
+        if (attention(m, l, pos, decode) || moe(m, l, 0))
             return -1;
     }
     /* the tail is queued before the decode launches' status is known: one
@@ -372,7 +371,7 @@ static int run_step(mia_gpu_model *m, int token, int pos, step_tail *t) {
         return mfail(m, "%s", mhip_error(m->gpu));
     if (moe(m, first, 1)) return -1;
     for (int l = first + 1; l < L; l++)
-        if (attention(m, l, pos) || moe(m, l, 1)) return -1;
+        if (attention(m, l, pos, 0) || moe(m, l, 1)) return -1;
     if (tail(m, t)) return -1;
     if (mhip_sync(m->gpu)) return mfail(m, "%s", mhip_error(m->gpu));
     m->logits_ok = !t->no_head;

@@ -33,6 +33,9 @@ struct mia_moe {
     float *d_bias;      /* [E] */
     void *d_blob;       /* one .mia blob */
     unsigned char *h_blob;
+    mhip_graph *graph; /* mia_moe_stack_graph's recording ... */
+    int g_l0, g_l1, g_T, g_flags;
+    float *g_x;         /* ... and the arguments it was recorded with */
     char err[512];
 };
 
@@ -79,6 +82,7 @@ void mia_moe_close(mia_moe *m) {
     if (!m) return;
     if (m->gpu) {
         mhip_sync(m->gpu);
+        mhip_graph_destroy(m->graph);
         mhip_free(m->gpu, m->d_table);
         mhip_free(m->gpu, m->d_router_t);
         mhip_free(m->gpu, m->d_router_dl);
@@ -267,6 +271,31 @@ int mia_moe_stack_dev(mia_moe *m, int l0, int l1, float *d_x, int T) {
     if (clear_status(m)) return -1;
     for (int l = l0; l < l1; l++)
         if (run_layer(m, l, d_x, T, NULL)) return -1;
+    return 0;
+}
+
+int mia_moe_stack_graph(mia_moe *m, int l0, int l1, float *d_x, int T) {
+    if (l0 < 0 || l1 > m->n_layers || l0 > l1)
+        return fail(m, "layer range [%d, %d) outside [0, %d)", l0, l1, m->n_layers);
+    if (T < 0 || T > m->max_tokens)
+        return fail(m, "T=%d outside [0, max_tokens=%d]", T, m->max_tokens);
+    if (!m->graph || m->g_l0 != l0 || m->g_l1 != l1 || m->g_x != d_x || m->g_T != T ||
+        m->g_flags != m->flags) {
+        mhip_graph_destroy(m->graph);
+        m->graph = NULL;
+        if (mhip_graph_begin(m->gpu)) return gpu_fail(m);
+        const int rc = mia_moe_stack_dev(m, l0, l1, d_x, T);
+        char why[512];
+        snprintf(why, sizeof why, "%s", m->err);
+        if (mhip_graph_end(m->gpu, rc ? NULL : &m->graph)) return gpu_fail(m);
+        if (rc) return fail(m, "recording the stack: %s", why);
+        m->g_l0 = l0;
+        m->g_l1 = l1;
+        m->g_x = d_x;
+        m->g_T = T;
+        m->g_flags = m->flags;
+    }
+    if (mhip_graph_launch(m->gpu, m->graph)) return gpu_fail(m);
     return 0;
 }
 
