@@ -363,6 +363,7 @@ struct Lds {
     alignas(16) uint64_t key[E];  // ranking key: S + bias made monotone, expert index in the low bits
     double c[E];                  // S + bias
     double bpart[E / 64];         // largest bound among each 64 experts
+    float mxpart[E / 64];         // exact router: largest logit among each 64 experts
     float lf[E];                  // fp32 logits (+ bias)
     alignas(16) float p[E];       // probabilities (fallback)
     float bias[E];
@@ -392,6 +393,40 @@ __device__ __forceinline__ float lds_seq_sum(const float *p, int n, float s) {
         s = s + q.y;
         s = s + q.z;
         s = s + q.w;
+    }
+    return s;
+}
+// The same for a compile-time length N (a multiple of 64), the reads of the
+// next 32 values issued before the additions of the current 32, so the
+// chain rarely waits for the LDS.
+template <int N>
+__device__ __forceinline__ float lds_seq_sum_pipe(const float *p, float s) {
+    static_assert(N % 64 == 0, "whole batches");
+    const float4 *v = (const float4 *)p;
+    float4 a[8], b[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) a[k] = v[k];
+    for (int c = 0; c < N / 4; c += 16) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) b[k] = v[c + 8 + k];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            s = s + a[k].x;
+            s = s + a[k].y;
+            s = s + a[k].z;
+            s = s + a[k].w;
+        }
+        if (c + 16 < N / 4) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) a[k] = v[c + 16 + k];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            s = s + b[k].x;
+            s = s + b[k].y;
+            s = s + b[k].z;
+            s = s + b[k].w;
+        }
     }
     return s;
 }
@@ -796,23 +831,32 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                 wave_lds_sync();
                 if (lane == 0) {
                     const int e = rank * LPW + wave - NGU;
-                    float s = lds_seq_sum(pw, D, 0.0f);
+                    float s = lds_seq_sum_pipe<D>(pw, 0.0f);
                     if (a.bias) s = s + sh.bias[e];
                     put_tagged<true>(&ws->lx[xcd][e], s, tag);
                 }
             }
             if (tid < E) get_tagged<1, true>(ws, &ws->lx[xcd][tid], 0, tag, &sh.lf[tid]);
             __syncthreads();
-            if (tid == 0) {
-                // forward.c:95-101 exactly: first maximum, sequential sum.
-                float mx = sh.lf[0];
-                for (int i = 1; i < E; i++) mx = sh.lf[i] > mx ? sh.lf[i] : mx;
-                sh.inv = mx;
+            // forward.c:95-101: the first maximum, then the sequential sum.
+            // With l[0] a NaN every comparison fails and the maximum stays
+            // NaN; otherwise it is the largest non-NaN logit, which a
+            // NaN-ignoring maximum finds in any order (equal maxima, +0 and
+            // -0 among them, give the same exponentials).
+            if (tid < E) {
+                const double m = wave_max_d((double)sh.lf[tid]);
+                if (lane == 0) sh.mxpart[tid >> 6] = (float)m;
             }
             __syncthreads();
-            if (tid < E) sh.p[tid] = mia_expf_glibc_tab(sh.lf[tid] - sh.inv, sh.etab);
+            if (tid < E) {
+                float mx = sh.mxpart[0];
+#pragma unroll
+                for (int q = 1; q < E / 64; q++) mx = fmaxf(mx, sh.mxpart[q]);
+                if (sh.lf[0] != sh.lf[0]) mx = sh.lf[0];
+                sh.p[tid] = mia_expf_glibc_tab(sh.lf[tid] - mx, sh.etab);
+            }
             __syncthreads();
-            if (tid == 0) sh.sum = lds_seq_sum(sh.p, E, 0.0f);
+            if (tid == 0) sh.sum = lds_seq_sum_n<E>(sh.p, 0.0f);
             __syncthreads();
             if (tid < E) {
                 const float pe = sh.p[tid] / sh.sum;
@@ -847,10 +891,17 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             }
             __syncthreads();
             if (tid == 0) {
+                // the K probabilities read first, then summed in rank order
+                float pk[KMAX];
+#pragma unroll
+                for (int j = 0; j < KMAX; j++) pk[j] = j < K ? sh.p[sh.idx[j]] : 0.0f;
                 float wsum = 0.0f;
-                for (int j = 0; j < K; j++) wsum = wsum + sh.p[sh.idx[j]];
-                for (int j = 0; j < K; j++)
-                    sh.w[j] = a.norm_topk ? sh.p[sh.idx[j]] / wsum : sh.p[sh.idx[j]];
+#pragma unroll
+                for (int j = 0; j < KMAX; j++)
+                    if (j < K) wsum = wsum + pk[j];
+#pragma unroll
+                for (int j = 0; j < KMAX; j++)
+                    if (j < K) sh.w[j] = a.norm_topk ? pk[j] / wsum : pk[j];
                 if (xcd == 0 && rank == 0) status_update(ws, ST_ROUTER, a.epoch, true, 0);
             }
             __syncthreads();
