@@ -187,3 +187,23 @@ def test_model_full_shape_decode_equals_per_stage():
         a.close()
         b.close()
         c.close()
+
+
+def test_model_long_context_attention_paths_agree(oracle, tmp_path):
+    """The per-head attention kernel keeps the scores in LDS; a context too
+    long for that runs the separate score and mix kernels. Both give the
+    same logits (the mini Qwen shape, head_dim 128, 40 positions, with a
+    4096-position and a 40000-position cache)."""
+    say("test_model_long_context_attention_paths_agree")
+    spec = json.load(open(os.path.join(GOLDEN, "MANIFEST_model.json")))["model_mini_qwen"]
+    path = str(tmp_path / "mini.mia")
+    MW.synthetic(oracle, path, spec["cfg"], MW.Q8_0, 9)
+    toks = np.random.default_rng(4).integers(0, spec["cfg"]["vocab"], 40).tolist()
+    a = M.GpuModel(path, 4096)
+    b = M.GpuModel(path, 40000)
+    try:
+        for p, tok in enumerate(toks):
+            assert np.array_equal(bits(a.step(tok, p)), bits(b.step(tok, p))), "position %d" % p
+    finally:
+        a.close()
+        b.close()
