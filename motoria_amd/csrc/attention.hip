@@ -205,28 +205,37 @@ __global__ __launch_bounds__(256) void k_attn_mix(float *__restrict__ scores, in
 // head's att values (head_dim % 32 == 0: its blocks lie inside the head).
 // The arithmetic of k_qk_rope, k_attn_scores, k_attn_mix and k_quant_rows,
 // in the same order. LDS: q, k, the scores [max_seq] after them.
-__device__ __forceinline__ void head_norm_rope(const float *src, const float *w, const double *rp,
-                                               int hd, float eps, float *dst, float *tmp,
-                                               float *inv_sh) {
-    const int tid = threadIdx.x;
-    for (int i = tid; i < hd; i += blockDim.x) tmp[i] = src[i];
-    __syncthreads();
-    if (tid == 0) {
-        double ss = 0.0;
-        for (int i = 0; i < hd; i++) ss = ss + (double)tmp[i] * (double)tmp[i];
-        *inv_sh = (float)(1.0 / sqrt(ss / hd + (double)eps));
+// forward.c:75-81 over one head's row in LDS (hd a multiple of 32): the
+// sum of squares in double in index order, rows read 32 values ahead.
+__device__ __forceinline__ float head_inv(const float *row, int hd, float eps) {
+    double ss = 0.0;
+    for (int i = 0; i < hd; i += 32) {
+        float4 r4[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) r4[j] = *(const float4 *)(row + i + 4 * j);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            ss = ss + (double)r4[j].x * (double)r4[j].x;
+            ss = ss + (double)r4[j].y * (double)r4[j].y;
+            ss = ss + (double)r4[j].z * (double)r4[j].z;
+            ss = ss + (double)r4[j].w * (double)r4[j].w;
+        }
     }
-    __syncthreads();
-    const float inv = *inv_sh;
+    return (float)(1.0 / sqrt(ss / hd + (double)eps));
+}
+
+// The head's normalized row, NeoX-rotated (forward.c:127-139): element i
+// with i + hd/2 by the angle whose (cos, sin) are rp[2i], rp[2i+1].
+__device__ __forceinline__ void head_rope(const float *row, float inv, const float *w,
+                                          const double *rp, int hd, float *dst) {
     const int half = hd / 2;
-    for (int i = tid; i < half; i += blockDim.x) {
-        const float x0 = (tmp[i] * inv) * w[i];
-        const float x1 = (tmp[i + half] * inv) * w[i + half];
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+        const float x0 = (row[i] * inv) * w[i];
+        const float x1 = (row[i + half] * inv) * w[i + half];
         const double c = rp[2 * i], sn = rp[2 * i + 1];
         dst[i] = (float)((double)x0 * c - (double)x1 * sn);
         dst[i + half] = (float)((double)x0 * sn + (double)x1 * c);
     }
-    __syncthreads();
 }
 
 __global__ __launch_bounds__(256) void k_attn_head(
@@ -235,32 +244,48 @@ __global__ __launch_bounds__(256) void k_attn_head(
     const double *__restrict__ rope, int pos, int nh, int nkv, int hd, float eps, float scale,
     float *__restrict__ kc, float *__restrict__ vc, int8_t *__restrict__ attq,
     float *__restrict__ atts) {
-    extern __shared__ float lds[];
+    extern __shared__ __align__(16) float lds[];
     __shared__ float red[256];
-    __shared__ float inv_sh, sum_sh;
+    __shared__ float inv_sh, inv2_sh, sum_sh;
     __shared__ uint64_t etab[32];
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const int group = nh / nkv, g = h / group, kvd = nkv * hd, n = pos + 1;
-    float *qs = lds, *ks = lds + hd, *tmp = lds + 2 * hd, *sc = lds + 3 * hd;
+    float *qs = lds, *ks = lds + hd, *tq = lds + 2 * hd, *tk = lds + 3 * hd, *sc = lds + 4 * hd;
     if (tid < 32) etab[tid] = mia_expf_tab[tid];
     const double *rp = rope + (size_t)pos * (hd / 2) * 2;
-    head_norm_rope(q + (size_t)h * hd, q_norm, rp, hd, eps, qs, tmp, &inv_sh);
-    head_norm_rope(k + (size_t)g * hd, k_norm, rp, hd, eps, ks, tmp, &inv_sh);
+    // the query head's and its key head's rows; their norms on two waves
+    for (int i = tid; i < hd; i += blockDim.x) {
+        tq[i] = q[(size_t)h * hd + i];
+        tk[i] = k[(size_t)g * hd + i];
+    }
+    __syncthreads();
+    if (tid == 0) inv_sh = head_inv(tq, hd, eps);
+    if (tid == 64) inv2_sh = head_inv(tk, hd, eps);
+    __syncthreads();
+    head_rope(tq, inv_sh, q_norm, rp, hd, qs);
+    head_rope(tk, inv2_sh, k_norm, rp, hd, ks);
+    __syncthreads();
     if (h % group == 0)
         for (int i = tid; i < hd; i += blockDim.x) {
             kc[(size_t)pos * kvd + (size_t)g * hd + i] = ks[i];
             vc[(size_t)pos * kvd + (size_t)g * hd + i] = v[(size_t)g * hd + i];
         }
-    // scores (forward.c:143-149): sequential fp32 dots, one position per thread
+    // scores (forward.c:143-149): sequential fp32 dots, one position per
+    // thread, the key row read 32 values ahead of the additions
     for (int t = tid; t < n; t += blockDim.x) {
         const float *kt = t == pos ? ks : kc + (size_t)t * kvd + (size_t)g * hd;
         float dot = 0.0f;
-        for (int i = 0; i < hd; i += 4) {
-            const float4 k4 = *(const float4 *)(kt + i);
-            dot = dot + qs[i] * k4.x;
-            dot = dot + qs[i + 1] * k4.y;
-            dot = dot + qs[i + 2] * k4.z;
-            dot = dot + qs[i + 3] * k4.w;
+        for (int i = 0; i < hd; i += 32) {
+            float4 k4[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) k4[j] = *(const float4 *)(kt + i + 4 * j);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                dot = dot + qs[i + 4 * j] * k4[j].x;
+                dot = dot + qs[i + 4 * j + 1] * k4[j].y;
+                dot = dot + qs[i + 4 * j + 2] * k4[j].z;
+                dot = dot + qs[i + 4 * j + 3] * k4[j].w;
+            }
         }
         sc[t] = dot * scale;
     }
@@ -290,8 +315,17 @@ __global__ __launch_bounds__(256) void k_attn_head(
     // mix (forward.c:157-162), then Q8 of the head's att (quant.c:11-27)
     float o = 0.0f;
     if (tid < hd) {
+        // the value rows of 16 positions read before their additions
         const float *vt = vc + (size_t)g * hd + tid;
-        for (int t = 0; t < pos; t++) o = o + sc[t] * vt[(size_t)t * kvd];
+        int t = 0;
+        for (; t + 16 <= pos; t += 16) {
+            float vv[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) vv[j] = vt[(size_t)(t + j) * kvd];
+#pragma unroll
+            for (int j = 0; j < 16; j++) o = o + sc[t + j] * vv[j];
+        }
+        for (; t < pos; t++) o = o + sc[t] * vt[(size_t)t * kvd];
         o = o + sc[pos] * v[(size_t)g * hd + tid];
         // the block's maximum by a 32-lane butterfly (order-free; from 0,
         // a NaN never wins, as in the sequential loop)
@@ -306,7 +340,7 @@ __global__ __launch_bounds__(256) void k_attn_head(
 }
 
 constexpr size_t HEAD_LDS_MAX = 150 * 1024;  // dynamic LDS of k_attn_head
-size_t head_lds(int hd, int max_seq) { return ((size_t)3 * hd + (size_t)max_seq) * sizeof(float); }
+size_t head_lds(int hd, int max_seq) { return ((size_t)4 * hd + (size_t)max_seq) * sizeof(float); }
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
