@@ -74,7 +74,9 @@ int mia_gpu_model_step_sample(mia_gpu_model *m, int token, int pos, mhip_sampler
  * ~5e-4 of max|logit| each, up to ~1e-2 in all). MHIP_EXACT_EXPERTS: the
  * per-stage kernels (bit-equal, no decode launch). MHIP_DECODE_FORCE_ABORT:
  * every decode launch aborts and the step reruns per stage (a test of that
- * fallback). */
+ * fallback). MHIP_DECODE_CHAINS_FIRST (with MHIP_FORCE_EXACT_ROUTER): the
+ * exact chains before the expert stream in every layer (the path of a
+ * layer whose ranking is not certified). */
 void mia_gpu_model_set_flags(mia_gpu_model *m, int flags);
 /* Decode launches of the last step that aborted (rerun per stage). */
 int mia_gpu_model_aborts(const mia_gpu_model *m);

@@ -155,11 +155,16 @@ int mhip_scratch_carve(const mhip_dims *s, int max_tokens, void *d_base,
 
 /* Flags for mhip_moe_layer and mhip_decode_stack. */
 #define MHIP_FORCE_SEQ_RMS 1      /* always take the sequential rmsnorm sum */
-#define MHIP_FORCE_EXACT_ROUTER 2 /* decode stack: always the exact router chain */
+#define MHIP_FORCE_EXACT_ROUTER 2 /* decode stack: the reference's exact router chains
+                                     (routing and gate weights bit-equal) */
 #define MHIP_DECODE_TRACE 4       /* decode stack: record stage timestamps */
 #define MHIP_EXACT_EXPERTS 8      /* layer: bit-exact expert products at every T */
 #define MHIP_DECODE_FORCE_ABORT 16 /* decode stack: report abort bit 4 and stop after the
                                       start barrier (tests the callers' abort handling) */
+#define MHIP_DECODE_CHAINS_FIRST 32 /* decode stack, with MHIP_FORCE_EXACT_ROUTER: the exact
+                                       chains before the expert stream in every layer, as for
+                                       a layer whose ranking is not certified (without it they
+                                       run beside the stream when it is) */
 
 /*
  * One MoE layer (rmsnorm -> router/top-K -> dispatch -> gate/up+SwiGLU ->
@@ -196,11 +201,15 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
  * launches). d_idx/d_w ([L][n_active]) receive the routing when non-NULL.
  * Expert indices are bit-equal to the reference (certified parallel router,
  * exact fallback); the gate weights come from the parallel logits, within
- * ~1e-6 relative of the reference's. After the stream completes,
- * mhip_decode_status reports [0] abort bits (1: workgroups not on the
- * expected XCDs, 2: a wait timed out, 4: MHIP_DECODE_FORCE_ABORT; the
- * output is then invalid),
- * [1] rmsnorm fallbacks, [2] layers routed by the exact fallback.
+ * ~1e-6 relative of the reference's; under MHIP_FORCE_EXACT_ROUTER the
+ * weights are the reference's too (its sequential logit chains: before the
+ * expert stream for a layer whose ranking is not certified, beside it
+ * otherwise). After the stream completes, mhip_decode_status reports [0]
+ * abort bits (1: workgroups not on the expected XCDs, 2: a wait timed out,
+ * 4: MHIP_DECODE_FORCE_ABORT, 8: a NaN probability in a layer routed from
+ * a certified ranking under MHIP_FORCE_EXACT_ROUTER; the output is then
+ * invalid and the layer is rerun per stage), [1] rmsnorm fallbacks, [2]
+ * layers whose gate weights came from the exact chains.
  */
 #define MHIP_DECODE_MAX_LAYERS 256 /* layers of one decode-stack launch */
 size_t mhip_decode_ws_bytes(void);

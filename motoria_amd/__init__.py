@@ -27,6 +27,7 @@ MHIP_FORCE_EXACT_ROUTER = 2
 MHIP_DECODE_TRACE = 4
 MHIP_EXACT_EXPERTS = 8
 MHIP_DECODE_FORCE_ABORT = 16
+MHIP_DECODE_CHAINS_FIRST = 32
 DECODE_MAX_LAYERS = 256  # MHIP_DECODE_MAX_LAYERS
 GEMM_MIN_A = 2048  # MHIP_GEMM_MIN_A
 TRACE_L0, TRACE_NL, TRACE_SLOTS = 8, 8, 32  # decode trace window (MHIP_TRACE_* in mia_hip.h)

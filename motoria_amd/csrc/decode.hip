@@ -378,60 +378,14 @@ struct Lds {
     int idx[KMAX];
     float w[KMAX];
     int fallback;
+    int shadow_on;                // exact router, certified ranking: the chains run in stage C
     int nanflag;
     int role[2];                  // this workgroup's XCD and rank within it
 };
 
-// Sequential fp32 sum of n (multiple of 4) LDS floats starting at p, in
-// order, with 16-byte reads.
-__device__ __forceinline__ float lds_seq_sum(const float *p, int n, float s) {
-    const float4 *v = (const float4 *)p;
-#pragma unroll 4
-    for (int k = 0; k < n / 4; k++) {
-        const float4 q = v[k];
-        s = s + q.x;
-        s = s + q.y;
-        s = s + q.z;
-        s = s + q.w;
-    }
-    return s;
-}
-// The same for a compile-time length N (a multiple of 64), the reads of the
-// next 32 values issued before the additions of the current 32, so the
-// chain rarely waits for the LDS.
-template <int N>
-__device__ __forceinline__ float lds_seq_sum_pipe(const float *p, float s) {
-    static_assert(N % 64 == 0, "whole batches");
-    const float4 *v = (const float4 *)p;
-    float4 a[8], b[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) a[k] = v[k];
-    for (int c = 0; c < N / 4; c += 16) {
-#pragma unroll
-        for (int k = 0; k < 8; k++) b[k] = v[c + 8 + k];
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            s = s + a[k].x;
-            s = s + a[k].y;
-            s = s + a[k].z;
-            s = s + a[k].w;
-        }
-        if (c + 16 < N / 4) {
-#pragma unroll
-            for (int k = 0; k < 8; k++) a[k] = v[c + 16 + k];
-        }
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            s = s + b[k].x;
-            s = s + b[k].y;
-            s = s + b[k].z;
-            s = s + b[k].w;
-        }
-    }
-    return s;
-}
-// The same for a compile-time length: every value is read before the first
-// addition, so the chain waits for the LDS once.
+// Sequential fp32 sum of N (a compile-time multiple of 4) LDS floats at p,
+// in order: every value is read before the first addition, so the chain
+// waits for the LDS once.
 template <int N>
 __device__ __forceinline__ float lds_seq_sum_n(const float *p, float s) {
     static_assert(N % 4 == 0, "whole float4s");
@@ -446,6 +400,38 @@ __device__ __forceinline__ float lds_seq_sum_n(const float *p, float s) {
         s = s + q[k].z;
         s = s + q[k].w;
     }
+    return s;
+}
+
+// Sequential fp32 sum, in order, of the wavefront's 64 x 32 values, lane L
+// holding values 32 L .. 32 L + 31 in v[0..31]: every lane adds its own 32
+// values to its running sum, then the sums move one lane up (DPP wave_shr:1),
+// so lane L starts from lane L - 1's total. Only lane L's additions count in
+// round L; the sum of all 2048 values ends in lane 63. 2048 dependent
+// additions with their operands in registers.
+__device__ __forceinline__ float wave_seq_sum_2048(const float (&v)[32]) {
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 32; k++) s = s + v[k];
+    for (int L = 1; L < 64; L++) {
+        s = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x138, 0xf, 0xf, false));
+#pragma unroll
+        for (int k = 0; k < 32; k++) s = s + v[k];
+    }
+    return s;
+}
+
+// Sequential fp32 sum, in order, of the wavefront's 128 values, lane L
+// holding value L in a and value 64 + L in b: each step adds a lane's value
+// to the running sum of the lane before it (DPP wave_ror:1, lane 0 taking
+// lane 63's), so step i's sum is correct in lane i % 64. The sum of all 128
+// ends in lane 63.
+__device__ __forceinline__ float wave_seq_sum_128(float a, float b) {
+    float s = 0.0f + a;
+    for (int i = 1; i < 64; i++)
+        s = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x13C, 0xf, 0xf, false)) + a;
+    for (int i = 0; i < 64; i++)
+        s = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x13C, 0xf, 0xf, false)) + b;
     return s;
 }
 
@@ -798,7 +784,12 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             // roundings between the logit and the probability (logit + bias,
             // l - mx, expf, division). The gate weights are computed later,
             // while the XCD waits for h.
-            bool ok = (a.flags & MHIP_FORCE_EXACT_ROUTER) == 0 && sh.nanflag == 0;
+            // Under the exact router (MHIP_FORCE_EXACT_ROUTER) a certified
+            // ranking is the reference's, so only the gate weights need the
+            // exact chains: they run beside the gate/up stream (stage C)
+            // unless MHIP_DECODE_CHAINS_FIRST asks for them before it.
+            const bool exact = (a.flags & MHIP_FORCE_EXACT_ROUTER) != 0;
+            bool ok = sh.nanflag == 0 && !(exact && (a.flags & MHIP_DECODE_CHAINS_FIRST));
             if (ok) {
                 const double top = sh.c[sh.order[0]], bmax = fmax(sh.bpart[0], sh.bpart[1]);
                 int bad = 0;
@@ -810,31 +801,31 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                 ok = __ballot(bad) == 0;
             }
             if (ok && lane < K) sh.idx[lane] = sh.order[lane];
-            if (lane == 0) sh.fallback = ok ? 0 : 1;
+            if (lane == 0) {
+                sh.fallback = ok ? 0 : 1;
+                sh.shadow_on = ok && exact ? 1 : 0;
+            }
         }
         __syncthreads();
         if (sh.fallback) {
             // Exact logits, the reference's sequential chain: each down wave
-            // computes one (products to LDS, lane 0 sums them in order), then
-            // the XCD exchanges them.
+            // computes one (products in registers, summed in order across
+            // the lanes), then the XCD exchanges them.
             if (!gu_wave) {
-                float *pw = &sh.scr[(wave - NGU) * D];
                 const float *xv = &sh.xn[lane * XN_LD];
+                float pr[32];
 #pragma unroll
                 for (int k = 0; k < 8; k++) {
                     const float4 wv = RROW(k);
-                    pw[lane * 32 + 4 * k + 0] = wv.x * xv[4 * k + 0];
-                    pw[lane * 32 + 4 * k + 1] = wv.y * xv[4 * k + 1];
-                    pw[lane * 32 + 4 * k + 2] = wv.z * xv[4 * k + 2];
-                    pw[lane * 32 + 4 * k + 3] = wv.w * xv[4 * k + 3];
+                    pr[4 * k + 0] = wv.x * xv[4 * k + 0];
+                    pr[4 * k + 1] = wv.y * xv[4 * k + 1];
+                    pr[4 * k + 2] = wv.z * xv[4 * k + 2];
+                    pr[4 * k + 3] = wv.w * xv[4 * k + 3];
                 }
-                wave_lds_sync();
-                if (lane == 0) {
-                    const int e = rank * LPW + wave - NGU;
-                    float s = lds_seq_sum_pipe<D>(pw, 0.0f);
-                    if (a.bias) s = s + sh.bias[e];
-                    put_tagged<true>(&ws->lx[xcd][e], s, tag);
-                }
+                float sl = wave_seq_sum_2048(pr);
+                const int e = rank * LPW + wave - NGU;
+                if (a.bias) sl = sl + sh.bias[e];
+                if (lane == 63) put_tagged<true>(&ws->lx[xcd][e], sl, tag);
             }
             if (tid < E) get_tagged<1, true>(ws, &ws->lx[xcd][tid], 0, tag, &sh.lf[tid]);
             __syncthreads();
@@ -965,8 +956,32 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                 TRACE_BY(17, 192);
             }
         } else {
+            const bool shadow = sh.shadow_on != 0;
+            if (shadow) {
+                // The exact logit of this wave's expert (forward.c:173-176:
+                // the reference's sequential chain) from its router row of
+                // this layer, still in registers, before the loads that reuse
+                // those registers: the HBM stream of the gate/up waves would
+                // hold the loads' issue, and the chain behind them, for most
+                // of this stage.
+                const float *xv = &sh.xn[lane * XN_LD];
+                float pr[32];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const float4 wv = RROW(k);
+                    pr[4 * k + 0] = wv.x * xv[4 * k + 0];
+                    pr[4 * k + 1] = wv.y * xv[4 * k + 1];
+                    pr[4 * k + 2] = wv.z * xv[4 * k + 2];
+                    pr[4 * k + 3] = wv.w * xv[4 * k + 3];
+                }
+                float sl = wave_seq_sum_2048(pr);
+                const int e = rank * LPW + wave - NGU;
+                if (a.bias) sl = sl + sh.bias[e];
+                if (lane == 63) put_tagged<true>(&ws->lx[xcd][e], sl, tag);
+                TRACE_BY(23, NGU * 64);
+            }
             // the down rows of this workgroup (used once h has arrived)
-            if (wave == NGU && !sh.fallback) {
+            if (wave == NGU && !sh.fallback && !shadow) {
                 // The gate weights, before this wave's loads (a wave waiting
                 // to issue a load runs nothing else, and the CU takes its
                 // vector memory instructions in order). Softmax of the
@@ -1031,10 +1046,6 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
             __syncthreads();
             TRACE(5);
             TRACE(13);
-            if (xcd == 0 && rank == 0 && tid < K) {
-                if (a.idx_out) a.idx_out[(size_t)l * K + tid] = sh.idx[tid];
-                if (a.w_out) a.w_out[(size_t)l * K + tid] = sh.w[tid];
-            }
             float *dterm = sh.scr;
             if (!gu_wave) {
 #pragma unroll
@@ -1061,14 +1072,66 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
         TRACE(6);
 
         // ---- E: combine rows rank*64 .. +64 in top-K order ---------------------------
+        if (sh.shadow_on && wave == 1) {
+            // Under the exact router with a certified ranking: the XCD's 128
+            // exact logits (the down waves' chains, long done) -> softmax
+            // (forward.c:95-101: the first maximum as in the exact router
+            // above, the sequential sum) -> the certified experts' weights
+            // (forward.c:178-181), first needed by the combine below. Wave 1
+            // computes them while the expert outputs are on their way (wave 0
+            // fetches expert 1's rows).
+            float lv[2];
+            get_tagged<2, true>(ws, &ws->lx[xcd][lane], 64, tag, lv);
+            float mx = (float)wave_max_d(fmax((double)lv[0], (double)lv[1]));
+            const float l0 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(lv[0])));
+            if (l0 != l0) mx = l0;
+            const float e0 = mia_expf_glibc_tab(lv[0] - mx, sh.etab);
+            const float e1 = mia_expf_glibc_tab(lv[1] - mx, sh.etab);
+            const float sum = __int_as_float(
+                __builtin_amdgcn_readlane(__float_as_int(wave_seq_sum_128(e0, e1)), 63));
+            const float p0 = e0 / sum, p1 = e1 / sum;
+            // a NaN probability would rank differently in the reference
+            // (forward.c:104-114): the launch reports it and the caller
+            // reruns the layer per stage
+            const bool nan = __ballot(p0 != p0 || p1 != p1) != 0;
+            sh.p[lane] = p0;
+            sh.p[lane + 64] = p1;
+            wave_lds_sync();
+            // lane j < K: the probability of rank j; their sum in rank order
+            // (lane j adds its own to lane j - 1's running sum)
+            const float pj = lane < K ? sh.p[sh.idx[lane]] : 0.0f;
+            float wsum = 0.0f + pj;
+            for (int j = 1; j < K; j++)
+                wsum = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(wsum), 0x138, 0xf, 0xf, false)) + pj;
+            wsum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wsum), K - 1));
+            if (lane < K) sh.w[lane] = a.norm_topk ? pj / wsum : pj;
+            if (lane == 0) {
+                if (nan) status_update(ws, ST_ABORT, a.epoch, false, 8);
+                if (xcd == 0 && rank == 0) status_update(ws, ST_ROUTER, a.epoch, true, 0);
+            }
+            TRACE_BY(24, 64);
+        }
         {
             // thread (j, r) fetches expert j's output row r; then one thread
             // per row adds them in top-K order
             const int j = tid / DROWS, r = tid % DROWS;
-            if (j < K) get_tagged<1, false>(ws, &ws->out[par][j][rank * DROWS + r], 0, tag, &sh.og[j * DROWS + r]);
+            if (sh.shadow_on && K > 1 && j < 2) {
+                if (j == 0) {
+                    float v2[2];
+                    get_tagged<2, false>(ws, &ws->out[par][0][rank * DROWS + r], D, tag, v2);
+                    sh.og[r] = v2[0];
+                    sh.og[DROWS + r] = v2[1];
+                }
+            } else if (j < K) {
+                get_tagged<1, false>(ws, &ws->out[par][j][rank * DROWS + r], 0, tag, &sh.og[j * DROWS + r]);
+            }
         }
         __syncthreads();
         TRACE(7);
+        if (xcd == 0 && rank == 0 && tid < K) {
+            if (a.idx_out) a.idx_out[(size_t)l * K + tid] = sh.idx[tid];
+            if (a.w_out) a.w_out[(size_t)l * K + tid] = sh.w[tid];
+        }
         if (tid < DROWS) {
             const int r = rank * DROWS + tid;
             float v = sh.x[r];

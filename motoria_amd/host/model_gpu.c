@@ -298,7 +298,8 @@ static int moe(mia_gpu_model *m, int l, int per_stage) {
                                   t->router_dl + (size_t)l * E * d, t->router_t + (size_t)l * E * d,
                                   t->norm + (size_t)l * d, NULL, m->d_x, 1, NULL, NULL,
                                   m->d_status + 4 * l,
-                                  m->flags & (MHIP_FORCE_EXACT_ROUTER | MHIP_DECODE_FORCE_ABORT)))
+                                  m->flags & (MHIP_FORCE_EXACT_ROUTER | MHIP_DECODE_FORCE_ABORT |
+                                              MHIP_DECODE_CHAINS_FIRST)))
         return mfail(m, "%s", mhip_error(m->gpu));
     return 0;
 }

@@ -94,11 +94,14 @@ def test_decode_full_stack_matches_oracle(oracle, qwen_dims, moe):
     assert e <= TOL
 
 
-def test_decode_exact_router_is_bit_equal(oracle, qwen_dims, moe):
-    say("test_decode_exact_router_is_bit_equal")
+@pytest.mark.parametrize("chains_first", [False, True])
+def test_decode_exact_router_is_bit_equal(oracle, qwen_dims, moe, chains_first):
+    """The exact chains beside the expert stream (a certified ranking) and
+    before it (the path of a ranking that is not certified)."""
+    say("test_decode_exact_router_is_bit_equal chains_first=%d" % chains_first)
     d = qwen_dims
     x = oracle.synth_x(W.X_SEED + 11, 1, d.dim)[0]
-    moe.set_flags(M.MHIP_FORCE_EXACT_ROUTER)
+    moe.set_flags(M.MHIP_FORCE_EXACT_ROUTER | (M.MHIP_DECODE_CHAINS_FIRST if chains_first else 0))
     try:
         for l in range(2):
             xo, io, wo, _, _ = run_oracle_layer(oracle, moe, d, l, x)
@@ -112,6 +115,29 @@ def test_decode_exact_router_is_bit_equal(oracle, qwen_dims, moe):
             x = xo[0]
     finally:
         moe.set_flags(0)
+
+
+@pytest.mark.parametrize("chains_first", [False, True])
+def test_decode_exact_router_stack_is_bit_equal(oracle, qwen_dims, moe, chains_first):
+    """One launch over LAYERS layers under the exact router: the exact
+    logits, weights and outputs of every layer carried to the next."""
+    say("test_decode_exact_router_stack_is_bit_equal chains_first=%d" % chains_first)
+    d = qwen_dims
+    x0 = oracle.synth_x(W.X_SEED + 17, 1, d.dim)[0]
+    moe.set_flags(M.MHIP_FORCE_EXACT_ROUTER | (M.MHIP_DECODE_CHAINS_FIRST if chains_first else 0))
+    try:
+        xg, ig, wg = moe.decode(0, LAYERS, x0)
+        st = moe.decode_status()
+    finally:
+        moe.set_flags(0)
+    assert st[0] == 0 and st[2] == LAYERS, st
+    x = x0
+    for l in range(LAYERS):
+        xo, io, wo, _, _ = run_oracle_layer(oracle, moe, d, l, x)
+        assert np.array_equal(ig[l], io[0]), "layer %d routing differs" % l
+        assert np.array_equal(wg[l].view(np.uint32), wo[0].view(np.uint32)), "layer %d weights" % l
+        x = xo[0]
+    assert np.array_equal(xg.view(np.uint32), x.view(np.uint32))
 
 
 def test_decode_forced_sequential_rmsnorm(oracle, qwen_dims, moe):

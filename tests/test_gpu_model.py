@@ -121,6 +121,7 @@ def qwen_model(oracle, tmp_path_factory):
 
 @pytest.mark.parametrize("flags,aborts", [
     (M.MHIP_FORCE_EXACT_ROUTER, 0),
+    (M.MHIP_FORCE_EXACT_ROUTER | M.MHIP_DECODE_CHAINS_FIRST, 0),
     (M.MHIP_FORCE_EXACT_ROUTER | M.MHIP_DECODE_FORCE_ABORT, 2),
     (M.MHIP_EXACT_EXPERTS, 0),
 ])
