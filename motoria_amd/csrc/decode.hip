@@ -507,11 +507,10 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
     float wsc[GU_R];
     // In the decode layout, load k of the row (1 KB, contiguous) gives lane
     // L its elements 32 L + 4 k .. + 3.
-#define LOAD_ROUTER(layer)                                                                 \
+#define LOAD_ROUTER(layer) LOAD_ROUTER_ROW((size_t)(layer) * E + rank * LPW + wave - NGU)
+#define LOAD_ROUTER_ROW(row)                                                               \
     do {                                                                                   \
-        const int4 *src_ = (const int4 *)(a.router +                                       \
-                                          ((size_t)(layer) * E + rank * LPW + wave - NGU) * D) + \
-                           lane;                                                           \
+        const int4 *src_ = (const int4 *)(a.router + (size_t)(row) * D) + lane;            \
         _Pragma("unroll") for (int k_ = 0; k_ < NR0; k_++) wq0[DPK + k_] = src_[64 * k_];  \
         _Pragma("unroll") for (int k_ = 0; k_ < 8 - NR0; k_++) wq1[DPK + k_] = src_[64 * (NR0 + k_)]; \
     } while (0)
@@ -904,10 +903,9 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
         const int ex = min(max(sh.idx[active ? xcd : 0], 0), E - 1);
         const uint8_t *eb = a.table + (size_t)l * layer_bytes + (size_t)ex * a.lay.expert_bytes;
         // The next layer's rmsnorm weights are requested first: they arrive
-        // before this wave's weight rows, so no later wait is held up by them.
-        // The prefetches below are issued on every path (the last layer
-        // reloads its own rows) so that the compiler's wait counts stay exact
-        // and a wait for the down rows never covers the router rows.
+        // before this wave's weight rows, so no later wait is held up by them
+        // (the last layer reloads its own). Its router rows follow in stage D,
+        // once this layer's rows are in.
         const int lnext = min(l + 1, a.L - 1);
         LOAD_NORM(lnext);
         if (gu_wave) {
@@ -1013,7 +1011,6 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                 const int p = (dt >> 1) + (NDN * 32) * (2 * k + (dt & 1));
                 wsc[k] = ((const float *)(eb + a.lay.down_s))[(size_t)rank * DROWS * NBH + p];
             }
-            LOAD_ROUTER(lnext);
         }
         TRACE(4);
         // ---- D: Q8(h) and down ------------------------------------------------------
@@ -1063,6 +1060,13 @@ __global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
                     dterm[row * DN_LD + blk] = mhip_dev::block_term((hf ? db : da) + other, wsc[k],
                                                                     sh.hsc[blk]);
                 }
+                // the next layer's router rows, after this layer's stream:
+                // they load while the expert outputs are exchanged. After the
+                // last layer every wave reads router row 0 instead (the same
+                // 8 KB, from the L2): the load is issued on every path, so
+                // the compiler's wait counts stay exact and the expert
+                // outputs' polls never wait for it.
+                LOAD_ROUTER_ROW(l + 1 < a.L ? (size_t)lnext * E + rank * LPW + wave - NGU : 0);
             }
             __syncthreads();
             if (wave == 0)
