@@ -76,9 +76,12 @@ int mia_gpu_model_step_sample(mia_gpu_model *m, int token, int pos, mhip_sampler
  * every decode launch aborts and the step reruns per stage (a test of that
  * fallback). MHIP_DECODE_CHAINS_FIRST (with MHIP_FORCE_EXACT_ROUTER): the
  * exact chains before the expert stream in every layer (the path of a
- * layer whose ranking is not certified). */
+ * layer whose ranking is not certified). MHIP_ATTN_FORCE_ABORT: every
+ * one-launch attention (mhip_attention_layer, used where the shape allows
+ * it) aborts and the step reruns from that layer per stage. */
 void mia_gpu_model_set_flags(mia_gpu_model *m, int flags);
-/* Decode launches of the last step that aborted (rerun per stage). */
+/* Launches of the last step (decode and one-launch attention) that aborted
+ * (their layers rerun per stage). */
 int mia_gpu_model_aborts(const mia_gpu_model *m);
 
 #ifdef __cplusplus

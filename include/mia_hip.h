@@ -282,6 +282,38 @@ int mhip_output_head(mhip_ctx *c, const mhip_attn_dims *s, const float *d_output
                      const void *d_output, int vocab, const float *d_x, float *d_logits,
                      void *d_scratch, int flags);
 
+/*
+ * No counterpart in the reference: mhip_attention in one launch for callers
+ * that step a whole model (the same forward.c:118-165 arithmetic, bit-equal;
+ * the Qwen3-30B-A3B attention shape only: dim 2048, 32/4 heads of 128). Every
+ * CU takes part: the rmsnorm, q/k/v rows, heads and Wo rows meet through
+ * tagged words in d_ws (mhip_attention_layer_ws_bytes(), 256-byte aligned,
+ * not shared by overlapping launches; the context clears it when it first
+ * sees it). d_x is updated in place; d_x_in / d_x_out (may be NULL) receive
+ * x before and after. *d_status (may be NULL) gets abort bits OR'ed in (2: a
+ * wait for another workgroup ran out, 4: MHIP_ATTN_FORCE_ABORT); the caller
+ * clears it. An aborted launch leaves d_x as it was (d_x_in is written in
+ * any case) but its cache row and d_x_out are invalid: the caller reruns
+ * the layer with mhip_attention. _supported: 1 when the shape, max_seq and the device
+ * (256 CUs, one 512-thread workgroup each) fit, 0 when not, -1 on an error.
+ */
+#define MHIP_ATTN_FORCE_ABORT 64 /* the one-launch attention reports abort bit 4 and
+                                    stops after its start barrier (a test of the
+                                    callers' rerun) */
+size_t mhip_attention_layer_ws_bytes(void);
+/* With MHIP_DECODE_TRACE in flags, a launch records the 100 MHz real-time
+ * counter of each of its 256 workgroups at MHIP_ATTN_TRACE_SLOTS phase
+ * boundaries (start, started, norm, q/k/v out, head in, head out, heads in,
+ * end); this copies them out (out[256][MHIP_ATTN_TRACE_SLOTS]). Diagnostic. */
+#define MHIP_ATTN_TRACE_SLOTS 8
+int mhip_attention_layer_trace(mhip_ctx *c, const void *d_ws, unsigned long long *out);
+int mhip_attention_layer_supported(mhip_ctx *c, const mhip_attn_dims *s, int max_seq);
+int mhip_attention_layer(mhip_ctx *c, const mhip_attn_dims *s, const float *d_attn_norm,
+                         const void *d_wq, const void *d_wk, const void *d_wv, const void *d_wo,
+                         const float *d_q_norm, const float *d_k_norm, const double *d_rope,
+                         float *d_kc, float *d_vc, int pos, int max_seq, float *d_x,
+                         float *d_x_in, float *d_x_out, void *d_ws, int *d_status, int flags);
+
 /* ---- HIP graphs -----------------------------------------------------------
  * No counterpart in the reference. The launches queued on a context between
  * mhip_graph_begin and mhip_graph_end are recorded (not run) into a graph,

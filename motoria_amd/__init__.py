@@ -28,6 +28,7 @@ MHIP_DECODE_TRACE = 4
 MHIP_EXACT_EXPERTS = 8
 MHIP_DECODE_FORCE_ABORT = 16
 MHIP_DECODE_CHAINS_FIRST = 32
+MHIP_ATTN_FORCE_ABORT = 64
 DECODE_MAX_LAYERS = 256  # MHIP_DECODE_MAX_LAYERS
 GEMM_MIN_A = 2048  # MHIP_GEMM_MIN_A
 TRACE_L0, TRACE_NL, TRACE_SLOTS = 8, 8, 32  # decode trace window (MHIP_TRACE_* in mia_hip.h)
@@ -143,6 +144,11 @@ SIGNATURES = {
     "mhip_attention": (_i, [_p, ctypes.POINTER(AttnDims), _p, _p, _p, _p, _p, _p, _p, _p, _p,
                             _p, _i, _i, _p, _p, _p, _i]),
     "mhip_output_head": (_i, [_p, ctypes.POINTER(AttnDims), _p, _p, _i, _p, _p, _p, _i]),
+    "mhip_attention_layer_ws_bytes": (_sz, []),
+    "mhip_attention_layer_trace": (_i, [_p, _p, _p]),
+    "mhip_attention_layer_supported": (_i, [_p, ctypes.POINTER(AttnDims), _i]),
+    "mhip_attention_layer": (_i, [_p, ctypes.POINTER(AttnDims), _p, _p, _p, _p, _p, _p, _p, _p,
+                                  _p, _p, _i, _i, _p, _p, _p, _p, _p, _i]),
     "mhip_graph_begin": (_i, [_p]),
     "mhip_graph_end": (_i, [_p, ctypes.POINTER(_p)]),
     "mhip_graph_launch": (_i, [_p, _p]),

@@ -5,12 +5,13 @@
  *
  * The .mia file's dense section is uploaded as it is laid out (36-byte
  * Q8_0 blocks, fp32 vectors), so each tensor's device address is the
- * dense walk's offset. The MoE layers run the one-layer launch of the
- * persistent decode kernel where the shape allows it (the exact router in
- * exact mode), else the per-stage kernels, which are bit-exact. Each decode
- * launch reports its status into a per-layer slot; should one abort, the
- * step restores x from the copy taken before that layer's MoE and reruns
- * from there per stage (the KV rows of the later layers are rewritten).
+ * dense walk's offset. Where the shape allows it, a layer is two launches:
+ * the one-launch attention (mhip_attention_layer) and the one-layer launch
+ * of the persistent decode kernel (the exact router in exact mode); else
+ * the per-stage kernels, which are bit-exact. Both launches report aborts
+ * into per-layer slots; should one abort, the step restores x from the copy
+ * taken before that launch and reruns from there per stage (the KV rows of
+ * the later layers are rewritten).
  */
 #define _FILE_OFFSET_BITS 64
 #define _POSIX_C_SOURCE 200809L
@@ -33,7 +34,7 @@ struct mia_gpu_model {
     mhip_ctx *gpu;
     mia_moe_tensors mt;
     mhip_attn_dims ad;
-    int max_seq, flags, decode_ok, aborts;
+    int max_seq, flags, decode_ok, attn_ok, aborts;
     int logits_ok; /* d_logits holds the last step's logits */
     unsigned char *d_dense;
     mia_layer_offsets *lo;   /* [L] */
@@ -43,7 +44,9 @@ struct mia_gpu_model {
     void *d_scratch;
     float *d_x;              /* [dim] residual */
     float *d_xsave;          /* [L][dim] x before each layer's MoE */
-    int *d_status;           /* [L][4] decode status per layer */
+    float *d_xin;            /* [L][dim] x before each layer's attention (one-launch path) */
+    void *d_aws;             /* workspace of the one-launch attention */
+    int *d_status;           /* [L][4] decode status per layer, then [L] attention aborts */
     float *d_logits;         /* [vocab] */
     void *d_sample;          /* mhip_sample scratch for vocab logits */
     int *d_token, *h_token;  /* the sampled token (device, pinned) */
@@ -76,6 +79,8 @@ void mia_gpu_model_close(mia_gpu_model *m) {
         mhip_free(m->gpu, m->d_scratch);
         mhip_free(m->gpu, m->d_x);
         mhip_free(m->gpu, m->d_xsave);
+        mhip_free(m->gpu, m->d_xin);
+        mhip_free(m->gpu, m->d_aws);
         mhip_free(m->gpu, m->d_status);
         mhip_free(m->gpu, m->d_logits);
         mhip_free(m->gpu, m->d_sample);
@@ -137,6 +142,9 @@ static int setup(mia_gpu_model *m, int max_seq, int device) {
     const int ok = mhip_decode_supported(m->gpu, &m->mt.dims);
     if (ok < 0) return mfail(m, "%s", mhip_error(m->gpu));
     m->decode_ok = ok > 0;
+    const int aok = mhip_attention_layer_supported(m->gpu, &m->ad, max_seq);
+    if (aok < 0) return mfail(m, "%s", mhip_error(m->gpu));
+    m->attn_ok = aok > 0 && m->decode_ok;
     const size_t L = h->n_layers, kvd = (size_t)h->n_kv_heads * h->head_dim;
     const size_t half = h->head_dim / 2, ws = mhip_attention_scratch_bytes(&m->ad, max_seq);
     m->lo = calloc(L, sizeof(*m->lo));
@@ -149,10 +157,15 @@ static int setup(mia_gpu_model *m, int max_seq, int device) {
     m->d_scratch = mhip_malloc(m->gpu, ws);
     m->d_x = mhip_malloc(m->gpu, (size_t)h->dim * 4);
     m->d_xsave = mhip_malloc(m->gpu, L * h->dim * 4);
-    m->d_status = mhip_malloc(m->gpu, L * 16);
+    m->d_status = mhip_malloc(m->gpu, L * 20);
     m->d_logits = mhip_malloc(m->gpu, (size_t)h->vocab * 4);
     m->h_logits = mhip_host_malloc(m->gpu, (size_t)h->vocab * 4);
-    m->h_status = mhip_host_malloc(m->gpu, L * 16);
+    m->h_status = mhip_host_malloc(m->gpu, L * 20);
+    if (m->attn_ok) {
+        m->d_xin = mhip_malloc(m->gpu, L * h->dim * 4);
+        m->d_aws = mhip_malloc(m->gpu, mhip_attention_layer_ws_bytes());
+        if (!m->d_xin || !m->d_aws) return mfail(m, "device memory: %s", mhip_error(m->gpu));
+    }
     const size_t sb = mhip_sample_scratch_bytes((int)h->vocab);
     if (!sb) return mfail(m, "vocabulary of %u tokens: no sampler for it", h->vocab);
     m->d_sample = mhip_malloc(m->gpu, sb);
@@ -281,6 +294,24 @@ static int attention(mia_gpu_model *m, int l, int pos, int save) {
     return 0;
 }
 
+/* The same as one launch (the step's common path): x before and after are
+ * kept for the reruns, aborts are reported into the layer's attention slot
+ * (after the decode status words). */
+static int attention_layer(mia_gpu_model *m, int l, int pos) {
+    const size_t kvd = (size_t)m->info.n_kv_heads * m->info.head_dim, d = m->info.dim;
+    const mia_layer_offsets *o = &m->lo[l];
+    const unsigned char *b = m->d_dense;
+    float *kc = m->d_kc + (size_t)l * m->max_seq * kvd, *vc = m->d_vc + (size_t)l * m->max_seq * kvd;
+    if (mhip_attention_layer(m->gpu, &m->ad, (const float *)(b + o->attn_norm), b + o->wq,
+                             b + o->wk, b + o->wv, b + o->wo, (const float *)(b + o->q_norm),
+                             (const float *)(b + o->k_norm), m->d_rope, kc, vc, pos, m->max_seq,
+                             m->d_x, m->d_xin + l * d, m->d_xsave + l * d, m->d_aws,
+                             m->d_status + 4 * (size_t)m->info.n_layers + l,
+                             m->flags & (MHIP_ATTN_FORCE_ABORT | MHIP_FORCE_SEQ_RMS)))
+        return mfail(m, "%s", mhip_error(m->gpu));
+    return 0;
+}
+
 /* Queues the MoE of layer l on d_x: one decode launch reporting into its
  * status slot, or (per_stage, or no decode launch for this shape) the
  * per-stage kernels. */
@@ -299,7 +330,7 @@ static int moe(mia_gpu_model *m, int l, int per_stage) {
                                   t->norm + (size_t)l * d, NULL, m->d_x, 1, NULL, NULL,
                                   m->d_status + 4 * l,
                                   m->flags & (MHIP_FORCE_EXACT_ROUTER | MHIP_DECODE_FORCE_ABORT |
-                                              MHIP_DECODE_CHAINS_FIRST)))
+                                              MHIP_DECODE_CHAINS_FIRST | MHIP_FORCE_SEQ_RMS)))
         return mfail(m, "%s", mhip_error(m->gpu));
     return 0;
 }
@@ -347,30 +378,39 @@ static int run_step(mia_gpu_model *m, int token, int pos, step_tail *t) {
     const size_t row = (size_t)(d / MIA_QK) * 36;
     if (mhip_dequantize_q8(m->gpu, m->d_dense + m->off_embd + (size_t)token * row, m->d_x, d))
         return mfail(m, "%s", mhip_error(m->gpu));
+    const int one = decode && m->attn_ok;
+    if (one && mhip_zero(m->gpu, m->d_status + 4 * (size_t)L, (size_t)L * 4))
+        return mfail(m, "%s", mhip_error(m->gpu));
     for (int l = 0; l < L; l++) {
-        if (attention(m, l, pos, decode) || moe(m, l, 0))
+        if ((one ? attention_layer(m, l, pos) : attention(m, l, pos, decode)) || moe(m, l, 0))
             return -1;
     }
-    /* the tail is queued before the decode launches' status is known: one
-     * wait per step; an abort (rare) reruns from the first aborted layer */
+    /* the tail is queued before the launches' status is known: one wait per
+     * step; an abort (rare) reruns from the first aborted launch */
     if (tail(m, t)) return -1;
-    if ((decode && mhip_d2h_async(m->gpu, m->h_status, m->d_status, (size_t)L * 16)) ||
+    if ((decode && mhip_d2h_async(m->gpu, m->h_status, m->d_status, (size_t)L * (one ? 20 : 16))) ||
         mhip_sync(m->gpu))
         return mfail(m, "%s", mhip_error(m->gpu));
     m->aborts = 0;
-    int first = -1;
-    for (int l = 0; decode && l < L; l++)
-        if (m->h_status[4 * l]) {
-            m->aborts++;
-            if (first < 0) first = l;
+    int first = -1, first_attn = 0;
+    for (int l = 0; decode && l < L; l++) {
+        const int a = one && m->h_status[4 * L + l], b = m->h_status[4 * l] != 0;
+        m->aborts += a + b;
+        if (first < 0 && (a || b)) {
+            first = l;
+            first_attn = a;
         }
+    }
     if (first < 0) {
         m->logits_ok = !t->no_head;
         return 0;
     }
-    if (mhip_d2d(m->gpu, m->d_x, m->d_xsave + (size_t)first * d, (size_t)d * 4))
+    /* an aborted attention launch restarts from x before it, an aborted MoE
+     * launch from x after its layer's attention */
+    if (mhip_d2d(m->gpu, m->d_x, (first_attn ? m->d_xin : m->d_xsave) + (size_t)first * d,
+                 (size_t)d * 4))
         return mfail(m, "%s", mhip_error(m->gpu));
-    if (moe(m, first, 1)) return -1;
+    if ((first_attn && attention(m, first, pos, 0)) || moe(m, first, 1)) return -1;
     for (int l = first + 1; l < L; l++)
         if (attention(m, l, pos, 0) || moe(m, l, 1)) return -1;
     if (tail(m, t)) return -1;

@@ -122,7 +122,10 @@ def qwen_model(oracle, tmp_path_factory):
 @pytest.mark.parametrize("flags,aborts", [
     (M.MHIP_FORCE_EXACT_ROUTER, 0),
     (M.MHIP_FORCE_EXACT_ROUTER | M.MHIP_DECODE_CHAINS_FIRST, 0),
+    (M.MHIP_FORCE_EXACT_ROUTER | M.MHIP_FORCE_SEQ_RMS, 0),
     (M.MHIP_FORCE_EXACT_ROUTER | M.MHIP_DECODE_FORCE_ABORT, 2),
+    (M.MHIP_FORCE_EXACT_ROUTER | M.MHIP_ATTN_FORCE_ABORT, 2),
+    (M.MHIP_FORCE_EXACT_ROUTER | M.MHIP_ATTN_FORCE_ABORT | M.MHIP_DECODE_FORCE_ABORT, 4),
     (M.MHIP_EXACT_EXPERTS, 0),
 ])
 def test_model_qwen_shape_bit_exact(qwen_model, flags, aborts):
@@ -188,6 +191,27 @@ def test_model_full_shape_decode_equals_per_stage():
         a.close()
         b.close()
         c.close()
+
+
+def test_model_full_shape_one_launch_attention_far_positions():
+    """The one-launch attention at positions past its 512 threads (several
+    scores per thread, a long mix), against the per-stage step; positions in
+    between are left empty (zero cache rows), so only the steps shown run."""
+    say("test_model_full_shape_one_launch_attention_far_positions")
+    a = M.GpuModel(None, 2048, synth=(QWEN_FULL, 6))
+    b = M.GpuModel(None, 2048, flags=M.MHIP_EXACT_EXPERTS, synth=(QWEN_FULL, 6))
+    try:
+        rng = np.random.default_rng(11)
+        for p in (0, 1, 700, 1500, 2047):
+            tok = int(rng.integers(0, QWEN_FULL["vocab"]))
+            la, lb = a.step(tok, p), b.step(tok, p)
+            assert a.aborts() == 0
+            assert np.all(np.isfinite(la))
+            assert np.array_equal(bits(la), bits(lb)), "position %d" % p
+        say("  positions 0, 1, 700, 1500, 2047: one-launch attention == per-stage")
+    finally:
+        a.close()
+        b.close()
 
 
 def test_model_long_context_attention_paths_agree(oracle, tmp_path):
