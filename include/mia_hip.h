@@ -353,6 +353,20 @@ void mhip_sampler_init(mhip_sampler *s, float temperature, float top_p, int n, u
 size_t mhip_sample_scratch_bytes(int n);
 int mhip_sample(mhip_ctx *c, mhip_sampler *s, const float *d_logits, void *d_scratch,
                 int *d_token);
+/* The sampler's running sums on their own (no counterpart in the reference,
+ * whose sampler.c:43,55,64 adds them in loops): s_0 = 0, s_{k+1} =
+ * fl(s_k + d_v[k]) for k < n, every addition in fp32 in index order, the
+ * result bit-equal to that loop, for d_v[n] (16-byte aligned, readable up
+ * to n rounded up to a multiple of 4 values) of values >= 0 (other values
+ * are added one at a time, as the loop would). mode
+ * MHIP_CHAIN_SUM runs all n additions; MHIP_CHAIN_GE stops after the first
+ * addition that makes s >= thr, MHIP_CHAIN_GT after the first that makes
+ * thr < s. d_out (device, 2 ints): [0] the bits of s after the last
+ * addition done, [1] the index of the stopping element (n if none). */
+#define MHIP_CHAIN_SUM 0
+#define MHIP_CHAIN_GE 1
+#define MHIP_CHAIN_GT 2
+int mhip_chain_f32(mhip_ctx *c, const float *d_v, int n, int mode, float thr, int *d_out);
 
 /* ---- reference tensor ops on device pointers ---------------------------- */
 /* Q8_0 blocks in the reference's 36-byte format. */

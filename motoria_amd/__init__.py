@@ -29,6 +29,7 @@ MHIP_EXACT_EXPERTS = 8
 MHIP_DECODE_FORCE_ABORT = 16
 MHIP_DECODE_CHAINS_FIRST = 32
 MHIP_ATTN_FORCE_ABORT = 64
+MHIP_CHAIN_SUM, MHIP_CHAIN_GE, MHIP_CHAIN_GT = 0, 1, 2
 DECODE_MAX_LAYERS = 256  # MHIP_DECODE_MAX_LAYERS
 GEMM_MIN_A = 2048  # MHIP_GEMM_MIN_A
 TRACE_L0, TRACE_NL, TRACE_SLOTS = 8, 8, 32  # decode trace window (MHIP_TRACE_* in mia_hip.h)
@@ -156,6 +157,7 @@ SIGNATURES = {
     "mhip_sampler_init": (None, [ctypes.POINTER(Sampler), _f, _f, _i, _u64]),
     "mhip_sample_scratch_bytes": (_sz, [_i]),
     "mhip_sample": (_i, [_p, ctypes.POINTER(Sampler), _p, _p, _p]),
+    "mhip_chain_f32": (_i, [_p, _p, _i, _i, _f, _p]),
     "mhip_quantize_q8": (_i, [_p, _p, _p, _i]),
     "mhip_dequantize_q8": (_i, [_p, _p, _p, _i]),
     "mhip_matvec": (_i, [_p, _p, _p, _i, _p, _p, _i, _i]),

@@ -10,9 +10,12 @@
 //            the running sum of the sorted p up to top_p, r = u * cum, the
 //            first candidate whose running sum exceeds r (k_sample_pick)
 //
-// The two running sums are fp32 chains in a fixed order, as the reference
-// adds them; one lane adds while the other waves of the workgroup stage
-// the next chunk into LDS. Everything else is parallel.
+// The running sums are fp32 chains in a fixed order, as the reference adds
+// them. They are computed exactly but not one addition at a time: while a
+// running sum stays inside one binade every addition adds a whole number of
+// that binade's ulps, so a workgroup turns 8192 additions at a time into an
+// integer prefix sum and walks only the few additions that leave the binade
+// (seq_scan). Everything else is parallel.
 #include <rocprim/device/device_radix_sort.hpp>
 
 #include "mhip_internal.h"
@@ -21,8 +24,6 @@ namespace {
 
 constexpr int NT = 256;          // threads of every sampler kernel
 constexpr int PARTS = 256;       // workgroups of the argmax's first pass
-constexpr int CH = 2048;         // chain chunk (values per LDS stage)
-constexpr int MAXCH = 1024;      // chunks the pick records (n <= 2M)
 constexpr uint64_t NONE = ~0ull; // key of a dropped token
 
 struct SampleState {
@@ -102,54 +103,250 @@ __global__ __launch_bounds__(NT) void k_sample_exp(const float *__restrict__ l, 
     if (i < n) e[i] = mia_expf_glibc_tab((l[i] - mx) / temperature, etab);
 }
 
-// Copies values [base, base + CH) of src (those below n) into an LDS chunk,
-// `nthr` threads numbered from 0.
-template <typename V>
-__device__ __forceinline__ void stage_chunk(V *dst, const V *__restrict__ src, int base, int n,
-                                            int t, int nthr) {
-    for (int j = t; j < CH; j += nthr)
-        if (base + j < n) dst[j] = src[base + j];
+// ---- exact running sums, 8192 additions at a time -------------------------------
+//
+// The chains s_0 = 0, s_{k+1} = fl(s_k + v_k) over v_k >= 0 (sampler.c:43,
+// 55, 64). Let s lie on the grid of spacing u = 2^(P-23) below 2^(P+1):
+// the binade [2^P, 2^(P+1)) for P >= -126, together with the subnormals for
+// P = -126 (spacing 2^-149 below 2^-125). Then s = M u with an integer
+// M < 2^24, and while s + v stays below 2^(P+1) - u/2 the rounded sum is
+// u (M + n) with n the integer nearest to v / u: every value of the grid
+// below 2^(P+1) is representable, and only an exact half (a tie, broken
+// towards an even M + n) makes the result depend on M. So as long as
+// M + n_0 + ... + n_j <= 2^24 - 1 (and no v_j / u is a tie), the chain's
+// values are u times an integer prefix sum. The workgroup holds a window
+// of SQ_W values (SQ_V consecutive per thread), forms every n_j and their
+// prefix sums, and finds the first element at which the chain leaves the
+// binade, meets a tie or a value that is not a finite v >= 0, or makes
+// the caller's predicate true; that one addition is done in fp32 by its
+// thread, the grid is taken from the new s, and the window goes on after
+// it, first over its next SQ_SHORT values only (exits come in bursts while
+// the sum is small; a short pass costs the waves that hold those values),
+// then over the rest. Ties, exits from a binade (at most one per binade the
+// sum passes through) and the stop are the only additions done one at a
+// time. The prefix sums are fp32 sums of whole numbers: exact below 2^24,
+// and at least 2^24 when the exact sum is, which is all the test needs (an
+// n too large for the binade is entered as 2^25). A chain that becomes
+// infinite, NaN or negative finishes one addition at a time on one lane.
+constexpr int SQ_T = 1024, SQ_V = 8, SQ_W = SQ_T * SQ_V, SQ_SHORT = 1024;
+constexpr float SQ_TOP = 16777216.0f;  // 2^24: a mantissa at or above it left the binade
+constexpr int SQ_PF = 2;               // windows loaded ahead
+constexpr size_t SQ_LDS = (size_t)(SQ_PF + 1) * SQ_W * sizeof(float);  // the window ring
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// 16 bytes from global memory straight into LDS at lds + 16 * lane.
+__device__ __forceinline__ void sq_dma16(unsigned lds, const void *g) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+enum { SQ_SUM = 0, SQ_GE = 1, SQ_GT = 2 };
+
+template <int MODE>
+__device__ __forceinline__ bool sq_pred(float s, float thr) {
+    return MODE == SQ_GE ? s >= thr : MODE == SQ_GT ? thr < s : false;
 }
 
-// s + v[0] + v[1] + ... + v[len-1], one addition at a time.
-__device__ __forceinline__ float chain_add(const float *v, int len, float s) {
-    int j = 0;
-    for (; j + 64 <= len; j += 64) {
-        float4 q[16];
-        const float4 *p = (const float4 *)(v + j);
+// The grid of s >= 0 finite: P with s = M 2^(P-23), M an integer < 2^24.
+__device__ __forceinline__ int sq_grid(float s) {
+    return s >= 0x1p-126f ? ilogbf(s) : -126;
+}
+
+// Runs the chain over v[0 .. n) (16-byte aligned) on a workgroup of SQ_T
+// threads, every thread calling. Returns the index of the first element
+// after whose addition MODE's predicate holds (n if none) and leaves in *s
+// the chain's value after that addition (after all n if none).
+template <int MODE>
+__device__ int seq_scan(const float *__restrict__ v, int n, float thr, float *s_out) {
+    __shared__ float wtot[2][SQ_T / 64];
+    __shared__ int wstop[2][SQ_T / 64];
+    __shared__ float s1_sh[2];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int P = -126;
+    float M = 0.0f;       // s = M 2^(P-23) = 0
+    int lo = 0;           // the chain has added v[0 .. lo)
+    int it = 0;           // parity of the LDS buffers
+    float s = 0.0f;
+    int stop = n;
+    bool seq = false;     // the chain left the finite non-negative values
+    const int nw = (n + SQ_W - 1) / SQ_W;
+    // Windows stream into an LDS ring of SQ_PF + 1 windows, SQ_PF ahead,
+    // straight from global memory (thread t's values land where it reads
+    // them: load q of a wavefront puts lane l's 16 bytes at 16 l); every
+    // load is a whole 16-byte vector at an in-range index (the last one
+    // reaches up to 3 values past n: callers pad to a multiple of 4), and
+    // values past n are zeroed when a window is taken.
+    extern __shared__ __align__(16) float sq_ring[];
+    const unsigned ring = (unsigned)(uintptr_t)sq_ring;
+    const int nl = n > 4 ? (n - 1) & ~3 : 0;
+    auto issue = [&](int w) {
+        const int i0 = w * SQ_W + SQ_V * tid;
+        const unsigned st = ring + (unsigned)(((w % (SQ_PF + 1)) * SQ_W + SQ_V * 64 * wave) * 4);
 #pragma unroll
-        for (int k = 0; k < 16; k++) q[k] = p[k];
+        for (int q = 0; q < SQ_V / 4; q++)
+            sq_dma16(st + (unsigned)(q * 64 * 16), v + min(i0 + 4 * q, nl));
+    };
+    if (n > 0) {
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
-            s = s + q[k].x;
-            s = s + q[k].y;
-            s = s + q[k].z;
-            s = s + q[k].w;
+        for (int q = 0; q < SQ_PF; q++) issue(q);
+    }
+    bool short_pass = false;
+    for (int w = 0; w < nw && stop == n && !seq; w++) {
+        // this wavefront's loads of window w are in (later ones may not be)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((SQ_PF - 1) * (SQ_V / 4)) : "memory");
+        const int base = w * SQ_W + SQ_V * tid;
+        float x[SQ_V];
+        {
+            const float4 *src = (const float4 *)(sq_ring + (w % (SQ_PF + 1)) * SQ_W + SQ_V * 64 * wave) + lane;
+#pragma unroll
+            for (int q = 0; q < SQ_V / 4; q++) {
+                const float4 r = src[64 * q];
+                x[4 * q] = base + 4 * q < n ? r.x : 0.0f;
+                x[4 * q + 1] = base + 4 * q + 1 < n ? r.y : 0.0f;
+                x[4 * q + 2] = base + 4 * q + 2 < n ? r.z : 0.0f;
+                x[4 * q + 3] = base + 4 * q + 3 < n ? r.w : 0.0f;
+            }
+        }
+        // window w + SQ_PF goes into the stage of window w - 1 (read before)
+        issue(w + SQ_PF);
+        const int wend = min(w * SQ_W + SQ_W, n);
+        const int wbase = w * SQ_W + SQ_V * 64 * wave;  // this wavefront's values
+        for (;;) {
+            const int hi = short_pass ? min(lo + SQ_SHORT, wend) : wend;
+            // a wavefront with none of [lo, hi) skips the element work
+            const bool busy = wbase + SQ_V * 64 > lo && wbase < hi;
+            const float lim = ldexpf(1.0f, P + 1);
+            float L[SQ_V];
+            bool sp[SQ_V];
+            float run = 0.0f;
+            if (busy) {
+#pragma unroll
+                for (int e = 0; e < SQ_V; e++) {
+                    const int i = base + e;
+                    const float xv = x[e];
+                    float k = 0.0f;
+                    bool special = false;
+                    if (i >= lo && i < hi) {
+                        if (!(xv >= 0.0f) || xv == __builtin_inff()) {
+                            special = true;  // NaN, infinite or negative
+                        } else if (xv >= lim) {
+                            k = 2.0f * SQ_TOP;  // leaves the binade
+                        } else {
+                            const float t = ldexpf(xv, 23 - P);  // < 2^24, exact
+                            k = rintf(t);
+                            special = t - truncf(t) == 0.5f;  // a tie
+                        }
+                    }
+                    sp[e] = special;
+                    run = run + k;
+                    L[e] = run;
+                }
+            }
+            // exclusive prefix of the thread totals over the workgroup
+            float incl = run;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const float y = __shfl_up(incl, o);
+                if (lane >= o) incl = incl + y;
+            }
+            const float up = __shfl_up(incl, 1);
+            const float exw = lane > 0 ? up : 0.0f;
+            if (lane == 63) wtot[it][wave] = incl;
+            __syncthreads();
+            float before = 0.0f, total = 0.0f;
+#pragma unroll
+            for (int k = 0; k < SQ_T / 64; k++) {
+                const float t = wtot[it][k];
+                if (k < wave) before = before + t;
+                total = total + t;
+            }
+            const float ex = M + (before + exw);
+            // the first element that leaves the binade, is special or stops
+            int first = SQ_V;
+            if (busy) {
+#pragma unroll
+                for (int e = SQ_V - 1; e >= 0; e--) {
+                    const float Me = ex + L[e];
+                    bool st = sp[e] || Me >= SQ_TOP;
+                    if (MODE != SQ_SUM && !st && base + e >= lo && base + e < hi)
+                        st = sq_pred<MODE>(ldexpf(Me, P - 23), thr);
+                    if (st) first = e;
+                }
+            }
+            const unsigned long long b = __ballot(first < SQ_V);
+            if (lane == (b ? __ffsll((long long)b) - 1 : 0))
+                wstop[it][wave] = b ? SQ_V * tid + first : SQ_W;
+            __syncthreads();
+            int f = SQ_W;
+#pragma unroll
+            for (int k = 0; k < SQ_T / 64; k++) f = min(f, wstop[it][k]);
+            it ^= 1;
+            if (f == SQ_W) {  // [lo, hi) stays in the binade
+                M = M + total;
+                s = ldexpf(M, P - 23);
+                lo = hi;
+                short_pass = false;
+                if (hi == wend) break;
+                continue;
+            }
+            // element f: its thread adds it in fp32
+            if (tid == f / SQ_V) {
+                const int e = f % SQ_V;
+                float Lp = 0.0f;
+#pragma unroll
+                for (int q = 0; q < SQ_V; q++)
+                    if (q < e) Lp = L[q];
+                float xe = x[0];
+#pragma unroll
+                for (int q = 1; q < SQ_V; q++)
+                    if (q == e) xe = x[q];
+                s1_sh[it ^ 1] = ldexpf(ex + Lp, P - 23) + xe;
+            }
+            __syncthreads();
+            s = s1_sh[it ^ 1];
+            const int fi = w * SQ_W + f;
+            lo = fi + 1;
+            short_pass = true;
+            if (MODE != SQ_SUM && sq_pred<MODE>(s, thr)) {
+                stop = fi;
+                break;
+            }
+            if (!(s >= 0.0f) || s == __builtin_inff()) {
+                seq = true;
+                break;
+            }
+            P = sq_grid(s);
+            M = ldexpf(s, 23 - P);
+            if (lo == wend) break;
         }
     }
-    for (; j < len; j++) s = s + v[j];
-    return s;
-}
-
-// sampler.c:43: sum = e_0 + e_1 + ... + e_{n-1} (fp32, index order). Lane 0
-// of wave 0 adds chunk c while waves 1-3 stage chunk c + 1.
-__global__ __launch_bounds__(NT) void k_chain_sum(const float *__restrict__ e, int n,
-                                                  SampleState *st) {
-    __shared__ __align__(16) float buf[2][CH];
-    const int tid = threadIdx.x;
-    const int nch = (n + CH - 1) / CH;
-    stage_chunk(buf[0], e, 0, n, tid, NT);
-    __syncthreads();
-    float s = 0.0f;
-    for (int c = 0; c < nch; c++) {
-        if (tid >= 64) {
-            if (c + 1 < nch) stage_chunk(buf[(c + 1) & 1], e, (c + 1) * CH, n, tid - 64, NT - 64);
-        } else if (tid == 0) {
-            s = chain_add(buf[c & 1], min(CH, n - c * CH), s);
+    if (seq) {  // the rest one addition at a time (NaN, infinite or negative sums)
+        if (tid == 0) {
+            int i = lo;
+            for (; i < n; i++) {
+                s = s + v[i];
+                if (MODE != SQ_SUM && sq_pred<MODE>(s, thr)) break;
+            }
+            s1_sh[0] = s;
+            wstop[0][0] = i;
         }
         __syncthreads();
+        s = s1_sh[0];
+        stop = MODE == SQ_SUM ? n : wstop[0][0];
     }
-    if (tid == 0) st->sum = s;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the loads past the end
+    *s_out = s;
+    return stop;
+}
+
+// sampler.c:43: sum = e_0 + e_1 + ... + e_{n-1} (fp32, index order).
+__global__ __launch_bounds__(SQ_T) void k_chain_sum(const float *__restrict__ e, int n,
+                                                    SampleState *st) {
+    float s;
+    seq_scan<SQ_SUM>(e, n, 0.0f, &s);
+    if (threadIdx.x == 0) st->sum = s;
 }
 
 // sampler.c:46-51: p_i = e_i / sum; a candidate when p_i >= cutoff, as the
@@ -189,114 +386,56 @@ __global__ __launch_bounds__(NT) void k_keys_split(const uint64_t *__restrict__ 
     if (i + 1 == n || keys[i + 1] == NONE) st->last = i;
 }
 
-// Adds v[0], v[1], ... (at most len) to s one at a time and stops after the
-// first addition that makes pred(s) true: returns that element's index (s
-// then holds the sum through it), or len (s the sum of all). pred is
-// monotone in s and every v >= 0, so a batch whose total leaves pred false
-// holds no stopping point; only the batch where it turns true is walked
-// element by element.
-template <class P>
-__device__ __forceinline__ int chain_until(const float *v, int len, float &s, P pred) {
-    int j = 0;
-    for (; j + 64 <= len; j += 64) {
-        float4 q[16];
-        const float4 *p = (const float4 *)(v + j);
-#pragma unroll
-        for (int k = 0; k < 16; k++) q[k] = p[k];
-        float t = s;
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-            t = t + q[k].x;
-            t = t + q[k].y;
-            t = t + q[k].z;
-            t = t + q[k].w;
-        }
-        if (pred(t)) {
-            for (int k = 0; k < 64; k++) {
-                s = s + v[j + k];
-                if (pred(s)) return j + k;
-            }
-        }
-        s = t;
-    }
-    for (; j < len; j++) {
-        s = s + v[j];
-        if (pred(s)) return j;
-    }
-    return len;
-}
-
-// sampler.c:53-66 on the m candidates (pf, pi; m - 1 in st->last). Pass 1
-// (lane 0; waves 1-3 stage the next chunk): cum = p_0 + p_1 + ... until cum
-// >= top_p (last = that candidate) or the candidates end, with the running
-// sum at every chunk's end kept in LDS. r = u * cum. The pick is the first
-// candidate whose running sum exceeds r: running sums never decrease, so it
-// lies in the first chunk whose end value exceeds r, which pass 2 adds again
-// from that chunk's starting value (the same additions, the same sums).
-__global__ __launch_bounds__(NT) void k_sample_pick(const float *__restrict__ pf,
-                                                    const int *__restrict__ pi, float top_p,
-                                                    float u, SampleState *st, int *token) {
-    __shared__ __align__(16) float buf[2][CH];
-    __shared__ float cend[MAXCH];
-    __shared__ int stop_sh, nch_used, pick_chunk, last_sh;
-    __shared__ float r_sh;
-    const int tid = threadIdx.x;
+// sampler.c:53-66 on the m candidates (pf, pi; m - 1 in st->last): cum =
+// p_0 + p_1 + ... until cum >= top_p (last = that candidate) or the
+// candidates end; r = u * cum; the pick is the first candidate up to last
+// whose running sum (the same additions from 0) exceeds r, else last.
+__global__ __launch_bounds__(SQ_T) void k_sample_pick(const float *__restrict__ pf,
+                                                      const int *__restrict__ pi, float top_p,
+                                                      float u, SampleState *st, int *token) {
     const int m = st->last + 1;
     if (m == 0) {  // no candidate
-        if (tid == 0) *token = st->best;
+        if (threadIdx.x == 0) *token = st->best;
         return;
     }
-    const int nch = (m + CH - 1) / CH;
-    if (tid == 0) stop_sh = 0;
-    stage_chunk(buf[0], pf, 0, m, tid, NT);
-    __syncthreads();
-    float cum = 0.0f;
-    for (int c = 0; c < nch; c++) {
-        if (tid >= 64) {
-            if (c + 1 < nch) stage_chunk(buf[(c + 1) & 1], pf, (c + 1) * CH, m, tid - 64, NT - 64);
-        } else if (tid == 0) {
-            const int len = min(CH, m - c * CH);
-            const int j = chain_until(buf[c & 1], len, cum, [=](float x) { return x >= top_p; });
-            cend[c] = cum;
-            if (j < len || c + 1 == nch) {
-                stop_sh = 1;
-                nch_used = c + 1;
-                last_sh = j < len ? c * CH + j : m - 1;
-            }
-        }
-        __syncthreads();
-        if (stop_sh) break;
-    }
-    if (tid == 0) {
-        const int last = last_sh;
+    float cum;
+    const int j = seq_scan<SQ_GE>(pf, m, top_p, &cum);
+    const int last = j < m ? j : m - 1;
+    const float r = u * cum;
+    float acc;
+    const int k = seq_scan<SQ_GT>(pf, last + 1, r, &acc);
+    if (threadIdx.x == 0) {
         st->cum = cum;
         st->last = last;
-        const float r = u * cum;
-        r_sh = r;
-        pick_chunk = -1;
-        for (int c = 0; c < nch_used; c++)
-            if (r < cend[c]) {
-                pick_chunk = c;
-                break;
-            }
-        if (pick_chunk < 0) *token = pi[last];
+        *token = pi[k <= last ? k : last];
     }
-    __syncthreads();
-    const int pc = pick_chunk;
-    if (pc < 0) return;
-    stage_chunk(buf[0], pf, pc * CH, m, tid, NT);
-    __syncthreads();
-    if (tid == 0) {
-        const float r = r_sh;
-        const int last = last_sh;
-        float acc = pc > 0 ? cend[pc - 1] : 0.0f;
-        const int len = min(CH, last - pc * CH + 1);
-        const int j = chain_until(buf[0], len, acc, [=](float x) { return r < x; });
-        *token = j < len ? pi[pc * CH + j] : pi[last];
+}
+
+template <int MODE>
+__global__ __launch_bounds__(SQ_T) void k_chain(const float *__restrict__ v, int n, float thr,
+                                                int *__restrict__ out) {
+    float s;
+    const int k = seq_scan<MODE>(v, n, thr, &s);
+    if (threadIdx.x == 0) {
+        out[0] = __float_as_int(s);
+        out[1] = k;
     }
 }
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+// The LDS ring of the running-sum kernels is above the default limit.
+int sq_lds_attr(mhip_ctx *c) {
+    const void *fns[] = {(const void *)k_chain_sum, (const void *)k_sample_pick,
+                         (const void *)k_chain<SQ_SUM>, (const void *)k_chain<SQ_GE>,
+                         (const void *)k_chain<SQ_GT>};
+    for (const void *f : fns)
+        if (mhip::check(c, hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)SQ_LDS),
+                        "sampler LDS attribute"))
+            return -1;
+    return 0;
+}
 
 struct SampleScratch {
     SampleState *st;
@@ -383,7 +522,8 @@ int mhip_sample(mhip_ctx *c, mhip_sampler *s, const float *d_logits, void *d_scr
     const float cutoff = (1.0f - s->top_p) / (float)(n > 1 ? n - 1 : 1);
     const unsigned nb = mhip::blocks_for(n, NT);
     k_sample_exp<<<nb, NT, 0, st>>>(d_logits, n, s->temperature, sc.st, sc.e);
-    k_chain_sum<<<1, NT, 0, st>>>(sc.e, n, sc.st);
+    if (sq_lds_attr(c)) return -1;
+    k_chain_sum<<<1, SQ_T, SQ_LDS, st>>>(sc.e, n, sc.st);
     k_sample_keys<<<nb, NT, 0, st>>>(sc.e, n, cutoff, sc.st, sc.kin);
     if (mhip::check_launch(c, "sampler")) return -1;
     size_t tb = sc.tmp_bytes;
@@ -393,8 +533,25 @@ int mhip_sample(mhip_ctx *c, mhip_sampler *s, const float *d_logits, void *d_scr
     float *pf = (float *)sc.kin;  // the unsorted keys are dead after the sort
     int *pi = (int *)sc.kin + n;
     k_keys_split<<<nb, NT, 0, st>>>(sc.kout, n, pf, pi, sc.st);
-    k_sample_pick<<<1, NT, 0, st>>>(pf, pi, s->top_p, u, sc.st, d_token);
+    k_sample_pick<<<1, SQ_T, SQ_LDS, st>>>(pf, pi, s->top_p, u, sc.st, d_token);
     return mhip::check_launch(c, "sampler pick");
+}
+
+int mhip_chain_f32(mhip_ctx *c, const float *d_v, int n, int mode, float thr, int *d_out) {
+    if (n < 0 || !d_out || (n > 0 && !d_v)) return mhip::fail(c, "chain: bad arguments (n=%d)", n);
+    if ((uintptr_t)d_v % 16) return mhip::fail(c, "chain: d_v is not 16-byte aligned");
+    if (mode != MHIP_CHAIN_SUM && mode != MHIP_CHAIN_GE && mode != MHIP_CHAIN_GT)
+        return mhip::fail(c, "chain: mode %d", mode);
+    if (mhip::use_device(c)) return -1;
+    if (sq_lds_attr(c)) return -1;
+    hipStream_t st = c->stream;
+    if (mode == MHIP_CHAIN_SUM)
+        k_chain<SQ_SUM><<<1, SQ_T, SQ_LDS, st>>>(d_v, n, thr, d_out);
+    else if (mode == MHIP_CHAIN_GE)
+        k_chain<SQ_GE><<<1, SQ_T, SQ_LDS, st>>>(d_v, n, thr, d_out);
+    else
+        k_chain<SQ_GT><<<1, SQ_T, SQ_LDS, st>>>(d_v, n, thr, d_out);
+    return mhip::check_launch(c, "chain");
 }
 
 }  // extern "C"

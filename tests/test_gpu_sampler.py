@@ -153,3 +153,92 @@ def test_model_generation_step_sample(oracle, tmp_path, t, p):
     finally:
         a.close()
         b.close()
+
+
+def _chain_cases():
+    """Vectors for the running sums: (name, values, thresholds)."""
+    rng = np.random.default_rng(31)
+    out = []
+    lg = rng.standard_normal(151936).astype(np.float32) * 3
+    e = np.exp((lg - lg.max()) / np.float32(0.8)).astype(np.float32)
+    out.append(("exp 151936", e))
+    p = np.sort(e / e.sum(dtype=np.float32))[::-1].astype(np.float32)
+    out.append(("sorted p", np.ascontiguousarray(p)))
+    # every addition a tie at s in [1, 2): u = 2^-23, v = 1.5 u
+    out.append(("ties", np.array([1.0] + [1.5 * 2.0 ** -23] * 3000, np.float32)))
+    # multiples of a half-ulp at several binades, mixed with exact ulps
+    k = rng.integers(0, 8, 20000)
+    out.append(("half-ulps", np.concatenate([[np.float32(3.0)],
+                                             (k * 2.0 ** -23).astype(np.float32)])))
+    # powers of two landing exactly on binade edges, zeros, subnormals
+    edge = np.array([0.0, 1e-45, 2e-45, 2.0 ** -126, 2.0 ** -125, 0.5, 0.5, 1.0, 2.0, 4.0,
+                     2.0 ** 24, 1.0, 1.0, 3.0, 2.0 ** 30, 0.0], np.float32)
+    out.append(("edges", np.tile(edge, 700)))
+    tiny = (rng.integers(0, 5000, 30000) * 2.0 ** -149).astype(np.float32)
+    out.append(("subnormals", tiny))
+    wide = (10.0 ** rng.uniform(-40, 30, 50000)).astype(np.float32)
+    out.append(("wide range", wide))
+    for n in (0, 1, 7, 8191, 8192, 8193, 16385):
+        out.append(("n=%d" % n, rng.random(n).astype(np.float32)))
+    x = rng.random(30000).astype(np.float32)
+    x[12345] = np.inf
+    out.append(("inf", x.copy()))
+    x[20000] = np.nan
+    out.append(("inf then nan", x.copy()))
+    y = rng.random(30000).astype(np.float32)
+    y[100] = np.nan
+    out.append(("nan", y))
+    z = rng.random(30000).astype(np.float32)
+    z[9000] = -5.0
+    out.append(("negative", z))
+    return out
+
+
+def test_chain_sums_bit_equal(gpu):
+    """mhip_chain_f32 (the sampler's running sums, computed 8192 additions at
+    a time within a binade) against the sequential fp32 loop (numpy's
+    float32 accumulate adds in index order): the final sum, and the stop
+    index and value of the >= and > searches, bit-equal, on exponentials,
+    sorted probabilities, all-tie and half-ulp sequences, binade edges,
+    subnormals, a 70-decade range, ragged lengths, and inf / NaN / negative
+    values."""
+    say("test_chain_sums_bit_equal")
+    d_out = gpu.malloc(8)
+    cases = _chain_cases()
+    # the values go up through one pinned staging buffer
+    cap = max(v.nbytes for _, v in cases) + 16
+    h_stage = M.lib().mhip_host_malloc(gpu.h, cap)
+    assert h_stage, M.lib().mhip_error(gpu.h).decode()
+    stage = np.ctypeslib.as_array(ctypes.cast(h_stage, ctypes.POINTER(ctypes.c_float)), (cap // 4,))
+    for name, v in cases:
+        n = v.size
+        d_v = gpu.malloc(16 * ((n + 3) // 4) + 16)  # n rounded up to 4 values, and more
+        if n:
+            stage[:n] = v
+            gpu.check(M.lib().mhip_h2d(gpu.h, d_v, h_stage, v.nbytes), "h2d")
+        with np.errstate(invalid="ignore", over="ignore"):
+            c = np.add.accumulate(v, dtype=np.float32) if n else np.zeros(0, np.float32)
+        total = c[-1] if n else np.float32(0.0)
+        fin = c[np.isfinite(c)]
+        thrs = [np.float32(0.5)] + ([fin[len(fin) // 3], fin[-1], np.float32(fin[-1] * 2)]
+                                    if fin.size else [])
+        runs = [(M.MHIP_CHAIN_SUM, np.float32(0.0))]
+        runs += [(m, t) for t in thrs for m in (M.MHIP_CHAIN_GE, M.MHIP_CHAIN_GT)]
+        for mode, thr in runs:
+            gpu.check(M.lib().mhip_chain_f32(gpu.h, d_v, n, mode, float(thr), d_out), name)
+            got = gpu.download(d_out, (2,), np.int32)
+            if mode == M.MHIP_CHAIN_SUM:
+                k, val = n, total
+            else:
+                with np.errstate(invalid="ignore"):
+                    hit = c >= thr if mode == M.MHIP_CHAIN_GE else thr < c
+                k = int(np.argmax(hit)) if hit.any() else n
+                val = c[k] if k < n else total
+            gv = np.array([got[0]], np.int32).view(np.float32)[0]
+            assert got[1] == k, (name, mode, float(thr), int(got[1]), k)
+            assert np.array([gv]).view(np.uint32)[0] == np.array([val], np.float32).view(np.uint32)[0], \
+                (name, mode, float(thr), float(gv), float(val))
+        gpu.free(d_v)
+        say("  %-14s n=%-6d sum %r and %d searches bit-equal" % (name, n, float(total), len(runs) - 1))
+    gpu.free(d_out)
+    M.lib().mhip_host_free(gpu.h, h_stage)
