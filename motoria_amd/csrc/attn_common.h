@@ -1,0 +1,239 @@
+// The one-token attention of a layer of the Qwen3-30B-A3B shape (dim 2048,
+// 32 query and 4 key/value heads of 128): the pieces that k_attn_layer
+// (attn_layer.hip, one launch per layer) and the model stack (decode.hip,
+// every layer of a token in one launch) share. Every value follows
+// src/model/forward.c:118-165 of the reference in its order.
+#pragma once
+
+#include "mhip_internal.h"
+
+namespace mhip_attn {
+
+constexpr int D = 2048, NH = 32, NKV = 4, HD = 128;
+constexpr int QD = NH * HD, KVD = NKV * HD, NROWS = QD + 2 * KVD;  // 4096, 512, 5120
+constexpr int NB = D / 32, NBO = QD / 32;                            // 64, 128 blocks
+constexpr int GROUP = NH / NKV;
+constexpr int NT = 512, NW = NT / 64;         // the workgroup of both kernels
+constexpr int NPRE = 64;                      // cache positions a head stages in LDS
+constexpr int KPF = NPRE * HD / 4 / NT;       // float4 of those K (and V) rows per thread
+constexpr int KLD = HD + 4;                   // K row stride in LDS (rows on distinct banks)
+static_assert(KPF * 4 * NT == NPRE * HD, "whole staging rounds");
+static_assert(NB == 64 && NBO == 128, "one (two) block(s) per lane");
+
+// One 36-byte block (scale, 32 codes) of a weight row as 9 dwords.
+struct Blk {
+    float d;
+    int4 c0, c1;
+};
+__device__ __forceinline__ Blk load_blk(const uint8_t *p) {
+    const unsigned *u = (const unsigned *)p;
+    Blk b;
+    b.d = __uint_as_float(u[0]);
+    b.c0 = make_int4((int)u[1], (int)u[2], (int)u[3], (int)u[4]);
+    b.c1 = make_int4((int)u[5], (int)u[6], (int)u[7], (int)u[8]);
+    return b;
+}
+
+// DPP moves of the whole wavefront by one lane (lane 0 receives 0, resp.
+// lane 63's value).
+__device__ __forceinline__ float shr1(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x138, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float ror1(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x13C, 0xf, 0xf, false));
+}
+
+// forward.c:75-81 over one head's row in LDS by one lane: the index-order
+// double sum of squares.
+__device__ inline float head_inv_seq(const float *row, float eps) {
+    double ss = 0.0;
+    for (int i = 0; i < HD; i += 32) {
+        float4 r4[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) r4[j] = *(const float4 *)(row + i + 4 * j);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            ss = ss + (double)r4[j].x * (double)r4[j].x;
+            ss = ss + (double)r4[j].y * (double)r4[j].y;
+            ss = ss + (double)r4[j].z * (double)r4[j].z;
+            ss = ss + (double)r4[j].w * (double)r4[j].w;
+        }
+    }
+    return (float)(1.0 / sqrt(ss / HD + (double)eps));
+}
+
+// The same by one wavefront: lane l squares elements 2l, 2l+1 in double
+// (exact), a butterfly adds the 128 squares in some order, and the bracket
+// S -/+ (n + 64) 2^-52 S, which holds the index-order sum as well, gives the
+// scale when both ends round to the same float; otherwise lane 0 runs the
+// index-order sum.
+__device__ __forceinline__ float head_inv_wave(const float *row, float eps, int lane, bool force_seq) {
+    const float2 v = *(const float2 *)(row + 2 * lane);
+    double ss = (double)v.x * (double)v.x + (double)v.y * (double)v.y;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss = ss + __shfl_xor(ss, o);
+    ss = __shfl(ss, 0);
+    const double m = ss * ((double)(HD + 64) * 0x1p-52);
+    const float lo = (float)(1.0 / sqrt((ss + m) / HD + (double)eps));
+    const float hi = (float)(1.0 / sqrt((ss - m) / HD + (double)eps));
+    if (lo == hi && !force_seq) return lo;  // the same in every lane
+    float r = 0.0f;
+    if (lane == 0) r = head_inv_seq(row, eps);
+    return __shfl(r, 0);
+}
+
+// The normalized row, NeoX-rotated (forward.c:127-139): element i with
+// i + HD/2 by the angle (c, sn), w0 = w[i], w1 = w[i + HD/2] the norm weight.
+__device__ __forceinline__ void head_rope(const float *row, float inv, float w0, float w1,
+                                          double c, double sn, float *dst, int i) {
+    const int half = HD / 2;
+    const float x0 = (row[i] * inv) * w0;
+    const float x1 = (row[i + half] * inv) * w1;
+    dst[i] = (float)((double)x0 * c - (double)x1 * sn);
+    dst[i + half] = (float)((double)x0 * sn + (double)x1 * c);
+}
+
+// LDS of one query head's work.
+struct HeadLds {
+    alignas(16) float tq[HD], tk[HD], tv[HD], qs[HD], ks[HD];
+    alignas(16) float Ks[NPRE][KLD];  // the head's first cache rows
+    alignas(16) float Vs[NPRE][HD];
+    float red[NW];
+    alignas(16) int8_t hq[HD];        // Q8 codes of the head's output
+    float dsc[HD / 32];               // and their block scales
+    float inv_q, inv_k, sum;
+};
+
+// What a head's threads request before they wait for its q/k/v rows: the
+// first NPRE rows of the group's key and value cache, and (threads < HD)
+// the RoPE angle and norm weights of element tid % (HD / 2) (threads below
+// HD / 2 rotate q, the next HD / 2 k).
+struct HeadPre {
+    float4 kp[KPF], vp[KPF];
+    float rw0, rw1;
+    double rc, rs;
+};
+__device__ __forceinline__ void head_prefetch(HeadPre &p, int h, int pos, const float *kc,
+                                              const float *vc, const float *q_norm,
+                                              const float *k_norm, const double *rope, int tid) {
+    const int g = h / GROUP, npre = min(pos, NPRE);
+    p.rw0 = p.rw1 = 0.0f;
+    p.rc = p.rs = 0.0;
+    if (tid < HD) {
+        const int i = tid % (HD / 2);
+        const float *w = tid < HD / 2 ? q_norm : k_norm;
+        p.rw0 = w[i];
+        p.rw1 = w[i + HD / 2];
+        const double *rp = rope + (size_t)pos * (HD / 2) * 2;
+        p.rc = rp[2 * i];
+        p.rs = rp[2 * i + 1];
+    }
+#pragma unroll
+    for (int j = 0; j < KPF; j++) {
+        const int f = tid + NT * j, t = f / (HD / 4), c = f % (HD / 4);
+        if (t < npre) {
+            p.kp[j] = *(const float4 *)(kc + (size_t)t * KVD + (size_t)g * HD + 4 * c);
+            p.vp[j] = *(const float4 *)(vc + (size_t)t * KVD + (size_t)g * HD + 4 * c);
+        }
+    }
+}
+
+// Query head h (forward.c:127-163) by a whole workgroup, every thread
+// calling, once s.tq, s.tk, s.tv hold its q row and its group's k and v
+// rows: the head norms, RoPE, the cache append (by the group's first head),
+// scores q.k_t * scale (sequential fp32 dots, one position per thread, the
+// key row read 32 values ahead), softmax (the maximum, the restated expf,
+// the sequential sum, the division), the mix in position order, and Q8 of
+// the head's output into s.hq / s.dsc. sc: pos + 1 floats of LDS.
+__device__ inline void head_run(HeadLds &s, float *sc, const HeadPre &p, int h, int pos,
+                                float *kc, float *vc, float eps, float scale, bool force_seq,
+                                const uint64_t *etab) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = h / GROUP, n = pos + 1, npre = min(pos, NPRE);
+#pragma unroll
+    for (int j = 0; j < KPF; j++) {
+        const int f = tid + NT * j, t = f / (HD / 4), c = f % (HD / 4);
+        if (t < npre) {
+            *(float4 *)&s.Ks[t][4 * c] = p.kp[j];
+            *(float4 *)&s.Vs[t][4 * c] = p.vp[j];
+        }
+    }
+    __syncthreads();
+    if (wave < 2) {
+        const float inv = head_inv_wave(wave == 0 ? s.tq : s.tk, eps, lane, force_seq);
+        if (lane == 0) (wave == 0 ? s.inv_q : s.inv_k) = inv;
+    }
+    __syncthreads();
+    if (tid < HD / 2) head_rope(s.tq, s.inv_q, p.rw0, p.rw1, p.rc, p.rs, s.qs, tid);
+    else if (tid < HD) head_rope(s.tk, s.inv_k, p.rw0, p.rw1, p.rc, p.rs, s.ks, tid - HD / 2);
+    __syncthreads();
+    if (h % GROUP == 0 && tid < HD) {
+        kc[(size_t)pos * KVD + (size_t)g * HD + tid] = s.ks[tid];
+        vc[(size_t)pos * KVD + (size_t)g * HD + tid] = s.tv[tid];
+    }
+    for (int t = tid; t < n; t += NT) {
+        const float *kt = t == pos ? s.ks
+                          : t < npre ? &s.Ks[t][0]
+                                     : kc + (size_t)t * KVD + (size_t)g * HD;
+        float dot = 0.0f;
+        for (int i = 0; i < HD; i += 32) {
+            float4 k4[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) k4[j] = *(const float4 *)(kt + i + 4 * j);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                dot = dot + s.qs[i + 4 * j] * k4[j].x;
+                dot = dot + s.qs[i + 4 * j + 1] * k4[j].y;
+                dot = dot + s.qs[i + 4 * j + 2] * k4[j].z;
+                dot = dot + s.qs[i + 4 * j + 3] * k4[j].w;
+            }
+        }
+        sc[t] = dot * scale;
+    }
+    __syncthreads();
+    float mx = -__builtin_inff();
+    for (int t = tid; t < n; t += NT) mx = fmaxf(mx, sc[t]);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+    if (lane == 0) s.red[wave] = mx;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < NW; w++) mx = fmaxf(mx, s.red[w]);
+    for (int t = tid; t < n; t += NT) sc[t] = mia_expf_glibc_tab(sc[t] - mx, etab);
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+        for (int t = 0; t < n; t++) sum = sum + sc[t];
+        s.sum = sum;
+    }
+    __syncthreads();
+    const float sum = s.sum;
+    for (int t = tid; t < n; t += NT) sc[t] = sc[t] / sum;
+    __syncthreads();
+    if (tid < HD) {
+        const float *vt = vc + (size_t)g * HD + tid;
+        float o = 0.0f;
+        int t = 0;
+        for (; t < npre; t++) o = o + sc[t] * s.Vs[t][tid];
+        for (; t + 16 <= pos; t += 16) {
+            float vv[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) vv[j] = vt[(size_t)(t + j) * KVD];
+#pragma unroll
+            for (int j = 0; j < 16; j++) o = o + sc[t + j] * vv[j];
+        }
+        for (; t < pos; t++) o = o + sc[t] * vt[(size_t)t * KVD];
+        o = o + sc[pos] * s.tv[tid];
+        float am = fmaxf(0.0f, fabsf(o));
+#pragma unroll
+        for (int m = 16; m >= 1; m >>= 1) am = fmaxf(am, __shfl_xor(am, m, 32));
+        const float d = am / 127.0f;
+        const float qi = d != 0.0f ? 1.0f / d : 0.0f;
+        s.hq[tid] = (int8_t)roundf(o * qi);
+        if ((lane & 31) == 0) s.dsc[tid / 32] = d;
+    }
+    __syncthreads();
+}
+
+}  // namespace mhip_attn

@@ -24,24 +24,17 @@
 // that runs out (a workgroup not resident) marks the launch aborted and
 // every later wait gives up at once; x is then left as it was and the caller
 // reruns the layer through the per-stage kernels.
-#include "mhip_internal.h"
+#include "attn_common.h"
 
 namespace {
 
-constexpr int D = 2048, NH = 32, NKV = 4, HD = 128;
-constexpr int QD = NH * HD, KVD = NKV * HD, NROWS = QD + 2 * KVD;  // 4096, 512, 5120
-constexpr int NB = D / 32, NBO = QD / 32;                            // 64, 128 blocks
-constexpr int NWG = 256, NT = 512, NW = NT / 64;
+using namespace mhip_attn;
+
+constexpr int NWG = 256;
 constexpr int GW = NWG * NW;                  // 2048 wavefronts
 constexpr int RPW = (NROWS + GW - 1) / GW;    // at most 3 q/k/v rows per wavefront
-constexpr int GROUP = NH / NKV;
-constexpr int NPRE = 64;                      // cache positions a head stages in LDS
-constexpr int KPF = NPRE * HD / 4 / NT;       // float4 of those K (and V) rows per thread
-constexpr int KLD = HD + 4;                   // K row stride in LDS (rows on distinct banks)
-static_assert(KPF * 4 * NT == NPRE * HD, "whole staging rounds");
 constexpr long SPIN = 1L << 18;
 static_assert(D == GW, "one Wo row per wavefront");
-static_assert(NB == 64 && NBO == 128, "one (two) block(s) per lane");
 
 typedef unsigned long long tw;
 
@@ -97,90 +90,12 @@ __device__ __forceinline__ unsigned get_word(const AttnArgs &a, const tw *p) {
     return (unsigned)v;
 }
 
-// One 36-byte block (scale, 32 codes) of a weight row as 9 dwords.
-struct Blk {
-    float d;
-    int4 c0, c1;
-};
-__device__ __forceinline__ Blk load_blk(const uint8_t *p) {
-    const unsigned *u = (const unsigned *)p;
-    Blk b;
-    b.d = __uint_as_float(u[0]);
-    b.c0 = make_int4((int)u[1], (int)u[2], (int)u[3], (int)u[4]);
-    b.c1 = make_int4((int)u[5], (int)u[6], (int)u[7], (int)u[8]);
-    return b;
-}
-
-// DPP moves of the whole wavefront by one lane (lane 0 receives 0, resp.
-// lane 63's value).
-__device__ __forceinline__ float shr1(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x138, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float ror1(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x13C, 0xf, 0xf, false));
-}
-
-// forward.c:75-81 over one head's row in LDS, by one wavefront: lane l
-// squares elements 2l, 2l+1 in double (exact), a butterfly adds the 128
-// squares in some order, and the bracket S -/+ (n + 64) 2^-52 S, which holds
-// the reference's index-order sum as well, gives the scale when both ends
-// round to the same float; otherwise lane 0 runs the index-order sum
-// (head_inv_seq).
-__device__ float head_inv_seq(const float *row, float eps);
-__device__ __forceinline__ float head_inv_wave(const float *row, float eps, int lane, bool force_seq) {
-    const float2 v = *(const float2 *)(row + 2 * lane);
-    double ss = (double)v.x * (double)v.x + (double)v.y * (double)v.y;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss = ss + __shfl_xor(ss, o);
-    ss = __shfl(ss, 0);
-    const double m = ss * ((double)(HD + 64) * 0x1p-52);
-    const float lo = (float)(1.0 / sqrt((ss + m) / HD + (double)eps));
-    const float hi = (float)(1.0 / sqrt((ss - m) / HD + (double)eps));
-    if (lo == hi && !force_seq) return lo;  // the same in every lane
-    float r = 0.0f;
-    if (lane == 0) r = head_inv_seq(row, eps);
-    return __shfl(r, 0);
-}
-// The index-order sum itself (one lane).
-__device__ float head_inv_seq(const float *row, float eps) {
-    double ss = 0.0;
-    for (int i = 0; i < HD; i += 32) {
-        float4 r4[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) r4[j] = *(const float4 *)(row + i + 4 * j);
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            ss = ss + (double)r4[j].x * (double)r4[j].x;
-            ss = ss + (double)r4[j].y * (double)r4[j].y;
-            ss = ss + (double)r4[j].z * (double)r4[j].z;
-            ss = ss + (double)r4[j].w * (double)r4[j].w;
-        }
-    }
-    return (float)(1.0 / sqrt(ss / HD + (double)eps));
-}
-
-// The normalized row, NeoX-rotated (forward.c:127-139): element i with
-// i + HD/2 by the angle (c, sn), w0 = w[i], w1 = w[i + HD/2] the norm weight.
-__device__ __forceinline__ void head_rope(const float *row, float inv, float w0, float w1,
-                                          double c, double sn, float *dst, int i) {
-    const int half = HD / 2;
-    const float x0 = (row[i] * inv) * w0;
-    const float x1 = (row[i + half] * inv) * w1;
-    dst[i] = (float)((double)x0 * c - (double)x1 * sn);
-    dst[i + half] = (float)((double)x0 * sn + (double)x1 * c);
-}
-
 struct Lds {
     alignas(16) int8_t xq[D];         // Q8(xn) codes
     alignas(16) int8_t attq[QD];      // the heads' codes
     float xs[NB];
     float atts[NBO];
-    alignas(16) float tq[HD], tk[HD], tv[HD], qs[HD], ks[HD];
-    alignas(16) float Ks[NPRE][KLD];  // the head's first cache rows
-    alignas(16) float Vs[NPRE][HD];
-    float red[NW];
-    int8_t hq[HD];
-    float inv_q, inv_k, sum;
+    HeadLds head;                     // the query head of workgroups 0..NH-1
     uint64_t etab[32];
 };
 
@@ -216,32 +131,8 @@ __global__ __launch_bounds__(NT) void k_attn_layer(AttnArgs a) {
         }
     }
     const float xold = a.x[gw];
-    const int npre = min(a.pos, NPRE);
-    float4 kp[KPF], vp[KPF];
-    // the RoPE angle and norm weights of element i = tid % 64 (threads < 64
-    // rotate q, 64..127 k)
-    float rw0 = 0.0f, rw1 = 0.0f;
-    double rc = 0.0, rs = 0.0;
-    if (b < NH && tid < HD) {
-        const int i = tid % (HD / 2);
-        const float *w = tid < HD / 2 ? a.q_norm : a.k_norm;
-        rw0 = w[i];
-        rw1 = w[i + HD / 2];
-        const double *rp = a.rope + (size_t)a.pos * (HD / 2) * 2;
-        rc = rp[2 * i];
-        rs = rp[2 * i + 1];
-    }
-    if (b < NH) {
-        const int g = b / GROUP;
-#pragma unroll
-        for (int j = 0; j < KPF; j++) {
-            const int f = tid + NT * j, t = f / (HD / 4), c = f % (HD / 4);
-            if (t < npre) {
-                kp[j] = *(const float4 *)(a.kc + (size_t)t * KVD + (size_t)g * HD + 4 * c);
-                vp[j] = *(const float4 *)(a.vc + (size_t)t * KVD + (size_t)g * HD + 4 * c);
-            }
-        }
-    }
+    HeadPre hp;
+    if (b < NH) head_prefetch(hp, b, a.pos, a.kc, a.vc, a.q_norm, a.k_norm, a.rope, tid);
     // (a barrier keeps the other wavefronts' weight rows behind those requests)
     __syncthreads();
     Blk wr[RPW];
@@ -350,102 +241,18 @@ __global__ __launch_bounds__(NT) void k_attn_layer(AttnArgs a) {
 
     // ---- P3: query head b (k_attn_head) --------------------------------------------
     if (b < NH) {
-        const int h = b, g = h / GROUP, n = a.pos + 1;
-        if (tid < HD) sh.tq[tid] = __uint_as_float(get_word(a, &a.ws->qkv[h * HD + tid]));
-        else if (tid < 2 * HD) sh.tk[tid - HD] = __uint_as_float(get_word(a, &a.ws->qkv[QD + g * HD + tid - HD]));
+        const int h = b, g = h / GROUP;
+        if (tid < HD) sh.head.tq[tid] = __uint_as_float(get_word(a, &a.ws->qkv[h * HD + tid]));
+        else if (tid < 2 * HD)
+            sh.head.tk[tid - HD] = __uint_as_float(get_word(a, &a.ws->qkv[QD + g * HD + tid - HD]));
         else if (tid < 3 * HD)
-            sh.tv[tid - 2 * HD] = __uint_as_float(get_word(a, &a.ws->qkv[QD + KVD + g * HD + tid - 2 * HD]));
-#pragma unroll
-        for (int j = 0; j < KPF; j++) {
-            const int f = tid + NT * j, t = f / (HD / 4), c = f % (HD / 4);
-            if (t < npre) {
-                *(float4 *)&sh.Ks[t][4 * c] = kp[j];
-                *(float4 *)&sh.Vs[t][4 * c] = vp[j];
-            }
-        }
-        __syncthreads();
+            sh.head.tv[tid - 2 * HD] =
+                __uint_as_float(get_word(a, &a.ws->qkv[QD + KVD + g * HD + tid - 2 * HD]));
         ATRACE(4, 0);
-        if (wave < 2) {
-            const float inv = head_inv_wave(wave == 0 ? sh.tq : sh.tk, a.eps, lane,
-                                            (a.flags & MHIP_FORCE_SEQ_RMS) != 0);
-            if (lane == 0) (wave == 0 ? sh.inv_q : sh.inv_k) = inv;
-        }
-        __syncthreads();
-        if (tid < HD / 2) head_rope(sh.tq, sh.inv_q, rw0, rw1, rc, rs, sh.qs, tid);
-        else if (tid < HD) head_rope(sh.tk, sh.inv_k, rw0, rw1, rc, rs, sh.ks, tid - HD / 2);
-        __syncthreads();
-        if (h % GROUP == 0 && tid < HD) {
-            a.kc[(size_t)a.pos * KVD + (size_t)g * HD + tid] = sh.ks[tid];
-            a.vc[(size_t)a.pos * KVD + (size_t)g * HD + tid] = sh.tv[tid];
-        }
-        // scores (forward.c:143-149): sequential fp32 dots, one position per
-        // thread, the key row read 32 values ahead of the additions
-        for (int t = tid; t < n; t += NT) {
-            const float *kt = t == a.pos ? sh.ks
-                              : t < npre ? &sh.Ks[t][0]
-                                         : a.kc + (size_t)t * KVD + (size_t)g * HD;
-            float dot = 0.0f;
-            for (int i = 0; i < HD; i += 32) {
-                float4 k4[8];
-#pragma unroll
-                for (int j = 0; j < 8; j++) k4[j] = *(const float4 *)(kt + i + 4 * j);
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    dot = dot + sh.qs[i + 4 * j] * k4[j].x;
-                    dot = dot + sh.qs[i + 4 * j + 1] * k4[j].y;
-                    dot = dot + sh.qs[i + 4 * j + 2] * k4[j].z;
-                    dot = dot + sh.qs[i + 4 * j + 3] * k4[j].w;
-                }
-            }
-            sc[t] = dot * a.scale;
-        }
-        __syncthreads();
-        // softmax (forward.c:150-156): the maximum (order-free), the restated
-        // expf, the sequential sum, the division
-        float mx = -__builtin_inff();
-        for (int t = tid; t < n; t += NT) mx = fmaxf(mx, sc[t]);
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
-        if (lane == 0) sh.red[wave] = mx;
-        __syncthreads();
-#pragma unroll
-        for (int w = 0; w < NW; w++) mx = fmaxf(mx, sh.red[w]);
-        for (int t = tid; t < n; t += NT) sc[t] = mia_expf_glibc_tab(sc[t] - mx, sh.etab);
-        __syncthreads();
-        if (tid == 0) {
-            float sum = 0.0f;
-            for (int t = 0; t < n; t++) sum = sum + sc[t];
-            sh.sum = sum;
-        }
-        __syncthreads();
-        const float sum = sh.sum;
-        for (int t = tid; t < n; t += NT) sc[t] = sc[t] / sum;
-        __syncthreads();
-        // mix (forward.c:157-162), then Q8 of the head's output (quant.c:11-27)
-        if (tid < HD) {
-            const float *vt = a.vc + (size_t)g * HD + tid;
-            float o = 0.0f;
-            int t = 0;
-            for (; t < npre; t++) o = o + sc[t] * sh.Vs[t][tid];
-            for (; t + 16 <= a.pos; t += 16) {
-                float vv[16];
-#pragma unroll
-                for (int j = 0; j < 16; j++) vv[j] = vt[(size_t)(t + j) * KVD];
-#pragma unroll
-                for (int j = 0; j < 16; j++) o = o + sc[t + j] * vv[j];
-            }
-            for (; t < a.pos; t++) o = o + sc[t] * vt[(size_t)t * KVD];
-            o = o + sc[a.pos] * sh.tv[tid];
-            float am = fmaxf(0.0f, fabsf(o));
-#pragma unroll
-            for (int m = 16; m >= 1; m >>= 1) am = fmaxf(am, __shfl_xor(am, m, 32));
-            const float d = am / 127.0f;
-            const float qi = d != 0.0f ? 1.0f / d : 0.0f;
-            sh.hq[tid] = (int8_t)roundf(o * qi);
-            if ((lane & 31) == 0) put_word(&a.ws->atts[h * (HD / 32) + tid / 32], __float_as_uint(d), a.tag);
-        }
-        __syncthreads();
-        if (tid < HD / 4) put_word(&a.ws->attq[h * (HD / 4) + tid], ((const unsigned *)sh.hq)[tid], a.tag);
+        head_run(sh.head, sc, hp, h, a.pos, a.kc, a.vc, a.eps, a.scale,
+                 (a.flags & MHIP_FORCE_SEQ_RMS) != 0, sh.etab);
+        if (tid < HD / 32) put_word(&a.ws->atts[h * (HD / 32) + tid], __float_as_uint(sh.head.dsc[tid]), a.tag);
+        if (tid < HD / 4) put_word(&a.ws->attq[h * (HD / 4) + tid], ((const unsigned *)sh.head.hq)[tid], a.tag);
         ATRACE(5, 0);
     }
 
