@@ -65,10 +65,13 @@ const mia_file_info *mia_gpu_model_info(const mia_gpu_model *m);
  * crosses PCIe; s->rng advances as mia_sample's would. */
 int mia_gpu_model_step_sample(mia_gpu_model *m, int token, int pos, mhip_sampler *s);
 
-/* Flags of the MoE layers (include/mia_hip.h), as mia_moe_set_flags:
- * MHIP_FORCE_EXACT_ROUTER (the default): the one-layer launch of the decode
- * kernel with the reference's sequential router chains; logits bit-equal to
- * the reference's. 0: the same launch with the certified parallel router
+/* Flags of the MoE layers (include/mia_hip.h), as mia_moe_set_flags. At the
+ * Qwen3-30B-A3B shape a step is one launch of the model stack (every
+ * layer's attention and MoE, mhip_model_stack); MHIP_MODEL_PER_LAYER asks
+ * for one attention and one MoE launch per layer instead (the same bits).
+ * MHIP_FORCE_EXACT_ROUTER (the default): the decode kernel's MoE with the
+ * reference's sequential router chains; logits bit-equal to the
+ * reference's. 0: the same with the certified parallel router
  * (expert indices bit-equal, gate weights within ~1e-6 relative; through the
  * requantizations of later layers the logits then move by whole Q8 steps,
  * ~5e-4 of max|logit| each, up to ~1e-2 in all). MHIP_EXACT_EXPERTS: the
@@ -78,11 +81,17 @@ int mia_gpu_model_step_sample(mia_gpu_model *m, int token, int pos, mhip_sampler
  * exact chains before the expert stream in every layer (the path of a
  * layer whose ranking is not certified). MHIP_ATTN_FORCE_ABORT: every
  * one-launch attention (mhip_attention_layer, used where the shape allows
- * it) aborts and the step reruns from that layer per stage. */
+ * it) aborts and the step reruns from that layer per stage. Either forced
+ * abort stops a model stack launch, and the token reruns per stage. */
 void mia_gpu_model_set_flags(mia_gpu_model *m, int flags);
-/* Launches of the last step (decode and one-launch attention) that aborted
- * (their layers rerun per stage). */
+/* Launches of the last step (model stack, or decode and one-launch
+ * attention) that aborted (their layers rerun per stage). */
 int mia_gpu_model_aborts(const mia_gpu_model *m);
+/* With MHIP_DECODE_TRACE in the flags, the model stack launch of the last
+ * step records the stage timestamps of mhip_decode_trace; this copies them
+ * out (out[MHIP_TRACE_NL][256][MHIP_TRACE_SLOTS]). 0 or -1 (no model stack
+ * at this shape). Diagnostic. */
+int mia_gpu_model_trace(mia_gpu_model *m, unsigned long long *out);
 
 #ifdef __cplusplus
 }

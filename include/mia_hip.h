@@ -249,7 +249,7 @@ int mhip_decode_status(mhip_ctx *c, const void *d_ws, int status[4]);
  * Diagnostic. */
 #define MHIP_TRACE_L0 8
 #define MHIP_TRACE_NL 8
-#define MHIP_TRACE_SLOTS 32
+#define MHIP_TRACE_SLOTS 40
 int mhip_decode_trace(mhip_ctx *c, const void *d_ws, unsigned long long *out);
 
 /* ---- attention and output head of one token (decode) ---------------------
@@ -313,6 +313,41 @@ int mhip_attention_layer(mhip_ctx *c, const mhip_attn_dims *s, const float *d_at
                          const float *d_q_norm, const float *d_k_norm, const double *d_rope,
                          float *d_kc, float *d_vc, int pos, int max_seq, float *d_x,
                          float *d_x_in, float *d_x_out, void *d_ws, int *d_status, int flags);
+
+/*
+ * No counterpart in the reference, whose mia_model_step (forward.c:199-217)
+ * calls the attention and moe() of each layer in turn: every layer of one
+ * token -- the attention of mhip_attention_layer, then the MoE of
+ * mhip_decode_stack -- in one launch, for callers that step a whole model at
+ * the Qwen3-30B-A3B shape (the MoE shape of mhip_decode_stack and the
+ * attention shape of mhip_attention_layer). Bit-equal to running those two
+ * per layer. d_al[L] (device) holds each layer's attention tensors and its
+ * K/V cache; d_x is the token's embedding row on entry and x after layer
+ * L - 1 on exit; d_ws: mhip_model_stack_ws_bytes() (256-byte aligned; the
+ * context clears it when it first sees it). *d_status (int[4], device)
+ * receives the launch's status words as mhip_decode_status gives them
+ * ([0] abort bits: 1, 2 as there, 4 when MHIP_DECODE_FORCE_ABORT or
+ * MHIP_ATTN_FORCE_ABORT asked for one); after an abort d_x and the cache
+ * rows at pos are invalid and the caller reruns the token per layer.
+ * _supported: 1 when the shapes, max_seq and the device fit, 0 when not, -1
+ * on an error.
+ */
+typedef struct {
+    const float *attn_norm, *q_norm, *k_norm; /* [dim], [head_dim], [head_dim] */
+    const void *wq, *wk, *wv, *wo;             /* Q8_0 rows */
+    float *kc, *vc;                            /* [max_seq][n_kv_heads*head_dim] */
+} mhip_attn_layer;
+#define MHIP_MODEL_STACK_MAX_SEQ 8192 /* positions whose scores fit the kernel's LDS */
+#define MHIP_MODEL_PER_LAYER 128      /* mia_gpu_model steps: one launch per layer's
+                                         attention and per layer's MoE, not the stack */
+size_t mhip_model_stack_ws_bytes(void);
+int mhip_model_stack_supported(mhip_ctx *c, const mhip_dims *s, const mhip_attn_dims *as,
+                               int max_seq);
+int mhip_model_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
+                     const void *d_table, const float *d_router_dl, const float *d_router_t,
+                     const float *d_norm, const float *d_bias, const mhip_attn_dims *as,
+                     const mhip_attn_layer *d_al, const double *d_rope, int pos, int max_seq,
+                     float *d_x, int L, void *d_ws, int *d_status, int flags);
 
 /* ---- HIP graphs -----------------------------------------------------------
  * No counterpart in the reference. The launches queued on a context between

@@ -30,9 +30,10 @@ MHIP_DECODE_FORCE_ABORT = 16
 MHIP_DECODE_CHAINS_FIRST = 32
 MHIP_ATTN_FORCE_ABORT = 64
 MHIP_CHAIN_SUM, MHIP_CHAIN_GE, MHIP_CHAIN_GT = 0, 1, 2
+MHIP_MODEL_PER_LAYER = 128
 DECODE_MAX_LAYERS = 256  # MHIP_DECODE_MAX_LAYERS
 GEMM_MIN_A = 2048  # MHIP_GEMM_MIN_A
-TRACE_L0, TRACE_NL, TRACE_SLOTS = 8, 8, 32  # decode trace window (MHIP_TRACE_* in mia_hip.h)
+TRACE_L0, TRACE_NL, TRACE_SLOTS = 8, 8, 40  # decode trace window (MHIP_TRACE_* in mia_hip.h)
 STAGES = ["rmsnorm", "router", "dispatch", "gateup", "down", "combine", "decode"]
 
 
@@ -158,6 +159,10 @@ SIGNATURES = {
     "mhip_sample_scratch_bytes": (_sz, [_i]),
     "mhip_sample": (_i, [_p, ctypes.POINTER(Sampler), _p, _p, _p]),
     "mhip_chain_f32": (_i, [_p, _p, _i, _i, _f, _p]),
+    "mhip_model_stack_ws_bytes": (_sz, []),
+    "mhip_model_stack_supported": (_i, [_p, _p, _p, _i]),
+    "mhip_model_stack": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _p, _i, _p,
+                              _p, _i]),
     "mhip_quantize_q8": (_i, [_p, _p, _p, _i]),
     "mhip_dequantize_q8": (_i, [_p, _p, _p, _i]),
     "mhip_matvec": (_i, [_p, _p, _p, _i, _p, _p, _i, _i]),
@@ -216,6 +221,7 @@ SIGNATURES = {
     "mia_gpu_model_info": (ctypes.POINTER(FileInfo), [_p]),
     "mia_gpu_model_set_flags": (None, [_p, _i]),
     "mia_gpu_model_aborts": (_i, [_p]),
+    "mia_gpu_model_trace": (_i, [_p, _p]),
     # include/mia/serve.h
     "mia_bpe_open": (_i, [ctypes.POINTER(_p), _p, _sz]),
     "mia_bpe_close": (None, [_p]),
@@ -545,6 +551,15 @@ class GpuModel:
     def aborts(self):
         """Decode launches of the last step that aborted (rerun per stage)."""
         return lib().mia_gpu_model_aborts(self.h)
+
+    def trace(self):
+        """Stage timestamps of the last step's model stack launch (flags with
+        MHIP_DECODE_TRACE): [TRACE_NL layers][256 workgroups][TRACE_SLOTS]."""
+        out = np.zeros((TRACE_NL, 256, TRACE_SLOTS), dtype=np.uint64)
+        if lib().mia_gpu_model_trace(self.h, out.ctypes.data):
+            raise RuntimeError("mia_gpu_model_trace: " +
+                               lib().mia_gpu_model_error(self.h).decode())
+        return out
 
     def step_sample(self, token, pos, sampler):
         """The next token picked on the device (sampler: a Sampler over the

@@ -14,25 +14,47 @@ constexpr int QD = NH * HD, KVD = NKV * HD, NROWS = QD + 2 * KVD;  // 4096, 512,
 constexpr int NB = D / 32, NBO = QD / 32;                            // 64, 128 blocks
 constexpr int GROUP = NH / NKV;
 constexpr int NT = 512, NW = NT / 64;         // the workgroup of both kernels
-constexpr int NPRE = 64;                      // cache positions a head stages in LDS
-constexpr int KPF = NPRE * HD / 4 / NT;       // float4 of those K (and V) rows per thread
 constexpr int KLD = HD + 4;                   // K row stride in LDS (rows on distinct banks)
-static_assert(KPF * 4 * NT == NPRE * HD, "whole staging rounds");
 static_assert(NB == 64 && NBO == 128, "one (two) block(s) per lane");
+
+// Pointers into global memory (address space 1). Loads and stores through
+// them compile to global_* instructions also where the pointer was read from
+// memory; a generic pointer of that kind gives flat_* ones, which the
+// compiler has to wait for together with LDS traffic.
+template <class T> using gptr = __attribute__((address_space(1))) T *;
+template <class T> __device__ __forceinline__ gptr<T> glob(T *p) { return (gptr<T>)p; }
+// 16 bytes through such a pointer (the load goes through the built-in vector
+// type: float4's assignment operators take generic references only)
+typedef float f4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld4(gptr<const float4> p) {
+    const f4v v = *(gptr<const f4v>)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 ld4(const float4 *p) { return *p; }
 
 // One 36-byte block (scale, 32 codes) of a weight row as 9 dwords.
 struct Blk {
     float d;
     int4 c0, c1;
 };
-__device__ __forceinline__ Blk load_blk(const uint8_t *p) {
-    const unsigned *u = (const unsigned *)p;
+__device__ __forceinline__ Blk load_blk(gptr<const uint8_t> p) {
+    const gptr<const unsigned> u = (gptr<const unsigned>)p;
     Blk b;
     b.d = __uint_as_float(u[0]);
     b.c0 = make_int4((int)u[1], (int)u[2], (int)u[3], (int)u[4]);
     b.c1 = make_int4((int)u[5], (int)u[6], (int)u[7], (int)u[8]);
     return b;
 }
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// 16 bytes per lane from global memory straight into LDS, lane i's at
+// lds + 16 i (lds wave-uniform); completion is counted by vmcnt.
+__device__ __forceinline__ void dma16(unsigned lds, const void *g) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
 
 // DPP moves of the whole wavefront by one lane (lane 0 receives 0, resp.
 // lane 63's value).
@@ -93,7 +115,8 @@ __device__ __forceinline__ void head_rope(const float *row, float inv, float w0,
     dst[i + half] = (float)((double)x0 * sn + (double)x1 * c);
 }
 
-// LDS of one query head's work.
+// LDS of one query head's work; NPRE cache positions are staged in LDS.
+template <int NPRE>
 struct HeadLds {
     alignas(16) float tq[HD], tk[HD], tv[HD], qs[HD], ks[HD];
     alignas(16) float Ks[NPRE][KLD];  // the head's first cache rows
@@ -107,56 +130,114 @@ struct HeadLds {
 // What a head's threads request before they wait for its q/k/v rows: the
 // first NPRE rows of the group's key and value cache, and (threads < HD)
 // the RoPE angle and norm weights of element tid % (HD / 2) (threads below
-// HD / 2 rotate q, the next HD / 2 k).
-struct HeadPre {
-    float4 kp[KPF], vp[KPF];
+// HD / 2 rotate q, the next HD / 2 k). The cache rows go to registers
+// (DMA false) or straight into the head's LDS (DMA true).
+struct HeadRope {
     float rw0, rw1;
     double rc, rs;
 };
-__device__ __forceinline__ void head_prefetch(HeadPre &p, int h, int pos, const float *kc,
-                                              const float *vc, const float *q_norm,
-                                              const float *k_norm, const double *rope, int tid) {
+template <int NPRE, bool DMA = false>
+struct HeadPre : HeadRope {
+    static constexpr int KPF = NPRE * HD / 4 / NT;  // float4 of the K (and V) rows per thread
+    static_assert(KPF * 4 * NT == NPRE * HD, "whole staging rounds");
+    float4 kp[KPF], vp[KPF];
+};
+template <int NPRE>
+struct HeadPre<NPRE, true> : HeadRope {};
+
+template <int NPRE, bool DMA>
+__device__ __forceinline__ void head_prefetch(HeadPre<NPRE, DMA> &p, HeadLds<NPRE> &s, int h,
+                                              int pos, gptr<const float> kc,
+                                              gptr<const float> vc, gptr<const float> q_norm,
+                                              gptr<const float> k_norm, gptr<const double> rope,
+                                              int tid) {
     const int g = h / GROUP, npre = min(pos, NPRE);
     p.rw0 = p.rw1 = 0.0f;
     p.rc = p.rs = 0.0;
     if (tid < HD) {
         const int i = tid % (HD / 2);
-        const float *w = tid < HD / 2 ? q_norm : k_norm;
+        const gptr<const float> w = tid < HD / 2 ? q_norm : k_norm;
         p.rw0 = w[i];
         p.rw1 = w[i + HD / 2];
-        const double *rp = rope + (size_t)pos * (HD / 2) * 2;
+        const gptr<const double> rp = rope + (size_t)pos * (HD / 2) * 2;
         p.rc = rp[2 * i];
         p.rs = rp[2 * i + 1];
     }
+    if constexpr (DMA) {
+        // wavefront w moves rows 2q, 2q + 1 for q = w, w + NW, ...: the V rows
+        // are contiguous in LDS (one instruction), the K rows KLD apart (one
+        // instruction per half wavefront). Rows past npre that a pair holds
+        // are read from row min(t, pos), in the cache, and never used.
+        static_assert(NPRE % 2 == 0, "row pairs");
+        const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int half = lane >> 5, c = lane & 31;
+        const unsigned ks = (unsigned)(uintptr_t)&s.Ks[0][0], vs = (unsigned)(uintptr_t)&s.Vs[0][0];
+        for (int q = wave; 2 * q < npre; q += NW) {
+            const int t0 = 2 * q, t = min(t0 + half, pos);
+            const size_t off = (size_t)t * KVD + (size_t)g * HD + 4 * c;
+            dma16(__builtin_amdgcn_readfirstlane(vs + (unsigned)(t0 * HD * 4)), (const float *)(vc + off));
+            const unsigned k0 = __builtin_amdgcn_readfirstlane(ks + (unsigned)(t0 * KLD * 4));
+            const unsigned k1 = __builtin_amdgcn_readfirstlane(ks + (unsigned)((t0 + 1) * KLD * 4 - 32 * 16));
+            if (half == 0) dma16(k0, (const float *)(kc + off));
+            else dma16(k1, (const float *)(kc + off));
+        }
+    } else {
 #pragma unroll
-    for (int j = 0; j < KPF; j++) {
-        const int f = tid + NT * j, t = f / (HD / 4), c = f % (HD / 4);
-        if (t < npre) {
-            p.kp[j] = *(const float4 *)(kc + (size_t)t * KVD + (size_t)g * HD + 4 * c);
-            p.vp[j] = *(const float4 *)(vc + (size_t)t * KVD + (size_t)g * HD + 4 * c);
+        for (int j = 0; j < HeadPre<NPRE>::KPF; j++) {
+            const int f = tid + NT * j, t = f / (HD / 4), c = f % (HD / 4);
+            if (t < npre) {
+                p.kp[j] = ld4((gptr<const float4>)(kc + (size_t)t * KVD + (size_t)g * HD + 4 * c));
+                p.vp[j] = ld4((gptr<const float4>)(vc + (size_t)t * KVD + (size_t)g * HD + 4 * c));
+            }
         }
     }
 }
 
+// q.k_t for one position: the sequential fp32 dot over the HD elements, the
+// key row (in LDS or global memory) read 32 values ahead.
+template <class P4>
+__device__ __forceinline__ float head_dot(const float *qs, P4 k4p) {
+    float dot = 0.0f;
+    for (int i = 0; i < HD / 4; i += 8) {
+        float4 k4[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) k4[j] = ld4(k4p + i + j);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            dot = dot + qs[4 * (i + j)] * k4[j].x;
+            dot = dot + qs[4 * (i + j) + 1] * k4[j].y;
+            dot = dot + qs[4 * (i + j) + 2] * k4[j].z;
+            dot = dot + qs[4 * (i + j) + 3] * k4[j].w;
+        }
+    }
+    return dot;
+}
+
 // Query head h (forward.c:127-163) by a whole workgroup, every thread
 // calling, once s.tq, s.tk, s.tv hold its q row and its group's k and v
-// rows: the head norms, RoPE, the cache append (by the group's first head),
+// rows (with DMA, after head_prefetch issued the cache rows' copies): the
+// head norms, RoPE, the cache append (by the group's first head),
 // scores q.k_t * scale (sequential fp32 dots, one position per thread, the
 // key row read 32 values ahead), softmax (the maximum, the restated expf,
 // the sequential sum, the division), the mix in position order, and Q8 of
 // the head's output into s.hq / s.dsc. sc: pos + 1 floats of LDS.
-__device__ inline void head_run(HeadLds &s, float *sc, const HeadPre &p, int h, int pos,
-                                float *kc, float *vc, float eps, float scale, bool force_seq,
-                                const uint64_t *etab) {
+template <int NPRE, bool DMA>
+__device__ inline void head_run(HeadLds<NPRE> &s, float *sc, const HeadPre<NPRE, DMA> &p, int h,
+                                int pos, gptr<float> kcg, gptr<float> vcg, float eps, float scale,
+                                bool force_seq, const uint64_t *etab) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = h / GROUP, n = pos + 1, npre = min(pos, NPRE);
+    if constexpr (DMA) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wavefront's cache rows are in
+    } else {
 #pragma unroll
-    for (int j = 0; j < KPF; j++) {
-        const int f = tid + NT * j, t = f / (HD / 4), c = f % (HD / 4);
-        if (t < npre) {
-            *(float4 *)&s.Ks[t][4 * c] = p.kp[j];
-            *(float4 *)&s.Vs[t][4 * c] = p.vp[j];
+        for (int j = 0; j < HeadPre<NPRE>::KPF; j++) {
+            const int f = tid + NT * j, t = f / (HD / 4), c = f % (HD / 4);
+            if (t < npre) {
+                *(float4 *)&s.Ks[t][4 * c] = p.kp[j];
+                *(float4 *)&s.Vs[t][4 * c] = p.vp[j];
+            }
         }
     }
     __syncthreads();
@@ -169,26 +250,15 @@ __device__ inline void head_run(HeadLds &s, float *sc, const HeadPre &p, int h, 
     else if (tid < HD) head_rope(s.tk, s.inv_k, p.rw0, p.rw1, p.rc, p.rs, s.ks, tid - HD / 2);
     __syncthreads();
     if (h % GROUP == 0 && tid < HD) {
-        kc[(size_t)pos * KVD + (size_t)g * HD + tid] = s.ks[tid];
-        vc[(size_t)pos * KVD + (size_t)g * HD + tid] = s.tv[tid];
+        kcg[(size_t)pos * KVD + (size_t)g * HD + tid] = s.ks[tid];
+        vcg[(size_t)pos * KVD + (size_t)g * HD + tid] = s.tv[tid];
     }
     for (int t = tid; t < n; t += NT) {
-        const float *kt = t == pos ? s.ks
-                          : t < npre ? &s.Ks[t][0]
-                                     : kc + (size_t)t * KVD + (size_t)g * HD;
-        float dot = 0.0f;
-        for (int i = 0; i < HD; i += 32) {
-            float4 k4[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) k4[j] = *(const float4 *)(kt + i + 4 * j);
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                dot = dot + s.qs[i + 4 * j] * k4[j].x;
-                dot = dot + s.qs[i + 4 * j + 1] * k4[j].y;
-                dot = dot + s.qs[i + 4 * j + 2] * k4[j].z;
-                dot = dot + s.qs[i + 4 * j + 3] * k4[j].w;
-            }
-        }
+        // a key row in LDS (the new one, or staged) or in the cache
+        const float dot = t == pos || t < npre
+                              ? head_dot(s.qs, (const float4 *)(t == pos ? s.ks : &s.Ks[t][0]))
+                              : head_dot(s.qs, (gptr<const float4>)(kcg + (size_t)t * KVD +
+                                                                    (size_t)g * HD));
         sc[t] = dot * scale;
     }
     __syncthreads();
@@ -212,7 +282,7 @@ __device__ inline void head_run(HeadLds &s, float *sc, const HeadPre &p, int h, 
     for (int t = tid; t < n; t += NT) sc[t] = sc[t] / sum;
     __syncthreads();
     if (tid < HD) {
-        const float *vt = vc + (size_t)g * HD + tid;
+        const gptr<const float> vt = vcg + (size_t)g * HD + tid;
         float o = 0.0f;
         int t = 0;
         for (; t < npre; t++) o = o + sc[t] * s.Vs[t][tid];

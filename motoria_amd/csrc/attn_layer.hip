@@ -34,6 +34,7 @@ constexpr int NWG = 256;
 constexpr int GW = NWG * NW;                  // 2048 wavefronts
 constexpr int RPW = (NROWS + GW - 1) / GW;    // at most 3 q/k/v rows per wavefront
 constexpr long SPIN = 1L << 18;
+constexpr int NPRE = 64;                      // cache positions a head stages in LDS
 static_assert(D == GW, "one Wo row per wavefront");
 
 typedef unsigned long long tw;
@@ -95,7 +96,7 @@ struct Lds {
     alignas(16) int8_t attq[QD];      // the heads' codes
     float xs[NB];
     float atts[NBO];
-    HeadLds head;                     // the query head of workgroups 0..NH-1
+    HeadLds<NPRE> head;               // the query head of workgroups 0..NH-1
     uint64_t etab[32];
 };
 
@@ -131,8 +132,10 @@ __global__ __launch_bounds__(NT) void k_attn_layer(AttnArgs a) {
         }
     }
     const float xold = a.x[gw];
-    HeadPre hp;
-    if (b < NH) head_prefetch(hp, b, a.pos, a.kc, a.vc, a.q_norm, a.k_norm, a.rope, tid);
+    HeadPre<NPRE> hp;
+    if (b < NH)
+        head_prefetch(hp, sh.head, b, a.pos, glob((const float *)a.kc), glob((const float *)a.vc),
+                      glob(a.q_norm), glob(a.k_norm), glob(a.rope), tid);
     // (a barrier keeps the other wavefronts' weight rows behind those requests)
     __syncthreads();
     Blk wr[RPW];
@@ -142,12 +145,13 @@ __global__ __launch_bounds__(NT) void k_attn_layer(AttnArgs a) {
         const uint8_t *w = r < QD ? a.wq + (size_t)r * NB * 36
                            : r < QD + KVD ? a.wk + (size_t)(r - QD) * NB * 36
                                           : a.wv + (size_t)(r - QD - KVD) * NB * 36;
-        wr[j] = load_blk(w + (size_t)lane * 36);
+        wr[j] = load_blk(glob(w + (size_t)lane * 36));
     }
     // (and the q/k/v rows of every wavefront ahead of the Wo rows)
     __syncthreads();
     const uint8_t *wo = a.wo + (size_t)gw * NBO * 36;
-    const Blk wo0 = load_blk(wo + (size_t)lane * 36), wo1 = load_blk(wo + (size_t)(lane + 64) * 36);
+    const Blk wo0 = load_blk(glob(wo + (size_t)lane * 36)),
+              wo1 = load_blk(glob(wo + (size_t)(lane + 64) * 36));
     // x's copy for a rerun: x is written back (in P4) only by a workgroup
     // whose waits all ended, and then every workgroup has started and read
     // its row and wavefront 0's part of x.
@@ -249,7 +253,7 @@ __global__ __launch_bounds__(NT) void k_attn_layer(AttnArgs a) {
             sh.head.tv[tid - 2 * HD] =
                 __uint_as_float(get_word(a, &a.ws->qkv[QD + KVD + g * HD + tid - 2 * HD]));
         ATRACE(4, 0);
-        head_run(sh.head, sc, hp, h, a.pos, a.kc, a.vc, a.eps, a.scale,
+        head_run(sh.head, sc, hp, h, a.pos, glob(a.kc), glob(a.vc), a.eps, a.scale,
                  (a.flags & MHIP_FORCE_SEQ_RMS) != 0, sh.etab);
         if (tid < HD / 32) put_word(&a.ws->atts[h * (HD / 32) + tid], __float_as_uint(sh.head.dsc[tid]), a.tag);
         if (tid < HD / 4) put_word(&a.ws->attq[h * (HD / 4) + tid], ((const unsigned *)sh.head.hq)[tid], a.tag);

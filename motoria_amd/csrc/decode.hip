@@ -44,9 +44,12 @@
 // reference's rounding order; the gate weights come from the parallel logits
 // (relative error ~1e-6 against the reference's), unless the exact fallback
 // ran for that layer.
+#include "attn_common.h"
 #include "mhip_internal.h"
 
 namespace {
+
+namespace at = mhip_attn;
 
 constexpr int NX = 8;            // XCDs
 constexpr int WPX = 32;          // workgroups per XCD
@@ -103,6 +106,16 @@ struct DecodeWs {
 static_assert(offsetof(DecodeWs, lgb) == offsetof(DecodeWs, lgs) + NX * E * sizeof(tw),
               "lgb follows lgs");
 
+// Exchange words of the attention of the model stack (every layer's
+// attention before its MoE, k_model_stack), tagged like the MoE's.
+struct AttnXWs {
+    alignas(256) tw qkv[at::NROWS];    // q, k, v of the token
+    alignas(256) tw attq[at::QD / 4];  // the heads' Q8 codes, four per word
+    alignas(256) tw atts[at::NBO];     // their block scales
+    alignas(256) tw xa[D];             // x after the attention
+    alignas(256) tw xl[NX][D];         // the same, republished in each XCD's L2
+};
+
 struct DecodeArgs {
     const uint8_t *table;         // layer 0, experts expert_bytes apart, layers E*expert_bytes
     mhip_layout lay;
@@ -117,6 +130,12 @@ struct DecodeArgs {
     int L, K, norm_topk, flags;
     float eps;
     unsigned epoch;               // tag of this launch (bits 8..31 of every tag)
+    // k_model_stack only: the attention of each layer before its MoE
+    const mhip_attn_layer *al;    // [L], device
+    AttnXWs *xw;
+    const double *rope;           // [max_seq][HD / 2] (cos, sin)
+    int pos;
+    float scale;                  // 1 / sqrt(head_dim)
 };
 
 // The allocation-free entry point's workspace (the array `scratch` below):
@@ -451,709 +470,253 @@ __device__ __forceinline__ float wave_seq_sum_128(float a, float b) {
             ws->trace[l - MHIP_TRACE_L0][xcd + NX * rank][slot] = __builtin_amdgcn_s_memtime();  \
     } while (0)
 
-__global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
-    __shared__ Lds sh;
-    DecodeWs *ws = a.ws;
-    int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int K = a.K;
-    const int need = K < E ? K + 1 : K;     // ranks certified: K and the first not taken
-    const size_t layer_bytes = (size_t)E * a.lay.expert_bytes;
-    const bool gu_wave = wave < NGU;
+// ---- the attention of a layer inside the model stack ------------------------------
+//
+// k_model_stack runs, for every layer, the attention of mhip_attention_layer
+// (attn_layer.hip: the same arithmetic, forward.c:118-165) before the MoE,
+// on x in LDS: every workgroup forms rmsnorm(x, attn_norm) and Q8 itself
+// (wavefront 0), every wavefront gw = 8 (32 xcd + rank) + wave its q/k/v
+// rows gw + 2048 j (the block-order sum passed lane to lane) and row gw of
+// Wo; workgroups of rank < 4 run query head h = 8 rank + xcd (a key/value
+// group's heads on one rank, its first head on XCD 0 appending the cache
+// row). q/k/v, the heads' codes and scales and the new x meet through
+// device-scope tagged words (AttnXWs), tagged like the MoE's words of the
+// layer; every workgroup then holds the new x in LDS for the MoE.
+constexpr int AT_NPRE = 32;                          // cache positions a head stages in LDS
+constexpr int AT_RPW = (at::NROWS + NWG * NWAVE - 1) / (NWG * NWAVE);  // 3 q/k/v rows per wave
+static_assert(at::D == D && at::NT == NT && D == NWG * NWAVE, "one Wo row per wavefront");
+static_assert(at::NH == 4 * NX, "four heads per XCD");
 
-    // Start: every workgroup reads its XCD from the hardware and takes a
-    // rank among that XCD's workgroups from the XCD's ticket counter of this
-    // launch (the dispatcher deals the 256 workgroups to the 8 XCDs in turn,
-    // 32 each, but which XCD receives the first one varies between launches
-    // of different queues); then a device-wide barrier (the counter gains
-    // NWG per launch; epochs count launches since the workspace was cleared).
-    if (tid == 0) {
-        const unsigned hx = xcc_id();
-        unsigned rk = WPX;
-        if (hx < NX)
-            rk = __hip_atomic_fetch_add(&ws->xtick[a.epoch & 1][hx].n, 1u, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
-        if (rk >= WPX) status_update(ws, ST_ABORT, a.epoch, false, 1);
-        sh.role[0] = hx < NX ? (int)hx : 0;
-        sh.role[1] = rk < WPX ? (int)rk : 0;
-        if ((a.flags & MHIP_DECODE_FORCE_ABORT) && blockIdx.x == 0)
-            status_update(ws, ST_ABORT, a.epoch, false, 4);
-        __builtin_amdgcn_s_waitcnt(0);
-        __hip_atomic_fetch_add(&ws->gstart[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        wait_flag(ws, &ws->gstart[0], NWG * a.epoch, a.epoch);
-        // every workgroup of this launch holds its ticket: the other parity's
-        // counters start the next launch from zero
-        if (blockIdx.x == 0)
-            for (int k = 0; k < NX; k++)
-                __hip_atomic_store(&ws->xtick[(a.epoch + 1) & 1][k].n, 0u, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+// A pointer read from LDS, made wave-uniform (scalar registers).
+template <class T> __device__ __forceinline__ T *uniform_ptr(T *p) {
+    const uint64_t v = (uint64_t)p;
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+    return (T *)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ void attn_stage(const DecodeArgs &a, Lds &sh, DecodeWs *ws, int tid, int lane,
+                           int wave, int xcd, int rank, int l, unsigned tag) {
+    __shared__ at::HeadLds<AT_NPRE> hs;
+    __shared__ alignas(16) int8_t attq[at::QD];
+    __shared__ float atts[at::NBO];
+    __shared__ mhip_attn_layer al_next;             // the next layer's tensors, read a layer ahead
+    extern __shared__ __align__(16) float asc[];  // a head's scores, [pos + 1]
+    constexpr int ALW = sizeof(mhip_attn_layer) / 4;
+    static_assert(ALW <= NT && sizeof(mhip_attn_layer) % 4 == 0, "table row in words");
+    // this layer's tensors, held in LDS: at layer 0 from the table, later
+    // as read during the previous layer (the table row of layer l + 1 is
+    // requested now and stored at the end of this stage)
+    if (l == 0) {
+        if (tid < ALW) ((unsigned *)&al_next)[tid] = ((const unsigned *)a.al)[tid];
+        __syncthreads();
+    }
+    const mhip_attn_layer L = al_next;
+    unsigned alw = 0;
+    if (tid < ALW && l + 1 < a.L) alw = ((const unsigned *)(a.al + l + 1))[tid];
+    const at::gptr<const float> attn_norm = at::glob(uniform_ptr(L.attn_norm));
+    const at::gptr<const uint8_t> wqg = at::glob((const uint8_t *)uniform_ptr(L.wq));
+    const at::gptr<const uint8_t> wkg = at::glob((const uint8_t *)uniform_ptr(L.wk));
+    const at::gptr<const uint8_t> wvg = at::glob((const uint8_t *)uniform_ptr(L.wv));
+    const at::gptr<const uint8_t> wog = at::glob((const uint8_t *)uniform_ptr(L.wo));
+    const at::gptr<float> kcg = at::glob(uniform_ptr(L.kc)), vcg = at::glob(uniform_ptr(L.vc));
+    AttnXWs *xw = a.xw;
+    const int gw = (xcd * WPX + rank) * NWAVE + wave;
+    const bool head = rank < at::NH / NX;
+    const int h = rank * NX + xcd;
+    // requests in the order they are needed: the norm weight (wavefront 0),
+    // the weight rows, then a head's first cache rows (copied into LDS)
+    float4 nv4[8];
+    if (wave == 0) {
+        const at::gptr<const float4> nr = (at::gptr<const float4>)(attn_norm + 32 * lane);
+#pragma unroll
+        for (int k = 0; k < 8; k++) nv4[k] = at::ld4(nr + k);
+    }
+    at::Blk wr[AT_RPW];
+#pragma unroll
+    for (int j = 0; j < AT_RPW; j++) {
+        const int r = min(gw + NWG * NWAVE * j, at::NROWS - 1);  // past the end: unused
+        const at::gptr<const uint8_t> w = r < at::QD ? wqg + (size_t)r * at::NB * 36
+                                          : r < at::QD + at::KVD
+                                              ? wkg + (size_t)(r - at::QD) * at::NB * 36
+                                              : wvg + (size_t)(r - at::QD - at::KVD) * at::NB * 36;
+        wr[j] = at::load_blk(w + (size_t)lane * 36);
+    }
+    const at::gptr<const uint8_t> wo = wog + (size_t)gw * at::NBO * 36;
+    const at::Blk wo0 = at::load_blk(wo + (size_t)lane * 36),
+                  wo1 = at::load_blk(wo + (size_t)(lane + 64) * 36);
+    at::HeadPre<AT_NPRE, true> hp;
+    if (head)
+        at::head_prefetch(hp, hs, h, a.pos, (at::gptr<const float>)kcg, (at::gptr<const float>)vcg,
+                          at::glob(uniform_ptr(L.q_norm)), at::glob(uniform_ptr(L.k_norm)),
+                          at::glob(a.rope), tid);
+    // the previous layer's MoE ends with every thread storing its own part
+    // of x in LDS: all of it is there before wavefront 0 reads it below
+    __syncthreads();
+
+    // rmsnorm(x, attn_norm) and Q8 (forward.c:123, quant.c:11-27): lane b
+    // owns 32-block b; the certified sum of squares, else the sequential one
+    if (wave == 0) {
+        float v[32];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float4 q = *(const float4 *)&sh.x[32 * lane + 4 * k];
+            v[4 * k] = q.x;
+            v[4 * k + 1] = q.y;
+            v[4 * k + 2] = q.z;
+            v[4 * k + 3] = q.w;
+        }
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < 32; k++) ss = ss + (double)v[k] * (double)v[k];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss = ss + __shfl_xor(ss, o);
+        ss = __shfl(ss, 0);
+        const double m = ss * ((double)(D + 64) * 0x1p-52);
+        const float lo = (float)(1.0 / sqrt((ss + m) / D + (double)a.eps));
+        const float hi = (float)(1.0 / sqrt((ss - m) / D + (double)a.eps));
+        float inv = lo;
+        if ((a.flags & MHIP_FORCE_SEQ_RMS) || lo != hi) {
+            float r = 0.0f;
+            if (lane == 0) {
+                double sq = 0.0;
+                for (int i = 0; i < D; i++) sq = sq + (double)sh.x[i] * (double)sh.x[i];
+                r = (float)(1.0 / sqrt(sq / D + (double)a.eps));
+            }
+            inv = __shfl(r, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float4 q = nv4[k];
+            v[4 * k] = (v[4 * k] * inv) * q.x;
+            v[4 * k + 1] = (v[4 * k + 1] * inv) * q.y;
+            v[4 * k + 2] = (v[4 * k + 2] * inv) * q.z;
+            v[4 * k + 3] = (v[4 * k + 3] * inv) * q.w;
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 32; k++) amax = fmaxf(amax, fabsf(v[k]));
+        const float dsc = amax / 127.0f;
+        const float qi = dsc != 0.0f ? 1.0f / dsc : 0.0f;
+        union {
+            int8_t c[32];
+            int4 q[2];
+        } qc;
+#pragma unroll
+        for (int k = 0; k < 32; k++) qc.c[k] = (int8_t)roundf(v[k] * qi);
+        *(int4 *)&sh.xq[32 * lane] = qc.q[0];
+        *(int4 *)&sh.xq[32 * lane + 16] = qc.q[1];
+        sh.xs[lane] = dsc;
     }
     __syncthreads();
-    const int xcd = __builtin_amdgcn_readfirstlane(sh.role[0]);
-    const int rank = __builtin_amdgcn_readfirstlane(sh.role[1]);
-    // An XCD without a routed slot has nothing that another XCD reads.
-    if (aborted(ws, a.epoch) || xcd >= K) return;
+    TRACE(25);
 
-    // One register array serves both roles. A gate/up wave holds its GU_R
-    // weight rows in wq0/wq1/wsc during stage C. A down wave holds its DPK
-    // down (row, block) pairs in slots 0..DPK-1 from stage C to D, and the
-    // router row of its logit (8 x 16 bytes per lane, as int bits) in the
-    // slots above: wq0[DPK..GU_R), then wq1[DPK..). Sharing the registers
-    // keeps the compiler from copying loads still in flight (which would wait
-    // for them) where the two roles' code paths meet.
-    constexpr int NR0 = GU_R - DPK;
-    static_assert(2 * NR0 >= 8, "router row slots");
-    int4 wq0[GU_R], wq1[GU_R];
-    float wsc[GU_R];
-    // In the decode layout, load k of the row (1 KB, contiguous) gives lane
-    // L its elements 32 L + 4 k .. + 3.
-#define LOAD_ROUTER(layer) LOAD_ROUTER_ROW((size_t)(layer) * E + rank * LPW + wave - NGU)
-#define LOAD_ROUTER_ROW(row)                                                               \
-    do {                                                                                   \
-        const int4 *src_ = (const int4 *)(a.router + (size_t)(row) * D) + lane;            \
-        _Pragma("unroll") for (int k_ = 0; k_ < NR0; k_++) wq0[DPK + k_] = src_[64 * k_];  \
-        _Pragma("unroll") for (int k_ = 0; k_ < 8 - NR0; k_++) wq1[DPK + k_] = src_[64 * (NR0 + k_)]; \
-    } while (0)
-#define RROW(k)                                                                            \
-    i4_as_f4((k) < NR0 ? wq0[DPK + ((k) < NR0 ? (k) : 0)] : wq1[DPK + ((k) < NR0 ? 0 : (k) - NR0)])
-    // rmsnorm weights of the next layer at this thread's 4 positions.
-    float wn[D / NT];
-#define LOAD_NORM(layer)                                                                   \
-    do {                                                                                   \
-        _Pragma("unroll") for (int k_ = 0; k_ < D / NT; k_++)                              \
-            wn[k_] = a.norm[(size_t)(layer) * D + tid + NT * k_];                          \
-    } while (0)
-    if (!gu_wave) LOAD_ROUTER(0);
-    LOAD_NORM(0);
-    for (int i = tid; i < D; i += NT) sh.x[i] = a.x[i];
-    if (tid < E) sh.bias[tid] = a.bias ? a.bias[tid] : 0.0f;
-    if (tid < 32) sh.etab[tid] = mia_expf_tab[tid];
-    // no tag of this launch ((epoch << 8) | layer) has this value
-    if (tid == 0) sh.invtag = (a.epoch + 1u) << 8;
-    if (tid < NGU) sh.ptag[tid] = (a.epoch + 1u) << 8;
-
-    for (int l = 0; l < a.L; l++) {
-        // Per-thread addresses are recomputed in every layer rather than held
-        // in registers across the loop (the thread index is made opaque).
-        asm volatile("" : "+v"(tid));
-        lane = tid & 63;
-        const int dt = tid - NGU * 64;          // index among the down waves' threads
-        const unsigned tag = (a.epoch << 8) | (unsigned)(l & 255);
-        TRACE(0);
-        TRACE_CLK(30);
-        // ---- A: rmsnorm (certified), xn, Q8(xn), logits -----------------------------
-        // Wavefront 0 computes the scale inv while the down waves form their
-        // logits' products without it, from xt_i = fl(x_i * w_i) (w the norm
-        // weight): p~_i = fl(W_ei * xt_i). The reference's product
-        // p_i = fl(W_ei * fl(fl(x_i * inv) * w_i)) is inv * p~_i * (1 + eta_i)
-        // with |eta_i| <= (1+u)^3 / (1-u)^2 - 1 < 5.0001 u (u = 2^-24, no
-        // underflow), so once inv is known the sums of p~ scaled by inv bound
-        // the reference's chain.
+    // q/k/v rows (forward.c:124-126): lane b the term of block b, the
+    // block-order sum passed lane to lane
+    {
+        const int4 xa = *(const int4 *)&sh.xq[32 * lane], xb = *(const int4 *)&sh.xq[32 * lane + 16];
+        const float dx = sh.xs[lane];
+        float t[AT_RPW], sv[AT_RPW];
 #pragma unroll
-        for (int k = 0; k < D / NT; k++) {
-            const int i = tid + NT * k;
-            sh.xt[(i / 32) * XN_LD + i % 32] = sh.x[i] * wn[k];
+        for (int j = 0; j < AT_RPW; j++) {
+            t[j] = mhip_dev::block_term(mhip_dev::dot32_i8(wr[j].c0, wr[j].c1, xa, xb), wr[j].d, dx);
+            sv[j] = 0.0f + t[j];
         }
-        __syncthreads();
-        TRACE(14);
-        // down waves, uniform in the wave: sum p~, sum_k |prefix_k|, sum |p~|
-        double lgS = 0.0, lgA = 0.0, lgP = 0.0;
-        if (gu_wave) {
-            // partial sums of squares, one per gate/up wave; wavefront 0
-            // adds them and brackets the scale. Any summation order is within
-            // (n + log2 n) 2^-53 S of the reference's sequential double sum
-            // (all terms >= 0); S -/+ m brackets it, and when both ends give
-            // the same fp32 scale it is the reference's. Otherwise lane 0
-            // runs the sequential sum.
-            double ss = 0.0;
+        for (int k = 1; k < at::NB; k++) {
 #pragma unroll
-            for (int k = 0; k < D / (NGU * 64); k++) {
-                const double v = (double)sh.x[tid + NGU * 64 * k];
-                ss = ss + v * v;
-            }
-            ss = lane63_d(wave_scan_d(ss));
-            if (lane == 0) {
-                sh.part[wave] = ss;
-                __hip_atomic_store(&sh.ptag[wave], tag, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-            }
-            if (wave == 0) {
-                long sp = 0;
-                for (;;) {
-                    const unsigned t = lane < NGU ? __hip_atomic_load(&sh.ptag[lane], __ATOMIC_ACQUIRE,
-                                                                      __HIP_MEMORY_SCOPE_WORKGROUP)
-                                                  : tag;
-                    if (__ballot(t != tag) == 0) break;
-                    __builtin_amdgcn_s_sleep(1);
-                    if (++sp > SPIN) {
-                        if (lane == 0) status_update(ws, ST_ABORT, a.epoch, false, 2);
-                        break;
-                    }
-                }
-                double S = 0.0;
-                for (int k = 0; k < NGU; k++) S = S + sh.part[k];
-                // lane 0 takes the lower end of the bracket, lane 1 the upper
-                const double m = S * ((double)(D + 64) * 0x1p-52);
-                const float end = (float)(1.0 / sqrt((lane == 1 ? S - m : S + m) / D + (double)a.eps));
-                const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(end), 0));
-                const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(end), 1));
-                float iv = lo;
-                if ((a.flags & MHIP_FORCE_SEQ_RMS) || lo != hi) {   // uniform in the wave
-                    float sq_inv = 0.0f;
-                    if (lane == 0) {
-                        double sq = 0.0;
-                        for (int i = 0; i < D; i++) sq = sq + (double)sh.x[i] * (double)sh.x[i];
-                        sq_inv = (float)(1.0 / sqrt(sq / D + (double)a.eps));
-                        if (xcd == 0 && rank == 0) status_update(ws, ST_RMS, a.epoch, true, 0);
-                    }
-                    iv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq_inv)));
-                }
-                if (lane == 0) {
-                    sh.inv = iv;
-                    sh.nanflag = 0;
-                    __hip_atomic_store(&sh.invtag, tag, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-                }
-            }
-        } else if (!gu_wave) {
-            // This lane's 32 products, summed in four independent stretches
-            // of 8; the prefix sums of the second pass restart each stretch
-            // from its own offset, so no dependency chain is longer than 8
-            // additions.
-            const float4 *xv4 = (const float4 *)&sh.xt[lane * XN_LD];
-            float pr[32];
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const float4 wv = RROW(k), xv = xv4[k];
-                pr[4 * k + 0] = wv.x * xv.x;
-                pr[4 * k + 1] = wv.y * xv.y;
-                pr[4 * k + 2] = wv.z * xv.z;
-                pr[4 * k + 3] = wv.w * xv.w;
-            }
-            // sum |p~| in fp32 (32 terms >= 0: within 32 u of the exact sum,
-            // covered by the factor applied to lgP below)
-            double cs[4];
-            float ap = 0.0f;
-#pragma unroll
-            for (int m = 0; m < 4; m++) {
-                cs[m] = 0.0;
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    cs[m] = cs[m] + (double)pr[8 * m + j];
-                    ap = ap + fabsf(pr[8 * m + j]);
-                }
-            }
-            const double tot = (cs[0] + cs[1]) + (cs[2] + cs[3]);
-            const double incl = wave_scan_d(tot);
-            TRACE_BY(21, NGU * 64);
-            double run[4], ab[4];
-            run[0] = incl - tot;  // exclusive prefix of this lane
-            run[1] = run[0] + cs[0];
-            run[2] = run[1] + cs[1];
-            run[3] = run[2] + cs[2];
-#pragma unroll
-            for (int m = 0; m < 4; m++) ab[m] = 0.0;
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-#pragma unroll
-                for (int m = 0; m < 4; m++) {
-                    run[m] = run[m] + (double)pr[8 * m + j];
-                    ab[m] = ab[m] + fabs(run[m]);
-                }
-            lgS = lane63_d(incl);
-            lgA = lane63_d(wave_scan_d((ab[0] + ab[1]) + (ab[2] + ab[3])));
-            lgP = lane63_d(wave_scan_d((double)ap)) * (1.0 + 0x1p-16);
-            TRACE_BY(22, NGU * 64);
+            for (int j = 0; j < AT_RPW; j++) sv[j] = at::shr1(sv[j]) + t[j];
         }
-        // every wave takes inv from wavefront 0 (LDS, release / acquire);
-        // wavefront 0 never waits for another, so the wait ends
-        {
-            long sp = 0;
-            while (__hip_atomic_load(&sh.invtag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != tag) {
-                __builtin_amdgcn_s_sleep(1);
-                if (++sp > SPIN) {
-                    if (lane == 0) status_update(ws, ST_ABORT, a.epoch, false, 2);
-                    break;
-                }
-            }
-        }
-        const float inv = sh.inv;
-        TRACE(15);
-        {
+        if (lane == 63) {
 #pragma unroll
-            for (int k = 0; k < D / NT; k++) {
-                const int i = tid + NT * k;
-                sh.xn[(i / 32) * XN_LD + i % 32] = (sh.x[i] * inv) * wn[k];
+            for (int j = 0; j < AT_RPW; j++) {
+                const int r = gw + NWG * NWAVE * j;
+                if (r < at::NROWS) put_tagged<false>(&xw->qkv[r], sv[j], tag);
             }
-        }
-        if (!gu_wave && lane == 0) {
-            // The logit S = inv * sum p~ (double) and its bound: the
-            // reference's chain L over p is within u (1 + 2^-8) sum_k |S_k|
-            // of the exact sum of p (S_k its prefix sums; the slack covers
-            // the chain's own drift and the double sums), sum_k |S_k| <=
-            // inv * lgA + D * Ep, and the exact sum of p is within
-            // Ep = 5.0001 u inv lgP of inv * lgS. S goes out rounded to fp32
-            // (|S - Sf| <= u |Sf|, 2^-52 |S| for the double product, 2^-100
-            // for subnormal products); the bound is rounded upwards to fp32
-            // by the (1 + 2^-22) factor.
-            const int e = rank * LPW + wave - NGU;
-            const double di = (double)inv;
-            const double S = di * lgS;
-            const float Sf = (float)S;
-            const double Ep = 5.0001 * 0x1p-24 * di * lgP;
-            const double B = 0x1p-24 * (1.0 + 0x1p-8) * (di * lgA + (double)D * Ep) + Ep +
-                             0x1p-24 * fabs((double)Sf) + 0x1p-52 * fabs(S) + 0x1p-100;
-            put_tagged<true>(&ws->lgs[xcd][e], Sf, tag);
-            put_tagged<true>(&ws->lgb[xcd][e], (float)(B * (1.0 + 0x1p-22)), tag);
-        }
-        __syncthreads();
-        TRACE_BY(20, NGU * 64);
-        if (!gu_wave) {
-            // Q8(xn) for stage C, while the logits travel (quant.c:11-27 per
-            // element): four lanes per 32-block, eight elements each, the
-            // block maximum over the quad by DPP (order-free).
-            {
-                const int blk = dt >> 2, sub = dt & 3;
-                const float4 *src = (const float4 *)&sh.xn[blk * XN_LD + sub * 8];
-                const float4 v0 = src[0], v1 = src[1];
-                const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-                float am = 0.0f;                                 // a NaN counts as 0
-#pragma unroll
-                for (int i = 0; i < 8; i++) am = fmaxf(am, fabsf(v[i]));
-                am = fmaxf(am, dpp_keep_f<0xB1>(am));            // quad_perm [1,0,3,2]
-                am = fmaxf(am, dpp_keep_f<0x4E>(am));            // quad_perm [2,3,0,1]
-                const float d = am / 127.0f;
-                const float qi = d != 0.0f ? 1.0f / d : 0.0f;
-                union {
-                    int8_t c[8];
-                    int2 w;
-                } q;
-#pragma unroll
-                for (int i = 0; i < 8; i++) q.c[i] = (int8_t)roundf(v[i] * qi);
-                *(int2 *)&sh.xq[blk * 32 + sub * 8] = q.w;
-                if (sub == 0) sh.xs[blk] = d;
-            }
-        }
-        TRACE_BY(1, NGU * 64);
-        TRACE(2);
-
-        // ---- B: ranks, certification ------------------------------------------------
-        if (tid < E) {
-            float sb[2];
-            get_tagged<2, true>(ws, &ws->lgs[xcd][tid], NX * E, tag, sb);
-            const double S = (double)sb[0], B = (double)sb[1];
-            const float bs = sh.bias[tid];
-            const double c = S + (double)bs;
-            // monotone 64-bit image of c with the low 7 bits replaced by
-            // 127 - e: distinct keys, lower index first among (near-)equal
-            // values; an order that differs from c's fails the gap test below
-            uint64_t u = (uint64_t)__double_as_longlong(c);
-            u = (u >> 63) ? ~u : (u | (1ull << 63));
-            sh.key[tid] = ((u >> 7) << 7) | (uint64_t)(E - 1 - tid);
-            sh.c[tid] = c;
-            sh.lf[tid] = a.bias ? sb[0] + bs : sb[0];
-            if (c != c) sh.nanflag = 1;
-            const double bm = wave_max_d(B);
-            if (lane == 0) sh.bpart[wave] = bm;
-        }
-        __syncthreads();
-        TRACE(10);
-        {
-            // rank of expert e among the 32 keys of quarter q
-            const int e = tid & (E - 1), q = tid >> 7;
-            const uint64_t ke = sh.key[e];
-            const ulonglong2 *kv = (const ulonglong2 *)&sh.key[q * 32];
-            int rk = 0;
-#pragma unroll
-            for (int k = 0; k < 16; k++) {
-                const ulonglong2 v = kv[k];
-                rk += (int)(v.x > ke) + (int)(v.y > ke);
-            }
-            sh.rk[q][e] = rk;
-        }
-        __syncthreads();
-        if (tid < E) {
-            const int rk = sh.rk[0][tid] + sh.rk[1][tid] + sh.rk[2][tid] + sh.rk[3][tid];
-            if (rk < need) sh.order[rk] = tid;
-        }
-        __syncthreads();
-        TRACE(11);
-        if (wave == 0) {
-            // Without NaN keys the ranks are a permutation, so order[0..need)
-            // is set. The order is the reference's when every consecutive gap
-            // exceeds twice the largest bound plus a margin for the fp32
-            // roundings between the logit and the probability (logit + bias,
-            // l - mx, expf, division). The gate weights are computed later,
-            // while the XCD waits for h.
-            // Under the exact router (MHIP_FORCE_EXACT_ROUTER) a certified
-            // ranking is the reference's, so only the gate weights need the
-            // exact chains: they run beside the gate/up stream (stage C)
-            // unless MHIP_DECODE_CHAINS_FIRST asks for them before it.
-            const bool exact = (a.flags & MHIP_FORCE_EXACT_ROUTER) != 0;
-            bool ok = sh.nanflag == 0 && !(exact && (a.flags & MHIP_DECODE_CHAINS_FIRST));
-            if (ok) {
-                const double top = sh.c[sh.order[0]], bmax = fmax(sh.bpart[0], sh.bpart[1]);
-                int bad = 0;
-                if (lane >= 1 && lane < need) {
-                    const double prev = sh.c[sh.order[lane - 1]], cw = sh.c[sh.order[lane]];
-                    const double tau = 0x1p-19 * (2.0 + fabs(top) + fabs(prev));
-                    bad = !(prev - cw > 2.0 * bmax + tau);
-                }
-                ok = __ballot(bad) == 0;
-            }
-            if (ok && lane < K) sh.idx[lane] = sh.order[lane];
-            if (lane == 0) {
-                sh.fallback = ok ? 0 : 1;
-                sh.shadow_on = ok && exact ? 1 : 0;
-            }
-        }
-        __syncthreads();
-        if (sh.fallback) {
-            // Exact logits, the reference's sequential chain: each down wave
-            // computes one (products in registers, summed in order across
-            // the lanes), then the XCD exchanges them.
-            if (!gu_wave) {
-                const float *xv = &sh.xn[lane * XN_LD];
-                float pr[32];
-#pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    const float4 wv = RROW(k);
-                    pr[4 * k + 0] = wv.x * xv[4 * k + 0];
-                    pr[4 * k + 1] = wv.y * xv[4 * k + 1];
-                    pr[4 * k + 2] = wv.z * xv[4 * k + 2];
-                    pr[4 * k + 3] = wv.w * xv[4 * k + 3];
-                }
-                float sl = wave_seq_sum_2048(pr);
-                const int e = rank * LPW + wave - NGU;
-                if (a.bias) sl = sl + sh.bias[e];
-                if (lane == 63) put_tagged<true>(&ws->lx[xcd][e], sl, tag);
-            }
-            if (tid < E) get_tagged<1, true>(ws, &ws->lx[xcd][tid], 0, tag, &sh.lf[tid]);
-            __syncthreads();
-            // forward.c:95-101: the first maximum, then the sequential sum.
-            // With l[0] a NaN every comparison fails and the maximum stays
-            // NaN; otherwise it is the largest non-NaN logit, which a
-            // NaN-ignoring maximum finds in any order (equal maxima, +0 and
-            // -0 among them, give the same exponentials).
-            if (tid < E) {
-                const double m = wave_max_d((double)sh.lf[tid]);
-                if (lane == 0) sh.mxpart[tid >> 6] = (float)m;
-            }
-            __syncthreads();
-            if (tid < E) {
-                float mx = sh.mxpart[0];
-#pragma unroll
-                for (int q = 1; q < E / 64; q++) mx = fmaxf(mx, sh.mxpart[q]);
-                if (sh.lf[0] != sh.lf[0]) mx = sh.lf[0];
-                sh.p[tid] = mia_expf_glibc_tab(sh.lf[tid] - mx, sh.etab);
-            }
-            __syncthreads();
-            if (tid == 0) sh.sum = lds_seq_sum_n<E>(sh.p, 0.0f);
-            __syncthreads();
-            if (tid < E) {
-                const float pe = sh.p[tid] / sh.sum;
-                sh.p[tid] = pe;
-                if (pe != pe) sh.nanflag = 2;
-            }
-            if (tid < KMAX) sh.idx[tid] = 0;
-            __syncthreads();
-            if (sh.nanflag == 2) {
-                // forward.c:104-114 literally (a NaN probability never wins a
-                // comparison; the first untaken index stands in for it).
-                if (tid == 0) {
-                    for (int j = 0; j < K; j++) {
-                        int best = -1;
-                        for (int i = 0; i < E; i++) {
-                            int taken = 0;
-                            for (int t = 0; t < j; t++) taken |= sh.idx[t] == i;
-                            if (!taken && (best < 0 || sh.p[i] > sh.p[best])) best = i;
-                        }
-                        sh.idx[j] = best;
-                    }
-                }
-            } else if (tid < E) {
-                // forward.c:104-114: descending p, lowest index on ties
-                const float pe = sh.p[tid];
-                int rk = 0;
-                for (int i = 0; i < E; i++) {
-                    const float pi = sh.p[i];
-                    rk += (int)(pi > pe) + ((int)(pi == pe) & (int)(i < tid));
-                }
-                if (rk < K) sh.idx[rk] = tid;
-            }
-            __syncthreads();
-            if (tid == 0) {
-                // the K probabilities read first, then summed in rank order
-                float pk[KMAX];
-#pragma unroll
-                for (int j = 0; j < KMAX; j++) pk[j] = j < K ? sh.p[sh.idx[j]] : 0.0f;
-                float wsum = 0.0f;
-#pragma unroll
-                for (int j = 0; j < KMAX; j++)
-                    if (j < K) wsum = wsum + pk[j];
-#pragma unroll
-                for (int j = 0; j < KMAX; j++)
-                    if (j < K) sh.w[j] = a.norm_topk ? pk[j] / wsum : pk[j];
-                if (xcd == 0 && rank == 0) status_update(ws, ST_ROUTER, a.epoch, true, 0);
-            }
-            __syncthreads();
-        }
-        TRACE(3);
-
-        // ---- C: gate/up + SwiGLU for expert slot `xcd` -----------------------------
-        const bool active = xcd < K;
-        const int ex = min(max(sh.idx[active ? xcd : 0], 0), E - 1);
-        const uint8_t *eb = a.table + (size_t)l * layer_bytes + (size_t)ex * a.lay.expert_bytes;
-        // The next layer's rmsnorm weights are requested first: they arrive
-        // before this wave's weight rows, so no later wait is held up by them
-        // (the last layer reloads its own). Its router rows follow in stage D,
-        // once this layer's rows are in.
-        const int lnext = min(l + 1, a.L - 1);
-        LOAD_NORM(lnext);
-        if (gu_wave) {
-            if (active) {
-                // this wave's rows: gate h0..h0+GU_H-1, then up h0..h0+GU_H-1.
-                // A row's 2 KB of codes arrive as two contiguous 1 KB loads:
-                // lane l holds half (l & 1) of block l/2 and of block 32 + l/2;
-                // the lane pair adds its two half dots, and lane l keeps
-                // block blk = l/2 (l even) or 32 + l/2 (l odd).
-                const int h0 = rank * HROWS + wave * GU_H;
-                const int hf = lane & 1, bm = lane >> 1;
-                const int blk = hf ? NB / 2 + bm : bm;
-                const int4 xa = *(const int4 *)&sh.xq[bm * 32 + 16 * hf];
-                const int4 xb = *(const int4 *)&sh.xq[(NB / 2 + bm) * 32 + 16 * hf];
-                const float dx = sh.xs[blk];
-#pragma unroll
-                for (int r = 0; r < GU_R; r++) {
-                    const int row = h0 + (r % GU_H);
-                    const size_t qoff = (r < GU_H ? a.lay.gate_q : a.lay.up_q) + (size_t)row * D +
-                                        (size_t)lane * 16;
-                    const size_t soff = (r < GU_H ? a.lay.gate_s : a.lay.up_s);
-                    const int4 *src = (const int4 *)(eb + qoff);
-                    wq0[r] = ld_stream(src);
-                    wq1[r] = ld_stream(src + 64);
-                    wsc[r] = ((const float *)(eb + soff))[(size_t)row * NB + blk];
-                }
-                float *terms = &sh.scr[wave * GU_R * GU_LD];
-#pragma unroll
-                for (int r = 0; r < GU_R; r++) {
-                    const int pa = dot16_i8(wq0[r], xa), pb = dot16_i8(wq1[r], xb);
-                    const int other = __builtin_amdgcn_update_dpp(0, hf ? pa : pb, 0xB1, 0xf, 0xf, false);
-                    terms[r * GU_LD + blk] =
-                        mhip_dev::block_term((hf ? pb : pa) + other, wsc[r], dx);
-                }
-                TRACE(12);
-                wave_lds_sync();
-                if (lane < GU_R) sh.gu[wave][lane] = lds_seq_sum_n<NB>(&terms[lane * GU_LD], 0.0f);
-                wave_lds_sync();
-                TRACE(19);
-                if (lane < GU_H) {
-                    const float g = sh.gu[wave][lane], u = sh.gu[wave][GU_H + lane];
-                    put_tagged<true>(&ws->h[xcd][h0 + lane],
-                               (g / (1.0f + mia_expf_glibc_tab(-g, sh.etab))) * u, tag);
-                }
-                TRACE_BY(16, 64);
-                TRACE_BY(17, 192);
-            }
-        } else {
-            const bool shadow = sh.shadow_on != 0;
-            if (shadow) {
-                // The exact logit of this wave's expert (forward.c:173-176:
-                // the reference's sequential chain) from its router row of
-                // this layer, still in registers, before the loads that reuse
-                // those registers: the HBM stream of the gate/up waves would
-                // hold the loads' issue, and the chain behind them, for most
-                // of this stage.
-                const float *xv = &sh.xn[lane * XN_LD];
-                float pr[32];
-#pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    const float4 wv = RROW(k);
-                    pr[4 * k + 0] = wv.x * xv[4 * k + 0];
-                    pr[4 * k + 1] = wv.y * xv[4 * k + 1];
-                    pr[4 * k + 2] = wv.z * xv[4 * k + 2];
-                    pr[4 * k + 3] = wv.w * xv[4 * k + 3];
-                }
-                float sl = wave_seq_sum_2048(pr);
-                const int e = rank * LPW + wave - NGU;
-                if (a.bias) sl = sl + sh.bias[e];
-                if (lane == 63) put_tagged<true>(&ws->lx[xcd][e], sl, tag);
-                TRACE_BY(23, NGU * 64);
-            }
-            // the down rows of this workgroup (used once h has arrived)
-            if (wave == NGU && !sh.fallback && !shadow) {
-                // The gate weights, before this wave's loads (a wave waiting
-                // to issue a load runs nothing else, and the CU takes its
-                // vector memory instructions in order). Softmax of the
-                // parallel logits (forward.c:95-101 in shape; the weights
-                // only need the 1e-3 tolerance); with renormalisation
-                // (forward.c:178-181) the full sum cancels and only the
-                // top K exponentials are needed.
-                const float mx = sh.lf[sh.idx[0]];
-                const float ek = mia_expf_glibc_tab(sh.lf[sh.idx[min(lane, K - 1)]] - mx, sh.etab);
-                const float ej = lane < K ? ek : 0.0f;
-                float den;
-                if (a.norm_topk)
-                    den = wave_sum_f(ej);
-                else
-                    den = wave_sum_f(mia_expf_glibc_tab(sh.lf[lane] - mx, sh.etab) +
-                                     mia_expf_glibc_tab(sh.lf[lane + 64] - mx, sh.etab));
-                if (lane < K) sh.w[lane] = ej / den;
-                TRACE_BY(18, NGU * 64);
-            }
-#pragma unroll
-            for (int k = 0; k < DPK; k++) {
-                // The workgroup's 64 rows are one contiguous 48 KB run, read
-                // as 16-byte pieces q = dt + 256 j (j < 12): the two halves of
-                // block q/2 sit in a lane pair. Loads 2k, 2k + 1 go to
-                // wq0[k], wq1[k]; the pair later keeps block P(2k + (dt & 1)).
-                const int4 *run = (const int4 *)(eb + a.lay.down_q + (size_t)rank * DROWS * EH);
-                wq0[k] = ld_stream(run + dt + NDN * 64 * (2 * k));
-                wq1[k] = ld_stream(run + dt + NDN * 64 * (2 * k + 1));
-                const int p = (dt >> 1) + (NDN * 32) * (2 * k + (dt & 1));
-                wsc[k] = ((const float *)(eb + a.lay.down_s))[(size_t)rank * DROWS * NBH + p];
-            }
-        }
-        TRACE(4);
-        // ---- D: Q8(h) and down ------------------------------------------------------
-        const int par = l & 1;
-        if (active) {
-            // h is polled by the gate/up waves, which have no loads in
-            // flight: wave w takes h[192w, 192w + 192), i.e. six Q8 blocks,
-            // two per register with one block per 32-lane half, and
-            // quantizes them in place (quant.c:11-27 per element; the block
-            // maximum is order-free).
-            if (gu_wave) {
-                constexpr int HPW = EH / (NGU * 64);
-                float hv[HPW];
-                get_tagged<HPW, true>(ws, &ws->h[xcd][wave * 64 * HPW + lane], 64, tag, hv);
-#pragma unroll
-                for (int k = 0; k < HPW; k++) {
-                    const int i = wave * 64 * HPW + 64 * k + lane;
-                    float am = fmaxf(0.0f, fabsf(hv[k]));   // a NaN counts as 0, as in the chain
-                    am = fmaxf(am, dpp_keep_f<0x121>(am));  // row_ror 1, 2, 4, 8: 16-lane max
-                    am = fmaxf(am, dpp_keep_f<0x122>(am));
-                    am = fmaxf(am, dpp_keep_f<0x124>(am));
-                    am = fmaxf(am, dpp_keep_f<0x128>(am));
-                    am = fmaxf(am, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(am), 0x401f)));
-                    const float d = am / 127.0f;
-                    const float qi = d != 0.0f ? 1.0f / d : 0.0f;
-                    sh.hq[i] = (int8_t)roundf(hv[k] * qi);
-                    if ((lane & 31) == 0) sh.hsc[i / 32] = d;
-                }
-            }
-            __syncthreads();
-            TRACE(5);
-            TRACE(13);
-            float *dterm = sh.scr;
-            if (!gu_wave) {
-#pragma unroll
-                for (int k = 0; k < DPK; k++) {
-                    // blocks pa, pb = pa + 128 of the workgroup's rows (row
-                    // p / 24, block p % 24); this lane keeps pa if even, pb if odd
-                    const int hf = dt & 1;
-                    const int pa = (dt >> 1) + (NDN * 32) * (2 * k), pb = pa + NDN * 32;
-                    const int4 ha = *(const int4 *)&sh.hq[(pa % NBH) * 32 + 16 * hf];
-                    const int4 hb = *(const int4 *)&sh.hq[(pb % NBH) * 32 + 16 * hf];
-                    const int da = dot16_i8(wq0[k], ha), db = dot16_i8(wq1[k], hb);
-                    const int other = __builtin_amdgcn_update_dpp(0, hf ? da : db, 0xB1, 0xf, 0xf, false);
-                    const int p = hf ? pb : pa;
-                    const int row = p / NBH, blk = p % NBH;
-                    dterm[row * DN_LD + blk] = mhip_dev::block_term((hf ? db : da) + other, wsc[k],
-                                                                    sh.hsc[blk]);
-                }
-                // the next layer's router rows, after this layer's stream:
-                // they load while the expert outputs are exchanged. After the
-                // last layer every wave reads router row 0 instead (the same
-                // 8 KB, from the L2): the load is issued on every path, so
-                // the compiler's wait counts stay exact and the expert
-                // outputs' polls never wait for it.
-                LOAD_ROUTER_ROW(l + 1 < a.L ? (size_t)lnext * E + rank * LPW + wave - NGU : 0);
-            }
-            __syncthreads();
-            if (wave == 0)
-                put_tagged<false>(&ws->out[par][xcd][rank * DROWS + lane],
-                           lds_seq_sum_n<NBH>(&dterm[lane * DN_LD], 0.0f), tag);
-        }
-        TRACE(6);
-
-        // ---- E: combine rows rank*64 .. +64 in top-K order ---------------------------
-        if (sh.shadow_on && wave == 1) {
-            // Under the exact router with a certified ranking: the XCD's 128
-            // exact logits (the down waves' chains, long done) -> softmax
-            // (forward.c:95-101: the first maximum as in the exact router
-            // above, the sequential sum) -> the certified experts' weights
-            // (forward.c:178-181), first needed by the combine below. Wave 1
-            // computes them while the expert outputs are on their way (wave 0
-            // fetches expert 1's rows).
-            float lv[2];
-            get_tagged<2, true>(ws, &ws->lx[xcd][lane], 64, tag, lv);
-            float mx = (float)wave_max_d(fmax((double)lv[0], (double)lv[1]));
-            const float l0 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(lv[0])));
-            if (l0 != l0) mx = l0;
-            const float e0 = mia_expf_glibc_tab(lv[0] - mx, sh.etab);
-            const float e1 = mia_expf_glibc_tab(lv[1] - mx, sh.etab);
-            const float sum = __int_as_float(
-                __builtin_amdgcn_readlane(__float_as_int(wave_seq_sum_128(e0, e1)), 63));
-            const float p0 = e0 / sum, p1 = e1 / sum;
-            // a NaN probability would rank differently in the reference
-            // (forward.c:104-114): the launch reports it and the caller
-            // reruns the layer per stage
-            const bool nan = __ballot(p0 != p0 || p1 != p1) != 0;
-            sh.p[lane] = p0;
-            sh.p[lane + 64] = p1;
-            wave_lds_sync();
-            // lane j < K: the probability of rank j; their sum in rank order
-            // (lane j adds its own to lane j - 1's running sum)
-            const float pj = lane < K ? sh.p[sh.idx[lane]] : 0.0f;
-            float wsum = 0.0f + pj;
-            for (int j = 1; j < K; j++)
-                wsum = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(wsum), 0x138, 0xf, 0xf, false)) + pj;
-            wsum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wsum), K - 1));
-            if (lane < K) sh.w[lane] = a.norm_topk ? pj / wsum : pj;
-            if (lane == 0) {
-                if (nan) status_update(ws, ST_ABORT, a.epoch, false, 8);
-                if (xcd == 0 && rank == 0) status_update(ws, ST_ROUTER, a.epoch, true, 0);
-            }
-            TRACE_BY(24, 64);
-        }
-        {
-            // thread (j, r) fetches expert j's output row r; then one thread
-            // per row adds them in top-K order
-            const int j = tid / DROWS, r = tid % DROWS;
-            if (sh.shadow_on && K > 1 && j < 2) {
-                if (j == 0) {
-                    float v2[2];
-                    get_tagged<2, false>(ws, &ws->out[par][0][rank * DROWS + r], D, tag, v2);
-                    sh.og[r] = v2[0];
-                    sh.og[DROWS + r] = v2[1];
-                }
-            } else if (j < K) {
-                get_tagged<1, false>(ws, &ws->out[par][j][rank * DROWS + r], 0, tag, &sh.og[j * DROWS + r]);
-            }
-        }
-        __syncthreads();
-        TRACE(7);
-        if (xcd == 0 && rank == 0 && tid < K) {
-            if (a.idx_out) a.idx_out[(size_t)l * K + tid] = sh.idx[tid];
-            if (a.w_out) a.w_out[(size_t)l * K + tid] = sh.w[tid];
-        }
-        if (tid < DROWS) {
-            const int r = rank * DROWS + tid;
-            float v = sh.x[r];
-            for (int j = 0; j < K; j++) v = v + sh.w[j] * sh.og[j * DROWS + tid];
-            if (l + 1 < a.L) put_tagged<true>(&ws->x[xcd][r], v, tag);
-            else if (xcd == 0) a.x[r] = v;
-        }
-        TRACE(8);
-        if (l + 1 < a.L) {
-            // the XCD's new residual stream; a row is written only after its
-            // old value was read above, so no barrier is needed before this
-            float xv[D / NT];
-            get_tagged<D / NT, true>(ws, &ws->x[xcd][tid], NT, tag, xv);
-#pragma unroll
-            for (int k = 0; k < D / NT; k++) sh.x[tid + NT * k] = xv[k];
-            TRACE(9);
         }
     }
+    TRACE_BY(26, 63);
+
+    // query head h (forward.c:127-163)
+    if (head) {
+        const int g = h / at::GROUP;
+        float v;
+        if (tid < at::HD) {
+            get_tagged<1, false>(ws, &xw->qkv[h * at::HD + tid], 0, tag, &v);
+            hs.tq[tid] = v;
+        } else if (tid < 2 * at::HD) {
+            get_tagged<1, false>(ws, &xw->qkv[at::QD + g * at::HD + tid - at::HD], 0, tag, &v);
+            hs.tk[tid - at::HD] = v;
+        } else if (tid < 3 * at::HD) {
+            get_tagged<1, false>(ws, &xw->qkv[at::QD + at::KVD + g * at::HD + tid - 2 * at::HD], 0,
+                                 tag, &v);
+            hs.tv[tid - 2 * at::HD] = v;
+        }
+        TRACE(27);
+        at::head_run(hs, asc, hp, h, a.pos, kcg, vcg, a.eps, a.scale,
+                     (a.flags & MHIP_FORCE_SEQ_RMS) != 0, sh.etab);
+        TRACE(28);
+        if (tid < at::HD / 32) put_tagged<false>(&xw->atts[h * (at::HD / 32) + tid], hs.dsc[tid], tag);
+        if (tid < at::HD / 4)
+            put_tagged<false>(&xw->attq[h * (at::HD / 4) + tid],
+                              __uint_as_float(((const unsigned *)hs.hq)[tid]), tag);
+    }
+
+    // row gw of Wo over the heads' codes, plus the residual (forward.c:164-165)
+    {
+        float q2[2];
+        get_tagged<2, false>(ws, &xw->attq[tid], NT, tag, q2);
+        ((unsigned *)attq)[tid] = __float_as_uint(q2[0]);
+        ((unsigned *)attq)[tid + NT] = __float_as_uint(q2[1]);
+        if (tid < at::NBO) get_tagged<1, false>(ws, &xw->atts[tid], 0, tag, &atts[tid]);
+        static_assert(at::QD / 4 == 2 * NT, "two code words per thread");
+        __syncthreads();
+        TRACE(29);
+        const int4 *q0 = (const int4 *)&attq[32 * lane], *q1 = (const int4 *)&attq[32 * (lane + 64)];
+        const float t0 = mhip_dev::block_term(mhip_dev::dot32_i8(wo0.c0, wo0.c1, q0[0], q0[1]), wo0.d,
+                                              atts[lane]);
+        const float t1 = mhip_dev::block_term(mhip_dev::dot32_i8(wo1.c0, wo1.c1, q1[0], q1[1]), wo1.d,
+                                              atts[lane + 64]);
+        // blocks 0..63 (t0 of lanes 0..63), then 64..127 (t1), in order
+        float sv = 0.0f + t0;
+        for (int k = 1; k < 64; k++) sv = at::ror1(sv) + t0;
+        for (int k = 0; k < 64; k++) sv = at::ror1(sv) + t1;
+        TRACE_BY(32, 63);
+        if (lane == 63) put_tagged<false>(&xw->xa[gw], sh.x[gw] + sv, tag);
+    }
+
+    // the new x in every workgroup: workgroup `rank` of each XCD fetches
+    // words 64 rank .. + 63 across the device and republishes them in its
+    // XCD's L2, where every workgroup of the XCD reads all D of them (one
+    // device-wide read of each word per XCD instead of one per workgroup)
+    static_assert(WPX * 64 == D, "64 words per workgroup");
+    if (wave == 0) {
+        float v;
+        get_tagged<1, false>(ws, &xw->xa[64 * rank + lane], 0, tag, &v);
+        put_tagged<true>(&xw->xl[xcd][64 * rank + lane], v, tag);
+    }
+    {
+        float xv[D / NT];
+        get_tagged<D / NT, true>(ws, &xw->xl[xcd][tid], NT, tag, xv);
+        TRACE(33);
+        __syncthreads();  // every read of the old x is done
+#pragma unroll
+        for (int k = 0; k < D / NT; k++) sh.x[tid + NT * k] = xv[k];
+        if (tid < ALW) ((unsigned *)&al_next)[tid] = alw;
+        __syncthreads();
+    }
+    TRACE(31);
+}
+
+// The kernels: one body (decode_body.inc) compiled twice.
+__global__ __launch_bounds__(NT) void k_decode_stack(DecodeArgs a) {
+#define DECODE_ATTN 0
+#include "decode_body.inc"
+#undef DECODE_ATTN
+}
+__global__ __launch_bounds__(NT) void k_model_stack(DecodeArgs a) {
+#define DECODE_ATTN 1
+#include "decode_body.inc"
+#undef DECODE_ATTN
 }
 
 // Once per context (the device properties query is slow): 1 when every CU
@@ -1224,12 +787,23 @@ __global__ void k_decode_status_out(const DecodeWs *ws, unsigned epoch, int *sta
 // start counter grows by NWG per launch: nothing is cleared between launches.
 // The workspace is cleared whole first (fill kernel, no memset) when `fresh`
 // or when the epoch is about to leave its 24 bits. Queues no allocation.
+// The model stack's part of a launch (k_model_stack): the attention of every
+// layer before its MoE.
+struct ModelPart {
+    const mhip_attn_layer *al;
+    AttnXWs *xw;
+    const double *rope;
+    int pos;
+};
+
 int launch_decode(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay, const void *d_table,
                   const float *d_router, const float *d_router_t, const float *d_norm,
                   const float *d_bias, float *d_x, int L, DecodeWs *ws, unsigned *epoch,
-                  bool fresh, int *d_idx, float *d_w, int *d_status, int flags) {
+                  bool fresh, int *d_idx, float *d_w, int *d_status, int flags,
+                  const ModelPart *mp = nullptr) {
     if (fresh || *epoch >= (1u << 24) - 1) {
         if (mhip_zero(c, ws, offsetof(DecodeWs, trace))) return -1;
+        if (mp && mhip_zero(c, mp->xw, sizeof(AttnXWs))) return -1;
         *epoch = 0;
     }
     if ((flags & MHIP_DECODE_TRACE) && mhip_zero(c, ws->trace, sizeof(ws->trace))) return -1;
@@ -1250,12 +824,20 @@ int launch_decode(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay, const
     a.flags = flags;
     a.eps = s->norm_eps;
     a.epoch = ++*epoch;
+    a.al = mp ? mp->al : nullptr;
+    a.xw = mp ? mp->xw : nullptr;
+    a.rope = mp ? mp->rope : nullptr;
+    a.pos = mp ? mp->pos : 0;
+    a.scale = 1.0f / sqrtf((float)at::HD);
     // An ordinary launch: one 512-thread workgroup fits each of the 256 CUs
     // (checked before), so on an otherwise idle device all of them are
     // resident at once. Should one not be, the start barrier times out and
     // the launch reports abort bit 2 instead of waiting for ever.
     int slot = mhip::stage_begin(c, MHIP_STAGE_DECODE);
-    k_decode_stack<<<NWG, NT, 0, c->stream>>>(a);
+    if (mp)  // a head's scores in dynamic LDS
+        k_model_stack<<<NWG, NT, ((size_t)mp->pos + 1) * 4, c->stream>>>(a);
+    else
+        k_decode_stack<<<NWG, NT, 0, c->stream>>>(a);
     const hipError_t e = hipGetLastError();
     mhip::stage_end(c, slot);
     if (e != hipSuccess) {
@@ -1266,6 +848,20 @@ int launch_decode(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay, const
         k_decode_status_out<<<1, 64, 0, c->stream>>>(ws, a.epoch, d_status);
         return mhip::check_launch(c, "decode status copy");
     }
+    return 0;
+}
+
+// The dynamic-LDS limit of k_model_stack (a head's scores), set once per
+// device.
+int g_model_lds_set[MAX_DEVICES];
+int model_lds_attr(mhip_ctx *c) {
+    if (c->device < 0 || c->device >= MAX_DEVICES || g_model_lds_set[c->device]) return 0;
+    if (mhip::check(c, hipFuncSetAttribute((const void *)k_model_stack,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           MHIP_MODEL_STACK_MAX_SEQ * 4),
+                    "model stack LDS attribute"))
+        return -1;
+    g_model_lds_set[c->device] = 1;
     return 0;
 }
 
@@ -1337,6 +933,61 @@ int mhip_decode_stack_noalloc(mhip_ctx *c, const mhip_dims *s, const mhip_layout
         return mhip::fail(c, "no-alloc decode: device %d has no set-up workspace", c->device);
     return launch_decode(c, s, lay, d_table, d_router, d_router_t, d_norm, d_bias, d_x, L,
                          (DecodeWs *)st->ptr, &st->epoch, false, d_idx, d_w, d_status, flags);
+}
+
+size_t mhip_model_stack_ws_bytes(void) { return mhip_decode_ws_bytes() + sizeof(AttnXWs); }
+
+int mhip_model_stack_supported(mhip_ctx *c, const mhip_dims *s, const mhip_attn_dims *as,
+                               int max_seq) {
+    if (!as || mhip::check_dims(c, s) || mhip::use_device(c)) return -1;
+    if (!decode_shape_fits(s) || s->n_active != NX) return 0;
+    if (as->dim != D || as->n_heads != at::NH || as->n_kv_heads != at::NKV ||
+        as->head_dim != at::HD)
+        return 0;
+    if (max_seq <= 0 || max_seq > MHIP_MODEL_STACK_MAX_SEQ) return 0;
+    const int fits = decode_device_fits(c);
+    if (fits <= 0) return fits;
+    int occ = 0;
+    if (model_lds_attr(c) ||
+        mhip::check(c, hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_model_stack, NT,
+                                                                     (size_t)max_seq * 4),
+                    "occupancy"))
+        return -1;
+    return occ >= 1 ? 1 : 0;
+}
+
+int mhip_model_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
+                     const void *d_table, const float *d_router_dl, const float *d_router_t,
+                     const float *d_norm, const float *d_bias, const mhip_attn_dims *as,
+                     const mhip_attn_layer *d_al, const double *d_rope, int pos, int max_seq,
+                     float *d_x, int L, void *d_ws, int *d_status, int flags) {
+    const int ok = check_decode_args(c, s, L);
+    if (ok <= 0) return ok;
+    if (!as || !d_al || !d_rope || !d_status)
+        return mhip::fail(c, "model stack: a null argument");
+    if (s->n_active != NX || as->dim != D || as->n_heads != at::NH ||
+        as->n_kv_heads != at::NKV || as->head_dim != at::HD)
+        return mhip::fail(c, "model stack: shape not supported (top-%d of the MoE, dim 2048, "
+                             "32/4 heads of 128)", NX);
+    if (max_seq <= 0 || max_seq > MHIP_MODEL_STACK_MAX_SEQ || pos < 0 || pos >= max_seq)
+        return mhip::fail(c, "model stack: pos=%d, max_seq=%d outside [0, %d]", pos, max_seq,
+                          MHIP_MODEL_STACK_MAX_SEQ);
+    if ((uintptr_t)d_ws % 256)
+        return mhip::fail(c, "model stack: workspace %p is not 256-byte aligned", d_ws);
+    if (model_lds_attr(c)) return -1;
+    DecodeWs *ws = (DecodeWs *)d_ws;
+    ModelPart mp;
+    mp.al = d_al;
+    mp.xw = (AttnXWs *)((uint8_t *)d_ws + mhip_decode_ws_bytes());
+    mp.rope = d_rope;
+    mp.pos = pos;
+    // a forced abort of either half stops the whole launch
+    const int f = (flags & MHIP_ATTN_FORCE_ABORT) ? (flags | MHIP_DECODE_FORCE_ABORT) : flags;
+    const int rc = launch_decode(c, s, lay, d_table, d_router_dl, d_router_t, d_norm, d_bias, d_x,
+                                 L, ws, &c->decode_epoch, ws != c->decode_ws, nullptr, nullptr,
+                                 d_status, f & ~MHIP_ATTN_FORCE_ABORT, &mp);
+    if (rc == 0) c->decode_ws = ws;
+    return rc;
 }
 
 int mhip_decode_status(mhip_ctx *c, const void *d_ws, int status[4]) {

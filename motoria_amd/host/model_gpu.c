@@ -34,7 +34,7 @@ struct mia_gpu_model {
     mhip_ctx *gpu;
     mia_moe_tensors mt;
     mhip_attn_dims ad;
-    int max_seq, flags, decode_ok, attn_ok, aborts;
+    int max_seq, flags, decode_ok, attn_ok, stack_ok, aborts;
     int logits_ok; /* d_logits holds the last step's logits */
     unsigned char *d_dense;
     mia_layer_offsets *lo;   /* [L] */
@@ -46,6 +46,8 @@ struct mia_gpu_model {
     float *d_xsave;          /* [L][dim] x before each layer's MoE */
     float *d_xin;            /* [L][dim] x before each layer's attention (one-launch path) */
     void *d_aws;             /* workspace of the one-launch attention */
+    mhip_attn_layer *d_al;   /* [L] each layer's attention tensors and cache (model stack) */
+    void *d_mws;             /* workspace of the model stack */
     int *d_status;           /* [L][4] decode status per layer, then [L] attention aborts */
     float *d_logits;         /* [vocab] */
     void *d_sample;          /* mhip_sample scratch for vocab logits */
@@ -68,6 +70,12 @@ int mia_gpu_model_vocab(const mia_gpu_model *m) { return (int)m->info.vocab; }
 void mia_gpu_model_set_flags(mia_gpu_model *m, int flags) { m->flags = flags; }
 int mia_gpu_model_aborts(const mia_gpu_model *m) { return m->aborts; }
 
+int mia_gpu_model_trace(mia_gpu_model *m, unsigned long long *out) {
+    if (!m->stack_ok) return mfail(m, "no model stack at this shape");
+    if (mhip_decode_trace(m->gpu, m->d_mws, out)) return mfail(m, "%s", mhip_error(m->gpu));
+    return 0;
+}
+
 void mia_gpu_model_close(mia_gpu_model *m) {
     if (!m) return;
     if (m->gpu) {
@@ -81,6 +89,8 @@ void mia_gpu_model_close(mia_gpu_model *m) {
         mhip_free(m->gpu, m->d_xsave);
         mhip_free(m->gpu, m->d_xin);
         mhip_free(m->gpu, m->d_aws);
+        mhip_free(m->gpu, m->d_al);
+        mhip_free(m->gpu, m->d_mws);
         mhip_free(m->gpu, m->d_status);
         mhip_free(m->gpu, m->d_logits);
         mhip_free(m->gpu, m->d_sample);
@@ -145,6 +155,9 @@ static int setup(mia_gpu_model *m, int max_seq, int device) {
     const int aok = mhip_attention_layer_supported(m->gpu, &m->ad, max_seq);
     if (aok < 0) return mfail(m, "%s", mhip_error(m->gpu));
     m->attn_ok = aok > 0 && m->decode_ok;
+    const int sok = mhip_model_stack_supported(m->gpu, &m->mt.dims, &m->ad, max_seq);
+    if (sok < 0) return mfail(m, "%s", mhip_error(m->gpu));
+    m->stack_ok = sok > 0 && m->attn_ok;
     const size_t L = h->n_layers, kvd = (size_t)h->n_kv_heads * h->head_dim;
     const size_t half = h->head_dim / 2, ws = mhip_attention_scratch_bytes(&m->ad, max_seq);
     m->lo = calloc(L, sizeof(*m->lo));
@@ -165,6 +178,30 @@ static int setup(mia_gpu_model *m, int max_seq, int device) {
         m->d_xin = mhip_malloc(m->gpu, L * h->dim * 4);
         m->d_aws = mhip_malloc(m->gpu, mhip_attention_layer_ws_bytes());
         if (!m->d_xin || !m->d_aws) return mfail(m, "device memory: %s", mhip_error(m->gpu));
+    }
+    if (m->stack_ok) {
+        m->d_al = mhip_malloc(m->gpu, L * sizeof(mhip_attn_layer));
+        m->d_mws = mhip_malloc(m->gpu, mhip_model_stack_ws_bytes());
+        if (!m->d_al || !m->d_mws || !m->lo || !m->d_dense || !m->d_kc || !m->d_vc)
+            return mfail(m, "device memory: %s", mhip_error(m->gpu));
+        mhip_attn_layer *al = malloc(L * sizeof(*al));
+        if (!al) return mfail(m, "out of host memory");
+        for (size_t l = 0; l < L; l++) {
+            const mia_layer_offsets *o = &m->lo[l];
+            const unsigned char *b = m->d_dense;
+            al[l].attn_norm = (const float *)(b + o->attn_norm);
+            al[l].q_norm = (const float *)(b + o->q_norm);
+            al[l].k_norm = (const float *)(b + o->k_norm);
+            al[l].wq = b + o->wq;
+            al[l].wk = b + o->wk;
+            al[l].wv = b + o->wv;
+            al[l].wo = b + o->wo;
+            al[l].kc = m->d_kc + l * max_seq * kvd;
+            al[l].vc = m->d_vc + l * max_seq * kvd;
+        }
+        const int e = mhip_h2d(m->gpu, m->d_al, al, L * sizeof(*al));
+        free(al);
+        if (e) return mfail(m, "%s", mhip_error(m->gpu));
     }
     const size_t sb = mhip_sample_scratch_bytes((int)h->vocab);
     if (!sb) return mfail(m, "vocabulary of %u tokens: no sampler for it", h->vocab);
@@ -363,6 +400,35 @@ static int tail(mia_gpu_model *m, step_tail *t) {
     return 0;
 }
 
+/* The step's layers as one launch of the model stack (x in d_x holds the
+ * embedding row), then the tail; one wait. After an abort (rare) the token
+ * reruns from the embedding row through the per-stage kernels. */
+static int run_stack(mia_gpu_model *m, int pos, step_tail *t) {
+    const int L = (int)m->info.n_layers, d = (int)m->info.dim;
+    const mia_moe_tensors *mt = &m->mt;
+    if (mhip_d2d(m->gpu, m->d_xin, m->d_x, (size_t)d * 4) ||
+        mhip_model_stack(m->gpu, &mt->dims, &mt->lay, mt->table, mt->router_dl, mt->router_t,
+                         mt->norm, NULL, &m->ad, m->d_al, m->d_rope, pos, m->max_seq, m->d_x, L,
+                         m->d_mws, m->d_status,
+                         m->flags & (MHIP_FORCE_EXACT_ROUTER | MHIP_DECODE_FORCE_ABORT |
+                                     MHIP_ATTN_FORCE_ABORT | MHIP_DECODE_CHAINS_FIRST |
+                                     MHIP_FORCE_SEQ_RMS | MHIP_DECODE_TRACE)))
+        return mfail(m, "%s", mhip_error(m->gpu));
+    if (tail(m, t)) return -1;
+    if (mhip_d2h_async(m->gpu, m->h_status, m->d_status, 4 * sizeof(int)) || mhip_sync(m->gpu))
+        return mfail(m, "%s", mhip_error(m->gpu));
+    m->aborts = m->h_status[0] != 0;
+    if (m->aborts) {
+        if (mhip_d2d(m->gpu, m->d_x, m->d_xin, (size_t)d * 4)) return mfail(m, "%s", mhip_error(m->gpu));
+        for (int l = 0; l < L; l++)
+            if (attention(m, l, pos, 0) || moe(m, l, 1)) return -1;
+        if (tail(m, t)) return -1;
+        if (mhip_sync(m->gpu)) return mfail(m, "%s", mhip_error(m->gpu));
+    }
+    m->logits_ok = !t->no_head;
+    return 0;
+}
+
 /* One step, then the tail; 0 or -1. */
 static int run_step(mia_gpu_model *m, int token, int pos, step_tail *t) {
     const mia_file_info *h = &m->info;
@@ -378,6 +444,8 @@ static int run_step(mia_gpu_model *m, int token, int pos, step_tail *t) {
     const size_t row = (size_t)(d / MIA_QK) * 36;
     if (mhip_dequantize_q8(m->gpu, m->d_dense + m->off_embd + (size_t)token * row, m->d_x, d))
         return mfail(m, "%s", mhip_error(m->gpu));
+    if (decode && m->stack_ok && !(m->flags & MHIP_MODEL_PER_LAYER))
+        return run_stack(m, pos, t);
     const int one = decode && m->attn_ok;
     if (one && mhip_zero(m->gpu, m->d_status + 4 * (size_t)L, (size_t)L * 4))
         return mfail(m, "%s", mhip_error(m->gpu));

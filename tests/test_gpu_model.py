@@ -10,14 +10,16 @@ rmsnorm and output head (src/model/forward.c:199-217 of the reference) over
   every position up to 300;
 - two layers of the Qwen3-30B-A3B shape (attention 32/4 heads of 128, MoE
   128 x 768, top-8) with a 1000-token vocabulary: bit-equal to the oracle
-  with the exact router (and after forced aborts of every decode launch,
-  which rerun per stage); with the certified router (gate weights within
+  with the exact router (and after forced aborts of the model stack or of
+  every attention and decode launch, which rerun per stage); with the certified router (gate weights within
   ~1e-6 relative) the later layers' Q8 requantizations turn that into whole
   quantization steps, ~5e-4 of max|logit| each: max|diff| / max|ref| <= 2e-2,
   and the same top token wherever the reference's top-two margin exceeds
   twice that;
 - the full Qwen3-30B-A3B shape (48 layers, vocabulary 151936) generated in
-  HBM: the decode-kernel step bit-equal to the per-stage step.
+  HBM: the model stack (every layer of a token in one launch), one attention
+  and one MoE launch per layer, and the per-stage kernels give the same
+  logits bits.
 """
 import hashlib
 import json
@@ -119,13 +121,23 @@ def qwen_model(oracle, tmp_path_factory):
     return path, toks, want
 
 
+EXACT, PER_LAYER = M.MHIP_FORCE_EXACT_ROUTER, M.MHIP_MODEL_PER_LAYER
+
+
+# Steps of the model stack (one launch per token: an abort is one launch) and
+# of one attention and one MoE launch per layer (MHIP_MODEL_PER_LAYER).
 @pytest.mark.parametrize("flags,aborts", [
-    (M.MHIP_FORCE_EXACT_ROUTER, 0),
-    (M.MHIP_FORCE_EXACT_ROUTER | M.MHIP_DECODE_CHAINS_FIRST, 0),
-    (M.MHIP_FORCE_EXACT_ROUTER | M.MHIP_FORCE_SEQ_RMS, 0),
-    (M.MHIP_FORCE_EXACT_ROUTER | M.MHIP_DECODE_FORCE_ABORT, 2),
-    (M.MHIP_FORCE_EXACT_ROUTER | M.MHIP_ATTN_FORCE_ABORT, 2),
-    (M.MHIP_FORCE_EXACT_ROUTER | M.MHIP_ATTN_FORCE_ABORT | M.MHIP_DECODE_FORCE_ABORT, 4),
+    (EXACT, 0),
+    (EXACT | M.MHIP_DECODE_CHAINS_FIRST, 0),
+    (EXACT | M.MHIP_FORCE_SEQ_RMS, 0),
+    (EXACT | M.MHIP_DECODE_FORCE_ABORT, 1),
+    (EXACT | M.MHIP_ATTN_FORCE_ABORT, 1),
+    (EXACT | PER_LAYER, 0),
+    (EXACT | PER_LAYER | M.MHIP_DECODE_CHAINS_FIRST, 0),
+    (EXACT | PER_LAYER | M.MHIP_FORCE_SEQ_RMS, 0),
+    (EXACT | PER_LAYER | M.MHIP_DECODE_FORCE_ABORT, 2),
+    (EXACT | PER_LAYER | M.MHIP_ATTN_FORCE_ABORT, 2),
+    (EXACT | PER_LAYER | M.MHIP_ATTN_FORCE_ABORT | M.MHIP_DECODE_FORCE_ABORT, 4),
     (M.MHIP_EXACT_EXPERTS, 0),
 ])
 def test_model_qwen_shape_bit_exact(qwen_model, flags, aborts):
@@ -151,10 +163,11 @@ def check_certified(got, want, where):
     return err
 
 
-def test_model_qwen_shape_certified(qwen_model):
-    say("test_model_qwen_shape_certified")
+@pytest.mark.parametrize("flags", [0, PER_LAYER])
+def test_model_qwen_shape_certified(qwen_model, flags):
+    say("test_model_qwen_shape_certified flags=%d" % flags)
     path, toks, want = qwen_model
-    m = M.GpuModel(path, QWEN_TOKENS, flags=0)
+    m = M.GpuModel(path, QWEN_TOKENS, flags=flags)
     worst = 0.0
     try:
         for p, tok in enumerate(toks):
@@ -172,46 +185,57 @@ QWEN_FULL = dict(dim=2048, n_layers=48, n_heads=32, n_kv_heads=4, head_dim=128, 
 
 
 def test_model_full_shape_decode_equals_per_stage():
+    """48 layers: the model stack (one launch per token), one attention and
+    one MoE launch per layer, and the per-stage kernels give the same logits
+    bits; the certified router stays within its tolerance."""
     say("test_model_full_shape_decode_equals_per_stage")
     n = 6
     a = M.GpuModel(None, 64, synth=(QWEN_FULL, 5))
     b = M.GpuModel(None, 64, flags=M.MHIP_EXACT_EXPERTS, synth=(QWEN_FULL, 5))
     c = M.GpuModel(None, 64, flags=0, synth=(QWEN_FULL, 5))
+    d = M.GpuModel(None, 64, flags=EXACT | PER_LAYER, synth=(QWEN_FULL, 5))
     try:
         toks = np.random.default_rng(3).integers(0, QWEN_FULL["vocab"], n).tolist()
         worst = 0.0
         for p, tok in enumerate(toks):
-            la, lb, lc = a.step(tok, p), b.step(tok, p), c.step(tok, p)
-            assert a.aborts() == 0 and c.aborts() == 0
+            la, lb, lc, ld = a.step(tok, p), b.step(tok, p), c.step(tok, p), d.step(tok, p)
+            assert a.aborts() == 0 and c.aborts() == 0 and d.aborts() == 0
             assert np.all(np.isfinite(la))
             assert np.array_equal(bits(la), bits(lb)), "position %d" % p
+            assert np.array_equal(bits(ld), bits(lb)), "position %d (per layer)" % p
             worst = max(worst, check_certified(lc, lb.astype(np.float64), "position %d" % p))
-        say("  %d positions: decode step == per-stage step; certified worst %.3g" % (n, worst))
+        say("  %d positions: stack == per-layer == per-stage step; certified worst %.3g" % (n, worst))
     finally:
         a.close()
         b.close()
         c.close()
+        d.close()
 
 
 def test_model_full_shape_one_launch_attention_far_positions():
-    """The one-launch attention at positions past its 512 threads (several
-    scores per thread, a long mix), against the per-stage step; positions in
-    between are left empty (zero cache rows), so only the steps shown run."""
+    """The one-launch attention (in the model stack and per layer) at
+    positions past its 512 threads (several scores per thread, a long mix)
+    and around its 64 staged cache rows, against the per-stage step;
+    positions in between are left empty (zero cache rows), so only the steps
+    shown run."""
     say("test_model_full_shape_one_launch_attention_far_positions")
     a = M.GpuModel(None, 2048, synth=(QWEN_FULL, 6))
     b = M.GpuModel(None, 2048, flags=M.MHIP_EXACT_EXPERTS, synth=(QWEN_FULL, 6))
+    c = M.GpuModel(None, 2048, flags=EXACT | PER_LAYER, synth=(QWEN_FULL, 6))
     try:
         rng = np.random.default_rng(11)
-        for p in (0, 1, 700, 1500, 2047):
+        for p in (0, 1, 35, 64, 65, 700, 1500, 2047):
             tok = int(rng.integers(0, QWEN_FULL["vocab"]))
-            la, lb = a.step(tok, p), b.step(tok, p)
-            assert a.aborts() == 0
+            la, lb, lc = a.step(tok, p), b.step(tok, p), c.step(tok, p)
+            assert a.aborts() == 0 and c.aborts() == 0
             assert np.all(np.isfinite(la))
             assert np.array_equal(bits(la), bits(lb)), "position %d" % p
-        say("  positions 0, 1, 700, 1500, 2047: one-launch attention == per-stage")
+            assert np.array_equal(bits(lc), bits(lb)), "position %d (per layer)" % p
+        say("  positions 0 .. 2047: model stack == per-layer launches == per-stage")
     finally:
         a.close()
         b.close()
+        c.close()
 
 
 def test_model_long_context_attention_paths_agree(oracle, tmp_path):
