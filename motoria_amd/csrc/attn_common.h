@@ -46,6 +46,10 @@ __device__ __forceinline__ Blk load_blk(gptr<const uint8_t> p) {
     return b;
 }
 
+// s_waitcnt vmcnt(0) with the other counters left alone (expcnt 7,
+// lgkmcnt 15), for __builtin_amdgcn_s_waitcnt
+constexpr int WAIT_VM0 = 0x0F70;
+
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 // 16 bytes per lane from global memory straight into LDS, lane i's at
@@ -151,9 +155,9 @@ __device__ __forceinline__ void head_prefetch(HeadPre<NPRE, DMA> &p, HeadLds<NPR
                                               gptr<const float> vc, gptr<const float> q_norm,
                                               gptr<const float> k_norm, gptr<const double> rope,
                                               int tid) {
+    // (only threads below HD read these: the others' stay unset, so no
+    // register write has to wait for an older load of the same register)
     const int g = h / GROUP, npre = min(pos, NPRE);
-    p.rw0 = p.rw1 = 0.0f;
-    p.rc = p.rs = 0.0;
     if (tid < HD) {
         const int i = tid % (HD / 2);
         const gptr<const float> w = tid < HD / 2 ? q_norm : k_norm;
@@ -229,7 +233,9 @@ __device__ inline void head_run(HeadLds<NPRE> &s, float *sc, const HeadPre<NPRE,
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = h / GROUP, n = pos + 1, npre = min(pos, NPRE);
     if constexpr (DMA) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wavefront's cache rows are in
+        // this wavefront's cache rows are in (a wait the compiler sees: it
+        // then also counts every earlier load of the wavefront as done)
+        __builtin_amdgcn_s_waitcnt(WAIT_VM0);
     } else {
 #pragma unroll
         for (int j = 0; j < HeadPre<NPRE>::KPF; j++) {

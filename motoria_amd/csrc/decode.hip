@@ -475,7 +475,7 @@ __device__ __forceinline__ float wave_seq_sum_128(float a, float b) {
 // k_model_stack runs, for every layer, the attention of mhip_attention_layer
 // (attn_layer.hip: the same arithmetic, forward.c:118-165) before the MoE,
 // on x in LDS: every workgroup forms rmsnorm(x, attn_norm) and Q8 itself
-// (wavefront 0), every wavefront gw = 8 (32 xcd + rank) + wave its q/k/v
+// (four elements per thread), every wavefront gw = 8 (32 xcd + rank) + wave its q/k/v
 // rows gw + 2048 j (the block-order sum passed lane to lane) and row gw of
 // Wo; workgroups of rank < 4 run query head h = 8 rank + xcd (a key/value
 // group's heads on one rank, its first head on XCD 0 appending the cache
@@ -495,8 +495,16 @@ template <class T> __device__ __forceinline__ T *uniform_ptr(T *p) {
     return (T *)(((uint64_t)hi << 32) | lo);
 }
 
-__device__ void attn_stage(const DecodeArgs &a, Lds &sh, DecodeWs *ws, int tid, int lane,
-                           int wave, int xcd, int rank, int l, unsigned tag) {
+// `before_x` runs once the Wo rows are published, before the new x is
+// waited for: the caller's requests for the MoE that follows go there.
+template <class F>
+__device__ __forceinline__ void attn_stage(const DecodeArgs &a, Lds &sh, DecodeWs *ws, int tid,
+                                           int lane, int wave, int xcd, int rank, int l,
+                                           unsigned tag, F &&before_x) {
+    // Values derived from the workgroup's place are recomputed in every
+    // layer rather than held across the loop (the place is made opaque): the
+    // registers they would hold are what the MoE stages need.
+    asm volatile("" : "+s"(xcd), "+s"(rank), "+s"(wave));
     __shared__ at::HeadLds<AT_NPRE> hs;
     __shared__ alignas(16) int8_t attq[at::QD];
     __shared__ float atts[at::NBO];
@@ -524,14 +532,12 @@ __device__ void attn_stage(const DecodeArgs &a, Lds &sh, DecodeWs *ws, int tid, 
     const int gw = (xcd * WPX + rank) * NWAVE + wave;
     const bool head = rank < at::NH / NX;
     const int h = rank * NX + xcd;
-    // requests in the order they are needed: the norm weight (wavefront 0),
-    // the weight rows, then a head's first cache rows (copied into LDS)
-    float4 nv4[8];
-    if (wave == 0) {
-        const at::gptr<const float4> nr = (at::gptr<const float4>)(attn_norm + 32 * lane);
+    // requests in the order they are needed: the norm weights of this
+    // thread's elements tid + NT k, the weight rows, then a head's first
+    // cache rows (copied into LDS)
+    float anw[D / NT];
 #pragma unroll
-        for (int k = 0; k < 8; k++) nv4[k] = at::ld4(nr + k);
-    }
+    for (int k = 0; k < D / NT; k++) anw[k] = attn_norm[tid + NT * k];
     at::Blk wr[AT_RPW];
 #pragma unroll
     for (int j = 0; j < AT_RPW; j++) {
@@ -550,63 +556,62 @@ __device__ void attn_stage(const DecodeArgs &a, Lds &sh, DecodeWs *ws, int tid, 
         at::head_prefetch(hp, hs, h, a.pos, (at::gptr<const float>)kcg, (at::gptr<const float>)vcg,
                           at::glob(uniform_ptr(L.q_norm)), at::glob(uniform_ptr(L.k_norm)),
                           at::glob(a.rope), tid);
+    TRACE(34);
     // the previous layer's MoE ends with every thread storing its own part
     // of x in LDS: all of it is there before wavefront 0 reads it below
     __syncthreads();
+    TRACE(35);
 
-    // rmsnorm(x, attn_norm) and Q8 (forward.c:123, quant.c:11-27): lane b
-    // owns 32-block b; the certified sum of squares, else the sequential one
-    if (wave == 0) {
-        float v[32];
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const float4 q = *(const float4 *)&sh.x[32 * lane + 4 * k];
-            v[4 * k] = q.x;
-            v[4 * k + 1] = q.y;
-            v[4 * k + 2] = q.z;
-            v[4 * k + 3] = q.w;
-        }
+    // rmsnorm(x, attn_norm) and Q8 (forward.c:123, quant.c:11-27) by every
+    // thread over its elements i = tid + NT k (block i / 32 is 32 lanes of
+    // one wavefront): the sum of squares in any order is within
+    // (n + 64) 2^-52 S of the reference's sequential double sum (terms >= 0),
+    // so when S -/+ that bound give the same fp32 scale it is the reference's;
+    // otherwise thread 0 runs the sequential sum.
+    {
+        __shared__ double ssw[NWAVE];
+        __shared__ float inv_seq;
+        float xv[D / NT];
         double ss = 0.0;
 #pragma unroll
-        for (int k = 0; k < 32; k++) ss = ss + (double)v[k] * (double)v[k];
+        for (int k = 0; k < D / NT; k++) {
+            xv[k] = sh.x[tid + NT * k];
+            ss = ss + (double)xv[k] * (double)xv[k];
+        }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) ss = ss + __shfl_xor(ss, o);
-        ss = __shfl(ss, 0);
-        const double m = ss * ((double)(D + 64) * 0x1p-52);
-        const float lo = (float)(1.0 / sqrt((ss + m) / D + (double)a.eps));
-        const float hi = (float)(1.0 / sqrt((ss - m) / D + (double)a.eps));
+        if (lane == 0) ssw[wave] = ss;
+        __syncthreads();
+        TRACE(36);
+        double tot = 0.0;
+#pragma unroll
+        for (int w = 0; w < NWAVE; w++) tot = tot + ssw[w];
+        const double m = tot * ((double)(D + 64) * 0x1p-52);
+        const float lo = (float)(1.0 / sqrt((tot + m) / D + (double)a.eps));
+        const float hi = (float)(1.0 / sqrt((tot - m) / D + (double)a.eps));
         float inv = lo;
-        if ((a.flags & MHIP_FORCE_SEQ_RMS) || lo != hi) {
-            float r = 0.0f;
-            if (lane == 0) {
+        if ((a.flags & MHIP_FORCE_SEQ_RMS) || lo != hi) {  // the same in every thread
+            if (tid == 0) {
                 double sq = 0.0;
                 for (int i = 0; i < D; i++) sq = sq + (double)sh.x[i] * (double)sh.x[i];
-                r = (float)(1.0 / sqrt(sq / D + (double)a.eps));
+                inv_seq = (float)(1.0 / sqrt(sq / D + (double)a.eps));
             }
-            inv = __shfl(r, 0);
+            __syncthreads();
+            inv = inv_seq;
         }
+        TRACE(37);
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const float4 q = nv4[k];
-            v[4 * k] = (v[4 * k] * inv) * q.x;
-            v[4 * k + 1] = (v[4 * k + 1] * inv) * q.y;
-            v[4 * k + 2] = (v[4 * k + 2] * inv) * q.z;
-            v[4 * k + 3] = (v[4 * k + 3] * inv) * q.w;
+        for (int k = 0; k < D / NT; k++) {
+            const float v = (xv[k] * inv) * anw[k];
+            float am = fmaxf(0.0f, fabsf(v));  // a NaN counts as 0, as in the sequential max
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 32));
+            const float dsc = am / 127.0f;
+            const float qi = dsc != 0.0f ? 1.0f / dsc : 0.0f;
+            const int i = tid + NT * k;
+            sh.xq[i] = (int8_t)roundf(v * qi);
+            if ((lane & 31) == 0) sh.xs[i / 32] = dsc;
         }
-        float amax = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 32; k++) amax = fmaxf(amax, fabsf(v[k]));
-        const float dsc = amax / 127.0f;
-        const float qi = dsc != 0.0f ? 1.0f / dsc : 0.0f;
-        union {
-            int8_t c[32];
-            int4 q[2];
-        } qc;
-#pragma unroll
-        for (int k = 0; k < 32; k++) qc.c[k] = (int8_t)roundf(v[k] * qi);
-        *(int4 *)&sh.xq[32 * lane] = qc.q[0];
-        *(int4 *)&sh.xq[32 * lane + 16] = qc.q[1];
-        sh.xs[lane] = dsc;
     }
     __syncthreads();
     TRACE(25);
@@ -683,6 +688,7 @@ __device__ void attn_stage(const DecodeArgs &a, Lds &sh, DecodeWs *ws, int tid, 
         TRACE_BY(32, 63);
         if (lane == 63) put_tagged<false>(&xw->xa[gw], sh.x[gw] + sv, tag);
     }
+    before_x();
 
     // the new x in every workgroup: workgroup `rank` of each XCD fetches
     // words 64 rank .. + 63 across the device and republishes them in its
@@ -704,6 +710,11 @@ __device__ void attn_stage(const DecodeArgs &a, Lds &sh, DecodeWs *ws, int tid, 
         if (tid < ALW) ((unsigned *)&al_next)[tid] = alw;
         __syncthreads();
     }
+    // every load of this stage has long arrived (the heads' values were
+    // used, the other threads' loads are older than the exchanges above); a
+    // wait the compiler sees keeps it from assuming any of them is still in
+    // flight when the next layer reuses their registers
+    __builtin_amdgcn_s_waitcnt(at::WAIT_VM0);
     TRACE(31);
 }
 
