@@ -102,3 +102,19 @@ def test_decode_stack_rejects_more_than_256_layers_before_any_device_call():
         rc = L.mhip_decode_stack(None, ctypes.byref(d), ctypes.byref(lay), None, None, None,
                                  None, None, None, bad, None, None, None, 0)
         assert rc == -1
+
+
+def test_python_constants_match_the_headers():
+    """Every MHIP_* constant the Python bindings mirror has the header's value
+    (and the decode trace's window, TRACE_L0 / TRACE_NL / TRACE_SLOTS)."""
+    defines = {}
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, h)).read(), flags=re.S)
+        for m in re.finditer(r"^#define\s+(MHIP_\w+)\s+(\d+)\s*$", text, flags=re.M):
+            defines[m.group(1)] = int(m.group(2))
+    mirrored = [k for k in defines if hasattr(M, k)]
+    assert len(mirrored) > 10
+    for k in mirrored:
+        assert getattr(M, k) == defines[k], k
+    assert (M.TRACE_L0, M.TRACE_NL, M.TRACE_SLOTS) == (
+        defines["MHIP_TRACE_L0"], defines["MHIP_TRACE_NL"], defines["MHIP_TRACE_SLOTS"])

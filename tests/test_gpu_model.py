@@ -238,6 +238,31 @@ def test_model_full_shape_one_launch_attention_far_positions():
         c.close()
 
 
+def test_model_full_shape_stack_at_its_longest_context():
+    """The model stack's largest context (MHIP_MODEL_STACK_MAX_SEQ positions:
+    the last position's 8192 scores fill the dynamic LDS) against the
+    per-stage step; one past it the model runs per layer (same bits)."""
+    say("test_model_full_shape_stack_at_its_longest_context")
+    n = M.MHIP_MODEL_STACK_MAX_SEQ
+    a = M.GpuModel(None, n, synth=(QWEN_FULL, 8))
+    b = M.GpuModel(None, n, flags=M.MHIP_EXACT_EXPERTS, synth=(QWEN_FULL, 8))
+    c = M.GpuModel(None, n + 1, synth=(QWEN_FULL, 8))
+    try:
+        rng = np.random.default_rng(12)
+        for p in (0, 33, n // 2, n - 1):
+            tok = int(rng.integers(0, QWEN_FULL["vocab"]))
+            la, lb, lc = a.step(tok, p), b.step(tok, p), c.step(tok, p)
+            assert a.aborts() == 0 and c.aborts() == 0
+            assert np.all(np.isfinite(la))
+            assert np.array_equal(bits(la), bits(lb)), "position %d" % p
+            assert np.array_equal(bits(lc), bits(lb)), "position %d (max_seq %d)" % (p, n + 1)
+        say("  positions 0, 33, %d, %d: stack == per-stage == per-layer" % (n // 2, n - 1))
+    finally:
+        a.close()
+        b.close()
+        c.close()
+
+
 def test_model_long_context_attention_paths_agree(oracle, tmp_path):
     """The per-head attention kernel keeps the scores in LDS; a context too
     long for that runs the separate score and mix kernels. Both give the
