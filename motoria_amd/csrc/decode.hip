@@ -44,6 +44,12 @@
 // reference's rounding order; the gate weights come from the parallel logits
 // (relative error ~1e-6 against the reference's), unless the exact fallback
 // ran for that layer.
+//
+// The same body (decode_body.inc) compiles twice: k_decode_stack, the MoE
+// alone, and k_model_stack, which runs each layer's attention (attn_stage:
+// rmsnorm, Q/K/V rows, the 32 heads with the KV cache, Wo and the residual,
+// src/model/forward.c:118-165) before that layer's MoE, so a whole decode
+// token is one launch (forward.c:210-213).
 #include "attn_common.h"
 #include "mhip_internal.h"
 
