@@ -249,7 +249,7 @@ int mhip_decode_status(mhip_ctx *c, const void *d_ws, int status[4]);
  * Diagnostic. */
 #define MHIP_TRACE_L0 8
 #define MHIP_TRACE_NL 8
-#define MHIP_TRACE_SLOTS 40
+#define MHIP_TRACE_SLOTS 48
 int mhip_decode_trace(mhip_ctx *c, const void *d_ws, unsigned long long *out);
 
 /* ---- attention and output head of one token (decode) ---------------------

@@ -34,7 +34,7 @@ MHIP_MODEL_PER_LAYER = 128
 MHIP_MODEL_STACK_MAX_SEQ = 8192  # longest context of the model stack (mia_hip.h)
 DECODE_MAX_LAYERS = 256  # MHIP_DECODE_MAX_LAYERS
 GEMM_MIN_A = 2048  # MHIP_GEMM_MIN_A
-TRACE_L0, TRACE_NL, TRACE_SLOTS = 8, 8, 40  # decode trace window (MHIP_TRACE_* in mia_hip.h)
+TRACE_L0, TRACE_NL, TRACE_SLOTS = 8, 8, 48  # decode trace window (MHIP_TRACE_* in mia_hip.h)
 STAGES = ["rmsnorm", "router", "dispatch", "gateup", "down", "combine", "decode"]
 
 

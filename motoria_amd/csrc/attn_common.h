@@ -217,6 +217,11 @@ __device__ __forceinline__ float head_dot(const float *qs, P4 k4p) {
     return dot;
 }
 
+// A phase mark that does nothing (head_run's default).
+struct NoMark {
+    __device__ void operator()(int) const {}
+};
+
 // Query head h (forward.c:127-163) by a whole workgroup, every thread
 // calling, once s.tq, s.tk, s.tv hold its q row and its group's k and v
 // rows (with DMA, after head_prefetch issued the cache rows' copies): the
@@ -225,10 +230,11 @@ __device__ __forceinline__ float head_dot(const float *qs, P4 k4p) {
 // key row read 32 values ahead), softmax (the maximum, the restated expf,
 // the sequential sum, the division), the mix in position order, and Q8 of
 // the head's output into s.hq / s.dsc. sc: pos + 1 floats of LDS.
-template <int NPRE, bool DMA>
+// mark(i), i = 0..8, runs after each of its barriers (a caller's phase trace).
+template <int NPRE, bool DMA, class Mark = NoMark>
 __device__ inline void head_run(HeadLds<NPRE> &s, float *sc, const HeadPre<NPRE, DMA> &p, int h,
                                 int pos, gptr<float> kcg, gptr<float> vcg, float eps, float scale,
-                                bool force_seq, const uint64_t *etab) {
+                                bool force_seq, const uint64_t *etab, Mark mark = Mark()) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = h / GROUP, n = pos + 1, npre = min(pos, NPRE);
@@ -247,14 +253,17 @@ __device__ inline void head_run(HeadLds<NPRE> &s, float *sc, const HeadPre<NPRE,
         }
     }
     __syncthreads();
+    mark(0);
     if (wave < 2) {
         const float inv = head_inv_wave(wave == 0 ? s.tq : s.tk, eps, lane, force_seq);
         if (lane == 0) (wave == 0 ? s.inv_q : s.inv_k) = inv;
     }
     __syncthreads();
+    mark(1);
     if (tid < HD / 2) head_rope(s.tq, s.inv_q, p.rw0, p.rw1, p.rc, p.rs, s.qs, tid);
     else if (tid < HD) head_rope(s.tk, s.inv_k, p.rw0, p.rw1, p.rc, p.rs, s.ks, tid - HD / 2);
     __syncthreads();
+    mark(2);
     if (h % GROUP == 0 && tid < HD) {
         kcg[(size_t)pos * KVD + (size_t)g * HD + tid] = s.ks[tid];
         vcg[(size_t)pos * KVD + (size_t)g * HD + tid] = s.tv[tid];
@@ -268,25 +277,30 @@ __device__ inline void head_run(HeadLds<NPRE> &s, float *sc, const HeadPre<NPRE,
         sc[t] = dot * scale;
     }
     __syncthreads();
+    mark(3);
     float mx = -__builtin_inff();
     for (int t = tid; t < n; t += NT) mx = fmaxf(mx, sc[t]);
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
     if (lane == 0) s.red[wave] = mx;
     __syncthreads();
+    mark(4);
 #pragma unroll
     for (int w = 0; w < NW; w++) mx = fmaxf(mx, s.red[w]);
     for (int t = tid; t < n; t += NT) sc[t] = mia_expf_glibc_tab(sc[t] - mx, etab);
     __syncthreads();
+    mark(5);
     if (tid == 0) {
         float sum = 0.0f;
         for (int t = 0; t < n; t++) sum = sum + sc[t];
         s.sum = sum;
     }
     __syncthreads();
+    mark(6);
     const float sum = s.sum;
     for (int t = tid; t < n; t += NT) sc[t] = sc[t] / sum;
     __syncthreads();
+    mark(7);
     if (tid < HD) {
         const gptr<const float> vt = vcg + (size_t)g * HD + tid;
         float o = 0.0f;
@@ -310,6 +324,7 @@ __device__ inline void head_run(HeadLds<NPRE> &s, float *sc, const HeadPre<NPRE,
         if ((lane & 31) == 0) s.dsc[tid / 32] = d;
     }
     __syncthreads();
+    mark(8);
 }
 
 }  // namespace mhip_attn

@@ -664,7 +664,8 @@ __device__ __forceinline__ void attn_stage(const DecodeArgs &a, Lds &sh, DecodeW
         }
         TRACE(27);
         at::head_run(hs, asc, hp, h, a.pos, kcg, vcg, a.eps, a.scale,
-                     (a.flags & MHIP_FORCE_SEQ_RMS) != 0, sh.etab);
+                     (a.flags & MHIP_FORCE_SEQ_RMS) != 0, sh.etab,
+                     [=](int i) { TRACE(38 + i); });
         TRACE(28);
         if (tid < at::HD / 32) put_tagged<false>(&xw->atts[h * (at::HD / 32) + tid], hs.dsc[tid], tag);
         if (tid < at::HD / 4)
