@@ -60,6 +60,48 @@ __device__ __forceinline__ void dma16(unsigned lds, const void *g) {
 }
 #pragma clang diagnostic pop
 
+// A DPP move of x (lanes of rows outside ROWS keep their own value, resp. 0
+// for the double).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), CTRL, ROWS, 0xf, false));
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ double dpp_d0(double x) {
+    const uint64_t u = (uint64_t)__double_as_longlong(x);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)u, CTRL, ROWS, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(u >> 32), CTRL, ROWS, 0xf, false);
+    return __longlong_as_double((long long)(((uint64_t)(unsigned)hi << 32) | (unsigned)lo));
+}
+
+// The maximum of v over each half wavefront (lanes 0-31, 32-63), in every
+// lane of that half, by DPP moves (quad exchanges, row mirrors, the row
+// broadcast): exact for values that are not NaN, in any order.
+__device__ __forceinline__ float max32(float v, int lane) {
+    v = fmaxf(v, dpp_f<0xB1, 0xf>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f<0x4E, 0xf>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f<0x141, 0xf>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_f<0x140, 0xf>(v));  // row_mirror: every lane holds its row's maximum
+    v = fmaxf(v, dpp_f<0x142, 0xa>(v));  // row_bcast:15 into rows 1 and 3
+    const float h0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+    const float h1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    return lane < 32 ? h0 : h1;
+}
+
+// The sum of v over the wavefront, in lane 63 (other lanes hold partial
+// sums), by DPP moves of the two halves of each double; the order of the
+// additions is fixed but not the index order.
+__device__ __forceinline__ double wave_sum63(double v) {
+    v = v + dpp_d0<0xB1, 0xf>(v);
+    v = v + dpp_d0<0x4E, 0xf>(v);
+    v = v + dpp_d0<0x141, 0xf>(v);
+    v = v + dpp_d0<0x140, 0xf>(v);
+    v = v + dpp_d0<0x142, 0xa>(v);  // rows 1, 3: + the row below (rows 0, 2: + 0)
+    v = v + dpp_d0<0x143, 0xc>(v);  // rows 2, 3: + lane 31 (rows 0, 1: + 0)
+    return v;
+}
+
 // DPP moves of the whole wavefront by one lane (lane 0 receives 0, resp.
 // lane 63's value).
 __device__ __forceinline__ float shr1(float v) {
@@ -315,9 +357,7 @@ __device__ inline void head_run(HeadLds<NPRE> &s, float *sc, const HeadPre<NPRE,
         }
         for (; t < pos; t++) o = o + sc[t] * vt[(size_t)t * KVD];
         o = o + sc[pos] * s.tv[tid];
-        float am = fmaxf(0.0f, fabsf(o));
-#pragma unroll
-        for (int m = 16; m >= 1; m >>= 1) am = fmaxf(am, __shfl_xor(am, m, 32));
+        const float am = max32(fmaxf(0.0f, fabsf(o)), lane);  // a NaN counts as 0
         const float d = am / 127.0f;
         const float qi = d != 0.0f ? 1.0f / d : 0.0f;
         s.hq[tid] = (int8_t)roundf(o * qi);

@@ -584,9 +584,8 @@ __device__ __forceinline__ void attn_stage(const DecodeArgs &a, Lds &sh, DecodeW
             xv[k] = sh.x[tid + NT * k];
             ss = ss + (double)xv[k] * (double)xv[k];
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss = ss + __shfl_xor(ss, o);
-        if (lane == 0) ssw[wave] = ss;
+        ss = at::wave_sum63(ss);
+        if (lane == 63) ssw[wave] = ss;
         __syncthreads();
         TRACE(36);
         double tot = 0.0;
@@ -609,9 +608,8 @@ __device__ __forceinline__ void attn_stage(const DecodeArgs &a, Lds &sh, DecodeW
 #pragma unroll
         for (int k = 0; k < D / NT; k++) {
             const float v = (xv[k] * inv) * anw[k];
-            float am = fmaxf(0.0f, fabsf(v));  // a NaN counts as 0, as in the sequential max
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 32));
+            // (a NaN counts as 0, as in the sequential max)
+            const float am = at::max32(fmaxf(0.0f, fabsf(v)), lane);
             const float dsc = am / 127.0f;
             const float qi = dsc != 0.0f ? 1.0f / dsc : 0.0f;
             const int i = tid + NT * k;
