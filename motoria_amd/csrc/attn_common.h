@@ -102,6 +102,26 @@ __device__ __forceinline__ double wave_sum63(double v) {
     return v;
 }
 
+// Lane L's double, in every lane.
+__device__ __forceinline__ double readlane_d(double x, int L) {
+    const uint64_t u = (uint64_t)__double_as_longlong(x);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)u, L);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(u >> 32), L);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// The maximum of v over the wavefront, in every lane (as max32, then lane
+// 31's value into rows 2 and 3).
+__device__ __forceinline__ float max64(float v) {
+    v = fmaxf(v, dpp_f<0xB1, 0xf>(v));
+    v = fmaxf(v, dpp_f<0x4E, 0xf>(v));
+    v = fmaxf(v, dpp_f<0x141, 0xf>(v));
+    v = fmaxf(v, dpp_f<0x140, 0xf>(v));
+    v = fmaxf(v, dpp_f<0x142, 0xa>(v));
+    v = fmaxf(v, dpp_f<0x143, 0xc>(v));  // row_bcast:31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // DPP moves of the whole wavefront by one lane (lane 0 receives 0, resp.
 // lane 63's value).
 __device__ __forceinline__ float shr1(float v) {
@@ -138,16 +158,14 @@ __device__ inline float head_inv_seq(const float *row, float eps) {
 __device__ __forceinline__ float head_inv_wave(const float *row, float eps, int lane, bool force_seq) {
     const float2 v = *(const float2 *)(row + 2 * lane);
     double ss = (double)v.x * (double)v.x + (double)v.y * (double)v.y;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss = ss + __shfl_xor(ss, o);
-    ss = __shfl(ss, 0);
+    ss = readlane_d(wave_sum63(ss), 63);
     const double m = ss * ((double)(HD + 64) * 0x1p-52);
     const float lo = (float)(1.0 / sqrt((ss + m) / HD + (double)eps));
     const float hi = (float)(1.0 / sqrt((ss - m) / HD + (double)eps));
     if (lo == hi && !force_seq) return lo;  // the same in every lane
     float r = 0.0f;
     if (lane == 0) r = head_inv_seq(row, eps);
-    return __shfl(r, 0);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r), 0));
 }
 
 // The normalized row, NeoX-rotated (forward.c:127-139): element i with
@@ -322,8 +340,7 @@ __device__ inline void head_run(HeadLds<NPRE> &s, float *sc, const HeadPre<NPRE,
     mark(3);
     float mx = -__builtin_inff();
     for (int t = tid; t < n; t += NT) mx = fmaxf(mx, sc[t]);
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+    mx = max64(mx);  // (fmaxf keeps the larger of a number and a NaN: any order gives this)
     if (lane == 0) s.red[wave] = mx;
     __syncthreads();
     mark(4);
