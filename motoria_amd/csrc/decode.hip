@@ -554,9 +554,11 @@ __device__ __forceinline__ void attn_stage(const DecodeArgs &a, Lds &sh, DecodeW
                                               : wvg + (size_t)(r - at::QD - at::KVD) * at::NB * 36;
         wr[j] = at::load_blk(w + (size_t)lane * 36);
     }
+    // This wavefront's Wo row is requested once its q/k/v rows are in (and,
+    // in a head's workgroup, once the head is done): the q/k/v rows, on the
+    // critical path, then do not share HBM with the Wo rows.
     const at::gptr<const uint8_t> wo = wog + (size_t)gw * at::NBO * 36;
-    const at::Blk wo0 = at::load_blk(wo + (size_t)lane * 36),
-                  wo1 = at::load_blk(wo + (size_t)(lane + 64) * 36);
+    at::Blk wo0, wo1;
     at::HeadPre<AT_NPRE, true> hp;
     if (head)
         at::head_prefetch(hp, hs, h, a.pos, (at::gptr<const float>)kcg, (at::gptr<const float>)vcg,
@@ -644,6 +646,10 @@ __device__ __forceinline__ void attn_stage(const DecodeArgs &a, Lds &sh, DecodeW
         }
     }
     TRACE_BY(26, 63);
+    if (!head) {
+        wo0 = at::load_blk(wo + (size_t)lane * 36);
+        wo1 = at::load_blk(wo + (size_t)(lane + 64) * 36);
+    }
 
     // query head h (forward.c:127-163)
     if (head) {
@@ -669,6 +675,8 @@ __device__ __forceinline__ void attn_stage(const DecodeArgs &a, Lds &sh, DecodeW
         if (tid < at::HD / 4)
             put_tagged<false>(&xw->attq[h * (at::HD / 4) + tid],
                               __uint_as_float(((const unsigned *)hs.hq)[tid]), tag);
+        wo0 = at::load_blk(wo + (size_t)lane * 36);
+        wo1 = at::load_blk(wo + (size_t)(lane + 64) * 36);
     }
 
     // row gw of Wo over the heads' codes, plus the residual (forward.c:164-165)
