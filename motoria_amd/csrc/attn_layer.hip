@@ -149,9 +149,11 @@ __global__ __launch_bounds__(NT) void k_attn_layer(AttnArgs a) {
     }
     // (and the q/k/v rows of every wavefront ahead of the Wo rows)
     __syncthreads();
+    // This wavefront's Wo row is requested once its q/k/v rows are out (in
+    // a head's workgroup once the head is done): the q/k/v rows, on the
+    // critical path, then do not share HBM with the Wo rows.
     const uint8_t *wo = a.wo + (size_t)gw * NBO * 36;
-    const Blk wo0 = load_blk(glob(wo + (size_t)lane * 36)),
-              wo1 = load_blk(glob(wo + (size_t)(lane + 64) * 36));
+    Blk wo0, wo1;
     // x's copy for a rerun: x is written back (in P4) only by a workgroup
     // whose waits all ended, and then every workgroup has started and read
     // its row and wavefront 0's part of x.
@@ -242,6 +244,10 @@ __global__ __launch_bounds__(NT) void k_attn_layer(AttnArgs a) {
         }
     }
     ATRACE(3, 63);
+    if (b >= NH) {
+        wo0 = load_blk(glob(wo + (size_t)lane * 36));
+        wo1 = load_blk(glob(wo + (size_t)(lane + 64) * 36));
+    }
 
     // ---- P3: query head b (k_attn_head) --------------------------------------------
     if (b < NH) {
@@ -257,6 +263,8 @@ __global__ __launch_bounds__(NT) void k_attn_layer(AttnArgs a) {
                  (a.flags & MHIP_FORCE_SEQ_RMS) != 0, sh.etab);
         if (tid < HD / 32) put_word(&a.ws->atts[h * (HD / 32) + tid], __float_as_uint(sh.head.dsc[tid]), a.tag);
         if (tid < HD / 4) put_word(&a.ws->attq[h * (HD / 4) + tid], ((const unsigned *)sh.head.hq)[tid], a.tag);
+        wo0 = load_blk(glob(wo + (size_t)lane * 36));
+        wo1 = load_blk(glob(wo + (size_t)(lane + 64) * 36));
         ATRACE(5, 0);
     }
 
