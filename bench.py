@@ -6,12 +6,16 @@ the configuration the HBM-roofline target is stated on. A step is one token
 through the 48 layers; inputs and weights are synthetic (seeded, generated in
 HBM) and resident before the timed region starts.
 
-Prints one JSON line: throughput (tokens/s), the whole-step HBM rate, the
-roofline of the dominant kernel (timed live with HIP events on the library's
-stream), the same for the T=4096 prefill layer on the matrix cores (the
-second target, measured in the same run), and the reference C path (the CPU
-oracle: one thread, all host cores, and -march=native) timed on a bounded
-sample of the same workload on this host.
+Prints one JSON line: throughput (tokens/s) of the exact-router decode
+kernel (every layer bit-equal to the reference), the whole-step HBM rate,
+the roofline of the dominant kernel (timed live with HIP events on the
+library's stream), the same stack with the opt-in certified router, every
+other configuration of the benchmark (one decode layer, prefill 512, the
+skewed 2048, 64 sequences x 48 layers, the T=4096 layer on the matrix cores
+-- the second target -- and 4096 tokens x 48 layers) with its bound and its
+dominant kernel's roofline fraction, the whole model step, and the reference
+C path (the CPU oracle: one thread, all host cores, and -march=native) timed
+on a bounded sample of the same workload on this host.
 """
 import argparse
 import json
@@ -47,18 +51,57 @@ def cpu_model():
     return platform.processor() or "unknown"
 
 
+# The source files each profiled kernel is compiled from (with the headers
+# it includes): a counter summary describes the kernel only while their
+# digest is the one it records.
+KERNEL_SOURCES = {
+    "k_decode_stack": ["motoria_amd/csrc/decode.hip", "motoria_amd/csrc/decode_body.inc",
+                       "motoria_amd/csrc/attn_common.h", "motoria_amd/csrc/mhip_internal.h",
+                       "motoria_amd/csrc/expf_glibc.h"],
+    "k_gateup_mfma": ["motoria_amd/csrc/moe_gemm.hip", "motoria_amd/csrc/mhip_internal.h",
+                      "motoria_amd/csrc/expf_glibc.h"],
+    "k_gateup": ["motoria_amd/csrc/moe_layer.hip", "motoria_amd/csrc/mhip_internal.h",
+                 "motoria_amd/csrc/expf_glibc.h"],
+}
+
+
+def sources_digest(kernel):
+    """First 16 hex digits of the SHA-256 over `kernel`'s source files, in
+    the order listed (each file's path, then its bytes)."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES[kernel]:
+        h.update(rel.encode() + b"\0")
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def profiled_traffic(workload, kernel):
     """HBM bytes per launch of `kernel` on `workload` from the committed
     rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, each scaled by the
-    same counter's reading over a copy of known size), or None."""
+    same counter's reading over a copy of known size), and a note. None when
+    there is no summary, or when the digest of the kernel's sources it
+    records is not that of the sources built now (it then describes another
+    build of the kernel)."""
     path = os.path.join(ROOT, "profiles", "%s_%s_traffic.md" % (workload, kernel))
+    value, digest = None, None
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_launch:"):
-                return int(line.split(":", 1)[1])
+                value = int(line.split(":", 1)[1])
+            elif line.startswith("sources_sha256:"):
+                digest = line.split(":", 1)[1].strip()
     except OSError:
-        pass
-    return None
+        return None, "no counter summary"
+    now = sources_digest(kernel) if kernel in KERNEL_SOURCES else None
+    if value is None or digest is None or digest != now:
+        log("traffic: %s records sources %s, the kernel's sources are %s: not used"
+            % (os.path.basename(path), digest, now))
+        return None, "profiles/%s is of other sources (%s, now %s)" % (
+            os.path.basename(path), digest, now)
+    return value, "profiles/%s (sources %s)" % (os.path.basename(path), digest)
 
 
 def routing_census(moe, d_x, d_x0, layers, T, nbytes, d_bias):
@@ -213,12 +256,14 @@ def gateup_bytes_matrix(n_touched, T, shape):
     return w + T * d * 2 + T * K * (d // 32) * 4 + T * K * eh * 2 + T * K * (eh // 32) * 4
 
 
-def measure(wl_name, steps, warmup, multi_kernel=False, graph=True):
+def measure(wl_name, steps, warmup, multi_kernel=False, graph=True, flags=0):
     """Times `steps` steps of one workload on a fresh handle (weights and x
     generated in HBM first). Returns (result dict, handle); the caller
     closes the handle. A multi-kernel stack without a bias runs as one HIP
     graph replay per step (graph=True), its dominant kernel then timed in a
-    separate eager pass."""
+    separate eager pass. `flags` go to mia_moe_set_flags (0: the exact
+    router, bit-equal to the reference; MHIP_DECODE_CERTIFIED: the decode
+    kernel's gate weights from the parallel logits)."""
     wl = W.WORKLOADS[wl_name]
     shape = dict(W.SHAPE)
     L, T = wl["layers"], wl["tokens"]
@@ -226,6 +271,7 @@ def measure(wl_name, steps, warmup, multi_kernel=False, graph=True):
     log("workload %s: %s" % (wl_name, wl["doc"]))
     t0 = time.perf_counter()
     moe = M.Moe(n_layers=L, max_tokens=T, device=0, **shape)
+    moe.set_flags(flags)
     moe.synth(W.WEIGHT_SEED)
     moe.sync()
     log("expert table (%d layers, %.2f GiB) generated in HBM in %.2f s"
@@ -342,20 +388,26 @@ def measure(wl_name, steps, warmup, multi_kernel=False, graph=True):
         achieved = flops / dom_avg_s / 1e12
         roof = {"kernel": dom_name, "bound": "mfma", "achieved": achieved,
                 "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / MFMA_PEAK_TFLOPS,
-                "traffic": profiled_traffic(wl_name, "k_gateup_mfma"), "flops_per_launch": flops,
+                "traffic": None, "flops_per_launch": flops,
                 "avg_launch_us": dom_avg_s * 1e6,
                 "layer_tflops": step_ops / (ms_step / 1e3) / 1e12,
                 "layer_frac": step_ops / (ms_step / 1e3) / 1e12 / MFMA_PEAK_TFLOPS}
     else:
         achieved = dom_bytes / dom_avg_s / 1e9
-        kname = ("k_decode_stack" if persistent else
-                 "k_gateup_mfma" if matrix else "k_gateup")
         roof = {"kernel": dom_name, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                "traffic": profiled_traffic(wl_name, kname), "bytes_per_launch": dom_bytes,
+                "traffic": None, "bytes_per_launch": dom_bytes,
                 "avg_launch_us": dom_avg_s * 1e6}
+    kname = "k_decode_stack" if persistent else "k_gateup_mfma" if matrix else "k_gateup"
+    roof["traffic"], roof["traffic_source"] = profiled_traffic(wl_name, kname)
+    path = ("persistent decode kernel, exact router" if persistent and not
+            (flags & M.MHIP_DECODE_CERTIFIED) else
+            "persistent decode kernel, certified router" if persistent else
+            ("one launch per stage, expert products on the matrix cores" if matrix else
+             "one launch per stage") + ("; the stack replayed as one HIP graph per step"
+                                        if graphed else ""))
     res = {
-        "workload": wl_name, "wl": wl, "shape": shape, "L": L, "T": T, "steps": steps,
+        "workload": wl_name, "wl": wl, "shape": shape, "L": L, "T": T, "steps": steps, "path": path,
         "warmup": warmup, "ms_step": ms_step, "tokens_per_s": tokens_per_s,
         "step_bytes": step_bytes, "step_ops": step_ops, "hbm_gbs": hbm_gbs,
         "intensity": ai, "touched": touched, "roofline": roof, "persistent": persistent,
@@ -388,7 +440,7 @@ def model_decode(steps, warmup):
     reference) at the full Qwen3-30B-A3B shape, weights generated in HBM,
     tokens fed back greedily on the device (mia_gpu_model_step_sample)."""
     out = {}
-    for name, flags in (("exact", M.MHIP_FORCE_EXACT_ROUTER), ("certified", 0)):
+    for name, flags in (("exact", 0), ("certified", M.MHIP_DECODE_CERTIFIED)):
         m = M.GpuModel(None, warmup + steps + 1, flags=flags, synth=(QWEN_MODEL, 5))
         s = M.sampler(0.0, 1.0, QWEN_MODEL["vocab"], 1)
         tok = 1
@@ -464,8 +516,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="decode48", choices=sorted(W.WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-prefill", action="store_true",
-                    help="skip the T=4096 layer measured beside the default workload")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other configurations (and the certified-router stack) "
+                         "measured beside the default workload")
     ap.add_argument("--no-model", action="store_true",
                     help="skip the whole-model step measured beside the default workload")
     ap.add_argument("--only-model", action="store_true",
@@ -508,15 +561,47 @@ def main():
             % (cpu["value"], cpu["cores"], time.perf_counter() - t0))
     moe.close()
 
-    # The second target (the T=4096 prefill layer on the matrix cores),
-    # measured in the same run beside the default workload.
-    prefill = None
-    if args.workload == "decode48" and not args.no_prefill:
-        pres, pmoe = measure("prefill4096", 10, 3)
-        pmoe.close()
-        prefill = dict(pres["roofline"], workload="prefill4096: " + pres["wl"]["doc"],
-                       layer_ms=pres["ms_step"], tokens_per_s=pres["tokens_per_s"],
-                       intensity=pres["intensity"])
+    # The same stack with the opt-in certified router (gate weights from the
+    # parallel logits: not the reference's bits over many layers), for
+    # comparison only.
+    certified = None
+    if args.workload == "decode48" and not args.no_configs:
+        cres, cmoe = measure("decode48", args.steps, args.warmup, flags=M.MHIP_DECODE_CERTIFIED)
+        cmoe.close()
+        certified = {"tokens_per_s": cres["tokens_per_s"], "ms_per_step": cres["ms_step"],
+                     "frac": cres["roofline"]["frac"],
+                     "note": "MHIP_DECODE_CERTIFIED: indices bit-equal, gate weights ~1e-6 "
+                             "relative off, so the 48-layer output drifts from the reference's"}
+
+    # Every other configuration of the benchmark, each on a fresh handle:
+    # throughput, the bound its arithmetic intensity gives, and the dominant
+    # kernel's roofline fraction. The T=4096 layer (the matrix-core target)
+    # is also reported as roofline_prefill4096.
+    prefill, configs = None, {}
+    if args.workload == "decode48" and not args.no_configs:
+        for name, steps, warm in (("decode1", 200, 20), ("prefill512", 20, 3),
+                                  ("skew2048", 20, 3), ("batch64x48", 10, 2),
+                                  ("prefill4096", 10, 3), ("prefill4096x48", 3, 1)):
+            cres, cmoe = measure(name, steps, warm)
+            cmoe.close()
+            roof = cres["roofline"]
+            configs[name] = {
+                "workload": cres["wl"]["doc"], "layers": cres["L"], "tokens_per_step": cres["T"],
+                "tokens_per_s": cres["tokens_per_s"], "ms_per_step": cres["ms_step"],
+                "steps": steps, "path": cres["path"],
+                "bound": "mfma" if cres["intensity"] >= RIDGE else "hbm",
+                "intensity_op_per_byte": cres["intensity"],
+                "hbm_frac": cres["hbm_gbs"] / HBM_PEAK_GBS,
+                "step_tflops": cres["step_ops"] / (cres["ms_step"] / 1e3) / 1e12,
+                "dominant_kernel": roof["kernel"], "kernel_bound": roof["bound"],
+                "kernel_achieved": roof["achieved"], "kernel_unit": roof["unit"],
+                "kernel_frac": roof["frac"], "kernel_avg_launch_us": roof["avg_launch_us"],
+                "experts_touched_per_layer_mean": float(np.mean(cres["touched"])),
+            }
+            if name == "prefill4096":
+                prefill = dict(roof, workload="prefill4096: " + cres["wl"]["doc"],
+                               layer_ms=cres["ms_step"], tokens_per_s=cres["tokens_per_s"],
+                               intensity=cres["intensity"])
 
     model = None
     if args.workload == "decode48" and not args.no_model:
@@ -550,11 +635,10 @@ def main():
                 "frac": res["hbm_gbs"] / HBM_PEAK_GBS, "ops_per_step": res["step_ops"],
                 "intensity_op_per_byte": res["intensity"]},
         "roofline": res["roofline"],
-        "path": ("persistent decode kernel" if persistent else
-                 ("one launch per stage, expert products on the matrix cores" if matrix else
-                  "one launch per stage") + ("; the stack replayed as one HIP graph per step"
-                                             if res["graphed"] else "")),
+        "path": res["path"],
         "roofline_prefill4096": prefill,
+        "decode48_certified_router": certified,
+        "configs": configs,
         "model_decode": model,
         "cpu_baseline": cpu,
     }

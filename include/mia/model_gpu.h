@@ -69,15 +69,16 @@ int mia_gpu_model_step_sample(mia_gpu_model *m, int token, int pos, mhip_sampler
  * Qwen3-30B-A3B shape a step is one launch of the model stack (every
  * layer's attention and MoE, mhip_model_stack); MHIP_MODEL_PER_LAYER asks
  * for one attention and one MoE launch per layer instead (the same bits).
- * MHIP_FORCE_EXACT_ROUTER (the default): the decode kernel's MoE with the
- * reference's sequential router chains; logits bit-equal to the
- * reference's. 0: the same with the certified parallel router
- * (expert indices bit-equal, gate weights within ~1e-6 relative; through the
- * requantizations of later layers the logits then move by whole Q8 steps,
- * ~5e-4 of max|logit| each, up to ~1e-2 in all). MHIP_EXACT_EXPERTS: the
+ * By default (0, or MHIP_FORCE_EXACT_ROUTER) the decode kernel's MoE uses the
+ * reference's sequential router chains: logits bit-equal to the
+ * reference's. MHIP_DECODE_CERTIFIED: the gate weights from the certified
+ * parallel router logits instead (expert indices bit-equal, gate weights
+ * within ~1e-6 relative; through the requantizations of later layers the
+ * logits then move by whole Q8 steps, ~5e-4 of max|logit| each, up to ~1e-2
+ * in all). MHIP_EXACT_EXPERTS: the
  * per-stage kernels (bit-equal, no decode launch). MHIP_DECODE_FORCE_ABORT:
  * every decode launch aborts and the step reruns per stage (a test of that
- * fallback). MHIP_DECODE_CHAINS_FIRST (with MHIP_FORCE_EXACT_ROUTER): the
+ * fallback). MHIP_DECODE_CHAINS_FIRST (under the exact router): the
  * exact chains before the expert stream in every layer (the path of a
  * layer whose ranking is not certified). MHIP_ATTN_FORCE_ABORT: every
  * one-launch attention (mhip_attention_layer, used where the shape allows

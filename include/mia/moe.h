@@ -131,11 +131,17 @@ int mia_moe_stack_graph(mia_moe *m, int l0, int l1, float *d_x, int T);
 /* Decode of one token through layers [l0, l1) in a single persistent launch
  * (the Qwen3-30B-A3B shape on a 256-CU MI355X; mhip_decode_stack). x[dim]
  * (host) is updated in place; idx/w ([l1-l0][K]) receive the routing when
- * not NULL; bias (E floats) applies to every layer when not NULL. Expert
- * indices are bit-equal to the reference; the output is within ~1e-6
- * relative of it (the gate weights come from the parallel router logits).
- * Should the launch abort, the layers are rerun per stage (bit-equal to the
- * reference) and mia_moe_decode_status shows the aborted launch. */
+ * not NULL; bias (E floats) applies to every layer when not NULL. Every
+ * layer is bit-equal to the reference's moe() on its input, so x, idx and w
+ * after any number of layers are bit-equal to the reference's chain of
+ * layers from the same x (forward.c:210-213 without the attention). With
+ * MHIP_DECODE_CERTIFIED set through mia_moe_set_flags the gate weights come
+ * from the parallel router logits instead: indices bit-equal layer by
+ * layer, each layer's output within ~1e-6 relative of the reference's on the
+ * same input, but a many-layer output that drifts (about 1e-1 relative after
+ * 48 layers, as those differences flip Q8 codes). Should the launch abort,
+ * the layers are rerun per stage (bit-equal to the reference) and
+ * mia_moe_decode_status shows the aborted launch. */
 int mia_moe_decode(mia_moe *m, int l0, int l1, float *x, const float *bias, int *idx, float *w);
 /* Same on device memory, queued on the handle's stream; check
  * mia_moe_decode_status after the stream completes. */

@@ -156,15 +156,20 @@ int mhip_scratch_carve(const mhip_dims *s, int max_tokens, void *d_base,
 /* Flags for mhip_moe_layer and mhip_decode_stack. */
 #define MHIP_FORCE_SEQ_RMS 1      /* always take the sequential rmsnorm sum */
 #define MHIP_FORCE_EXACT_ROUTER 2 /* decode stack: the reference's exact router chains
-                                     (routing and gate weights bit-equal) */
+                                     (routing and gate weights bit-equal); the default,
+                                     and it overrides MHIP_DECODE_CERTIFIED */
 #define MHIP_DECODE_TRACE 4       /* decode stack: record stage timestamps */
 #define MHIP_EXACT_EXPERTS 8      /* layer: bit-exact expert products at every T */
 #define MHIP_DECODE_FORCE_ABORT 16 /* decode stack: report abort bit 4 and stop after the
                                       start barrier (tests the callers' abort handling) */
-#define MHIP_DECODE_CHAINS_FIRST 32 /* decode stack, with MHIP_FORCE_EXACT_ROUTER: the exact
+#define MHIP_DECODE_CHAINS_FIRST 32 /* decode stack, under the exact router: the exact
                                        chains before the expert stream in every layer, as for
                                        a layer whose ranking is not certified (without it they
                                        run beside the stream when it is) */
+#define MHIP_DECODE_CERTIFIED 256 /* decode stack: gate weights from the certified
+                                     parallel router logits (expert indices still bit-equal,
+                                     weights within ~1e-6 relative, so over many layers the
+                                     output drifts from the reference's; not the default) */
 
 /*
  * One MoE layer (rmsnorm -> router/top-K -> dispatch -> gate/up+SwiGLU ->
@@ -199,17 +204,22 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
  * most MHIP_DECODE_MAX_LAYERS (-1 beyond, before any device work). d_ws is a
  * workspace of mhip_decode_ws_bytes() bytes (not shared by concurrent
  * launches). d_idx/d_w ([L][n_active]) receive the routing when non-NULL.
- * Expert indices are bit-equal to the reference (certified parallel router,
- * exact fallback); the gate weights come from the parallel logits, within
- * ~1e-6 relative of the reference's; under MHIP_FORCE_EXACT_ROUTER the
- * weights are the reference's too (its sequential logit chains: before the
- * expert stream for a layer whose ranking is not certified, beside it
- * otherwise). After the stream completes, mhip_decode_status reports [0]
- * abort bits (1: workgroups not on the expected XCDs, 2: a wait timed out,
- * 4: MHIP_DECODE_FORCE_ABORT, 8: a NaN probability in a layer routed from
- * a certified ranking under MHIP_FORCE_EXACT_ROUTER; the output is then
- * invalid and the layer is rerun per stage), [1] rmsnorm fallbacks, [2]
- * layers whose gate weights came from the exact chains.
+ * Every layer is bit-equal to the reference's moe() (forward.c:167-197) on
+ * its input, so the output of any number of layers is the reference's
+ * chain's, bit for bit: the ranking is certified from parallel logits with
+ * a rigorous bound (or, where it cannot be, taken from the reference's
+ * sequential logit chains), and the gate weights come from those sequential
+ * chains, which run beside the expert stream. With MHIP_DECODE_CERTIFIED
+ * (and without MHIP_FORCE_EXACT_ROUTER) the gate weights come from the
+ * parallel logits instead: indices still bit-equal, weights within ~1e-6
+ * relative, a layer's output within a few ulps, and a many-layer output
+ * that drifts from the reference's as those differences flip Q8 codes
+ * (about 1e-1 relative after 48 layers). After the stream completes,
+ * mhip_decode_status reports [0] abort bits (1: workgroups not on the
+ * expected XCDs, 2: a wait timed out, 4: MHIP_DECODE_FORCE_ABORT, 8: a NaN
+ * probability in a layer routed from a certified ranking; the output is
+ * then invalid and the layer is rerun per stage), [1] rmsnorm fallbacks,
+ * [2] layers whose gate weights came from the exact chains.
  */
 #define MHIP_DECODE_MAX_LAYERS 256 /* layers of one decode-stack launch */
 size_t mhip_decode_ws_bytes(void);

@@ -239,6 +239,19 @@ template <> struct L2Load<4> {
                      : "v"(p), "v"(p + s), "v"(p + 2 * s), "v"(p + 3 * s) : "memory");
     }
 };
+// Three words p[0], p[s], p[2s] and two words q[0], q[t], read from the L2
+// with one wait.
+struct L2Load32 {
+    __device__ static void run(tw *v, const tw *p, int s, const tw *q, int t) {
+        asm volatile("global_load_dwordx2 %0, %5, off nt\n\t"
+                     "global_load_dwordx2 %1, %6, off nt\n\t"
+                     "global_load_dwordx2 %2, %7, off nt\n\t"
+                     "global_load_dwordx2 %3, %8, off nt\n\t"
+                     "global_load_dwordx2 %4, %9, off nt\n\ts_waitcnt vmcnt(0)"
+                     : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4])
+                     : "v"(p), "v"(p + s), "v"(p + 2 * s), "v"(q), "v"(q + t) : "memory");
+    }
+};
 template <int N, bool LOCAL>
 __device__ __forceinline__ void load_words(tw *v, const tw *p, int stride) {
     if (LOCAL) {
@@ -272,6 +285,29 @@ __device__ __forceinline__ void get_tagged(DecodeWs *ws, const tw *p, int stride
     }
 #pragma unroll
     for (int k = 0; k < N; k++) out[k] = __uint_as_float((unsigned)v[k]);
+}
+
+// get_tagged over the XCD-local words p[0], p[s], p[2s] (out[0..2]) and
+// q[0], q[t] (out[3..4]), polled together: words that are long published
+// cost no wait of their own beside words still on their way.
+__device__ __forceinline__ void get_tagged_3_2(DecodeWs *ws, const tw *p, int s, const tw *q,
+                                               int t, unsigned tag, float *out) {
+    tw v[5];
+    L2Load32::run(v, p, s, q, t);
+    long n = 0;
+    for (;;) {
+        bool ready = true;
+#pragma unroll
+        for (int k = 0; k < 5; k++) ready = ready && (unsigned)(v[k] >> 32) == tag;
+        if (ready) break;
+        if (++n > SPIN || ((n & 255) == 0 && aborted(ws, tag >> 8))) {
+            status_update(ws, ST_ABORT, tag >> 8, false, 2);
+            break;
+        }
+        L2Load32::run(v, p, s, q, t);
+    }
+#pragma unroll
+    for (int k = 0; k < 5; k++) out[k] = __uint_as_float((unsigned)v[k]);
 }
 
 __device__ void wait_flag(DecodeWs *ws, const unsigned *flag, unsigned value, unsigned epoch) {

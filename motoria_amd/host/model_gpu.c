@@ -366,8 +366,9 @@ static int moe(mia_gpu_model *m, int l, int per_stage) {
                                   t->router_dl + (size_t)l * E * d, t->router_t + (size_t)l * E * d,
                                   t->norm + (size_t)l * d, NULL, m->d_x, 1, NULL, NULL,
                                   m->d_status + 4 * l,
-                                  m->flags & (MHIP_FORCE_EXACT_ROUTER | MHIP_DECODE_FORCE_ABORT |
-                                              MHIP_DECODE_CHAINS_FIRST | MHIP_FORCE_SEQ_RMS)))
+                                  m->flags & (MHIP_FORCE_EXACT_ROUTER | MHIP_DECODE_CERTIFIED |
+                                              MHIP_DECODE_FORCE_ABORT | MHIP_DECODE_CHAINS_FIRST |
+                                              MHIP_FORCE_SEQ_RMS)))
         return mfail(m, "%s", mhip_error(m->gpu));
     return 0;
 }
@@ -410,8 +411,9 @@ static int run_stack(mia_gpu_model *m, int pos, step_tail *t) {
         mhip_model_stack(m->gpu, &mt->dims, &mt->lay, mt->table, mt->router_dl, mt->router_t,
                          mt->norm, NULL, &m->ad, m->d_al, m->d_rope, pos, m->max_seq, m->d_x, L,
                          m->d_mws, m->d_status,
-                         m->flags & (MHIP_FORCE_EXACT_ROUTER | MHIP_DECODE_FORCE_ABORT |
-                                     MHIP_ATTN_FORCE_ABORT | MHIP_DECODE_CHAINS_FIRST |
+                         m->flags & (MHIP_FORCE_EXACT_ROUTER | MHIP_DECODE_CERTIFIED |
+                                     MHIP_DECODE_FORCE_ABORT | MHIP_ATTN_FORCE_ABORT |
+                                     MHIP_DECODE_CHAINS_FIRST |
                                      MHIP_FORCE_SEQ_RMS | MHIP_DECODE_TRACE)))
         return mfail(m, "%s", mhip_error(m->gpu));
     if (tail(m, t)) return -1;
