@@ -14,23 +14,31 @@
 // the K expert outputs (K x 8 KB) gathered by the combine.
 //
 // Inside a workgroup the waves have two roles. Waves 0-3 stream the gate/up
-// rows and finish their h values without a workgroup barrier. Waves 4-7 hold
-// the workgroup's down rows and the next layer's router rows in registers:
-// they issue those loads during the gate/up pass and never wait for them at a
-// synchronisation, so the h exchange overlaps the rest of the weight stream.
+// rows, finish their h values without a workgroup barrier, and stream the
+// workgroup's down rows behind them: each wave requests a down row pair in
+// the registers of a gate/up row it has just used, so the down rows follow
+// the gate/up rows in the CU's queue (which takes vector memory instructions
+// in order, and holds a wave that waits to issue one) and need no registers
+// of their own. Waves 4-7 (the router waves) hold the router rows: they form
+// the parallel logits, Q8(xn) and, under the exact router, the reference's
+// sequential logit chains, which run beside the stream because these waves
+// issue no load during it (the next layer's router rows are requested once
+// h is in).
 //
 // Per layer, on every XCD:
 //   A  x (8 KB) -> certified rmsnorm -> xn, Q8(xn) in LDS; 4 router logits per
 //      workgroup (one per down wave) by a parallel sum with a rigorous bound
 //      on the distance to the reference's sequential fp32 chain  [XCD sync]
 //   B  all 128 logits -> ranks (LDS, 512 threads) -> top-K + certification
-//      -> gate weights (if the ordering is not certified, the exact
-//      sequential logits are computed and routing follows the reference bit
-//      for bit)
+//      (if the ordering is not certified, the exact sequential logits are
+//      computed and routing follows the reference bit for bit)
 //   C  gate/up rows of expert idx[k] + SwiGLU -> h (768 floats) [XCD sync]
-//      (the down rows and the next layer's router rows are loaded meanwhile)
+//      (the down rows are loaded behind them; the router waves run the
+//      exact logit chains meanwhile)
 //   D  Q8(h) -> down rows -> the expert's output rows, published device-wide
-//   E  combine x_r += w_j * out_j,r in top-K order for 64 rows [XCD sync]
+//      (the next layer's router rows are loaded meanwhile)
+//   E  softmax of the exact logits -> gate weights; combine
+//      x_r += w_j * out_j,r in top-K order for 64 rows [XCD sync]
 //
 // Exchanged data carries its own readiness: every value goes out as one
 // 64-bit device-scope store of (fp32 value, tag), the tag naming the launch
@@ -41,9 +49,10 @@
 //
 // Results: top-K indices bit-equal to the reference (certified, with an exact
 // fallback); expert products, SwiGLU, Q8(h), down and combine follow the
-// reference's rounding order; the gate weights come from the parallel logits
-// (relative error ~1e-6 against the reference's), unless the exact fallback
-// ran for that layer.
+// reference's rounding order; the gate weights come from the reference's
+// sequential logit chains (the default: every layer bit-equal), or with
+// MHIP_DECODE_CERTIFIED from the parallel logits (relative error ~1e-6
+// against the reference's) unless the exact fallback ran for that layer.
 //
 // The same body (decode_body.inc) compiles twice: k_decode_stack, the MoE
 // alone, and k_model_stack, which runs each layer's attention (attn_stage:
@@ -68,10 +77,10 @@ constexpr int HROWS = EH / WPX;                 // 24 h rows per workgroup
 constexpr int DROWS = D / WPX;                  // 64 down rows per workgroup
 constexpr int LPW = E / WPX;                    // 4 logits per workgroup
 constexpr int NGU = 4;                          // waves 0..3: gate/up
-constexpr int NDN = NWAVE - NGU;                // waves 4..7: down + router rows
+constexpr int NDN = NWAVE - NGU;                // waves 4..7: router rows
 constexpr int GU_H = HROWS / NGU;               // 6 h rows per gate/up wave
 constexpr int GU_R = 2 * GU_H;                  // its 12 weight rows
-constexpr int DPK = DROWS * NBH / (NDN * 64);   // 6 (row, block) pairs per down thread
+constexpr int DPK = DROWS * NBH / (NGU * 64);   // 6 down (row, block) pairs per gate/up thread
 constexpr long SPIN = 1L << 18;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -82,7 +91,7 @@ __device__ __forceinline__ int4 ld_stream(const void *p) {
 
 static_assert(NB == 64, "one 32-block per lane");
 static_assert(LPW == NDN, "one router row per down wave");
-static_assert(GU_H * NGU == HROWS && DPK * NDN * 64 == DROWS * NBH, "tiling");
+static_assert(GU_H * NGU == HROWS && DPK * NGU * 64 == DROWS * NBH && DPK <= GU_R, "tiling");
 static_assert(NT == 4 * E, "ranks: four threads per expert");
 
 // Tagged words: (tag << 32) | fp32 bits.
