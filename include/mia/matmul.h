@@ -5,7 +5,8 @@
  * include/mia/matmul.h:11-16. W is row-major of type `t`; for Q8_0, `xq`
  * receives x quantized to cols/MIA_QK blocks (as in the reference); for F32
  * it may be NULL. Runs on the GPU with results bit-equal to the reference's
- * scalar x86 kernels (src/tensor/matmul.c:13-28). Aborts on a GPU failure.
+ * scalar x86 kernels (src/tensor/matmul.c:13-28). A GPU failure fills `out`
+ * with NaN and is reported by mia_tensor_error (include/mia/tensor_error.h).
  */
 #include "mia/quant.h"
 

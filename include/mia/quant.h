@@ -6,8 +6,9 @@
  *
  * The ops run on the GPU (HIP kernels through include/mia_hip.h) on the
  * default device context; host pointers are copied in and out. There is no
- * CPU implementation: a missing or failing GPU aborts with a message, since
- * these functions have no error return in the reference interface.
+ * CPU implementation. These functions have no error return in the reference
+ * interface: a missing or failing GPU fills the outputs with NaN and is
+ * reported by mia_tensor_error (include/mia/tensor_error.h).
  */
 #include <stddef.h>
 #include <stdint.h>

@@ -193,6 +193,9 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
                    const void *d_table_layer, const float *d_router_t,
                    const float *d_norm, const float *d_bias, float *d_x, int T,
                    const mhip_scratch *sc, int flags);
+/* Calls of mhip_moe_layer on this context whose expert products ran on the
+ * matrix-core kernels (diagnostic: which path a call took). */
+unsigned long long mhip_matrix_layers(const mhip_ctx *c);
 
 /*
  * Decode (one token) through L consecutive layers in one persistent launch:

@@ -123,6 +123,7 @@ SIGNATURES = {
     "mhip_elapsed": (_i, [_p, _i, _i, ctypes.POINTER(_f)]),
     "mhip_stage_timing": (_i, [_p, ctypes.c_uint, _i]),
     "mhip_stage_time": (_i, [_p, _i, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i)]),
+    "mhip_matrix_layers": (ctypes.c_ulonglong, [_p]),
     "mhip_table_repack": (_i, [_p, ctypes.POINTER(Dims), _p, _i, ctypes.POINTER(_i), _i, _p,
                                _sz, _sz, _sz]),
     "mhip_table_unpack": (_i, [_p, ctypes.POINTER(Dims), _p, _i, _i, _p, _sz, _sz, _sz]),
@@ -177,6 +178,8 @@ SIGNATURES = {
     # include/mia/matvec_cache.h
     "mia_matvec_register": (_i, [_p, _i, _i, _i]),
     "mia_matvec_unregister": (_i, [_p]),
+    # include/mia/tensor_error.h
+    "mia_tensor_error": (ctypes.c_char_p, []),
     # include/mia/moe.h
     "mia_moe_open": (_i, [ctypes.POINTER(_p), ctypes.POINTER(MoeConfig), ctypes.c_char_p, _sz]),
     "mia_moe_close": (None, [_p]),

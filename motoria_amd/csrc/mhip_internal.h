@@ -23,6 +23,7 @@ struct mhip_ctx {
     int decode_checked;           // 0 unknown, 1 the decode launch fits the device, 2 it does not
     int decode_cus, decode_occ;   // the CU count and occupancy that check found
     int capturing;                // between mhip_graph_begin and mhip_graph_end
+    unsigned long long matrix_layers;  // mhip_moe_layer calls that took the matrix-core kernels
     unsigned attn_epoch;          // launches of the one-launch attention (its exchange tags)
     const void *attn_ws;          // the workspace those tags were written to
     char err[512];

@@ -1285,6 +1285,7 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     hipStream_t st = c->stream;
     const bool mfma = !(flags & MHIP_EXACT_EXPERTS) && A >= MHIP_GEMM_MIN_A &&
                       mhip::gemm_path_fits(s);
+    if (mfma) c->matrix_layers++;
 
     int slot = mhip::stage_begin(c, MHIP_STAGE_RMSNORM);
     if (d == RN_D)
@@ -1428,5 +1429,7 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     mhip::stage_end(c, slot);
     return mhip::check_launch(c, "combine");
 }
+
+unsigned long long mhip_matrix_layers(const mhip_ctx *c) { return c ? c->matrix_layers : 0; }
 
 }  // extern "C"

@@ -10,7 +10,7 @@ import motoria_amd as M
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADERS = ["include/mia_hip.h", "include/mia/quant.h", "include/mia/matmul.h",
            "include/mia/matvec_cache.h", "include/mia/moe.h", "include/mia/model_gpu.h",
-           "include/mia/serve.h"]
+           "include/mia/serve.h", "include/mia/tensor_error.h"]
 
 
 def declared_functions():
@@ -118,3 +118,47 @@ def test_python_constants_match_the_headers():
         assert getattr(M, k) == defines[k], k
     assert (M.TRACE_L0, M.TRACE_NL, M.TRACE_SLOTS) == (
         defines["MHIP_TRACE_L0"], defines["MHIP_TRACE_NL"], defines["MHIP_TRACE_SLOTS"])
+
+
+def test_tensor_ops_report_a_missing_gpu():
+    """The reference's void tensor ops (mia_matvec, mia_quantize_row_q8,
+    mia_dequantize_row) cannot return an error: without a GPU they fill their
+    outputs with NaN and mia_tensor_error reports the failure once (reading
+    it clears it). Runs only where no GPU is visible (the error path)."""
+    import numpy as np
+    import pytest
+
+    L = M.lib()
+    if L.mhip_device_count() > 0:
+        pytest.skip("a GPU is visible: the failure path is not reachable")
+    L.mia_tensor_error()
+    out = np.zeros(4, np.float32)
+    w = np.ones((4, 32), np.float32)
+    x = np.ones(32, np.float32)
+    L.mia_matvec(out.ctypes.data, w.ctypes.data, 0, x.ctypes.data, None, 4, 32)
+    assert np.all(np.isnan(out))
+    y = np.zeros(4 * 36, np.uint8)
+    L.mia_quantize_row_q8(np.ones(128, np.float32).ctypes.data, y.ctypes.data, 128)
+    assert np.all(np.isnan(y.view(np.float32).reshape(4, 9)[:, 0]))
+    msg = L.mia_tensor_error()
+    assert msg is not None and b"cannot open a GPU" in msg and b"more failures" in msg
+    assert L.mia_tensor_error() is None
+
+
+def test_tensor_ops_can_abort_instead():
+    """With MIA_ABORT_ON_GPU_ERROR set, a failing tensor op aborts the
+    process with its message (the reference engine's own behaviour on an
+    unrecoverable error). Runs only where no GPU is visible."""
+    import sys
+
+    import pytest
+
+    if M.lib().mhip_device_count() > 0:
+        pytest.skip("a GPU is visible: the failure path is not reachable")
+    code = ("import numpy as np, motoria_amd as M; o = np.zeros(4, np.float32); "
+            "w = np.ones((4, 32), np.float32); x = np.ones(32, np.float32); "
+            "M.lib().mia_matvec(o.ctypes.data, w.ctypes.data, 0, x.ctypes.data, None, 4, 32)")
+    env = dict(os.environ, MIA_ABORT_ON_GPU_ERROR="1", PYTHONPATH=ROOT)
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode != 0 and "cannot open a GPU" in r.stderr

@@ -127,6 +127,7 @@ def test_quantize_and_matvec_bit_exact(oracle):
         deq = np.zeros(cols, np.float32)
         L.mia_dequantize_row(1, wq.ctypes.data, deq.ctypes.data, cols)
         assert_bits(deq, oracle.dequantize_row_q8(wq[: cols // 32 * 36], cols), "dequantize")
+    assert L.mia_tensor_error() is None  # no op of this test failed
 
 
 def test_matvec_registered_weights(oracle):
@@ -223,14 +224,15 @@ def _compare_layer(O, moe, d, layer, x, router, bias=None, label="", matrix=Fals
     assert_bits(w, wo, label + " gate weights")
     assert_bits(xg, xo, label + " layer output")
     if matrix:
+        n0 = M.lib().mhip_matrix_layers(moe.gpu)
         xm, im, wm, lm = _gpu_layer(moe, layer, x, bias, 0)
+        assert M.lib().mhip_matrix_layers(moe.gpu) == n0 + 1, "%s: matrix path not taken" % label
         e_delta, e_out = rel_err(xm - x, xo - x), rel_err(xm, xo)
         say("  %s matrix-core path: rel err update %.3e, output %.3e" % (label, e_delta, e_out))
         assert np.array_equal(im, io), "%s: matrix path expert indices differ" % label
         assert_bits(lm, lo, label + " matrix path logits")
         assert_bits(wm, wo, label + " matrix path gate weights")
         assert e_delta <= TOL and e_out <= TOL, label
-        assert not np.array_equal(bits(xm), bits(xo)), "%s: matrix path not taken" % label
     return idx
 
 
