@@ -98,7 +98,9 @@ int mia_file_layer_offsets(const mia_file_info *info, int layer, uint64_t *ffn_n
  * (mia_moe_set_layer) and every (layer, expert) blob into the HBM table,
  * bit-identical to filling it through the loader port with the reference's
  * mia_file_read_expert. The file's shape, norm settings and Q8_0 weight type
- * must be the handle's. */
+ * must be the handle's. Reading the file overlaps the uploads (two pinned
+ * staging batches); the call records stream marks 14 and 15 of the handle's
+ * context (mhip_mark). */
 int mia_moe_load_file(mia_moe *m, const char *path);
 
 /* One layer, moe() semantics, in place on host x[T][dim]. Bit-equal to the

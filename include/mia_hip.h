@@ -71,6 +71,9 @@ int mhip_sync(mhip_ctx *c);
 /* Milliseconds between two points of the context's stream (HIP events). */
 int mhip_mark(mhip_ctx *c, int slot); /* slot 0..15 */
 int mhip_elapsed(mhip_ctx *c, int slot0, int slot1, float *ms);
+/* Waits on the host until the stream has passed the last mhip_mark of slot
+ * (at once if the slot was never marked). */
+int mhip_mark_wait(mhip_ctx *c, int slot);
 
 /* Per-stage kernel timing. While a mask is set, every launch of a selected
  * stage of mhip_moe_layer is bracketed by two HIP events on the context's
@@ -246,8 +249,12 @@ int mhip_decode_stack(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
  * of this launch's status words ([0] abort bits, [1] rmsnorm fallbacks,
  * [2] exact-router layers, [3] 0) into it; it allocates nothing. L is at most
  * MHIP_DECODE_MAX_LAYERS (-1 beyond). Every call on one GPU shares that
- * GPU's workspace: calls that overlap on one GPU (two streams, two threads)
- * race; calls in stream order do not.
+ * GPU's workspace, so the calls of one GPU are serialized: the host side
+ * under a lock (calls from several threads are safe), the launches in order
+ * (a call on another stream than the previous call's waits for that launch
+ * through an event, which is not an allocation). Under stream capture the
+ * capturing caller must order the captured calls against any other call on
+ * the same GPU itself: the launch is captured without that wait.
  */
 int mhip_decode_stack_noalloc(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
                               const void *d_table, const float *d_router,

@@ -121,6 +121,7 @@ SIGNATURES = {
     "mhip_sync": (_i, [_p]),
     "mhip_mark": (_i, [_p, _i]),
     "mhip_elapsed": (_i, [_p, _i, _i, ctypes.POINTER(_f)]),
+    "mhip_mark_wait": (_i, [_p, _i]),
     "mhip_stage_timing": (_i, [_p, ctypes.c_uint, _i]),
     "mhip_stage_time": (_i, [_p, _i, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i)]),
     "mhip_matrix_layers": (ctypes.c_ulonglong, [_p]),

@@ -274,6 +274,11 @@ int mhip_mark(mhip_ctx *c, int slot) {
     return mhip::check(c, hipEventRecord(c->marks[slot], c->stream), "hipEventRecord");
 }
 
+int mhip_mark_wait(mhip_ctx *c, int slot) {
+    if (slot < 0 || slot >= 16) return mhip::fail(c, "mark slot %d out of range", slot);
+    return mhip::check(c, hipEventSynchronize(c->marks[slot]), "hipEventSynchronize");
+}
+
 int mhip_elapsed(mhip_ctx *c, int slot0, int slot1, float *ms) {
     if (slot0 < 0 || slot0 >= 16 || slot1 < 0 || slot1 >= 16)
         return mhip::fail(c, "mark slot out of range");

@@ -59,6 +59,8 @@
 // rmsnorm, Q/K/V rows, the 32 heads with the KV cache, Wo and the residual,
 // src/model/forward.c:118-165) before that layer's MoE, so a whole decode
 // token is one launch (forward.c:210-213).
+#include <mutex>
+
 #include "attn_common.h"
 #include "mhip_internal.h"
 
@@ -160,8 +162,11 @@ struct DecodeArgs {
 constexpr size_t STATIC_WS_BYTES = (sizeof(DecodeWs) + 255) / 256 * 256;
 constexpr int MAX_DEVICES = 64;
 struct StaticWs {
-    void *ptr;       // device address of this device's copy (0 until set up)
-    unsigned epoch;  // launches since it was last cleared
+    std::mutex mu;        // held while a call sets up, tags and queues its launch
+    void *ptr;            // device address of this device's copy (0 until set up)
+    unsigned epoch;       // launches since it was last cleared
+    hipEvent_t done;      // recorded after each launch queued outside stream capture
+    hipStream_t last;     // the stream of that launch (null before the first)
 };
 StaticWs g_static_ws[MAX_DEVICES];
 
@@ -948,16 +953,24 @@ namespace mhip {
 int decode_noalloc_setup(mhip_ctx *c) {
     if (c->device < 0 || c->device >= MAX_DEVICES) return 0;  // the entry point then refuses
     StaticWs &st = g_static_ws[c->device];
+    std::lock_guard<std::mutex> lock(st.mu);
     if (st.ptr) return 0;
     void *ptr = nullptr;
     if (check(c, hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)),
               "hipGetSymbolAddress (decode workspace)"))
         return -1;
     if (!ptr || (uintptr_t)ptr % 256) return fail(c, "decode workspace symbol at %p", ptr);
+    if (check(c, hipEventCreateWithFlags(&st.done, hipEventDisableTiming),
+              "hipEventCreate (decode workspace)"))
+        return -1;
     // cleared once here; afterwards the launches' epochs keep it consistent
-    if (mhip_zero(c, ptr, STATIC_WS_BYTES) || mhip_sync(c)) return -1;
-    st.ptr = ptr;
+    if (mhip_zero(c, ptr, STATIC_WS_BYTES) || mhip_sync(c)) {
+        hipEventDestroy(st.done);
+        return -1;
+    }
+    st.last = nullptr;
     st.epoch = 0;
+    st.ptr = ptr;
     return 0;
 }
 
@@ -998,10 +1011,29 @@ int mhip_decode_stack_noalloc(mhip_ctx *c, const mhip_dims *s, const mhip_layout
     const int ok = check_decode_args(c, s, L);
     if (ok <= 0) return ok;
     StaticWs *st = c->device < MAX_DEVICES ? &g_static_ws[c->device] : nullptr;
-    if (!st || !st->ptr)
+    if (!st) return mhip::fail(c, "no-alloc decode: device %d has no set-up workspace", c->device);
+    // Calls on one device are serialized: the host side (the epoch, the
+    // queueing) under the mutex, and the launches in stream order, a call
+    // on another stream than the previous one waiting for that one's event.
+    // Under stream capture the capturing caller orders its calls (an event
+    // recorded outside the capture cannot be waited for inside it).
+    std::lock_guard<std::mutex> lock(st->mu);
+    if (!st->ptr)
         return mhip::fail(c, "no-alloc decode: device %d has no set-up workspace", c->device);
-    return launch_decode(c, s, lay, d_table, d_router, d_router_t, d_norm, d_bias, d_x, L,
-                         (DecodeWs *)st->ptr, &st->epoch, false, d_idx, d_w, d_status, flags);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (mhip::check(c, hipStreamIsCapturing(c->stream, &cs), "hipStreamIsCapturing")) return -1;
+    const bool captured = cs != hipStreamCaptureStatusNone;
+    if (!captured && st->last && st->last != c->stream &&
+        mhip::check(c, hipStreamWaitEvent(c->stream, st->done, 0), "hipStreamWaitEvent"))
+        return -1;
+    const int rc = launch_decode(c, s, lay, d_table, d_router, d_router_t, d_norm, d_bias, d_x,
+                                 L, (DecodeWs *)st->ptr, &st->epoch, false, d_idx, d_w, d_status,
+                                 flags);
+    if (rc == 0 && !captured) {
+        if (mhip::check(c, hipEventRecord(st->done, c->stream), "hipEventRecord")) return -1;
+        st->last = c->stream;
+    }
+    return rc;
 }
 
 size_t mhip_model_stack_ws_bytes(void) { return mhip_decode_ws_bytes() + sizeof(AttnXWs); }

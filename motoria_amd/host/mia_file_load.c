@@ -178,6 +178,10 @@ int mia_file_layer_offsets(const mia_file_info *h, int layer, uint64_t *ffn_norm
 
 /* Reads the blobs of (l, e0 .. e0+n) into pinned host memory and queues
  * their upload and repack; `d_stage` is device staging for n blobs. */
+/* The stream marks (include/mia_hip.h) mia_moe_load_file records after
+ * each of its two staging buffers' batches. */
+#define LOAD_MARK 14
+
 static int stage_batch(mia_moe *m, int fd, const mia_file_info *h, int l, int e0, int n,
                        unsigned char *h_stage, void *d_stage) {
     mhip_ctx *g = mia_moe_gpu(m);
@@ -234,13 +238,15 @@ int mia_moe_load_file(mia_moe *m, const char *path) {
         else if (mia_moe_set_layer(m, (int)l, norm, router))
             rc = -1;
     }
-    /* experts: two pinned batches, so a batch is read while the previous
-     * one uploads; a buffer is reused only after the stream has passed it */
+    /* experts: two pinned batches, so batch k is read from the file while
+     * batch k - 1 uploads and is repacked. Buffer k & 1 is reused only once
+     * the stream has passed batch k - 2's repack (stream mark LOAD_MARK +
+     * (k & 1), recorded after it), not the whole stream. */
     int k = 0;
     for (uint32_t l = 0; !rc && l < h.n_layers; l++)
         for (int e0 = 0; !rc && e0 < (int)E; e0 += nb, k++) {
             const int n = (int)E - e0 < nb ? (int)E - e0 : nb;
-            if (k >= 2 && mhip_sync(g)) {
+            if (k >= 2 && mhip_mark_wait(g, LOAD_MARK + (k & 1))) {
                 rc = mia_moe_fail(m, "%s", mhip_error(g));
                 break;
             }
@@ -248,7 +254,7 @@ int mia_moe_load_file(mia_moe *m, const char *path) {
             if (r == -2)
                 rc = mia_moe_fail(m, "%s: reading experts %d..%d of layer %u", path, e0,
                                   e0 + n - 1, l);
-            else if (r)
+            else if (r || mhip_mark(g, LOAD_MARK + (k & 1)))
                 rc = mia_moe_fail(m, "%s", mhip_error(g));
         }
     if (mhip_sync(g) && !rc) rc = mia_moe_fail(m, "%s", mhip_error(g));

@@ -117,6 +117,40 @@ def test_noalloc_decode_shared_by_contexts_of_one_device(oracle, stack):
     _same(ref, b, "first context after the second")
 
 
+def test_noalloc_decode_ordered_across_streams(oracle, stack):
+    """Two contexts (two streams) of one GPU queue calls back to back with
+    no host wait between them: the second call waits for the first launch
+    (an event on the shared workspace), so both results equal the workspace
+    entry point's."""
+    say("test_noalloc_decode_ordered_across_streams")
+    L = M.lib()
+    K = stack.dims.n_active
+    xs = [oracle.synth_x(W.X_SEED + 43 + i, 1, 2048)[0] for i in range(2)]
+    refs = [stack.run(False, NL, x) for x in xs]
+    g2 = M.Gpu(0)
+    try:
+        ctxs = [stack.g, g2]
+        bufs = []
+        for g, x in zip(ctxs, xs):
+            bufs.append((g.upload(np.ascontiguousarray(x, np.float32)), g.malloc(NL * K * 4),
+                         g.malloc(NL * K * 4), g.malloc(16)))
+        for g, (dx, didx, dw, dst) in zip(ctxs, bufs):
+            g.check(L.mhip_decode_stack_noalloc(
+                g.h, ctypes.byref(stack.dims), ctypes.byref(stack.lay), stack.table, stack.rdl,
+                stack.rt, stack.norm, None, dx, NL, didx, dw, dst, 0), "noalloc")
+        for g in ctxs:
+            g.check(L.mhip_sync(g.h), "sync")
+        for i, (g, (dx, didx, dw, dst)) in enumerate(zip(ctxs, bufs)):
+            got = (g.download(dx, 2048, np.float32), g.download(didx, (NL, K), np.int32),
+                   g.download(dw, (NL, K), np.float32), g.download(dst, 4, np.int32))
+            assert got[3][0] == 0, got[3]
+            _same(refs[i], got, "stream %d" % i)
+            for p in (dx, didx, dw, dst):
+                g.free(p)
+    finally:
+        g2.close()
+
+
 def test_noalloc_decode_rejects_more_than_256_layers(stack):
     say("test_noalloc_decode_rejects_more_than_256_layers")
     L = M.lib()
