@@ -1,11 +1,10 @@
 /*
- * mia-serve on the GPU engine: the reference's server command line
- * (src/app/serve.c:145-160) over mia_serve (include/mia/serve.h).
+ * mia-serve on the GPU engine (include/mia/serve.h). Its options are the
+ * ones the reference's Go engine passes to the server it starts
+ * (tools/internal/engine): -m, -c, --seed, and --ram, which is accepted and
+ * ignored since every expert is resident in HBM; --device picks the GPU.
  *
  *   mia-serve -m model.mia [-c 4096] [--seed N] [--device D] [--ram SIZE]
- *
- * --ram is accepted for the reference's callers (tools/internal/engine
- * passes it) and ignored: every expert is resident in HBM.
  */
 #include <stdio.h>
 #include <stdlib.h>
@@ -14,24 +13,50 @@
 
 #include "mia/serve.h"
 
+typedef struct {
+    const char *model;
+    int ctx, device;
+    unsigned long long seed;
+} options;
+
+static void set_model(options *o, const char *v) { o->model = v; }
+static void set_ctx(options *o, const char *v) { o->ctx = atoi(v); }
+static void set_seed(options *o, const char *v) { o->seed = strtoull(v, NULL, 10); }
+static void set_device(options *o, const char *v) { o->device = atoi(v); }
+static void ignore(options *o, const char *v) {
+    (void)o;
+    (void)v;
+}
+
+static const struct {
+    const char *name;
+    void (*set)(options *, const char *);
+} OPTIONS[] = {
+    {"-m", set_model}, {"-c", set_ctx}, {"--seed", set_seed},
+    {"--device", set_device}, {"--ram", ignore},
+};
+
+static int usage(const char *prog) {
+    fprintf(stderr, "usage: %s -m model.mia [-c 4096] [--seed N] [--device D] [--ram SIZE]\n",
+            prog);
+    return 2;
+}
+
 int main(int argc, char **argv) {
-    const char *model = NULL;
-    int ctx = 4096, device = 0;
-    unsigned long long seed = (unsigned long long)time(NULL);
-    for (int i = 1; i + 1 < argc; i += 2) {
-        if (!strcmp(argv[i], "-m")) model = argv[i + 1];
-        else if (!strcmp(argv[i], "-c")) ctx = atoi(argv[i + 1]);
-        else if (!strcmp(argv[i], "--seed")) seed = strtoull(argv[i + 1], NULL, 10);
-        else if (!strcmp(argv[i], "--device")) device = atoi(argv[i + 1]);
-        else if (strcmp(argv[i], "--ram") != 0) {
-            fprintf(stderr, "unknown option %s\n", argv[i]);
-            return 2;
+    options o = {NULL, 4096, 0, (unsigned long long)time(NULL)};
+    for (int i = 1; i < argc; i += 2) {
+        size_t k = 0;
+        while (k < sizeof OPTIONS / sizeof OPTIONS[0] && strcmp(argv[i], OPTIONS[k].name)) k++;
+        if (k == sizeof OPTIONS / sizeof OPTIONS[0]) {
+            fprintf(stderr, "%s: unknown option %s\n", argv[0], argv[i]);
+            return usage(argv[0]);
         }
+        if (i + 1 >= argc) {
+            fprintf(stderr, "%s: option %s needs a value\n", argv[0], argv[i]);
+            return usage(argv[0]);
+        }
+        OPTIONS[k].set(&o, argv[i + 1]);
     }
-    if (!model) {
-        fprintf(stderr, "usage: %s -m model.mia [-c 4096] [--seed N] [--device D] [--ram SIZE]\n",
-                argv[0]);
-        return 2;
-    }
-    return mia_serve(model, ctx, (uint64_t)seed, device, stdin, stdout);
+    if (!o.model) return usage(argv[0]);
+    return mia_serve(o.model, o.ctx, (uint64_t)o.seed, o.device, stdin, stdout);
 }

@@ -965,7 +965,7 @@ int decode_noalloc_setup(mhip_ctx *c) {
         return -1;
     // cleared once here; afterwards the launches' epochs keep it consistent
     if (mhip_zero(c, ptr, STATIC_WS_BYTES) || mhip_sync(c)) {
-        hipEventDestroy(st.done);
+        (void)hipEventDestroy(st.done);
         return -1;
     }
     st.last = nullptr;

@@ -1,5 +1,5 @@
 """The mia-serve line protocol on the GPU engine (motoria_amd/mia-serve,
-host/serve.c), driven over pipes as the reference's engine package drives
+host/server.c), driven over pipes as the reference's engine package drives
 it (tools/internal/engine/protocol.go:1-13), on the tiny model with the
 serve test's chat vocabulary (tools/e2e/serve_test.go:16-47). Besides the
 reference's own serve checks (context kept across turns, only the new turn

@@ -50,3 +50,56 @@ def test_layer_bit_equal(shape, T, seed):
     assert np.array_equal(idx, ir) and np.array_equal(il, ir)
     for a, b in [(xo, xr), (w, wr), (logits, lr), (xn, xnr)]:
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_tokenizer_random_texts_equal_the_reference():
+    """The serve path's tokenizer (host/tokenizer.c) against the reference's
+    own (src/tokenizer/bpe.c, through oracle/_ref) on seeded random texts
+    built from the characters its rules distinguish: both letter cases,
+    digits, space / tab / newline / carriage return, ASCII punctuation,
+    apostrophes with contraction letters, two- to four-byte UTF-8 (the C2
+    and E2 80 / E3 80 punctuation rows among them), stray continuation
+    bytes, special tokens, and multi-byte characters cut by a special token
+    or by the end of the text; under the four vocabularies of the golden
+    fixtures, and with too small an output for some."""
+    import ctypes
+    import json
+    import os
+
+    import motoria_amd as M
+
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                             "tokenizer.npz"))
+    vocabs = sorted(k[5:] for k in g.files if k.startswith("blob_"))
+    R = O.ref()
+    R.ref_tok_encode.restype = ctypes.c_int
+    R.ref_tok_encode.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_char_p,
+                                 ctypes.c_void_p, ctypes.c_int]
+    atoms = [b"a", b"Z", b"q", b"7", b"0", b" ", b"  ", b"\t", b"\n", b"\r\n", b"\n\n", b"\v",
+             b"!", b",", b".", b"(", b"'", b"'s", b"'T", b"'re", b"'VE", b"'ll", b"'d", b"'m",
+             b"'x", b"\xc2\xa0", b"\xc2\xbf", b"\xc3\xa9", b"\xe2\x80\x94", b"\xe2\x80\x9c",
+             b"\xe3\x80\x82", b"\xe4\xbd\xa0", b"\xe2\x82\xac", b"\xf0\x9f\x98\x80", b"\x80",
+             b"\xbf", b"<|im_start|>", b"<|im_end|>", b"<|endoftext|>", b"<think>", b"hello",
+             b"Hello", b"world", b"12345", b" the", b"--", b"==>", b"<|im_", b"|>"]
+    rng = np.random.default_rng(2024)
+    checked = 0
+    for v in vocabs:
+        blob = g["blob_" + v].tobytes()
+        tok = M.Bpe(blob)
+        for trial in range(300):
+            parts = [atoms[i] for i in rng.integers(0, len(atoms), int(rng.integers(1, 40)))]
+            if trial % 7 == 0:  # a multi-byte character cut by a special token or the end
+                parts.append(b"\xe4\xbd" if trial % 2 else b"\xf0\x9f\x98")
+                if trial % 3 == 0:
+                    parts.append(b"<|im_end|>")
+            text = b"".join(parts)
+            cap = 1 << 14 if trial % 5 else int(rng.integers(1, 12))
+            want = np.zeros(cap, np.int32)
+            nw = R.ref_tok_encode(blob, len(blob), text, want.ctypes.data, cap)
+            got = tok.encode(text, max_ids=cap)
+            if nw < 0:
+                assert got is None, (v, text)
+            else:
+                assert got == want[:nw].tolist(), (v, text)
+            checked += 1
+    assert checked == 300 * len(vocabs)

@@ -1,4 +1,4 @@
-"""The .mia tokenizer and chat text of the serve path (host/bpe.c), on the
+"""The .mia tokenizer and chat text of the serve path (host/tokenizer.c), on the
 CPU: ids equal to the reference's own tokenizer (src/tokenizer/bpe.c,
 tests/golden/tokenizer.npz from oracle/_ref) for 46 texts under four
 vocabularies, the reference's unit tests (tests/test_tokenizer.c), decoding
