@@ -186,6 +186,93 @@ __global__ __launch_bounds__(256) void k_rmsnorm_q8_w(const float *__restrict__ 
     xs[(size_t)t * (RN_D / QK) + b] = dsc;
 }
 
+// The same for many tokens, with every access coalesced: load k (k < 8) of
+// a wavefront is one contiguous 1 KB run, lane L taking elements
+// 256 k + 4 L .. + 3, so a 32-block is the four values of eight consecutive
+// lanes of one load and its maximum is taken over them by DPP (order-free).
+// The sum of squares is the per-lane sequential sums and a wavefront tree,
+// bracketed as above. Without xq (the matrix-core path reads only the fp16
+// codes) the int8 codes are not written.
+template <int CTRL>
+__device__ __forceinline__ float dpp_max_f(float v) {
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v),
+                                                                CTRL, 0xf, 0xf, false)));
+}
+__global__ __launch_bounds__(256) void k_rmsnorm_q8_c(const float *__restrict__ x,
+                                                     const float *__restrict__ w,
+                                                     float *__restrict__ xn,
+                                                     int8_t *__restrict__ xq,
+                                                     float *__restrict__ xs,
+                                                     _Float16 *__restrict__ xq16, int T,
+                                                     float eps, int force_seq, int *status) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6), L = threadIdx.x & 63;
+    if (t >= T) return;  // a whole wavefront: no workgroup barrier follows
+    const float4 *xr = (const float4 *)(x + (size_t)t * RN_D) + L;
+    float4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = xr[64 * k];
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        ss = ss + (double)v[k].x * (double)v[k].x;
+        ss = ss + (double)v[k].y * (double)v[k].y;
+        ss = ss + (double)v[k].z * (double)v[k].z;
+        ss = ss + (double)v[k].w * (double)v[k].w;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss = ss + __shfl_xor(ss, o);
+    ss = __shfl(ss, 0);  // one value for the whole wavefront (lanes summed in different orders)
+    const double m = ss * ((double)(RN_D + 64) * 0x1p-52);
+    const float lo = (float)(1.0 / sqrt((ss + m) / RN_D + (double)eps));
+    const float hi = (float)(1.0 / sqrt((ss - m) / RN_D + (double)eps));
+    float inv = lo;
+    if (force_seq || lo != hi) {  // the same branch in every lane of the wavefront
+        float r = 0.0f;
+        if (L == 0) {
+            const float *xt = x + (size_t)t * RN_D;
+            double sq = 0.0;
+            for (int i = 0; i < RN_D; i++) sq = sq + (double)xt[i] * (double)xt[i];
+            r = (float)(1.0 / sqrt(sq / RN_D + (double)eps));
+            atomicAdd(&status[1], 1);
+        }
+        inv = __shfl(r, 0);
+    }
+    const float4 *wr = (const float4 *)w + L;
+    float4 *xo = (float4 *)(xn + (size_t)t * RN_D) + L;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const float4 q = wr[64 * k];
+        v[k] = make_float4((v[k].x * inv) * q.x, (v[k].y * inv) * q.y, (v[k].z * inv) * q.z,
+                           (v[k].w * inv) * q.w);
+        xo[64 * k] = v[k];
+    }
+    typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        // a NaN counts as 0 in the block maximum, as in the sequential max
+        float am = fmaxf(fmaxf(fmaxf(0.0f, fabsf(v[k].x)), fabsf(v[k].y)),
+                         fmaxf(fabsf(v[k].z), fabsf(v[k].w)));
+        am = dpp_max_f<0xB1>(am);   // quad_perm [1,0,3,2]
+        am = dpp_max_f<0x4E>(am);   // quad_perm [2,3,0,1]
+        am = dpp_max_f<0x141>(am);  // row_half_mirror: the other quad of the 8 lanes
+        const float dsc = am / 127.0f;
+        const float qi = dsc != 0.0f ? 1.0f / dsc : 0.0f;
+        const int c0 = (int)roundf(v[k].x * qi), c1 = (int)roundf(v[k].y * qi),
+                  c2 = (int)roundf(v[k].z * qi), c3 = (int)roundf(v[k].w * qi);
+        if (xq)
+            ((int *)(xq + (size_t)t * RN_D))[L + 64 * k] =
+                (c0 & 0xff) | (c1 & 0xff) << 8 | (c2 & 0xff) << 16 | (int)((unsigned)c3 << 24);
+        if (xq16) {
+            const h4v hv = {(_Float16)c0, (_Float16)c1, (_Float16)c2, (_Float16)c3};
+            ((h4v *)(xq16 + (size_t)t * RN_D))[L + 64 * k] = hv;
+        }
+        if ((L & 7) == 0) xs[(size_t)t * (RN_D / QK) + 8 * k + L / 8] = dsc;
+    }
+}
+// Tokens from which the coalesced kernel takes over (fewer tokens fill too
+// few CUs for its shorter per-lane work to pay).
+constexpr int RN_COALESCED_T = 256;
+
 // ---- router ---------------------------------------------------------------
 //
 // Thread e computes logit e as the reference's sequential fp32 chain
@@ -1162,7 +1249,13 @@ __global__ __launch_bounds__(256) void k_combine(float *__restrict__ x,
         float4 tv[8];
 #pragma unroll
         for (int j = 0; j < 8; j++)
-            if (j0 + j < K) tv[j] = *(const float4 *)(tmp + (size_t)pos[t * K + j0 + j] * d + i);
+            if (j0 + j < K) {
+                // read once: non-temporal (55 against 66 us at T = 4096)
+                typedef float f4n __attribute__((ext_vector_type(4)));
+                const f4n q = __builtin_nontemporal_load(
+                    (const f4n *)(tmp + (size_t)pos[t * K + j0 + j] * d + i));
+                tv[j] = make_float4(q.x, q.y, q.z, q.w);
+            }
 #pragma unroll
         for (int j = 0; j < 8; j++)
             if (j0 + j < K) {
@@ -1288,7 +1381,13 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     if (mfma) c->matrix_layers++;
 
     int slot = mhip::stage_begin(c, MHIP_STAGE_RMSNORM);
-    if (d == RN_D)
+    if (d == RN_D && T >= RN_COALESCED_T)
+        k_rmsnorm_q8_c<<<(T + 3) / 4, 256, 0, st>>>(d_x, d_norm, sc->xn, mfma ? nullptr : sc->xq,
+                                                    sc->xs, mfma ? (_Float16 *)sc->xdq : nullptr,
+                                                    T, s->norm_eps,
+                                                    (flags & MHIP_FORCE_SEQ_RMS) ? 1 : 0,
+                                                    sc->status);
+    else if (d == RN_D)
         k_rmsnorm_q8_w<<<(T + 3) / 4, 256, 0, st>>>(d_x, d_norm, sc->xn, sc->xq, sc->xs,
                                                     mfma ? (_Float16 *)sc->xdq : nullptr, T,
                                                     s->norm_eps,
