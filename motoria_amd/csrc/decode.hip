@@ -478,6 +478,33 @@ __device__ __forceinline__ float lds_seq_sum_n(const float *p, float s) {
     return s;
 }
 
+// Sequential fp32 sum of N LDS floats at p, in order, read B at a time: the
+// reads of the next B values are issued before the additions of these, so
+// the chain waits for the LDS only at its start.
+template <int N, int B>
+__device__ __forceinline__ float lds_seq_sum_pipe(const float *p, float s) {
+    static_assert(B % 4 == 0 && N % B == 0, "whole float4s per batch");
+    const float4 *v = (const float4 *)p;
+    float4 q[2][B / 4];
+#pragma unroll
+    for (int k = 0; k < B / 4; k++) q[0][k] = v[k];
+#pragma unroll
+    for (int b = 0; b < N / B; b++) {
+        if (b + 1 < N / B) {
+#pragma unroll
+            for (int k = 0; k < B / 4; k++) q[(b + 1) & 1][k] = v[(b + 1) * (B / 4) + k];
+        }
+#pragma unroll
+        for (int k = 0; k < B / 4; k++) {
+            s = s + q[b & 1][k].x;
+            s = s + q[b & 1][k].y;
+            s = s + q[b & 1][k].z;
+            s = s + q[b & 1][k].w;
+        }
+    }
+    return s;
+}
+
 // Sequential fp32 sum, in order, of the wavefront's 64 x 32 values, lane L
 // holding values 32 L .. 32 L + 31 in v[0..31]: every lane adds its own 32
 // values to its running sum, then the sums move one lane up (DPP wave_shr:1),
@@ -493,20 +520,6 @@ __device__ __forceinline__ float wave_seq_sum_2048(const float (&v)[32]) {
 #pragma unroll
         for (int k = 0; k < 32; k++) s = s + v[k];
     }
-    return s;
-}
-
-// Sequential fp32 sum, in order, of the wavefront's 128 values, lane L
-// holding value L in a and value 64 + L in b: each step adds a lane's value
-// to the running sum of the lane before it (DPP wave_ror:1, lane 0 taking
-// lane 63's), so step i's sum is correct in lane i % 64. The sum of all 128
-// ends in lane 63.
-__device__ __forceinline__ float wave_seq_sum_128(float a, float b) {
-    float s = 0.0f + a;
-    for (int i = 1; i < 64; i++)
-        s = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x13C, 0xf, 0xf, false)) + a;
-    for (int i = 0; i < 64; i++)
-        s = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x13C, 0xf, 0xf, false)) + b;
     return s;
 }
 
