@@ -30,8 +30,11 @@
 //      workgroup (one per down wave) by a parallel sum with a rigorous bound
 //      on the distance to the reference's sequential fp32 chain  [XCD sync]
 //   B  all 128 logits -> ranks (LDS, 512 threads) -> top-K + certification
+//      on a router wave, which hands its verdict to the others in LDS, while
+//      the gate/up waves request their first rows of the rank-k expert
 //      (if the ordering is not certified, the exact sequential logits are
-//      computed and routing follows the reference bit for bit)
+//      computed, routing follows the reference bit for bit, and the rows are
+//      requested again)
 //   C  gate/up rows of expert idx[k] + SwiGLU -> h (768 floats) [XCD sync]
 //      (the down rows are loaded behind them; the router waves run the
 //      exact logit chains meanwhile)
@@ -83,6 +86,9 @@ constexpr int NDN = NWAVE - NGU;                // waves 4..7: router rows
 constexpr int GU_H = HROWS / NGU;               // 6 h rows per gate/up wave
 constexpr int GU_R = 2 * GU_H;                  // its 12 weight rows
 constexpr int DPK = DROWS * NBH / (NGU * 64);   // 6 down (row, block) pairs per gate/up thread
+// gate/up rows of a gate/up wave requested while the ranking is certified
+// (all 12 held across the certification and its fallback spill registers)
+constexpr int GU_SPEC = 8;
 constexpr long SPIN = 1L << 18;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -447,6 +453,7 @@ struct Lds {
     double part[NGU];             // the gate/up waves' partial sums of squares
     unsigned ptag[NGU];           // the layer tag once part[w] is set
     unsigned invtag;              // the layer tag once inv is set
+    unsigned ctag;                // the layer tag once the ranking's verdict is set
     int order[E];                 // expert of each rank (ranks 0..K used)
     float inv;
     float sum;
