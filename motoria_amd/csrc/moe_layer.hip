@@ -273,6 +273,81 @@ __global__ __launch_bounds__(256) void k_rmsnorm_q8_c(const float *__restrict__ 
 // few CUs for its shorter per-lane work to pay).
 constexpr int RN_COALESCED_T = 256;
 
+// Softmax, top-K and renormalisation of token t's logits (forward.c:95-114,
+// 178-181): thread e < E holds logit l (threads >= E hold -inf); every
+// thread of the workgroup calls it (E <= blockDim.x). p: E floats of LDS;
+// keys (16-byte aligned), red, sum_sh, top: LDS scratch (E keys,
+// blockDim.x / 64 floats, one float, K ints).
+__device__ __forceinline__ void route_select(float l, int t, int E, int K, int norm_topk,
+                                             float *p, unsigned long long *keys, float *red,
+                                             float *sum_sh, int *top,
+                                             int *__restrict__ idx_out,
+                                             float *__restrict__ w_out) {
+    const int tid = threadIdx.x;
+    // max over E (order-free)
+    float mx = l;
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = red[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); i++) mx = fmaxf(mx, red[i]);
+    if (tid < E) p[tid] = mhip_dev::expf_glibc(l - mx);
+    __syncthreads();
+    if (tid == 0) {
+        // in index order, sixteen values read ahead of their additions
+        float sum = 0.0f;
+        int i = 0;
+        for (; i + 16 <= E; i += 16) {
+            float4 q[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) q[k] = *(const float4 *)&p[i + 4 * k];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                sum = sum + q[k].x;
+                sum = sum + q[k].y;
+                sum = sum + q[k].z;
+                sum = sum + q[k].w;
+            }
+        }
+        for (; i < E; i++) sum = sum + p[i];
+        *sum_sh = sum;
+    }
+    __syncthreads();
+    if (tid < E) p[tid] = p[tid] / *sum_sh;
+    __syncthreads();
+
+    // Top-K (forward.c:104-114: the largest untaken probability, the lowest
+    // index among equal ones) as ranks: probabilities are >= +0, so their
+    // bit patterns order like the values, and the low word ~index makes the
+    // lowest index win a tie; an entry's rank is the number of larger keys,
+    // and ranks 0..K-1 are the K picks in order.
+    if (tid < E)
+        keys[tid] = ((unsigned long long)__float_as_uint(p[tid]) << 32) |
+                    (unsigned long long)(0xFFFFFFFFu - (unsigned)tid);
+    __syncthreads();
+    if (tid < E) {
+        const unsigned long long ke = keys[tid];
+        int rk = 0;
+        int i = 0;
+        for (; i + 2 <= E; i += 2) {
+            const ulonglong2 kv = *(const ulonglong2 *)&keys[i];
+            rk += (int)(kv.x > ke) + (int)(kv.y > ke);
+        }
+        for (; i < E; i++) rk += (int)(keys[i] > ke);
+        if (rk < K) top[rk] = tid;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+        for (int j = 0; j < K; j++) sum = sum + p[top[j]];
+        for (int j = 0; j < K; j++) {
+            const float wj = p[top[j]];
+            idx_out[(size_t)t * K + j] = top[j];
+            w_out[(size_t)t * K + j] = norm_topk ? wj / sum : wj;
+        }
+    }
+}
+
 // ---- router ---------------------------------------------------------------
 //
 // Thread e computes logit e as the reference's sequential fp32 chain
@@ -295,6 +370,7 @@ __global__ __launch_bounds__(256) void k_router(const float *__restrict__ xn,
     extern __shared__ __align__(16) float sh[];
     float *p = sh;        // [E]
     float *xs = sh + E;   // [d] (chains computed here)
+    __shared__ __align__(16) unsigned long long keys[256];
     __shared__ float red[4];
     __shared__ float sum_sh;
     __shared__ int top[64];
@@ -324,79 +400,7 @@ __global__ __launch_bounds__(256) void k_router(const float *__restrict__ xn,
         l = s;
         logits[(size_t)t * E + tid] = s;
     }
-    // max over E (order-free)
-    float mx = l;
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if ((tid & 63) == 0) red[tid >> 6] = mx;
-    __syncthreads();
-    mx = red[0];
-    for (int i = 1; i < (int)(blockDim.x >> 6); i++) mx = fmaxf(mx, red[i]);
-    if (tid < E) p[tid] = mhip_dev::expf_glibc(l - mx);
-    __syncthreads();
-    if (tid == 0) {
-        // in index order, sixteen values read ahead of their additions
-        float sum = 0.0f;
-        int i = 0;
-        for (; i + 16 <= E; i += 16) {
-            float4 q[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) q[k] = *(const float4 *)&p[i + 4 * k];
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                sum = sum + q[k].x;
-                sum = sum + q[k].y;
-                sum = sum + q[k].z;
-                sum = sum + q[k].w;
-            }
-        }
-        for (; i < E; i++) sum = sum + p[i];
-        sum_sh = sum;
-    }
-    __syncthreads();
-    if (tid < E) p[tid] = p[tid] / sum_sh;
-    __syncthreads();
-
-    if (tid < 64) {
-        // Lane owns entries lane + 64c, c < 4 (E <= 256). Probabilities are
-        // >= +0, so their bit patterns order like the values; the low word
-        // ~index makes the lowest index win a tie.
-        float pv[4];
-        unsigned taken = 0;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int e = tid + 64 * c;
-            pv[c] = e < E ? p[e] : 0.0f;
-        }
-        for (int j = 0; j < K; j++) {
-            unsigned long long best = 0;
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const int e = tid + 64 * c;
-                if (e < E && !(taken & (1u << c))) {
-                    unsigned long long key =
-                        ((unsigned long long)__float_as_uint(pv[c]) << 32) |
-                        (unsigned long long)(0xFFFFFFFFu - (unsigned)e);
-                    best = key > best ? key : best;
-                }
-            }
-            for (int o = 32; o > 0; o >>= 1) {
-                unsigned long long other = __shfl_xor(best, o);
-                best = other > best ? other : best;
-            }
-            const int win = (int)(0xFFFFFFFFu - (unsigned)(best & 0xFFFFFFFFu));
-            if ((win & 63) == tid) taken |= 1u << (win >> 6);
-            if (tid == 0) top[j] = win;
-        }
-        if (tid == 0) {
-            float sum = 0.0f;
-            for (int j = 0; j < K; j++) sum = sum + p[top[j]];
-            for (int j = 0; j < K; j++) {
-                const float wj = p[top[j]];
-                idx_out[(size_t)t * K + j] = top[j];
-                w_out[(size_t)t * K + j] = norm_topk ? wj / sum : wj;
-            }
-        }
-    }
+    route_select(l, t, E, K, norm_topk, p, keys, red, &sum_sh, top, idx_out, w_out);
 }
 
 // ---- router logits for many tokens ----------------------------------------------
@@ -723,6 +727,192 @@ __global__ __launch_bounds__(64 * (NC + 1)) void k_router_logits_lanes(
         body(c + 1, 1);
     }
     if (t < T) logits[(size_t)t * E + e] = bias ? s + bias[e] : s;
+}
+
+// ---- rmsnorm, router and selection of one token, fused -----------------------------
+//
+// For a few tokens (each layer's chains are latency-bound there), one
+// workgroup per token does the whole front of the layer, in place of the
+// rmsnorm, router-logit and selection launches: wavefront 0 forms the
+// rmsnorm and Q8(xn) as k_rmsnorm_q8_w does (lane b owns block b;
+// forward.c:75-81, quant.c:11-27) and keeps xn in LDS; wavefronts 0 and 1
+// then run the chains of experts 64 w + lane (matmul.c:13-17: the products
+// and additions in i order, bit for bit) over the transposed router, which
+// wavefronts 2 and 3 stream into an NR_NS-stage LDS ring with
+// global_load_lds, NR_CI rows (16 KB) per chunk, NR_NS - 1 chunks ahead, one
+// workgroup barrier per chunk (as k_router_logits_lanes, for all 128 experts
+// of one token); a chain wave reads chunk c + 1's router values and xn while
+// it adds chunk c. The logits (+ bias) then go through route_select. Needs
+// d == 2048, E == 128.
+constexpr int NR_CI = 32;                    // rows of i per chunk
+constexpr int NR_NS = 8;                     // ring stages (NR_NS - 1 chunks, 112 KB, in flight)
+constexpr int NR_E = 128;
+constexpr int NR_W = 4;                      // wavefronts: 2 chains, 2 ring loaders
+constexpr int NR_DQ = NR_CI * NR_E * 4 / 1024 / 2;  // 1 KB loads per chunk per loader wave (8)
+static_assert((NR_NS - 1) * NR_DQ <= 63, "the loads in flight fit the wait counter");
+constexpr int NR_MAX_T = 256;                // tokens per layer up to which the fused front runs
+
+__global__ __launch_bounds__(64 * NR_W) void k_norm_route(const float *__restrict__ x,
+                                                    const float *__restrict__ w,
+                                                    const float *__restrict__ wt,
+                                                    const float *__restrict__ bias,
+                                                    float *__restrict__ xn,
+                                                    int8_t *__restrict__ xq,
+                                                    float *__restrict__ xs,
+                                                    float *__restrict__ logits,
+                                                    int *__restrict__ idx_out,
+                                                    float *__restrict__ w_out, int K,
+                                                    int norm_topk, float eps, int force_seq,
+                                                    int *status) {
+    __shared__ __align__(16) float ring[NR_NS][NR_CI][NR_E];
+    __shared__ __align__(16) float xn_l[RN_D];
+    __shared__ __align__(16) float p[NR_E];
+    __shared__ __align__(16) unsigned long long keys[NR_E];
+    __shared__ float red[NR_W];
+    __shared__ float sum_sh;
+    __shared__ int top[64];
+    constexpr int NCH = RN_D / NR_CI;
+    const int t = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // loader wave 2 + q takes loads NR_DQ q .. of a chunk: load k gives lane
+    // L row 2 k + L / 32 of the chunk, experts 4 (L % 32) .. + 3 (the chunk
+    // is one contiguous 16 KB run of the transposed router)
+    const unsigned ring0 = (unsigned)(uintptr_t)&ring[0][0][0];
+    auto issue = [&](int c) {
+        const int k0 = NR_DQ * (wave - 2);
+        const int cc = c < NCH ? c : NCH - 1;  // past the end: reload the last chunk
+        const unsigned st = ring0 + (unsigned)((c % NR_NS) * NR_CI * NR_E * 4);
+        const float *src = wt + (size_t)cc * NR_CI * NR_E + 4 * lane;
+#pragma unroll
+        for (int q = 0; q < NR_DQ; q++)
+            rl_dma16(st + (unsigned)((k0 + q) * 1024), src + (size_t)(k0 + q) * 256);
+    };
+    if (wave >= 2)
+        for (int c = 0; c < NR_NS - 1; c++) issue(c);
+    if (wave == 0) {
+        const int b = lane;
+        const float4 *xr = (const float4 *)(x + (size_t)t * RN_D + 32 * b);
+        const float4 *wr = (const float4 *)(w + 32 * b);
+        float v[32];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float4 q = xr[k];
+            v[4 * k] = q.x;
+            v[4 * k + 1] = q.y;
+            v[4 * k + 2] = q.z;
+            v[4 * k + 3] = q.w;
+        }
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < 32; k++) ss = ss + (double)v[k] * (double)v[k];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss = ss + __shfl_xor(ss, o);
+        ss = __shfl(ss, 0);
+        const double m = ss * ((double)(RN_D + 64) * 0x1p-52);
+        const float lo = (float)(1.0 / sqrt((ss + m) / RN_D + (double)eps));
+        const float hi = (float)(1.0 / sqrt((ss - m) / RN_D + (double)eps));
+        float inv = lo;
+        if (force_seq || lo != hi) {
+            float r = 0.0f;
+            if (b == 0) {
+                const float *xt = x + (size_t)t * RN_D;
+                double sq = 0.0;
+                for (int i = 0; i < RN_D; i++) sq = sq + (double)xt[i] * (double)xt[i];
+                r = (float)(1.0 / sqrt(sq / RN_D + (double)eps));
+                atomicAdd(&status[1], 1);
+            }
+            inv = __shfl(r, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float4 q = wr[k];
+            v[4 * k] = (v[4 * k] * inv) * q.x;
+            v[4 * k + 1] = (v[4 * k + 1] * inv) * q.y;
+            v[4 * k + 2] = (v[4 * k + 2] * inv) * q.z;
+            v[4 * k + 3] = (v[4 * k + 3] * inv) * q.w;
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 32; k++) amax = fmaxf(amax, fabsf(v[k]));
+        const float dsc = amax / 127.0f;
+        const float qi = dsc != 0.0f ? 1.0f / dsc : 0.0f;
+        float4 *xo = (float4 *)(xn + (size_t)t * RN_D + 32 * b);
+        float4 *xl = (float4 *)(xn_l + 32 * b);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float4 q = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+            xo[k] = q;
+            xl[k] = q;
+        }
+        union {
+            int8_t c[32];
+            int4 q[2];
+        } qc;
+#pragma unroll
+        for (int k = 0; k < 32; k++) qc.c[k] = (int8_t)roundf(v[k] * qi);
+        int4 *qo = (int4 *)(xq + (size_t)t * RN_D + 32 * b);
+        qo[0] = qc.q[0];
+        qo[1] = qc.q[1];
+        xs[(size_t)t * (RN_D / QK) + b] = dsc;
+    }
+    float s = 0.0f;
+    if (wave >= 2) {
+        // chunk 0 is in; then, before each chunk c's barrier, chunk c + 1
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NR_NS - 2) * NR_DQ) : "memory");
+        __syncthreads();  // xn and chunk 0
+        for (int c = 0; c < NCH; c++) {
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NR_NS - 3) * NR_DQ) : "memory");
+            __syncthreads();
+            issue(c + NR_NS - 1);  // into the stage of chunk c - 1, read before
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the reloads past the end
+    } else {
+        const int e = 64 * wave + lane;
+        float wr[2][NR_CI], xv[2][NR_CI];
+        auto lread = [&](int c, int b) {
+            const float *W = &ring[c % NR_NS][0][e];
+            const float *X = &xn_l[(c < NCH ? c : NCH - 1) * NR_CI];
+#pragma unroll
+            for (int j = 0; j < NR_CI; j++) wr[b][j] = W[j * NR_E];
+#pragma unroll
+            for (int j = 0; j < NR_CI; j += 4) {
+                const float4 q = *(const float4 *)&X[j];
+                xv[b][j] = q.x;
+                xv[b][j + 1] = q.y;
+                xv[b][j + 2] = q.z;
+                xv[b][j + 3] = q.w;
+            }
+        };
+        // the reads of a chunk pass through an opaque copy after the
+        // additions of the chunk before, so their wait lands there
+        auto settle = [&](int b) {
+#pragma unroll
+            for (int j = 0; j < NR_CI; j++) rx_opaque_v(wr[b][j]);
+#pragma unroll
+            for (int j = 0; j < NR_CI; j++) rx_opaque_v(xv[b][j]);
+        };
+        auto body = [&](int c, int cur) {
+            __syncthreads();  // chunk c + 1 is in the ring
+            lread(c + 1, cur ^ 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < NR_CI; j++) s = s + wr[cur][j] * xv[cur][j];
+            __builtin_amdgcn_sched_barrier(0);
+            settle(cur ^ 1);
+        };
+        __syncthreads();  // xn and chunk 0
+        lread(0, 0);
+        settle(0);
+        for (int c = 0; c < NCH; c += 2) {
+            body(c, 0);
+            body(c + 1, 1);
+        }
+        if (bias) s = s + bias[e];
+        logits[(size_t)t * NR_E + e] = s;
+    }
+    const float l = tid < NR_E ? s : -__builtin_inff();
+    route_select(l, t, NR_E, K, norm_topk, p, keys, red, &sum_sh, top, idx_out, w_out);
 }
 
 // ---- dispatch -------------------------------------------------------------
@@ -1380,8 +1570,13 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
                       mhip::gemm_path_fits(s);
     if (mfma) c->matrix_layers++;
 
-    int slot = mhip::stage_begin(c, MHIP_STAGE_RMSNORM);
-    if (d == RN_D && T >= RN_COALESCED_T)
+    // a few tokens: rmsnorm, router and selection as one launch per layer
+    // (recorded as the router stage)
+    const bool fused = !mfma && d == RN_D && E == NR_E && K <= 64 && T <= NR_MAX_T;
+    int slot = fused ? -1 : mhip::stage_begin(c, MHIP_STAGE_RMSNORM);
+    if (fused)
+        ;
+    else if (d == RN_D && T >= RN_COALESCED_T)
         k_rmsnorm_q8_c<<<(T + 3) / 4, 256, 0, st>>>(d_x, d_norm, sc->xn, mfma ? nullptr : sc->xq,
                                                     sc->xs, mfma ? (_Float16 *)sc->xdq : nullptr,
                                                     T, s->norm_eps,
@@ -1397,8 +1592,10 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
         k_rmsnorm_q8<<<T, NT, 0, st>>>(d_x, d_norm, sc->xn, sc->xq, sc->xs,
                                        mfma ? (_Float16 *)sc->xdq : nullptr, d, s->norm_eps,
                                        (flags & MHIP_FORCE_SEQ_RMS) ? 1 : 0, sc->status);
-    mhip::stage_end(c, slot);
-    if (mhip::check_launch(c, "rmsnorm_q8")) return -1;
+    if (!fused) {
+        mhip::stage_end(c, slot);
+        if (mhip::check_launch(c, "rmsnorm_q8")) return -1;
+    }
 
     const int rthreads = E <= 64 ? 64 : E <= 128 ? 128 : 256;
     // The tiled chains for more than one token; one workgroup per token else.
@@ -1415,7 +1612,11 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
     const bool have_logits = lanes || wide || tiled;
     const size_t rsh = (size_t)(E + (have_logits ? 0 : d)) * sizeof(float);
     slot = mhip::stage_begin(c, MHIP_STAGE_ROUTER);
-    if (lanes) {
+    if (fused) {
+        k_norm_route<<<T, 64 * NR_W, 0, st>>>(d_x, d_norm, d_router_t, d_bias, sc->xn, sc->xq, sc->xs,
+                                        sc->logits, sc->idx, sc->w, K, s->norm_topk, s->norm_eps,
+                                        (flags & MHIP_FORCE_SEQ_RMS) ? 1 : 0, sc->status);
+    } else if (lanes) {
         // one chain wavefront per workgroup while that fills at most one
         // workgroup per CU, two beyond
         const size_t lsh = router_lanes_lds();
@@ -1457,8 +1658,9 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
         else
             k_router_logits<1><<<(T + 1) / 2, 256, lsh, st>>>(sc->xn, d_router_t, d_bias, sc->logits, T, d);
     }
-    k_router<<<T, rthreads, rsh, st>>>(sc->xn, d_router_t, d_bias, sc->logits, sc->idx, sc->w, d,
-                                       E, K, s->norm_topk, have_logits ? 1 : 0);
+    if (!fused)
+        k_router<<<T, rthreads, rsh, st>>>(sc->xn, d_router_t, d_bias, sc->logits, sc->idx, sc->w,
+                                           d, E, K, s->norm_topk, have_logits ? 1 : 0);
     mhip::stage_end(c, slot);
     if (mhip::check_launch(c, "router")) return -1;
 

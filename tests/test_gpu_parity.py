@@ -244,6 +244,26 @@ def test_layer_decode_shapes(oracle, qwen_dims, qwen_moe, T):
     _compare_layer(oracle, qwen_moe, qwen_dims, 0, x, router, label="T=%d" % T)
 
 
+def test_layer_vector_path_255_with_bias(oracle, qwen_dims, qwen_moe):
+    """The most tokens the one-launch rmsnorm + router + selection front takes
+    (255 x 8 assignments stay below the matrix-core threshold), with the
+    skewed logit bias: bit-exact with and without MHIP_EXACT_EXPERTS."""
+    say("test_layer_vector_path_255_with_bias")
+    x = oracle.synth_x(W.X_SEED + 21, 255, qwen_dims.dim)
+    router = oracle.synth_router(W.WEIGHT_SEED, 0, qwen_dims)
+    bias = W.zipf_bias(qwen_dims.n_experts)
+    _compare_layer(oracle, qwen_moe, qwen_dims, 0, x, router, bias=bias, label="T=255 bias")
+    n0 = M.lib().mhip_matrix_layers(qwen_moe.gpu)
+    xg, idx, w, logits = _gpu_layer(qwen_moe, 0, x, bias, 0)
+    assert M.lib().mhip_matrix_layers(qwen_moe.gpu) == n0, "T=255 took the matrix path"
+    xo, io, wo, lo, _ = oracle_layer(oracle, qwen_moe, qwen_dims, 0, x, router, bias=bias,
+                                    need=idx.ravel().tolist())
+    assert np.array_equal(idx, io)
+    assert_bits(logits, lo, "T=255 default path logits")
+    assert_bits(w, wo, "T=255 default path gate weights")
+    assert_bits(xg, xo, "T=255 default path layer output")
+
+
 def test_layer_prefill_512(oracle, qwen_dims, qwen_moe):
     say("test_layer_prefill_512")
     x = oracle.synth_x(W.X_SEED, 512, qwen_dims.dim)
