@@ -309,15 +309,19 @@ __device__ __forceinline__ void gemm_tile(Step *ring, const Src &src, int nk, f4
 template <bool EXACT>
 __device__ __forceinline__ void gemm_tile_rows(Step *ring, const Src &src, int nk, int nrows,
                                                f4v acc[MI][NJ]) {
-    const int nj = (nrows + 15) / 16;
-    if (nj > 4)
-        gemm_tile<EXACT, 8>(ring, src, nk, acc);
-    else if (nj > 2)
-        gemm_tile<EXACT, 4>(ring, src, nk, acc);
-    else if (nj > 1)
-        gemm_tile<EXACT, 2>(ring, src, nk, acc);
-    else
-        gemm_tile<EXACT, 1>(ring, src, nk, acc);
+    // one instantiation per count of 16-row tiles, so a bucket's last tile
+    // runs no empty tile (gate/up 468 -> 459 us at T = 4096, 157 -> 149 us
+    // at T = 512, against rounding the count up to a power of two)
+    switch ((nrows + 15) / 16) {
+    case 8: gemm_tile<EXACT, 8>(ring, src, nk, acc); break;
+    case 7: gemm_tile<EXACT, 7>(ring, src, nk, acc); break;
+    case 6: gemm_tile<EXACT, 6>(ring, src, nk, acc); break;
+    case 5: gemm_tile<EXACT, 5>(ring, src, nk, acc); break;
+    case 4: gemm_tile<EXACT, 4>(ring, src, nk, acc); break;
+    case 3: gemm_tile<EXACT, 3>(ring, src, nk, acc); break;
+    case 2: gemm_tile<EXACT, 2>(ring, src, nk, acc); break;
+    default: gemm_tile<EXACT, 1>(ring, src, nk, acc); break;
+    }
 }
 
 // ---- x block scales in bucketed, block-major order --------------------------------
