@@ -50,6 +50,15 @@ const float *mia_gpu_model_step(mia_gpu_model *m, int token, int pos);
  * reads, src/app/serve.c:91-106). 0 or -1. */
 int mia_gpu_model_feed(mia_gpu_model *m, int token, int pos);
 
+/* n feeds in one call (no counterpart in the reference, whose serve loop
+ * feeds a prompt one token at a time): tokens[0..n) at positions
+ * pos .. pos + n - 1, a batch of up to 64 tokens through each layer at once
+ * (the attention of the batch with mhip_attention_batch, its MoE on the
+ * per-stage kernels), so the weights are read once per batch instead of once
+ * per token. The KV rows written are bit-equal to n calls of
+ * mia_gpu_model_feed; no logits are formed. 0 or -1. */
+int mia_gpu_model_prefill(mia_gpu_model *m, const int *tokens, int n, int pos);
+
 /* The token sampler (mhip_sample) on the logits of the last
  * mia_gpu_model_step / _step_sample call, left on the device: the picked
  * id, or -1 (also when the last call was a feed or failed). */

@@ -296,6 +296,19 @@ int mhip_attention(mhip_ctx *c, const mhip_attn_dims *s, const float *d_attn_nor
                    const float *d_q_norm, const float *d_k_norm, const double *d_rope,
                    float *d_kc, float *d_vc, int pos, int max_seq, float *d_x,
                    float *d_x_copy, void *d_scratch, int flags);
+/* No counterpart in the reference, which feeds a prompt one token at a time:
+ * mhip_attention for the n consecutive tokens at positions pos .. pos + n - 1
+ * in one go, in place on d_x[n][dim]. Every token's result and cache rows
+ * are bit-equal to n calls of mhip_attention in position order (the rows of
+ * all n tokens are appended before any score; token t reads rows
+ * 0 .. pos + t). d_scratch: mhip_attention_batch_scratch_bytes(s, n,
+ * max_seq) bytes (0 for invalid arguments). */
+size_t mhip_attention_batch_scratch_bytes(const mhip_attn_dims *s, int n, int max_seq);
+int mhip_attention_batch(mhip_ctx *c, const mhip_attn_dims *s, const float *d_attn_norm,
+                         const void *d_wq, const void *d_wk, const void *d_wv, const void *d_wo,
+                         const float *d_q_norm, const float *d_k_norm, const double *d_rope,
+                         float *d_kc, float *d_vc, int pos, int n, int max_seq, float *d_x,
+                         void *d_scratch, int flags);
 /* logits[vocab] = output Q8(rmsnorm(x, output_norm)) (forward.c:214-215);
  * d_scratch as for mhip_attention. */
 int mhip_output_head(mhip_ctx *c, const mhip_attn_dims *s, const float *d_output_norm,

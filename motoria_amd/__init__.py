@@ -149,6 +149,9 @@ SIGNATURES = {
     "mhip_attention_scratch_bytes": (_sz, [ctypes.POINTER(AttnDims), _i]),
     "mhip_attention": (_i, [_p, ctypes.POINTER(AttnDims), _p, _p, _p, _p, _p, _p, _p, _p, _p,
                             _p, _i, _i, _p, _p, _p, _i]),
+    "mhip_attention_batch_scratch_bytes": (_sz, [ctypes.POINTER(AttnDims), _i, _i]),
+    "mhip_attention_batch": (_i, [_p, ctypes.POINTER(AttnDims), _p, _p, _p, _p, _p, _p, _p, _p,
+                                  _p, _p, _i, _i, _i, _p, _p, _i]),
     "mhip_output_head": (_i, [_p, ctypes.POINTER(AttnDims), _p, _p, _i, _p, _p, _p, _i]),
     "mhip_attention_layer_ws_bytes": (_sz, []),
     "mhip_attention_layer_trace": (_i, [_p, _p, _p]),
@@ -223,6 +226,7 @@ SIGNATURES = {
     "mia_gpu_model_step": (ctypes.POINTER(_f), [_p, _i, _i]),
     "mia_gpu_model_step_sample": (_i, [_p, _i, _i, ctypes.POINTER(Sampler)]),
     "mia_gpu_model_feed": (_i, [_p, _i, _i]),
+    "mia_gpu_model_prefill": (_i, [_p, _p, _i, _i]),
     "mia_gpu_model_sample": (_i, [_p, ctypes.POINTER(Sampler)]),
     "mia_gpu_model_info": (ctypes.POINTER(FileInfo), [_p]),
     "mia_gpu_model_set_flags": (None, [_p, _i]),
@@ -580,6 +584,13 @@ class GpuModel:
         """A prompt step without the output head."""
         if lib().mia_gpu_model_feed(self.h, token, pos) != 0:
             raise RuntimeError("mia_gpu_model_feed: " +
+                               lib().mia_gpu_model_error(self.h).decode())
+
+    def prefill(self, tokens, pos):
+        """Prompt steps for tokens at pos, pos + 1, ... in batches (no logits)."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        if lib().mia_gpu_model_prefill(self.h, t.ctypes.data, len(t), pos) != 0:
+            raise RuntimeError("mia_gpu_model_prefill: " +
                                lib().mia_gpu_model_error(self.h).decode())
 
     def sample(self, sampler):

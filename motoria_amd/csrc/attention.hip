@@ -339,6 +339,345 @@ __global__ __launch_bounds__(256) void k_attn_head(
     }
 }
 
+// ---- the same for n consecutive tokens (a prompt) -----------------------------------
+//
+// Each token's values are the one-token path's: the row kernel below gives
+// token t's output row r as k_rows_q8 does (the block terms added in block
+// order), and the scores, softmax, mix and Q8 are k_qk_rope, k_attn_scores,
+// k_attn_mix and k_quant_rows with a token index, token t at position pos + t
+// reading the cache rows 0 .. pos + t, all of which (its own and the
+// earlier tokens' of the batch among them) are appended before any score.
+
+// out[k] + t * ld[k] + r = (resid ? resid[t * ld_r + r] : 0) + the Q8 dot of
+// weight row r of segment k with token t's codes xq[t][nb*32] and scales
+// xs[t][nb] (the block terms added in block order, as k_rows_q8 does), for
+// the tokens 64 blockIdx.y .. + 63. Workgroup: RT_W wavefronts of RR rows
+// each, lane i for token 64 blockIdx.y + i; the tokens' codes and scales and
+// the rows' blocks are staged in LDS RT_BC blocks at a time.
+constexpr int RT_W = 8, RT_BC = 16, RT_XLD = RT_BC * QK + 16;  // x row stride (bytes)
+
+template <int RR>
+__global__ __launch_bounds__(64 * RT_W) void k_rows_q8_t(RowSegs sg, int nb, int n,
+                                                       const int8_t *__restrict__ xq,
+                                                       const float *__restrict__ xs,
+                                                       const float *resid, int ld_r) {
+    constexpr int NR = RT_W * RR;  // rows of the workgroup
+    __shared__ __align__(16) int8_t xq_l[64 * RT_XLD];
+    __shared__ float xs_l[RT_BC][64];
+    __shared__ __align__(16) int4 wq_l[NR][RT_BC][2];
+    __shared__ float wd_l[NR][RT_BC];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t0 = blockIdx.y * 64, nt = n - t0 < 64 ? n - t0 : 64;
+    const int row0 = blockIdx.x * NR, nrows = sg.r0[3];
+    float sum[RR];
+#pragma unroll
+    for (int j = 0; j < RR; j++) sum[j] = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += RT_BC) {
+        const int nbc = nb - b0 < RT_BC ? nb - b0 : RT_BC;
+        __syncthreads();
+        for (int f = tid; f < nt * nbc * 2; f += 64 * RT_W) {
+            const int tt = f / (nbc * 2), c = f % (nbc * 2);
+            *(int4 *)&xq_l[tt * RT_XLD + c * 16] =
+                *(const int4 *)(xq + ((size_t)(t0 + tt) * nb + b0) * QK + c * 16);
+        }
+        for (int f = tid; f < nt * nbc; f += 64 * RT_W) {
+            const int tt = f / nbc, c = f % nbc;
+            xs_l[c][tt] = xs[(size_t)(t0 + tt) * nb + b0 + c];
+        }
+        for (int f = tid; f < NR * nbc * 9; f += 64 * RT_W) {
+            const int rr = f / (nbc * 9), c = f % (nbc * 9), b = c / 9, wd = c % 9;
+            const int row = row0 + rr;
+            if (row < nrows) {
+                const int k = row >= sg.r0[1] ? (row >= sg.r0[2] ? 2 : 1) : 0;
+                const uint32_t v = ((const uint32_t *)(sg.w[k] + ((size_t)(row - sg.r0[k]) * nb + b0 + b) * 36))[wd];
+                if (wd == 0) wd_l[rr][b] = __uint_as_float(v);
+                else ((uint32_t *)&wq_l[rr][b][0])[wd - 1] = v;
+            }
+        }
+        __syncthreads();
+        if (lane < nt) {
+            for (int b = 0; b < nbc; b++) {
+                const int4 *xv = (const int4 *)&xq_l[lane * RT_XLD + b * QK];
+                const int4 x0 = xv[0], x1 = xv[1];
+                const float dx = xs_l[b][lane];
+#pragma unroll
+                for (int j = 0; j < RR; j++) {
+                    const int rr = wave * RR + j;
+                    sum[j] = sum[j] + mhip_dev::block_term(
+                                          mhip_dev::dot32_i8(wq_l[rr][b][0], wq_l[rr][b][1], x0, x1),
+                                          wd_l[rr][b], dx);
+                }
+            }
+        }
+    }
+    if (lane < nt) {
+        const int t = t0 + lane;
+#pragma unroll
+        for (int j = 0; j < RR; j++) {
+            const int row = row0 + wave * RR + j;
+            if (row < nrows) {
+                const int k = row >= sg.r0[1] ? (row >= sg.r0[2] ? 2 : 1) : 0;
+                const int r = row - sg.r0[k], ld = sg.r0[k + 1] - sg.r0[k];
+                sg.out[k][(size_t)t * ld + r] = resid ? resid[(size_t)t * ld_r + r] + sum[j] : sum[j];
+            }
+        }
+    }
+}
+
+// k_qk_rope for token blockIdx.y at position pos + blockIdx.y: its q (in
+// place), k and v rows at [t][qd], [t][kvd]; the cache rows at pos + t.
+__global__ __launch_bounds__(256) void k_qk_rope_b(float *__restrict__ q,
+                                                   const float *__restrict__ k,
+                                                   const float *__restrict__ v,
+                                                   const float *__restrict__ q_norm,
+                                                   const float *__restrict__ k_norm,
+                                                   const double *__restrict__ rope, int pos,
+                                                   int nh, int nkv, int hd, float eps,
+                                                   float *__restrict__ kc,
+                                                   float *__restrict__ vc) {
+    __shared__ float hv[4][256];
+    __shared__ float inv_sh[4];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int h = blockIdx.x * 4 + wave, t = blockIdx.y, p = pos + t;
+    const int qd = nh * hd, kvd = nkv * hd;
+    if (h >= nh + 2 * nkv) return;
+    float *kc_row = kc + (size_t)p * kvd, *vc_row = vc + (size_t)p * kvd;
+    if (h >= nh + nkv) {
+        const int j = h - nh - nkv;
+        for (int i = lane; i < hd; i += 64) vc_row[j * hd + i] = v[(size_t)t * kvd + j * hd + i];
+        return;
+    }
+    const bool isq = h < nh;
+    const float *src = isq ? q + (size_t)t * qd + (size_t)h * hd
+                           : k + (size_t)t * kvd + (size_t)(h - nh) * hd;
+    const float *w = isq ? q_norm : k_norm;
+    float *row = hv[wave];
+    for (int i = lane; i < hd; i += 64) row[i] = src[i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane == 0) {
+        double ss = 0.0;
+        for (int i = 0; i < hd; i++) ss = ss + (double)row[i] * (double)row[i];
+        inv_sh[wave] = (float)(1.0 / sqrt(ss / hd + (double)eps));
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float inv = inv_sh[wave];
+    const int half = hd / 2;
+    const double *rp = rope + (size_t)p * half * 2;
+    float *dst = isq ? q + (size_t)t * qd + (size_t)h * hd : kc_row + (size_t)(h - nh) * hd;
+    for (int i = lane; i < half; i += 64) {
+        const float x0 = (row[i] * inv) * w[i];
+        const float x1 = (row[i + half] * inv) * w[i + half];
+        const double c = rp[2 * i], sn = rp[2 * i + 1];
+        dst[i] = (float)((double)x0 * c - (double)x1 * sn);
+        dst[i + half] = (float)((double)x0 * sn + (double)x1 * c);
+    }
+}
+
+// k_attn_scores for token blockIdx.y: scores[t][h][0 .. pos + t].
+__global__ __launch_bounds__(256) void k_attn_scores_b(const float *__restrict__ q,
+                                                       const float *__restrict__ kc, int pos,
+                                                       int nh, int group, int hd, int kvd,
+                                                       float scale, float *__restrict__ scores,
+                                                       int ld) {
+    const int t = blockIdx.y, np = pos + t + 1;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= nh * np) return;
+    const int h = idx / np, u = idx % np;
+    const float *qh = q + (size_t)t * nh * hd + (size_t)h * hd;
+    const float *kt = kc + (size_t)u * kvd + (size_t)(h / group) * hd;
+    float dot = 0.0f;
+    for (int i = 0; i < hd; i++) dot = dot + qh[i] * kt[i];
+    scores[((size_t)t * nh + h) * ld + u] = dot * scale;
+}
+
+// k_attn_mix for head blockIdx.x of token blockIdx.y (positions 0 .. pos + t).
+__global__ __launch_bounds__(256) void k_attn_mix_b(float *__restrict__ scores, int ld, int pos,
+                                                    int nh, const float *__restrict__ vc,
+                                                    int group, int hd, int kvd,
+                                                    float *__restrict__ att) {
+    __shared__ float red[256];
+    __shared__ float sum_sh;
+    __shared__ uint64_t etab[32];
+    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, n = pos + t + 1;
+    float *s = scores + ((size_t)t * nh + h) * ld;
+    if (tid < 32) etab[tid] = mia_expf_tab[tid];
+    float mx = -__builtin_inff();
+    for (int u = tid; u < n; u += 256) mx = fmaxf(mx, s[u]);
+    red[tid] = mx;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) red[tid] = fmaxf(red[tid], red[tid + o]);
+        __syncthreads();
+    }
+    mx = red[0];
+    for (int u = tid; u < n; u += 256) s[u] = mia_expf_glibc_tab(s[u] - mx, etab);
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+        for (int u = 0; u < n; u++) sum = sum + s[u];
+        sum_sh = sum;
+    }
+    __syncthreads();
+    const float sum = sum_sh;
+    for (int u = tid; u < n; u += 256) s[u] = s[u] / sum;
+    __syncthreads();
+    if (tid < hd) {
+        const float *vt = vc + (size_t)(h / group) * hd + tid;
+        float o = 0.0f;
+        for (int u = 0; u < n; u++) o = o + s[u] * vt[(size_t)u * kvd];
+        att[(size_t)t * nh * hd + (size_t)h * hd + tid] = o;
+    }
+}
+
+// k_attn_scores_b, k_attn_mix_b for key/value head blockIdx.x of token
+// blockIdx.y and all `group` query heads that read it (head_dim AG_HD):
+// the group shares each key and value row it loads. Scores: chunks of
+// C = 256 / group positions, the chunk's key rows staged in LDS, thread
+// (head tid / C, position tid % C) with its q row in registers. Softmax:
+// wavefront w takes heads w, w + 4, ...; the sequential sums run on lanes
+// 0 .. group - 1 of wavefront 0, one head each. Mix: thread (element
+// tid % AG_HD, heads tid / AG_HD + 2 j), the value rows read 16 positions
+// ahead of their additions. Scores (row stride sld, a multiple of 4) in
+// LDS behind the key rows (SC_LDS) or at scores + ((t * nh + h) * sld).
+constexpr int AG_HD = 128, AG_KLD = AG_HD + 4, AG_MAXG = 16;
+constexpr size_t AG_LDS_MAX = 150 * 1024;
+size_t ag_lds(int group, int sld, bool sc_lds) {
+    return (size_t)(256 / group) * AG_KLD * 4 + (sc_lds ? (size_t)group * sld * 4 : 0);
+}
+
+template <bool SC_LDS>
+__global__ __launch_bounds__(256) void k_attn_group_b(const float *__restrict__ q,
+                                                      const float *__restrict__ kc,
+                                                      const float *__restrict__ vc, int pos,
+                                                      int nh, int group, int kvd, float scale,
+                                                      float *__restrict__ scores, int sld,
+                                                      float *__restrict__ att) {
+    extern __shared__ __align__(16) float ag_sh[];
+    __shared__ uint64_t etab[32];
+    __shared__ float sum_sh[AG_MAXG];
+    const int g = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int wave = tid >> 6, np = pos + t + 1, C = 256 / group;
+    float *kt = ag_sh;
+    float *sc = SC_LDS ? ag_sh + (size_t)C * AG_KLD
+                       : scores + ((size_t)t * nh + (size_t)g * group) * sld;
+    if (tid < 32) etab[tid] = mia_expf_tab[tid];
+    {
+        const int hh = tid / C, c = tid % C;
+        float4 qr[AG_HD / 4];
+        const float4 *qh =
+            (const float4 *)(q + (size_t)t * nh * AG_HD + (size_t)(g * group + hh) * AG_HD);
+#pragma unroll
+        for (int j = 0; j < AG_HD / 4; j++) qr[j] = qh[j];
+        for (int u0 = 0; u0 < np; u0 += C) {
+            const int nc = np - u0 < C ? np - u0 : C;
+            __syncthreads();
+            for (int f = tid; f < nc * (AG_HD / 4); f += 256) {
+                const int row = f / (AG_HD / 4), c4 = f % (AG_HD / 4);
+                *(float4 *)&kt[row * AG_KLD + 4 * c4] =
+                    *(const float4 *)(kc + (size_t)(u0 + row) * kvd + (size_t)g * AG_HD + 4 * c4);
+            }
+            __syncthreads();
+            if (c < nc) {
+                const float4 *kr = (const float4 *)&kt[c * AG_KLD];
+                float dot = 0.0f;
+                for (int i = 0; i < AG_HD / 4; i += 8) {
+                    float4 k4[8];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) k4[j] = kr[i + j];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        dot = dot + qr[i + j].x * k4[j].x;
+                        dot = dot + qr[i + j].y * k4[j].y;
+                        dot = dot + qr[i + j].z * k4[j].z;
+                        dot = dot + qr[i + j].w * k4[j].w;
+                    }
+                }
+                sc[(size_t)hh * sld + u0 + c] = dot * scale;
+            }
+        }
+    }
+    __syncthreads();
+    for (int hh = wave; hh < group; hh += 4) {
+        float *s = sc + (size_t)hh * sld;
+        float mx = -__builtin_inff();
+        for (int u = lane; u < np; u += 64) mx = fmaxf(mx, s[u]);
+        // (fmaxf keeps the larger of a number and a NaN: any order gives this)
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+        for (int u = lane; u < np; u += 64) s[u] = mia_expf_glibc_tab(s[u] - mx, etab);
+    }
+    __syncthreads();
+    if (tid < group) {
+        const float *s = sc + (size_t)tid * sld;
+        float sum = 0.0f;
+        int u = 0;
+        for (; u + 16 <= np; u += 16) {
+            float4 b[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) b[j] = *(const float4 *)(s + u + 4 * j);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                sum = sum + b[j].x;
+                sum = sum + b[j].y;
+                sum = sum + b[j].z;
+                sum = sum + b[j].w;
+            }
+        }
+        for (; u < np; u++) sum = sum + s[u];
+        sum_sh[tid] = sum;
+    }
+    __syncthreads();
+    for (int hh = 0; hh < group; hh++) {
+        float *s = sc + (size_t)hh * sld;
+        const float sum = sum_sh[hh];
+        for (int u = tid; u < np; u += 256) s[u] = s[u] / sum;
+    }
+    __syncthreads();
+    {
+        const int i = tid % AG_HD, r = tid / AG_HD;
+        constexpr int NO = AG_MAXG / 2;
+        float o[NO];
+#pragma unroll
+        for (int j = 0; j < NO; j++) o[j] = 0.0f;
+        const float *vt = vc + (size_t)g * AG_HD + i;
+        int u = 0;
+        for (; u + 16 <= np; u += 16) {
+            float vv[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) vv[j] = vt[(size_t)(u + j) * kvd];
+#pragma unroll
+            for (int jj = 0; jj < NO; jj++) {
+                if (r + 2 * jj < group) {
+                    const float4 *p4 = (const float4 *)(sc + (size_t)(r + 2 * jj) * sld + u);
+#pragma unroll
+                    for (int j4 = 0; j4 < 4; j4++) {
+                        const float4 p = p4[j4];
+                        o[jj] = o[jj] + p.x * vv[4 * j4];
+                        o[jj] = o[jj] + p.y * vv[4 * j4 + 1];
+                        o[jj] = o[jj] + p.z * vv[4 * j4 + 2];
+                        o[jj] = o[jj] + p.w * vv[4 * j4 + 3];
+                    }
+                }
+            }
+        }
+        for (; u < np; u++) {
+            const float vu = vt[(size_t)u * kvd];
+#pragma unroll
+            for (int jj = 0; jj < NO; jj++)
+                if (r + 2 * jj < group) o[jj] = o[jj] + sc[(size_t)(r + 2 * jj) * sld + u] * vu;
+        }
+#pragma unroll
+        for (int jj = 0; jj < NO; jj++)
+            if (r + 2 * jj < group)
+                att[(size_t)t * nh * AG_HD + (size_t)(g * group + r + 2 * jj) * AG_HD + i] = o[jj];
+    }
+}
+
 constexpr size_t HEAD_LDS_MAX = 150 * 1024;  // dynamic LDS of k_attn_head
 size_t head_lds(int hd, int max_seq) { return ((size_t)4 * hd + (size_t)max_seq) * sizeof(float); }
 
@@ -447,6 +786,97 @@ int mhip_attention(mhip_ctx *c, const mhip_attn_dims *s, const float *d_attn_nor
     k_rows_q8<<<mhip::blocks_for(d, 4), 256, 0, st>>>(one_seg(d_wo, d_x, d), qd / QK, a.attq,
                                                        a.atts, d_x, d_x_copy);
     return mhip::check_launch(c, "attention");
+}
+
+size_t mhip_attention_batch_scratch_bytes(const mhip_attn_dims *s, int n, int max_seq) {
+    if (!s || n <= 0 || max_seq <= 0) return 0;
+    const size_t d = s->dim, qd = (size_t)s->n_heads * s->head_dim,
+                 kvd = (size_t)s->n_kv_heads * s->head_dim, N = (size_t)n;
+    return align256(N * d * 4) + align256(N * d) + align256(N * (d / QK) * 4) +
+           align256(N * qd * 4) + 2 * align256(N * kvd * 4) + align256(N * qd * 4) +
+           align256(N * qd) + align256(N * (qd / QK) * 4) +
+           align256(N * s->n_heads * (size_t)((max_seq + 3) & ~3) * 4) + align256(16);
+}
+
+int mhip_attention_batch(mhip_ctx *c, const mhip_attn_dims *s, const float *d_attn_norm,
+                         const void *d_wq, const void *d_wk, const void *d_wv, const void *d_wo,
+                         const float *d_q_norm, const float *d_k_norm, const double *d_rope,
+                         float *d_kc, float *d_vc, int pos, int n, int max_seq, float *d_x,
+                         void *d_scratch, int flags) {
+    if (check_attn(c, s, max_seq)) return -1;
+    if (n <= 0 || pos < 0 || pos + n > max_seq)
+        return mhip::fail(c, "attention batch: positions %d .. %d outside [0, max_seq=%d)", pos,
+                          pos + n - 1, max_seq);
+    if (mhip::use_device(c)) return -1;
+    const int d = s->dim, nh = s->n_heads, nkv = s->n_kv_heads, hd = s->head_dim;
+    const int qd = nh * hd, kvd = nkv * hd, nb = d / QK;
+    // carve the batch scratch
+    uint8_t *p = (uint8_t *)d_scratch;
+    auto take = [&](size_t bytes) {
+        void *r = p;
+        p += align256(bytes);
+        return r;
+    };
+    const size_t N = (size_t)n;
+    float *xn = (float *)take(N * d * 4);
+    int8_t *xq = (int8_t *)take(N * d);
+    float *xs = (float *)take(N * nb * 4);
+    float *q = (float *)take(N * qd * 4);
+    float *k = (float *)take(N * kvd * 4);
+    float *v = (float *)take(N * kvd * 4);
+    float *att = (float *)take(N * qd * 4);
+    int8_t *attq = (int8_t *)take(N * qd);
+    float *atts = (float *)take(N * (qd / QK) * 4);
+    const int sld = (max_seq + 3) & ~3;  // row stride of the scores
+    float *scores = (float *)take(N * nh * (size_t)sld * 4);
+    int *status = (int *)take(16);
+    hipStream_t st = c->stream;
+    static int lds_set[64];  // per device ordinal
+    if (c->device >= 0 && c->device < 64 && !lds_set[c->device]) {
+        if (mhip::check(c, hipFuncSetAttribute((const void *)k_attn_group_b<true>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)AG_LDS_MAX),
+                        "attention LDS attribute") ||
+            mhip::check(c, hipFuncSetAttribute((const void *)k_attn_group_b<false>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)AG_LDS_MAX),
+                        "attention LDS attribute"))
+            return -1;
+        lds_set[c->device] = 1;
+    }
+    mhip::launch_rmsnorm_q8(st, d_x, d_attn_norm, xn, xq, xs, n, d, s->norm_eps,
+                            (flags & MHIP_FORCE_SEQ_RMS) ? 1 : 0, status);
+    RowSegs qkv = {{(const uint8_t *)d_wq, (const uint8_t *)d_wk, (const uint8_t *)d_wv},
+                   {q, k, v},
+                   {0, qd, qd + kvd, qd + 2 * kvd}};
+    k_rows_q8_t<2><<<dim3(mhip::blocks_for(qd + 2 * kvd, 2 * RT_W), mhip::blocks_for(N, 64)),
+                     64 * RT_W, 0, st>>>(qkv, nb, n, xq, xs, nullptr, 0);
+    if (mhip::check_launch(c, "attention batch qkv")) return -1;
+    k_qk_rope_b<<<dim3(mhip::blocks_for(nh + 2 * nkv, 4), n), 256, 0, st>>>(
+        q, k, v, d_q_norm, d_k_norm, d_rope, pos, nh, nkv, hd, s->norm_eps, d_kc, d_vc);
+    const float scale = 1.0f / sqrtf((float)hd);
+    const int group = nh / nkv;
+    if (hd == AG_HD && group <= AG_MAXG && 256 % group == 0) {
+        // the group's heads together; their scores in LDS while they fit
+        const int sl = (pos + n + 3) & ~3;
+        if (ag_lds(group, sl, true) <= AG_LDS_MAX)
+            k_attn_group_b<true><<<dim3(nkv, n), 256, ag_lds(group, sl, true), st>>>(
+                q, d_kc, d_vc, pos, nh, group, kvd, scale, nullptr, sl, att);
+        else
+            k_attn_group_b<false><<<dim3(nkv, n), 256, ag_lds(group, sld, false), st>>>(
+                q, d_kc, d_vc, pos, nh, group, kvd, scale, scores, sld, att);
+    } else {
+        k_attn_scores_b<<<dim3(mhip::blocks_for((size_t)nh * (pos + n), 256), n), 256, 0, st>>>(
+            q, d_kc, pos, nh, group, hd, kvd, scale, scores, sld);
+        k_attn_mix_b<<<dim3(nh, n), 256, 0, st>>>(scores, sld, pos, nh, d_vc, group, hd, kvd,
+                                                  att);
+    }
+    if (mhip::check_launch(c, "attention batch scores")) return -1;
+    k_quant_rows<<<mhip::blocks_for(N * qd / QK, 256), 256, 0, st>>>(att, (int)(N * qd / QK),
+                                                                      attq, atts);
+    k_rows_q8_t<1><<<dim3(mhip::blocks_for(d, RT_W), mhip::blocks_for(N, 64)), 64 * RT_W, 0,
+                     st>>>(one_seg(d_wo, d_x, d), qd / QK, n, attq, atts, d_x, d);
+    return mhip::check_launch(c, "attention batch");
 }
 
 int mhip_output_head(mhip_ctx *c, const mhip_attn_dims *s, const float *d_output_norm,

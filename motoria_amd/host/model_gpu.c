@@ -54,8 +54,20 @@ struct mia_gpu_model {
     int *d_token, *h_token;  /* the sampled token (device, pinned) */
     float *h_logits;         /* pinned [vocab] */
     int *h_status;           /* pinned [L][4] */
+    float *d_xb;             /* [PREFILL_MAX][dim] the residuals of a prompt batch */
+    void *d_bscratch;        /* mhip_attention_batch scratch for PREFILL_MAX tokens */
     char err[512];
 };
+
+/* Prompt tokens per batch of mia_gpu_model_prefill, at most: a batch also
+ * keeps T x n_active below MHIP_GEMM_MIN_A, so its MoE stays on the
+ * bit-exact per-stage kernels (255 tokens at n_active 8). */
+enum { PREFILL_MAX = 256 };
+
+static int prefill_batch_max(const mia_file_info *h) {
+    const int k = (MHIP_GEMM_MIN_A - 1) / (int)h->n_active;
+    return k < PREFILL_MAX ? k : PREFILL_MAX;
+}
 
 static int mfail(mia_gpu_model *m, const char *fmt, ...) {
     va_list ap;
@@ -87,6 +99,8 @@ void mia_gpu_model_close(mia_gpu_model *m) {
         mhip_free(m->gpu, m->d_scratch);
         mhip_free(m->gpu, m->d_x);
         mhip_free(m->gpu, m->d_xsave);
+        mhip_free(m->gpu, m->d_xb);
+        mhip_free(m->gpu, m->d_bscratch);
         mhip_free(m->gpu, m->d_xin);
         mhip_free(m->gpu, m->d_aws);
         mhip_free(m->gpu, m->d_al);
@@ -141,7 +155,8 @@ static int setup(mia_gpu_model *m, int max_seq, int device) {
         return mfail(m, "weight type %u; the GPU model runs Q8_0 models", h->wtype);
     if (max_seq < 1) return mfail(m, "max_seq=%d", max_seq);
     mia_moe_config c = {(int)h->dim, (int)h->n_layers, (int)h->n_experts, (int)h->n_active,
-                        (int)h->expert_hidden, (int)h->norm_topk, h->norm_eps, 1, device};
+                        (int)h->expert_hidden, (int)h->norm_topk, h->norm_eps, PREFILL_MAX,
+                        device};
     if (mia_moe_open(&m->moe, &c, e2, sizeof e2)) return mfail(m, "%s", e2);
     m->gpu = mia_moe_gpu(m->moe);
     m->max_seq = max_seq;
@@ -497,6 +512,57 @@ const float *mia_gpu_model_step(mia_gpu_model *m, int token, int pos) {
 int mia_gpu_model_feed(mia_gpu_model *m, int token, int pos) {
     step_tail t = {NULL, 0, 1};
     return run_step(m, token, pos, &t);
+}
+
+/* n prompt tokens at positions pos .. pos + n - 1 in batches of equal size
+ * (up to prefill_batch_max): each layer's attention for the batch
+ * (mhip_attention_batch) and its MoE for the batch (the per-stage kernels
+ * for T tokens), the KV rows written as n feeds write them
+ * (forward.c:205-213 per token, bit-equal). */
+int mia_gpu_model_prefill(mia_gpu_model *m, const int *tokens, int n, int pos) {
+    const mia_file_info *h = &m->info;
+    m->logits_ok = 0;
+    if (n < 0 || !tokens || pos < 0 || pos + n > m->max_seq)
+        return mfail(m, "prefill of %d tokens at position %d outside [0, %d)", n, pos,
+                     m->max_seq);
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= (int)h->vocab)
+            return mfail(m, "token %d outside [0, %u)", tokens[i], h->vocab);
+    const int L = (int)h->n_layers, d = (int)h->dim;
+    const size_t kvd = (size_t)h->n_kv_heads * h->head_dim, row = (size_t)(d / MIA_QK) * 36;
+    const int bmax = prefill_batch_max(h);
+    if (n == 0) return 0;
+    if (!m->d_xb) {
+        m->d_xb = mhip_malloc(m->gpu, (size_t)bmax * d * 4);
+        m->d_bscratch =
+            mhip_malloc(m->gpu, mhip_attention_batch_scratch_bytes(&m->ad, bmax, m->max_seq));
+        if (!m->d_xb || !m->d_bscratch) return mfail(m, "device memory: %s", mhip_error(m->gpu));
+    }
+    const int nbat = (n + bmax - 1) / bmax, bsz = (n + nbat - 1) / nbat;
+    for (int b0 = 0; b0 < n; b0 += bsz) {
+        const int nb = n - b0 < bsz ? n - b0 : bsz;
+        for (int i = 0; i < nb; i++)
+            if (mhip_dequantize_q8(m->gpu, m->d_dense + m->off_embd + (size_t)tokens[b0 + i] * row,
+                                   m->d_xb + (size_t)i * d, d))
+                return mfail(m, "%s", mhip_error(m->gpu));
+        for (int l = 0; l < L; l++) {
+            const mia_layer_offsets *o = &m->lo[l];
+            const unsigned char *b = m->d_dense;
+            float *kc = m->d_kc + (size_t)l * m->max_seq * kvd;
+            float *vc = m->d_vc + (size_t)l * m->max_seq * kvd;
+            if (mhip_attention_batch(m->gpu, &m->ad, (const float *)(b + o->attn_norm), b + o->wq,
+                                     b + o->wk, b + o->wv, b + o->wo,
+                                     (const float *)(b + o->q_norm),
+                                     (const float *)(b + o->k_norm), m->d_rope, kc, vc,
+                                     pos + b0, nb, m->max_seq, m->d_xb, m->d_bscratch,
+                                     m->flags & MHIP_FORCE_SEQ_RMS))
+                return mfail(m, "%s", mhip_error(m->gpu));
+            if (mia_moe_layer_dev(m->moe, l, m->d_xb, nb, NULL))
+                return mfail(m, "%s", mia_moe_error(m->moe));
+        }
+    }
+    if (mhip_sync(m->gpu)) return mfail(m, "%s", mhip_error(m->gpu));
+    return 0;
 }
 
 int mia_gpu_model_sample(mia_gpu_model *m, mhip_sampler *s) {

@@ -17,17 +17,19 @@
  * phases:
  *   admit    the turn's chat text is tokenized and must leave room for at
  *            least one reply token (else ERR context_full);
- *   prefill  each prompt token is run at the next position, PROG after
- *            each; positions before the last skip the output head
- *            (mia_gpu_model_feed); a cancel here takes the conversation
- *            back to where the turn started;
+ *   prefill  the prompt tokens before the last run in batches of up to
+ *            PREFILL_CHUNK at the next positions without the output head
+ *            (mia_gpu_model_prefill: the KV rows n feeds would write), a
+ *            PROG for each token once its batch is done; the last token is
+ *            a step; a cancel here (checked between batches) takes the
+ *            conversation back to where the turn started;
  *   generate the sampler draws from the device logits of the last step
  *            (mia_gpu_model_sample) while tokens and context remain; a stop
  *            token ends the turn without being sent; each sent token is
  *            run to give the logits of the next draw, so the sampler state
  *            (carried from turn to turn) advances once per draw.
- * SIGUSR1 cancels a running CHAT (checked before each prompt token and
- * after each generated one). A failing GPU step answers ERR engine and
+ * SIGUSR1 cancels a running CHAT (checked before each prompt batch and
+ * after each generated token). A failing GPU step answers ERR engine and
  * starts a new conversation. Every expert is resident in HBM: the
  * expert-cache counters of TOK and DONE count each expert use as a hit.
  */
@@ -44,7 +46,7 @@
 #include "mia/model_gpu.h"
 #include "mia/serve.h"
 
-enum { MESSAGE_MAX = 1 << 20 };
+enum { MESSAGE_MAX = 1 << 20, PREFILL_CHUNK = 255 };
 
 static volatile sig_atomic_t g_stop_turn;
 static void on_cancel_signal(int sig) {
@@ -102,12 +104,10 @@ static void engine_lost(session *s) {
     s->used = 0;
 }
 
-/* Runs `id` at the next position; with `head` the step ends in the logits
- * the sampler draws from. 0, or -1 (reported). */
-static int advance(session *s, int id, int head) {
-    const int rc = head ? (mia_gpu_model_step(s->model, id, s->used) ? 0 : -1)
-                        : mia_gpu_model_feed(s->model, id, s->used);
-    if (rc) {
+/* Runs `id` at the next position, ending in the logits the sampler draws
+ * from. 0, or -1 (reported). */
+static int advance(session *s, int id) {
+    if (!mia_gpu_model_step(s->model, id, s->used)) {
         engine_lost(s);
         return -1;
     }
@@ -141,7 +141,7 @@ static void run_chat(session *s, const char *text, int max_tokens, float tempera
     /* prefill */
     turn t = {n, 0, now_s(), 0.0, 0.0};
     const int first = s->used;
-    for (int i = 0; i < n; i++) {
+    for (int i = 0; i < n;) {
         if (g_stop_turn) {
             s->used = first; /* the next turn overwrites these positions */
             t.prompt = i;
@@ -149,8 +149,20 @@ static void run_chat(session *s, const char *text, int max_tokens, float tempera
             reply_done(s, "cancel", &t);
             return;
         }
-        if (advance(s, s->prompt[i], i == n - 1)) return;
-        reply(s, "PROG %d %d", i + 1, n);
+        if (i == n - 1) {
+            if (advance(s, s->prompt[i])) return;
+            reply(s, "PROG %d %d", n, n);
+            break;
+        }
+        const int c = n - 1 - i < PREFILL_CHUNK ? n - 1 - i : PREFILL_CHUNK;
+        if (mia_gpu_model_prefill(s->model, s->prompt + i, c, s->used)) {
+            engine_lost(s);
+            return;
+        }
+        s->used += c;
+        s->uses += (unsigned long long)s->uses_per_step * (unsigned long long)c;
+        for (int j = 1; j <= c; j++) reply(s, "PROG %d %d", i + j, n);
+        i += c;
     }
     t.t_prefill = now_s();
 
@@ -176,7 +188,7 @@ static void run_chat(session *s, const char *text, int max_tokens, float tempera
         fwrite(bytes, 1, (size_t)len, s->out);
         fflush(s->out);
         t.gen++;
-        if (advance(s, id, 1)) return;
+        if (advance(s, id)) return;
         if (g_stop_turn) {
             why = "cancel";
             break;

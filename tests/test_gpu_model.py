@@ -286,3 +286,79 @@ def test_model_long_context_attention_paths_agree(oracle, tmp_path):
     finally:
         a.close()
         b.close()
+
+
+@pytest.mark.parametrize("name", ["model_tiny", "model_mini_qwen"])
+def test_model_prefill_equals_feeds_golden(oracle, tmp_path, name):
+    """mia_gpu_model_prefill of the first k tokens, then steps: the logits are
+    the reference's own (the golden files) at every later position, for k
+    across the 64-token batch size."""
+    say("test_model_prefill_equals_feeds_golden", name)
+    g = np.load(os.path.join(GOLDEN, name + ".npz"))
+    spec = json.load(open(os.path.join(GOLDEN, "MANIFEST_model.json")))[name]
+    path = str(tmp_path / (name + ".mia"))
+    MW.synthetic(oracle, path, spec["cfg"], MW.Q8_0, int(g["seed"]))
+    toks = g["tokens"].tolist()
+    n = len(toks)
+    m = M.GpuModel(path, int(g["max_seq"]))
+    try:
+        for k in sorted({1, n // 2, n - 1}):
+            m.prefill(toks[:k], 0)
+            for p in range(k, n):
+                got = m.step(toks[p], p)
+                assert np.array_equal(bits(got), g["logits_bits"][p]), \
+                    "%s prefill %d, position %d" % (name, k, p)
+        say("  prefill of 1, %d, %d tokens then steps: bit-equal to the reference" % (n // 2, n - 1))
+        with pytest.raises(RuntimeError, match="outside"):
+            m.prefill([0, 1], int(g["max_seq"]) - 1)
+    finally:
+        m.close()
+
+
+def test_model_full_shape_prefill_equals_feeds():
+    """48 layers at the Qwen3-30B-A3B shape: a 300-token prompt (two batches
+    of 150: three 64-token row chunks and a partial one each) through
+    mia_gpu_model_prefill, then steps, gives the logits bits of 300 feeds and
+    the same steps."""
+    say("test_model_full_shape_prefill_equals_feeds")
+    n = 300
+    a = M.GpuModel(None, 512, synth=(QWEN_FULL, 9))
+    b = M.GpuModel(None, 512, synth=(QWEN_FULL, 9))
+    try:
+        toks = np.random.default_rng(13).integers(0, QWEN_FULL["vocab"], n + 3).tolist()
+        a.prefill(toks[:n], 0)
+        for p in range(n):
+            b.feed(toks[p], p)
+        for p in range(n, n + 3):
+            la, lb = a.step(toks[p], p), b.step(toks[p], p)
+            assert np.all(np.isfinite(la))
+            assert np.array_equal(bits(la), bits(lb)), "position %d" % p
+        say("  300-token prefill + 3 steps == 300 feeds + 3 steps (bits)")
+    finally:
+        a.close()
+        b.close()
+
+
+def test_model_full_shape_prefill_far_positions():
+    """A prompt batch whose context is too long for its scores in LDS (the
+    scores in device memory), at positions 4300 .. 4309, against feeds; the
+    positions before are left empty (zero cache rows) on both handles."""
+    say("test_model_full_shape_prefill_far_positions")
+    a = M.GpuModel(None, 4400, synth=(QWEN_FULL, 10))
+    b = M.GpuModel(None, 4400, synth=(QWEN_FULL, 10))
+    try:
+        toks = np.random.default_rng(14).integers(0, QWEN_FULL["vocab"], 12).tolist()
+        a.prefill(toks[:3], 0)
+        a.prefill(toks[3:10], 4300)
+        for p in range(3):
+            b.feed(toks[p], p)
+        for p in range(7):
+            b.feed(toks[3 + p], 4300 + p)
+        for p, tok in ((4307, toks[10]), (4308, toks[11])):
+            la, lb = a.step(tok, p), b.step(tok, p)
+            assert np.all(np.isfinite(la))
+            assert np.array_equal(bits(la), bits(lb)), "position %d" % p
+        say("  prefill at 4300 .. 4306 + 2 steps == feeds + 2 steps (bits)")
+    finally:
+        a.close()
+        b.close()
