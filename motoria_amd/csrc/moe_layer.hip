@@ -896,18 +896,8 @@ __global__ __launch_bounds__(64 * NR_W) void k_norm_route(const float *__restric
             __syncthreads();  // chunk c + 1 is in the ring
             lread(c + 1, cur ^ 1);
             __builtin_amdgcn_sched_barrier(0);
-            // the chunk's products first (independent), through an opaque
-            // copy so that they are not formed one by one between the
-            // dependent additions, which would put each product's latency
-            // on the chain
-            float pr[NR_CI];
 #pragma unroll
-            for (int j = 0; j < NR_CI; j++) pr[j] = wr[cur][j] * xv[cur][j];
-#pragma unroll
-            for (int j = 0; j < NR_CI; j++) rx_opaque_v(pr[j]);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int j = 0; j < NR_CI; j++) s = s + pr[j];
+            for (int j = 0; j < NR_CI; j++) s = s + wr[cur][j] * xv[cur][j];
             __builtin_amdgcn_sched_barrier(0);
             settle(cur ^ 1);
         };
