@@ -423,6 +423,11 @@ __device__ __forceinline__ void rl_dma16(unsigned lds, const void *g) {
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g)
                  : "memory", "m0");
 }
+// 4 bytes per lane, lane i's at lds + 4 i.
+__device__ __forceinline__ void rl_dma4(unsigned lds, const void *g) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(g)
+                 : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 template <int C>
@@ -1251,9 +1256,33 @@ __global__ __launch_bounds__(NT, 6) void k_gateup(const uint8_t *__restrict__ ta
     const int ld = nb + 1;
     float *gu = terms + TB * 2 * R * ld;
     float *xs_l = gu + TB * 2 * R;
-    int *tk = (int *)(xs_l + TB * nb);
     int8_t *xq_l = (int8_t *)(terms + gateup_xq_off(d, R));
 
+    // A pass's tokens (uniform loads); their Q8 rows and scales go straight
+    // into LDS, 1 KB of codes or 64 scales per wavefront instruction. The
+    // first pass's copies are issued before the weights, so they arrive
+    // with them.
+    auto stage = [&](int base, int ntok) {
+        int tkn[TB];
+#pragma unroll
+        for (int j = 0; j < TB; j++) tkn[j] = j < ntok ? perm[base + j] / K : 0;
+        const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const int nck = (d + 1023) / 1024, ncs = (nb + 63) / 64;
+        const unsigned xl = (unsigned)(uintptr_t)xq_l, sl = (unsigned)(uintptr_t)xs_l;
+        for (int j = wave; j < ntok * nck; j += NT / 64) {
+            const int tb = j / nck, q = j % nck, off = 1024 * q + 16 * lane;
+            if (off < d)
+                rl_dma16(__builtin_amdgcn_readfirstlane(xl + (unsigned)(tb * d + 1024 * q)),
+                         xq + (size_t)tkn[tb] * d + off);
+        }
+        for (int j = wave; j < ntok * ncs; j += NT / 64) {
+            const int tb = j / ncs, q = j % ncs, b = 64 * q + lane;
+            if (b < nb)
+                rl_dma4(__builtin_amdgcn_readfirstlane(sl + (unsigned)(4 * (tb * nb + 64 * q))),
+                        xs + (size_t)tkn[tb] * nb + b);
+        }
+    };
+    if (b0 < b1) stage(b0, b1 - b0 < TB ? b1 - b0 : TB);
     int4 wc0[PK], wc1[PK];
     float wd[PK];
     int prow[PK], pblk[PK];
@@ -1276,14 +1305,8 @@ __global__ __launch_bounds__(NT, 6) void k_gateup(const uint8_t *__restrict__ ta
     }
     for (int base = b0; base < b1; base += TB) {
         const int ntok = b1 - base < TB ? b1 - base : TB;
-        if (threadIdx.x < ntok) tk[threadIdx.x] = perm[base + threadIdx.x] / K;
-        __syncthreads();
-        const int nq = d / 16;
-        for (int c = threadIdx.x; c < ntok * nq; c += NT)
-            ((int4 *)(xq_l + (size_t)(c / nq) * d))[c % nq] =
-                ((const int4 *)(xq + (size_t)tk[c / nq] * d))[c % nq];
-        for (int c = threadIdx.x; c < ntok * nb; c += NT)
-            xs_l[c] = xs[(size_t)tk[c / nb] * nb + c % nb];
+        if (base != b0) stage(base, ntok);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < PK; k++) {
@@ -1375,6 +1398,28 @@ __global__ __launch_bounds__(NT) void k_down(const uint8_t *__restrict__ table, 
     float *hs = terms + TB * R * ld;
     int8_t *hq = (int8_t *)(hs + TB * nbh);
 
+    // A pass's rows base .. base + ntok - 1 of the bucket (contiguous):
+    // codes and scales straight into LDS, 1 KB of codes or 64 scales per
+    // wavefront instruction; the first pass's copies are issued before the
+    // weights, so they arrive with them.
+    auto stage = [&](int base, int ntok) {
+        const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const int nbytes = ntok * eh, nst = ntok * nbh;
+        const unsigned ql = (unsigned)(uintptr_t)hq, sl = (unsigned)(uintptr_t)hs;
+        for (int q = wave; 1024 * q < nbytes; q += NT / 64) {
+            const int off = 1024 * q + 16 * lane;
+            if (off < nbytes)
+                rl_dma16(__builtin_amdgcn_readfirstlane(ql + (unsigned)(1024 * q)),
+                         hq_g + (size_t)base * eh + off);
+        }
+        for (int q = wave; 64 * q < nst; q += NT / 64) {
+            const int b = 64 * q + lane;
+            if (b < nst)
+                rl_dma4(__builtin_amdgcn_readfirstlane(sl + (unsigned)(256 * q)),
+                        hs_g + (size_t)base * nbh + b);
+        }
+    };
+    if (b0 < b1) stage(b0, b1 - b0 < TB ? b1 - b0 : TB);
     int4 wc0[PK], wc1[PK];
     float wd[PK];
     int prow[PK], pblk[PK];
@@ -1394,11 +1439,8 @@ __global__ __launch_bounds__(NT) void k_down(const uint8_t *__restrict__ table, 
     }
     for (int base = b0; base < b1; base += TB) {
         const int ntok = b1 - base < TB ? b1 - base : TB;
-        // the bucket's rows base .. base + ntok - 1 are contiguous
-        const int nq = ntok * eh / 16;
-        for (int c = threadIdx.x; c < nq; c += NT)
-            ((int4 *)hq)[c] = ((const int4 *)(hq_g + (size_t)base * eh))[c];
-        for (int c = threadIdx.x; c < ntok * nbh; c += NT) hs[c] = hs_g[(size_t)base * nbh + c];
+        if (base != b0) stage(base, ntok);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < PK; k++) {
