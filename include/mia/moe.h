@@ -104,7 +104,8 @@ int mia_file_layer_offsets(const mia_file_info *info, int layer, uint64_t *ffn_n
 int mia_moe_load_file(mia_moe *m, const char *path);
 
 /* One layer, moe() semantics, in place on host x[T][dim]. Bit-equal to the
- * reference (below MHIP_GEMM_MIN_A assignments; within 1e-3 above). One
+ * reference at every T (with MHIP_FAST_DOWN set through mia_moe_set_flags,
+ * within ~1e-6 relative from MHIP_GEMM_MIN_A assignments on). One
  * token (T = 1) runs as one launch of the persistent decode kernel with the
  * exact router where mhip_decode_supported allows it, else per stage; a
  * decode launch that aborts is rerun per stage (same bits). A failing call

@@ -173,6 +173,9 @@ int mhip_scratch_carve(const mhip_dims *s, int max_tokens, void *d_base,
                                      parallel router logits (expert indices still bit-equal,
                                      weights within ~1e-6 relative, so over many layers the
                                      output drifts from the reference's; not the default) */
+#define MHIP_FAST_DOWN 512        /* layer, matrix-core path: each down block term added
+                                     with one fused multiply-add (expert outputs within a
+                                     few fp32 ulps instead of bit-equal; not the default) */
 
 /*
  * One MoE layer (rmsnorm -> router/top-K -> dispatch -> gate/up+SwiGLU ->
@@ -181,15 +184,14 @@ int mhip_scratch_carve(const mhip_dims *s, int max_tokens, void *d_base,
  * this layer's experts, transposed router and ffn_norm. d_bias (E floats) is
  * added to the logits when non-NULL.
  *
- * Routing (indices, order, gate weights) is bit-equal to the reference at
- * every T. The expert products are bit-equal too for small batches; from
- * MHIP_GEMM_MIN_A assignments on (and when the shape allows: d a multiple of
- * 256, expert_hidden of 128) they run on the matrix cores: the gate/up and
- * down block dots stay exact integers; gate/up adds each block term in the
- * reference's rounding order (h and Q8(h) bit-equal), down with one fused
- * multiply-add (expert outputs within a few fp32 ulps), so the layer output
- * is within ~1e-6 relative of the reference (max|diff| / max|ref|).
- * MHIP_EXACT_EXPERTS keeps the bit-exact vector path at every T.
+ * Routing (indices, order, gate weights) and the layer output are bit-equal
+ * to the reference at every T. From MHIP_GEMM_MIN_A assignments on (and when
+ * the shape allows: d a multiple of 256, expert_hidden of 128) the expert
+ * products run on the matrix cores: the gate/up and down block dots stay
+ * exact integers and each block term is added in the reference's rounding
+ * order. MHIP_FAST_DOWN adds the down terms with one fused multiply-add
+ * instead (outputs within ~1e-6 relative); MHIP_EXACT_EXPERTS keeps the
+ * vector kernels at every T.
  */
 #define MHIP_GEMM_MIN_A 2048
 int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,

@@ -32,6 +32,7 @@ MHIP_ATTN_FORCE_ABORT = 64
 MHIP_CHAIN_SUM, MHIP_CHAIN_GE, MHIP_CHAIN_GT = 0, 1, 2
 MHIP_MODEL_PER_LAYER = 128
 MHIP_DECODE_CERTIFIED = 256
+MHIP_FAST_DOWN = 512
 MHIP_MODEL_STACK_MAX_SEQ = 8192  # longest context of the model stack (mia_hip.h)
 DECODE_MAX_LAYERS = 256  # MHIP_DECODE_MAX_LAYERS
 GEMM_MIN_A = 2048  # MHIP_GEMM_MIN_A

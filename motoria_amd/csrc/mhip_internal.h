@@ -66,7 +66,7 @@ int gemm_max_tiles(int A, int E);
 int launch_gateup_mfma(hipStream_t st, const mhip_dims *s, const mhip_layout *lay,
                        const void *d_table_layer, const mhip_scratch *sc, int A);
 int launch_down_mfma(hipStream_t st, const mhip_dims *s, const mhip_layout *lay,
-                     const void *d_table_layer, const mhip_scratch *sc, int A);
+                     const void *d_table_layer, const mhip_scratch *sc, int A, bool exact);
 
 }  // namespace mhip
 

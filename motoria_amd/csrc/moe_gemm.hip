@@ -464,6 +464,9 @@ __global__ __launch_bounds__(GT, 2) void k_gateup_mfma(
 // bucketed order, contiguous) with its block-major scales. Results go out
 // through LDS a wavefront's 64 columns at a time, so every assignment row is
 // written as 256 contiguous bytes.
+// EXACT: the reference's roundings of each block term (the expert outputs
+// bit-equal); otherwise one fused multiply-add per term (a few ulps).
+template <bool EXACT>
 __global__ __launch_bounds__(GT, 2) void k_down_mfma(const uint8_t *__restrict__ table,
                                                      mhip_layout lay,
                                                      const _Float16 *__restrict__ hq16,
@@ -502,7 +505,7 @@ __global__ __launch_bounds__(GT, 2) void k_down_mfma(const uint8_t *__restrict__
     for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = (f4v){0.0f, 0.0f, 0.0f, 0.0f};
-    gemm_tile_rows<false>(L.ring, src, eh / KB, nrows, acc);
+    gemm_tile_rows<EXACT>(L.ring, src, eh / KB, nrows, acc);
 
     const int c = lane >> 4, l16 = lane & 15;
 #pragma unroll
@@ -561,12 +564,17 @@ int launch_gateup_mfma(hipStream_t st, const mhip_dims *s, const mhip_layout *la
 }
 
 int launch_down_mfma(hipStream_t st, const mhip_dims *s, const mhip_layout *lay,
-                     const void *d_table_layer, const mhip_scratch *sc, int A) {
+                     const void *d_table_layer, const mhip_scratch *sc, int A, bool exact) {
     const int d = s->dim, eh = s->expert_hidden;
     const unsigned grid = gemm_grid(A, s->n_experts, d / TN);
-    k_down_mfma<<<grid, GT, 0, st>>>((const uint8_t *)d_table_layer, *lay,
-                                     (const _Float16 *)sc->hdq, sc->hs, sc->groups, sc->gtile,
-                                     sc->glight, sc->tmp, d, eh, A);
+    if (exact)
+        k_down_mfma<true><<<grid, GT, 0, st>>>((const uint8_t *)d_table_layer, *lay,
+                                               (const _Float16 *)sc->hdq, sc->hs, sc->groups,
+                                               sc->gtile, sc->glight, sc->tmp, d, eh, A);
+    else
+        k_down_mfma<false><<<grid, GT, 0, st>>>((const uint8_t *)d_table_layer, *lay,
+                                                (const _Float16 *)sc->hdq, sc->hs, sc->groups,
+                                                sc->gtile, sc->glight, sc->tmp, d, eh, A);
     return (int)hipGetLastError();
 }
 

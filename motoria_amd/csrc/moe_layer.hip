@@ -1734,7 +1734,7 @@ int mhip_moe_layer(mhip_ctx *c, const mhip_dims *s, const mhip_layout *lay,
         mhip::stage_end(c, slot);
         if (mhip::check(c, (hipError_t)e, "gateup_mfma launch")) return -1;
         slot = mhip::stage_begin(c, MHIP_STAGE_DOWN);
-        e = mhip::launch_down_mfma(st, s, lay, d_table_layer, sc, A);
+        e = mhip::launch_down_mfma(st, s, lay, d_table_layer, sc, A, !(flags & MHIP_FAST_DOWN));
         mhip::stage_end(c, slot);
         if (mhip::check(c, (hipError_t)e, "down_mfma launch")) return -1;
         dim3 cg(mhip::blocks_for(d, 1024), T);

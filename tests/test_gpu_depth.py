@@ -17,9 +17,8 @@ decode kernel's prefetch of the next layer's norm are all exercised.
   oracle, each on the previous layer's output, and the one-call 48-layer
   stack bit-equal to the oracle's stack.
 - prefill4096x48 (4096 tokens, the matrix-core kernels): each layer on the
-  GPU's own previous output; every token's logits, expert indices and gate
-  weights bit-equal to the oracle's at every layer, and the layer outputs of
-  all 4096 tokens within TOL at every layer.
+  GPU's own previous output; every token's logits, expert indices, gate
+  weights and layer output bit-equal to the oracle's at every layer.
 
 TOL: max|diff| / max|ref| <= 1e-3 (tools/e2e/e2e_test.go:101-107), on the
 update x_out - x_in and on x_out.
@@ -259,7 +258,6 @@ def test_prefill4096x48_every_token(oracle, qwen_dims, deep, prefill_chain, grou
     moe, norms, routers = deep
     d = qwen_dims
     xs, routing = prefill_chain
-    worst = 0.0
     for l in range(12 * group, 12 * group + 12):
         x = xs[l]
         ig, wg, lg = routing[l]
@@ -267,7 +265,5 @@ def test_prefill4096x48_every_token(oracle, qwen_dims, deep, prefill_chain, grou
         assert np.array_equal(bits(lg), bits(lo)), "layer %d logits" % l
         assert np.array_equal(ig, io), "layer %d expert indices" % l
         assert np.array_equal(bits(wg), bits(wo)), "layer %d gate weights" % l
-        e_up, e_out = rel(xs[l + 1] - x, xo - x), rel(xs[l + 1], xo)
-        worst = max(worst, e_up)
-        assert e_up <= TOL and e_out <= TOL, "layer %d: rel err %.2e / %.2e" % (l, e_up, e_out)
-    say("  4096 tokens x 12 layers: routing bit-equal, worst update rel err %.2e" % worst)
+        assert np.array_equal(bits(xs[l + 1]), bits(xo)), "layer %d output" % l
+    say("  4096 tokens x 12 layers: routing and outputs bit-equal")

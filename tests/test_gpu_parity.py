@@ -1,11 +1,12 @@
 """GPU parity: the HIP path (through the C ABI) against the CPU oracle.
 
 Integer and index results (expert indices, dispatch order, Q8 codes) must be
-bit-equal. On the bit-exact path (small batches, or MHIP_EXACT_EXPERTS) the
-fp32 results are required bit-equal too: the kernels keep the reference's
-rounding order, so any difference is a defect. On the matrix-core path
-(large batches) routing stays bit-equal and the layer output must be within
-the reference's e2e tolerance, max|diff| / max|ref| <= 1e-3
+bit-equal. The fp32 results are required bit-equal too, on the vector path
+(small batches, or MHIP_EXACT_EXPERTS) and on the matrix-core path (large
+batches): the kernels keep the reference's rounding order, so any difference
+is a defect. With MHIP_FAST_DOWN (the matrix-core down terms as fused
+multiply-adds, an option) routing stays bit-equal and the layer output must
+be within the reference's e2e tolerance, max|diff| / max|ref| <= 1e-3
 (tools/e2e/e2e_test.go:101-107), for both the update x_out - x_in and x_out.
 """
 import ctypes
@@ -213,8 +214,9 @@ def _gpu_layer(moe, layer, x, bias, flags):
 
 
 def _compare_layer(O, moe, d, layer, x, router, bias=None, label="", matrix=False):
-    """Bit-exact path against the oracle; with matrix=True also the default
-    (matrix-core) path of the same call, routing bit-equal, output within TOL."""
+    """Vector path against the oracle; with matrix=True also the default
+    (matrix-core) path of the same call (bit-equal) and the MHIP_FAST_DOWN
+    option (routing bit-equal, output within TOL)."""
     xg, idx, w, logits = _gpu_layer(moe, layer, x, bias, M.MHIP_EXACT_EXPERTS)
     xo, io, wo, lo, _ = oracle_layer(O, moe, d, layer, x, router, bias=bias,
                                     need=idx.ravel().tolist())
@@ -227,11 +229,17 @@ def _compare_layer(O, moe, d, layer, x, router, bias=None, label="", matrix=Fals
         n0 = M.lib().mhip_matrix_layers(moe.gpu)
         xm, im, wm, lm = _gpu_layer(moe, layer, x, bias, 0)
         assert M.lib().mhip_matrix_layers(moe.gpu) == n0 + 1, "%s: matrix path not taken" % label
-        e_delta, e_out = rel_err(xm - x, xo - x), rel_err(xm, xo)
-        say("  %s matrix-core path: rel err update %.3e, output %.3e" % (label, e_delta, e_out))
+        say("  %s matrix-core path: bit-equal" % label)
         assert np.array_equal(im, io), "%s: matrix path expert indices differ" % label
         assert_bits(lm, lo, label + " matrix path logits")
         assert_bits(wm, wo, label + " matrix path gate weights")
+        assert_bits(xm, xo, label + " matrix path layer output")
+        xf, i_f, wf, lf = _gpu_layer(moe, layer, x, bias, M.MHIP_FAST_DOWN)
+        assert M.lib().mhip_matrix_layers(moe.gpu) == n0 + 2, "%s: matrix path not taken" % label
+        e_delta, e_out = rel_err(xf - x, xo - x), rel_err(xf, xo)
+        say("  %s fused-down option: rel err update %.3e, output %.3e" % (label, e_delta, e_out))
+        assert np.array_equal(i_f, io), "%s: fused-down expert indices differ" % label
+        assert_bits(wf, wo, label + " fused-down gate weights")
         assert e_delta <= TOL and e_out <= TOL, label
     return idx
 
@@ -289,9 +297,9 @@ def test_layer_skewed_2048(oracle, qwen_dims, qwen_moe):
 
 def _every_token(oracle, d, T, seed, bias=None):
     """One matrix-core layer at T tokens on a fresh one-layer handle with a
-    non-unit ffn_norm: every token's logits, expert indices and gate weights
-    bit-equal to the oracle's, and the layer output of every token within
-    TOL (the oracle's expert-bucketed layer, same bits as its per-token one)."""
+    non-unit ffn_norm: every token's logits, expert indices, gate weights and
+    layer output bit-equal to the oracle's (its expert-bucketed layer, same
+    bits as its per-token one)."""
     moe = M.Moe(n_layers=1, max_tokens=T, device=0, **W.SHAPE)
     try:
         moe.synth(W.WEIGHT_SEED)
@@ -309,9 +317,8 @@ def _every_token(oracle, d, T, seed, bias=None):
         assert_bits(lm, lo, "logits")
         assert np.array_equal(im, io), "expert indices"
         assert_bits(wm, wo, "gate weights")
-        e_delta, e_out = rel_err(xm - x, xo - x), rel_err(xm, xo)
-        say("  all %d tokens: rel err update %.3e, output %.3e" % (T, e_delta, e_out))
-        assert e_delta <= TOL and e_out <= TOL
+        assert_bits(xm, xo, "layer output")
+        say("  all %d tokens bit-equal" % T)
     finally:
         moe.close()
 
@@ -357,9 +364,7 @@ def test_matrix_path_ragged_buckets(oracle, qwen_dims, qwen_moe):
                                     need=im.ravel().tolist())
     assert np.array_equal(im, io)
     assert_bits(wm, wo, "gate weights")
-    e_delta, e_out = rel_err(xm - x, xo - x), rel_err(xm, xo)
-    say("  rel err update %.3e, output %.3e" % (e_delta, e_out))
-    assert e_delta <= TOL and e_out <= TOL
+    assert_bits(xm, xo, "layer output")
 
 
 def test_dispatch_matches_oracle(oracle, qwen_dims, qwen_moe):
