@@ -52,11 +52,11 @@ int mia_gpu_model_feed(mia_gpu_model *m, int token, int pos);
 
 /* n feeds in one call (no counterpart in the reference, whose serve loop
  * feeds a prompt one token at a time): tokens[0..n) at positions
- * pos .. pos + n - 1, in batches of equal size (at most 255 tokens, and
- * fewer than MHIP_GEMM_MIN_A / n_active) through each layer at once (the
- * attention of the batch with mhip_attention_batch, its MoE on the bit-exact
- * per-stage kernels), so the weights are read once per batch instead of once
- * per token. The KV rows written are bit-equal to n calls of
+ * pos .. pos + n - 1, in batches of equal size (at most 1024 tokens)
+ * through each layer at once (the attention of the batch with
+ * mhip_attention_batch, its MoE on the per-stage kernels for T tokens, the
+ * matrix-core ones from MHIP_GEMM_MIN_A assignments on), so the weights are
+ * read once per batch instead of once per token. The KV rows written are bit-equal to n calls of
  * mia_gpu_model_feed; no logits are formed. 0 or -1. */
 int mia_gpu_model_prefill(mia_gpu_model *m, const int *tokens, int n, int pos);
 

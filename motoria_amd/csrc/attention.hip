@@ -788,6 +788,10 @@ int mhip_attention(mhip_ctx *c, const mhip_attn_dims *s, const float *d_attn_nor
     return mhip::check_launch(c, "attention");
 }
 
+// Tokens per pass of the scores kept in device memory (contexts too long for
+// LDS, other head shapes): the scratch holds this many tokens' scores.
+constexpr int AB_SUB = 64;
+
 size_t mhip_attention_batch_scratch_bytes(const mhip_attn_dims *s, int n, int max_seq) {
     if (!s || n <= 0 || max_seq <= 0) return 0;
     const size_t d = s->dim, qd = (size_t)s->n_heads * s->head_dim,
@@ -795,7 +799,8 @@ size_t mhip_attention_batch_scratch_bytes(const mhip_attn_dims *s, int n, int ma
     return align256(N * d * 4) + align256(N * d) + align256(N * (d / QK) * 4) +
            align256(N * qd * 4) + 2 * align256(N * kvd * 4) + align256(N * qd * 4) +
            align256(N * qd) + align256(N * (qd / QK) * 4) +
-           align256(N * s->n_heads * (size_t)((max_seq + 3) & ~3) * 4) + align256(16);
+           align256((size_t)(n < AB_SUB ? n : AB_SUB) * s->n_heads * (size_t)((max_seq + 3) & ~3) * 4) +
+           align256(16);
 }
 
 int mhip_attention_batch(mhip_ctx *c, const mhip_attn_dims *s, const float *d_attn_norm,
@@ -828,7 +833,7 @@ int mhip_attention_batch(mhip_ctx *c, const mhip_attn_dims *s, const float *d_at
     int8_t *attq = (int8_t *)take(N * qd);
     float *atts = (float *)take(N * (qd / QK) * 4);
     const int sld = (max_seq + 3) & ~3;  // row stride of the scores
-    float *scores = (float *)take(N * nh * (size_t)sld * 4);
+    float *scores = (float *)take((size_t)(n < AB_SUB ? n : AB_SUB) * nh * (size_t)sld * 4);
     int *status = (int *)take(16);
     hipStream_t st = c->stream;
     static int lds_set[64];  // per device ordinal
@@ -863,13 +868,21 @@ int mhip_attention_batch(mhip_ctx *c, const mhip_attn_dims *s, const float *d_at
             k_attn_group_b<true><<<dim3(nkv, n), 256, ag_lds(group, sl, true), st>>>(
                 q, d_kc, d_vc, pos, nh, group, kvd, scale, nullptr, sl, att);
         else
-            k_attn_group_b<false><<<dim3(nkv, n), 256, ag_lds(group, sld, false), st>>>(
-                q, d_kc, d_vc, pos, nh, group, kvd, scale, scores, sld, att);
+            for (int t0 = 0; t0 < n; t0 += AB_SUB) {
+                const int ns = n - t0 < AB_SUB ? n - t0 : AB_SUB;
+                k_attn_group_b<false><<<dim3(nkv, ns), 256, ag_lds(group, sld, false), st>>>(
+                    q + (size_t)t0 * qd, d_kc, d_vc, pos + t0, nh, group, kvd, scale, scores, sld,
+                    att + (size_t)t0 * qd);
+            }
     } else {
-        k_attn_scores_b<<<dim3(mhip::blocks_for((size_t)nh * (pos + n), 256), n), 256, 0, st>>>(
-            q, d_kc, pos, nh, group, hd, kvd, scale, scores, sld);
-        k_attn_mix_b<<<dim3(nh, n), 256, 0, st>>>(scores, sld, pos, nh, d_vc, group, hd, kvd,
-                                                  att);
+        for (int t0 = 0; t0 < n; t0 += AB_SUB) {
+            const int ns = n - t0 < AB_SUB ? n - t0 : AB_SUB;
+            k_attn_scores_b<<<dim3(mhip::blocks_for((size_t)nh * (pos + t0 + ns), 256), ns), 256, 0,
+                              st>>>(q + (size_t)t0 * qd, d_kc, pos + t0, nh, group, hd, kvd, scale,
+                                    scores, sld);
+            k_attn_mix_b<<<dim3(nh, ns), 256, 0, st>>>(scores, sld, pos + t0, nh, d_vc, group, hd,
+                                                       kvd, att + (size_t)t0 * qd);
+        }
     }
     if (mhip::check_launch(c, "attention batch scores")) return -1;
     k_quant_rows<<<mhip::blocks_for(N * qd / QK, 256), 256, 0, st>>>(att, (int)(N * qd / QK),

@@ -59,15 +59,10 @@ struct mia_gpu_model {
     char err[512];
 };
 
-/* Prompt tokens per batch of mia_gpu_model_prefill, at most: a batch also
- * keeps T x n_active below MHIP_GEMM_MIN_A, so its MoE stays on the
- * bit-exact per-stage kernels (255 tokens at n_active 8). */
-enum { PREFILL_MAX = 256 };
-
-static int prefill_batch_max(const mia_file_info *h) {
-    const int k = (MHIP_GEMM_MIN_A - 1) / (int)h->n_active;
-    return k < PREFILL_MAX ? k : PREFILL_MAX;
-}
+/* Prompt tokens per batch of mia_gpu_model_prefill, at most (every MoE
+ * path is bit-exact, so a batch of any size gives the feeds' bits; from
+ * MHIP_GEMM_MIN_A assignments on its experts run on the matrix cores). */
+enum { PREFILL_MAX = 1024 };
 
 static int mfail(mia_gpu_model *m, const char *fmt, ...) {
     va_list ap;
@@ -515,7 +510,7 @@ int mia_gpu_model_feed(mia_gpu_model *m, int token, int pos) {
 }
 
 /* n prompt tokens at positions pos .. pos + n - 1 in batches of equal size
- * (up to prefill_batch_max): each layer's attention for the batch
+ * (up to PREFILL_MAX): each layer's attention for the batch
  * (mhip_attention_batch) and its MoE for the batch (the per-stage kernels
  * for T tokens), the KV rows written as n feeds write them
  * (forward.c:205-213 per token, bit-equal). */
@@ -530,7 +525,7 @@ int mia_gpu_model_prefill(mia_gpu_model *m, const int *tokens, int n, int pos) {
             return mfail(m, "token %d outside [0, %u)", tokens[i], h->vocab);
     const int L = (int)h->n_layers, d = (int)h->dim;
     const size_t kvd = (size_t)h->n_kv_heads * h->head_dim, row = (size_t)(d / MIA_QK) * 36;
-    const int bmax = prefill_batch_max(h);
+    const int bmax = PREFILL_MAX;
     if (n == 0) return 0;
     if (!m->d_xb) {
         m->d_xb = mhip_malloc(m->gpu, (size_t)bmax * d * 4);

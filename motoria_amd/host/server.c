@@ -46,7 +46,7 @@
 #include "mia/model_gpu.h"
 #include "mia/serve.h"
 
-enum { MESSAGE_MAX = 1 << 20, PREFILL_CHUNK = 255 };
+enum { MESSAGE_MAX = 1 << 20, PREFILL_CHUNK = 1024 };
 
 static volatile sig_atomic_t g_stop_turn;
 static void on_cancel_signal(int sig) {

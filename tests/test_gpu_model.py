@@ -315,15 +315,16 @@ def test_model_prefill_equals_feeds_golden(oracle, tmp_path, name):
         m.close()
 
 
-def test_model_full_shape_prefill_equals_feeds():
-    """48 layers at the Qwen3-30B-A3B shape: a 300-token prompt (two batches
-    of 150: three 64-token row chunks and a partial one each) through
-    mia_gpu_model_prefill, then steps, gives the logits bits of 300 feeds and
-    the same steps."""
-    say("test_model_full_shape_prefill_equals_feeds")
-    n = 300
-    a = M.GpuModel(None, 512, synth=(QWEN_FULL, 9))
-    b = M.GpuModel(None, 512, synth=(QWEN_FULL, 9))
+@pytest.mark.parametrize("n", [70, 300, 1100])
+def test_model_full_shape_prefill_equals_feeds(n):
+    """48 layers at the Qwen3-30B-A3B shape: an n-token prompt through
+    mia_gpu_model_prefill, then steps, gives the logits bits of n feeds and
+    the same steps. 70 tokens: one batch, its MoE on the vector kernels (560
+    assignments); 300: one batch on the matrix-core kernels (2400); 1100: two
+    batches of 550, each nine 64-token row chunks (the last partial)."""
+    say("test_model_full_shape_prefill_equals_feeds n=%d" % n)
+    a = M.GpuModel(None, 1200, synth=(QWEN_FULL, 9))
+    b = M.GpuModel(None, 1200, synth=(QWEN_FULL, 9))
     try:
         toks = np.random.default_rng(13).integers(0, QWEN_FULL["vocab"], n + 3).tolist()
         a.prefill(toks[:n], 0)
@@ -333,7 +334,7 @@ def test_model_full_shape_prefill_equals_feeds():
             la, lb = a.step(toks[p], p), b.step(toks[p], p)
             assert np.all(np.isfinite(la))
             assert np.array_equal(bits(la), bits(lb)), "position %d" % p
-        say("  300-token prefill + 3 steps == 300 feeds + 3 steps (bits)")
+        say("  %d-token prefill + 3 steps == %d feeds + 3 steps (bits)" % (n, n))
     finally:
         a.close()
         b.close()
@@ -341,24 +342,25 @@ def test_model_full_shape_prefill_equals_feeds():
 
 def test_model_full_shape_prefill_far_positions():
     """A prompt batch whose context is too long for its scores in LDS (the
-    scores in device memory), at positions 4300 .. 4309, against feeds; the
-    positions before are left empty (zero cache rows) on both handles."""
+    scores in device memory, 64 tokens per pass: 70 tokens at positions
+    4300 .. 4369), against feeds; the positions before are left empty (zero
+    cache rows) on both handles."""
     say("test_model_full_shape_prefill_far_positions")
     a = M.GpuModel(None, 4400, synth=(QWEN_FULL, 10))
     b = M.GpuModel(None, 4400, synth=(QWEN_FULL, 10))
     try:
-        toks = np.random.default_rng(14).integers(0, QWEN_FULL["vocab"], 12).tolist()
+        toks = np.random.default_rng(14).integers(0, QWEN_FULL["vocab"], 75).tolist()
         a.prefill(toks[:3], 0)
-        a.prefill(toks[3:10], 4300)
+        a.prefill(toks[3:73], 4300)
         for p in range(3):
             b.feed(toks[p], p)
-        for p in range(7):
+        for p in range(70):
             b.feed(toks[3 + p], 4300 + p)
-        for p, tok in ((4307, toks[10]), (4308, toks[11])):
+        for p, tok in ((4370, toks[73]), (4371, toks[74])):
             la, lb = a.step(tok, p), b.step(tok, p)
             assert np.all(np.isfinite(la))
             assert np.array_equal(bits(la), bits(lb)), "position %d" % p
-        say("  prefill at 4300 .. 4306 + 2 steps == feeds + 2 steps (bits)")
+        say("  prefill at 4300 .. 4369 + 2 steps == feeds + 2 steps (bits)")
     finally:
         a.close()
         b.close()
