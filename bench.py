@@ -464,6 +464,32 @@ def model_decode(steps, warmup):
     return out
 
 
+def model_prefill(n=1024, n_feeds=64):
+    """Tokens/s of a prompt through mia_gpu_model_prefill (the prompt's
+    tokens in one batch through every layer, no output head; KV rows
+    bit-equal to per-token feeds) at the full Qwen3-30B-A3B shape, against
+    n_feeds per-token feeds (mia_gpu_model_feed) on the same handle; the
+    second of two prefills of the same prompt is timed."""
+    m = M.GpuModel(None, n + 1, synth=(QWEN_MODEL, 5))
+    toks = np.random.default_rng(7).integers(0, QWEN_MODEL["vocab"], n).tolist()
+    m.prefill(toks, 0)
+    t0 = time.perf_counter()
+    m.prefill(toks, 0)
+    dt = time.perf_counter() - t0
+    t1 = time.perf_counter()
+    for p in range(n_feeds):
+        m.feed(toks[p], p)
+    df = time.perf_counter() - t1
+    m.close()
+    log("model prefill: %d tokens in %.1f ms (%.0f tokens/s); feeds %.0f tokens/s"
+        % (n, dt * 1e3, n / dt, n_feeds / df))
+    return {"tokens": n, "ms": dt * 1e3, "tokens_per_s": n / dt,
+            "feeds_tokens_per_s": n_feeds / df,
+            "workload": "a %d-token prompt at positions 0..%d through mia_gpu_model_prefill "
+                        "(host clock around the call); feeds: %d tokens through "
+                        "mia_gpu_model_feed" % (n, n - 1, n_feeds)}
+
+
 def sampler_timing(draws=50):
     """Microseconds per mhip_sample over vocabulary-sized logits (N(0, 3)):
     greedy, and temperature/top-p draws (the two fp32 running sums of the
@@ -547,7 +573,7 @@ def main():
         return
     if args.only_model:
         print(json.dumps({"model_decode": model_decode(args.steps, args.warmup),
-                          "sampler": sampler_timing()}))
+                          "sampler": sampler_timing(), "prefill": model_prefill()}))
         return
 
     res, moe = measure(args.workload, args.steps, args.warmup, args.multi_kernel,
@@ -607,6 +633,7 @@ def main():
     if args.workload == "decode48" and not args.no_model:
         model = model_decode(32, 4)
         model["sampler"] = sampler_timing()
+        model["prefill"] = model_prefill()
 
     out = {
         "metric": METRIC,

@@ -310,7 +310,18 @@ int mhip_attention_batch(mhip_ctx *c, const mhip_attn_dims *s, const float *d_at
                          const void *d_wq, const void *d_wk, const void *d_wv, const void *d_wo,
                          const float *d_q_norm, const float *d_k_norm, const double *d_rope,
                          float *d_kc, float *d_vc, int pos, int n, int max_seq, float *d_x,
-                         void *d_scratch, int flags);
+                         const void *d_pack, void *d_scratch, int flags);
+/* The layer's Q, K, V and O weights repacked for mhip_attention_batch's
+ * matrix-core rows (no counterpart in the reference): codes as fp16
+ * integers, scales block-major; d_pack holds mhip_attention_pack_bytes(s)
+ * bytes (0 for shapes whose rows are not multiples of 64, which keep the
+ * vector kernels). With d_pack given, batches of 512
+ * tokens or more form their Q/K/V and O rows on the matrix cores, with the
+ * same bits (exact block dots, block terms in block order); NULL keeps the
+ * vector kernels. */
+size_t mhip_attention_pack_bytes(const mhip_attn_dims *s);
+int mhip_attention_pack(mhip_ctx *c, const mhip_attn_dims *s, const void *d_wq, const void *d_wk,
+                        const void *d_wv, const void *d_wo, void *d_pack);
 /* logits[vocab] = output Q8(rmsnorm(x, output_norm)) (forward.c:214-215);
  * d_scratch as for mhip_attention. */
 int mhip_output_head(mhip_ctx *c, const mhip_attn_dims *s, const float *d_output_norm,

@@ -152,7 +152,9 @@ SIGNATURES = {
                             _p, _i, _i, _p, _p, _p, _i]),
     "mhip_attention_batch_scratch_bytes": (_sz, [ctypes.POINTER(AttnDims), _i, _i]),
     "mhip_attention_batch": (_i, [_p, ctypes.POINTER(AttnDims), _p, _p, _p, _p, _p, _p, _p, _p,
-                                  _p, _p, _i, _i, _i, _p, _p, _i]),
+                                  _p, _p, _i, _i, _i, _p, _p, _p, _i]),
+    "mhip_attention_pack_bytes": (_sz, [ctypes.POINTER(AttnDims)]),
+    "mhip_attention_pack": (_i, [_p, ctypes.POINTER(AttnDims), _p, _p, _p, _p, _p]),
     "mhip_output_head": (_i, [_p, ctypes.POINTER(AttnDims), _p, _p, _i, _p, _p, _p, _i]),
     "mhip_attention_layer_ws_bytes": (_sz, []),
     "mhip_attention_layer_trace": (_i, [_p, _p, _p]),

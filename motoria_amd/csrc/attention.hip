@@ -425,6 +425,136 @@ __global__ __launch_bounds__(64 * RT_W) void k_rows_q8_t(RowSegs sg, int nb, int
     }
 }
 
+// ---- the batch's weight rows on the matrix cores --------------------------------------
+//
+// For a batch the rows are products of the row tile's weight codes with the
+// tokens' codes: v_mfma_f32_16x16x32_f16 over one 32-code block multiplies
+// Q8 codes held as fp16 integers and gives the exact int32 block dot (32
+// products below 2^14 each, every partial sum an integer below 2^24), so
+// the block term ((float)dot * d_w) * d_x and the sum in block order are the
+// reference's (matmul.c:19-28). The weights are repacked once for this:
+// codes as fp16 [R][nb*32], scales block-major [nb][R]; the tokens' codes
+// are converted to fp16 [n][nb*32] per batch.
+typedef _Float16 rh8 __attribute__((ext_vector_type(8)));
+typedef float rf4 __attribute__((ext_vector_type(4)));
+#ifndef RM_J
+#define RM_J 2  // 16-token tiles per wavefront
+#endif
+constexpr int RM_R = 64, RM_T = 64 * RM_J;  // weight rows and tokens of a workgroup
+constexpr int RM_MIN_N = 512;                // batches from which the rows run here
+
+// Row r of a .mia Q8_0 matrix (36-byte blocks) into the packed form, one
+// thread per block.
+__global__ __launch_bounds__(256) void k_pack_rows_h(const uint8_t *__restrict__ w, int R, int nb,
+                                                     _Float16 *__restrict__ qh,
+                                                     float *__restrict__ sc) {
+    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= (size_t)R * nb) return;
+    const int r = (int)(q / nb), b = (int)(q % nb);
+    const uint8_t *blk = w + q * 36;
+    sc[(size_t)b * R + r] = *(const float *)blk;
+    const int8_t *c = (const int8_t *)(blk + 4);
+    _Float16 *o = qh + q * QK;
+#pragma unroll
+    for (int i = 0; i < QK; i++) o[i] = (_Float16)c[i];
+}
+
+// Q8 codes as fp16 integers (exact).
+__global__ __launch_bounds__(256) void k_codes_h(const int8_t *__restrict__ q, size_t n,
+                                                 _Float16 *__restrict__ o) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) o[i] = (_Float16)q[i];
+}
+
+struct RowPack {
+    const _Float16 *q[3];  // packed codes of segment k
+    const float *s[3];     // its block-major scales
+    float *out[3];
+    int r0[4];             // rows of segment k: [r0[k], r0[k+1]), multiples of RM_R
+};
+
+// out[k][t * ld_k + r] = (resid ? resid[t * ld_r + r] : 0) + the Q8 dot of
+// packed row r of segment k with token t (codes xh[t][nb*32], scales
+// xs[t][nb]), for RM_R rows x RM_T tokens per workgroup: wavefront w takes
+// tokens 16 RM_J w .. + 16 RM_J - 1 (RM_J 16-token tiles) against the 64
+// rows (four 16-row tiles); lane l's results are rows 16 i + 4 (l / 16) + 0..3 of
+// token 16 j + l % 16. The operands of block b + 1 are loaded while block
+// b's products and terms are formed.
+__global__ __launch_bounds__(256) void k_rows_mfma(RowPack sg, int nb, int n,
+                                                   const _Float16 *__restrict__ xh,
+                                                   const float *__restrict__ xs,
+                                                   const float *resid, int ld_r) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, c = lane >> 4;
+    const int row0 = blockIdx.x * RM_R;
+    const int k = row0 >= sg.r0[1] ? (row0 >= sg.r0[2] ? 2 : 1) : 0;
+    const int rl0 = row0 - sg.r0[k], R = sg.r0[k + 1] - sg.r0[k];
+    const _Float16 *wq = sg.q[k];
+    const float *ws = sg.s[k];
+    const int t0 = blockIdx.y * RM_T + 16 * RM_J * wave;
+    int tj[RM_J];
+#pragma unroll
+    for (int j = 0; j < RM_J; j++) tj[j] = min(t0 + 16 * j + l16, n - 1);
+    rf4 acc[4][RM_J];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < RM_J; j++) acc[i][j] = (rf4){0.0f, 0.0f, 0.0f, 0.0f};
+    struct Ops {
+        rh8 a[4], x[RM_J];
+        rf4 dw[4];
+        float dx[RM_J];
+    };
+    auto load = [&](int b, Ops &o) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            o.a[i] = *(const rh8 *)(wq + ((size_t)(rl0 + 16 * i + l16) * nb + b) * QK + 8 * c);
+#pragma unroll
+        for (int j = 0; j < RM_J; j++)
+            o.x[j] = *(const rh8 *)(xh + ((size_t)tj[j] * nb + b) * QK + 8 * c);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            o.dw[i] = *(const rf4 *)(ws + (size_t)b * R + rl0 + 16 * i + 4 * c);
+#pragma unroll
+        for (int j = 0; j < RM_J; j++) o.dx[j] = xs[(size_t)tj[j] * nb + b];
+    };
+    auto step = [&](const Ops &o) {
+        const rf4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < RM_J; j++) {
+                const rf4 blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.a[i], o.x[j], z, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float t = blk[r] * o.dw[i][r];
+                    acc[i][j][r] = acc[i][j][r] + t * o.dx[j];  // (no contraction)
+                }
+            }
+    };
+    Ops o0, o1;
+    load(0, o0);
+    for (int b = 0; b < nb; b += 2) {
+        if (b + 1 < nb) load(b + 1, o1);
+        step(o0);
+        if (b + 2 < nb) load(b + 2, o0);
+        if (b + 1 < nb) step(o1);
+    }
+#pragma unroll
+    for (int j = 0; j < RM_J; j++) {
+        const int t = t0 + 16 * j + l16;
+        if (t < n) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int row = rl0 + 16 * i + 4 * c + r;
+                    const float v = acc[i][j][r];
+                    sg.out[k][(size_t)t * R + row] = resid ? resid[(size_t)t * ld_r + row] + v : v;
+                }
+        }
+    }
+}
+
 // k_qk_rope for token blockIdx.y at position pos + blockIdx.y: its q (in
 // place), k and v rows at [t][qd], [t][kvd]; the cache rows at pos + t.
 __global__ __launch_bounds__(256) void k_qk_rope_b(float *__restrict__ q,
@@ -798,16 +928,102 @@ size_t mhip_attention_batch_scratch_bytes(const mhip_attn_dims *s, int n, int ma
                  kvd = (size_t)s->n_kv_heads * s->head_dim, N = (size_t)n;
     return align256(N * d * 4) + align256(N * d) + align256(N * (d / QK) * 4) +
            align256(N * qd * 4) + 2 * align256(N * kvd * 4) + align256(N * qd * 4) +
-           align256(N * qd) + align256(N * (qd / QK) * 4) +
+           align256(N * qd) + align256(N * (qd / QK) * 4) + align256(N * d * 2) +
+           align256(N * qd * 2) +
            align256((size_t)(n < AB_SUB ? n : AB_SUB) * s->n_heads * (size_t)((max_seq + 3) & ~3) * 4) +
            align256(16);
 }
+
+}  // extern "C"
+
+namespace {
+
+// The packed weights of one layer (mhip_attention_pack): fp16 codes of Q, K,
+// V and O, then their block-major scales, each 256-byte aligned.
+struct AttnPack {
+    _Float16 *q[4];
+    float *s[4];
+};
+AttnPack pack_carve(const mhip_attn_dims *s, void *base) {
+    const size_t d = s->dim, qd = (size_t)s->n_heads * s->head_dim,
+                 kvd = (size_t)s->n_kv_heads * s->head_dim;
+    const size_t rows[4] = {qd, kvd, kvd, d}, cols[4] = {d, d, d, qd};
+    AttnPack a;
+    uint8_t *p = (uint8_t *)base;
+    for (int m = 0; m < 4; m++) {
+        a.q[m] = (_Float16 *)p;
+        p += align256(rows[m] * cols[m] * 2);
+    }
+    for (int m = 0; m < 4; m++) {
+        a.s[m] = (float *)p;
+        p += align256(rows[m] * (cols[m] / QK) * 4);
+    }
+    return a;
+}
+bool pack_fits(const mhip_attn_dims *s) {
+    const int qd = s->n_heads * s->head_dim, kvd = s->n_kv_heads * s->head_dim;
+    return qd % RM_R == 0 && kvd % RM_R == 0 && s->dim % RM_R == 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mhip_attention_pack_bytes(const mhip_attn_dims *s) {
+    if (!s || s->dim <= 0 || s->n_heads <= 0 || s->n_kv_heads <= 0 || s->head_dim <= 0 ||
+        !pack_fits(s))
+        return 0;
+    const size_t d = s->dim, qd = (size_t)s->n_heads * s->head_dim,
+                 kvd = (size_t)s->n_kv_heads * s->head_dim;
+    const size_t rows[4] = {qd, kvd, kvd, d}, cols[4] = {d, d, d, qd};
+    size_t n = 0;
+    for (int m = 0; m < 4; m++) n += align256(rows[m] * cols[m] * 2) + align256(rows[m] * (cols[m] / QK) * 4);
+    return n;
+}
+
+int mhip_attention_pack(mhip_ctx *c, const mhip_attn_dims *s, const void *d_wq, const void *d_wk,
+                        const void *d_wv, const void *d_wo, void *d_pack) {
+    if (check_attn(c, s, 1)) return -1;
+    if (!pack_fits(s))
+        return mhip::fail(c, "attention pack: rows not multiples of %d", RM_R);
+    if (mhip::use_device(c)) return -1;
+    const int d = s->dim, qd = s->n_heads * s->head_dim, kvd = s->n_kv_heads * s->head_dim;
+    const AttnPack a = pack_carve(s, d_pack);
+    const void *w[4] = {d_wq, d_wk, d_wv, d_wo};
+    const int rows[4] = {qd, kvd, kvd, d}, nbs[4] = {d / QK, d / QK, d / QK, qd / QK};
+    for (int m = 0; m < 4; m++)
+        k_pack_rows_h<<<mhip::blocks_for((size_t)rows[m] * nbs[m], 256), 256, 0, c->stream>>>(
+            (const uint8_t *)w[m], rows[m], nbs[m], a.q[m], a.s[m]);
+    return mhip::check_launch(c, "attention pack");
+}
+
+}  // extern "C"
+
+namespace {
+
+void rows_mfma(hipStream_t st, const AttnPack &a, int m0, int nseg, float *const *out,
+               const int *r0, int nb, int n, const _Float16 *xh, const float *xs, const float *resid,
+               int ld_r) {
+    RowPack g = {{nullptr, nullptr, nullptr}, {nullptr, nullptr, nullptr}, {nullptr, nullptr, nullptr},
+                 {r0[0], r0[1], r0[2], r0[3]}};
+    for (int k = 0; k < nseg; k++) {
+        g.q[k] = a.q[m0 + k];
+        g.s[k] = a.s[m0 + k];
+        g.out[k] = out[k];
+    }
+    k_rows_mfma<<<dim3((unsigned)(r0[3] / RM_R), (unsigned)((n + RM_T - 1) / RM_T)), 256, 0, st>>>(
+        g, nb, n, xh, xs, resid, ld_r);
+}
+
+}  // namespace
+
+extern "C" {
 
 int mhip_attention_batch(mhip_ctx *c, const mhip_attn_dims *s, const float *d_attn_norm,
                          const void *d_wq, const void *d_wk, const void *d_wv, const void *d_wo,
                          const float *d_q_norm, const float *d_k_norm, const double *d_rope,
                          float *d_kc, float *d_vc, int pos, int n, int max_seq, float *d_x,
-                         void *d_scratch, int flags) {
+                         const void *d_pack, void *d_scratch, int flags) {
     if (check_attn(c, s, max_seq)) return -1;
     if (n <= 0 || pos < 0 || pos + n > max_seq)
         return mhip::fail(c, "attention batch: positions %d .. %d outside [0, max_seq=%d)", pos,
@@ -832,6 +1048,8 @@ int mhip_attention_batch(mhip_ctx *c, const mhip_attn_dims *s, const float *d_at
     float *att = (float *)take(N * qd * 4);
     int8_t *attq = (int8_t *)take(N * qd);
     float *atts = (float *)take(N * (qd / QK) * 4);
+    _Float16 *xh = (_Float16 *)take(N * d * 2);
+    _Float16 *atth = (_Float16 *)take(N * qd * 2);
     const int sld = (max_seq + 3) & ~3;  // row stride of the scores
     float *scores = (float *)take((size_t)(n < AB_SUB ? n : AB_SUB) * nh * (size_t)sld * 4);
     int *status = (int *)take(16);
@@ -854,8 +1072,19 @@ int mhip_attention_batch(mhip_ctx *c, const mhip_attn_dims *s, const float *d_at
     RowSegs qkv = {{(const uint8_t *)d_wq, (const uint8_t *)d_wk, (const uint8_t *)d_wv},
                    {q, k, v},
                    {0, qd, qd + kvd, qd + 2 * kvd}};
-    k_rows_q8_t<2><<<dim3(mhip::blocks_for(qd + 2 * kvd, 2 * RT_W), mhip::blocks_for(N, 64)),
-                     64 * RT_W, 0, st>>>(qkv, nb, n, xq, xs, nullptr, 0);
+    // the matrix cores from 512 tokens on, when the layer's weights are packed
+    // (below that the vector rows measured as fast or faster)
+    const bool mm = d_pack && pack_fits(s) && n >= RM_MIN_N;
+    const AttnPack pk = mm ? pack_carve(s, (void *)d_pack) : AttnPack{};
+    if (mm) {
+        k_codes_h<<<mhip::blocks_for(N * d, 256), 256, 0, st>>>(xq, N * d, xh);
+        float *outs[3] = {q, k, v};
+        const int r0[4] = {0, qd, qd + kvd, qd + 2 * kvd};
+        rows_mfma(st, pk, 0, 3, outs, r0, nb, n, xh, xs, nullptr, 0);
+    } else {
+        k_rows_q8_t<2><<<dim3(mhip::blocks_for(qd + 2 * kvd, 2 * RT_W), mhip::blocks_for(N, 64)),
+                         64 * RT_W, 0, st>>>(qkv, nb, n, xq, xs, nullptr, 0);
+    }
     if (mhip::check_launch(c, "attention batch qkv")) return -1;
     k_qk_rope_b<<<dim3(mhip::blocks_for(nh + 2 * nkv, 4), n), 256, 0, st>>>(
         q, k, v, d_q_norm, d_k_norm, d_rope, pos, nh, nkv, hd, s->norm_eps, d_kc, d_vc);
@@ -887,8 +1116,15 @@ int mhip_attention_batch(mhip_ctx *c, const mhip_attn_dims *s, const float *d_at
     if (mhip::check_launch(c, "attention batch scores")) return -1;
     k_quant_rows<<<mhip::blocks_for(N * qd / QK, 256), 256, 0, st>>>(att, (int)(N * qd / QK),
                                                                       attq, atts);
-    k_rows_q8_t<1><<<dim3(mhip::blocks_for(d, RT_W), mhip::blocks_for(N, 64)), 64 * RT_W, 0,
-                     st>>>(one_seg(d_wo, d_x, d), qd / QK, n, attq, atts, d_x, d);
+    if (mm) {
+        k_codes_h<<<mhip::blocks_for(N * qd, 256), 256, 0, st>>>(attq, N * qd, atth);
+        float *outs[1] = {d_x};
+        const int r0[4] = {0, d, d, d};
+        rows_mfma(st, pk, 3, 1, outs, r0, qd / QK, n, atth, atts, d_x, d);
+    } else {
+        k_rows_q8_t<1><<<dim3(mhip::blocks_for(d, RT_W), mhip::blocks_for(N, 64)), 64 * RT_W, 0,
+                         st>>>(one_seg(d_wo, d_x, d), qd / QK, n, attq, atts, d_x, d);
+    }
     return mhip::check_launch(c, "attention batch");
 }
 

@@ -56,6 +56,8 @@ struct mia_gpu_model {
     int *h_status;           /* pinned [L][4] */
     float *d_xb;             /* [PREFILL_MAX][dim] the residuals of a prompt batch */
     void *d_bscratch;        /* mhip_attention_batch scratch for PREFILL_MAX tokens */
+    unsigned char *d_apack;  /* [L] each layer's attention weights packed for batches */
+    size_t apack_bytes;      /* per layer (0: not packed, the vector rows run) */
     char err[512];
 };
 
@@ -96,6 +98,7 @@ void mia_gpu_model_close(mia_gpu_model *m) {
         mhip_free(m->gpu, m->d_xsave);
         mhip_free(m->gpu, m->d_xb);
         mhip_free(m->gpu, m->d_bscratch);
+        mhip_free(m->gpu, m->d_apack);
         mhip_free(m->gpu, m->d_xin);
         mhip_free(m->gpu, m->d_aws);
         mhip_free(m->gpu, m->d_al);
@@ -532,6 +535,23 @@ int mia_gpu_model_prefill(mia_gpu_model *m, const int *tokens, int n, int pos) {
         m->d_bscratch =
             mhip_malloc(m->gpu, mhip_attention_batch_scratch_bytes(&m->ad, bmax, m->max_seq));
         if (!m->d_xb || !m->d_bscratch) return mfail(m, "device memory: %s", mhip_error(m->gpu));
+        /* the attention weights packed once for the matrix-core rows; a
+         * shape they do not fit keeps the vector rows */
+        const size_t pb = mhip_attention_pack_bytes(&m->ad);
+        m->d_apack = pb ? mhip_malloc(m->gpu, pb * (size_t)L) : NULL;
+        if (m->d_apack) {
+            for (int l = 0; l < L; l++) {
+                const mia_layer_offsets *o = &m->lo[l];
+                const unsigned char *b = m->d_dense;
+                if (mhip_attention_pack(m->gpu, &m->ad, b + o->wq, b + o->wk, b + o->wv, b + o->wo,
+                                        m->d_apack + (size_t)l * pb)) {
+                    mhip_free(m->gpu, m->d_apack);
+                    m->d_apack = NULL;
+                    break;
+                }
+            }
+        }
+        m->apack_bytes = m->d_apack ? pb : 0;
     }
     const int nbat = (n + bmax - 1) / bmax, bsz = (n + nbat - 1) / nbat;
     for (int b0 = 0; b0 < n; b0 += bsz) {
@@ -549,8 +569,9 @@ int mia_gpu_model_prefill(mia_gpu_model *m, const int *tokens, int n, int pos) {
                                      b + o->wk, b + o->wv, b + o->wo,
                                      (const float *)(b + o->q_norm),
                                      (const float *)(b + o->k_norm), m->d_rope, kc, vc,
-                                     pos + b0, nb, m->max_seq, m->d_xb, m->d_bscratch,
-                                     m->flags & MHIP_FORCE_SEQ_RMS))
+                                     pos + b0, nb, m->max_seq, m->d_xb,
+                                     m->d_apack ? m->d_apack + (size_t)l * m->apack_bytes : NULL,
+                                     m->d_bscratch, m->flags & MHIP_FORCE_SEQ_RMS))
                 return mfail(m, "%s", mhip_error(m->gpu));
             if (mia_moe_layer_dev(m->moe, l, m->d_xb, nb, NULL))
                 return mfail(m, "%s", mia_moe_error(m->moe));
