@@ -328,11 +328,32 @@ __device__ __forceinline__ void gemm_tile_rows(Step *ring, const Src &src, int n
 //
 // xsb[k][p] = xs[t][k] for the assignment p = (t, j) in bucketed order, so a
 // tile's 128 rows read their scales of block k as one contiguous run.
+// Thread p copies blocks XB y .. XB y + XB - 1 of its token's row: four
+// 16-byte reads of one row (rather than a 4-byte gather per block), then
+// stores that are contiguous across the wavefront for each block.
+constexpr int XB = 16;
 __global__ __launch_bounds__(256) void k_xs_bucket(const float *__restrict__ xs,
                                                    const int *__restrict__ perm,
                                                    float *__restrict__ xsb, int A, int nb, int K) {
-    const int p = blockIdx.x * 256 + threadIdx.x, k = blockIdx.y;
-    if (p < A) xsb[(size_t)k * A + p] = xs[(size_t)(perm[p] / K) * nb + k];
+    const int p = blockIdx.x * 256 + threadIdx.x, k0 = blockIdx.y * XB;
+    if (p >= A) return;
+    const float *row = xs + (size_t)(perm[p] / K) * nb + k0;
+    float *dst = xsb + (size_t)k0 * A + p;
+    if (nb % 4 == 0 && k0 + XB <= nb) {
+        float v[XB];
+#pragma unroll
+        for (int q = 0; q < XB / 4; q++) {
+            const float4 f = *(const float4 *)(row + 4 * q);
+            v[4 * q] = f.x;
+            v[4 * q + 1] = f.y;
+            v[4 * q + 2] = f.z;
+            v[4 * q + 3] = f.w;
+        }
+#pragma unroll
+        for (int k = 0; k < XB; k++) dst[(size_t)k * A] = v[k];
+    } else {
+        for (int k = 0; k < XB && k0 + k < nb; k++) dst[(size_t)k * A] = row[k];
+    }
 }
 
 union alignas(16) GateUpLds {
@@ -553,8 +574,8 @@ static unsigned gemm_grid(int A, int E, int ny) {
 int launch_gateup_mfma(hipStream_t st, const mhip_dims *s, const mhip_layout *lay,
                        const void *d_table_layer, const mhip_scratch *sc, int A) {
     const int d = s->dim, eh = s->expert_hidden;
-    k_xs_bucket<<<dim3((A + 255) / 256, d / KB), 256, 0, st>>>(sc->xs, sc->perm, sc->xsb, A,
-                                                              d / KB, s->n_active);
+    k_xs_bucket<<<dim3((A + 255) / 256, (d / KB + XB - 1) / XB), 256, 0, st>>>(
+        sc->xs, sc->perm, sc->xsb, A, d / KB, s->n_active);
     const unsigned grid = gemm_grid(A, s->n_experts, eh / (TN / 2));
     k_gateup_mfma<<<grid, GT, 0, st>>>((const uint8_t *)d_table_layer, *lay,
                                        (const _Float16 *)sc->xdq, sc->xsb, sc->groups,

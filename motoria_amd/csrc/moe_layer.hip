@@ -949,16 +949,6 @@ __device__ __forceinline__ void wave_order() {
     asm volatile("" ::: "memory");
 }
 
-__device__ __forceinline__ int disp_key(const int *idx, int a, int A, int E, int *status) {
-    if (a >= A) return -1;
-    const int e = idx[a];
-    if (e < 0 || e >= E) {
-        atomicOr(&status[0], 1);
-        atomicCAS(&status[2], 0, status[3] + 1);
-        return 0;
-    }
-    return e;
-}
 
 // Lanes of the wavefront whose key equals this lane's (keys < 2^bits; -1
 // matches no lane).
@@ -971,25 +961,52 @@ __device__ __forceinline__ uint64_t same_key_lanes(int key, int bits) {
     return key >= 0 ? m : 0ull;
 }
 
-// One wavefront counts chunk ch into cnt[E] (zeroed by the caller).
-__device__ __forceinline__ void disp_count_chunk(const int *idx, int A, int E, int ch, int *cnt,
-                                                 int *status) {
+constexpr int DSTEP = DCH / 64;  // assignments of a chunk per lane
+
+// This lane's keys of chunk ch, one per step of 64 (-1 past the end; an
+// expert id outside 0..E-1 counts as expert 0 and is reported in status):
+// the loads are issued together, then validated.
+__device__ __forceinline__ void disp_chunk_keys(const int *idx, int A, int E, int ch, int *status,
+                                                int (&key)[DSTEP]) {
     const int lane = threadIdx.x & 63;
-    for (int s = 0; s < DCH / 64; s++) {
-        const int k = disp_key(idx, ch * DCH + s * 64 + lane, A, E, status);
-        if (k >= 0) atomicAdd(&cnt[k], 1);
+    int raw[DSTEP];
+#pragma unroll
+    for (int s = 0; s < DSTEP; s++) {
+        const int a = ch * DCH + s * 64 + lane;
+        raw[s] = a < A ? idx[a] : 0;
+    }
+#pragma unroll
+    for (int s = 0; s < DSTEP; s++) {
+        const int a = ch * DCH + s * 64 + lane;
+        if (a >= A) {
+            key[s] = -1;
+        } else if (raw[s] < 0 || raw[s] >= E) {
+            atomicOr(&status[0], 1);
+            atomicCAS(&status[2], 0, status[3] + 1);
+            key[s] = 0;
+        } else {
+            key[s] = raw[s];
+        }
     }
 }
 
-// One wavefront places chunk ch in order; bs[E] holds each expert's next
-// position and is advanced.
-__device__ __forceinline__ void disp_scatter_chunk(const int *idx, int A, int E, int ch, int bits,
-                                                   int *bs, int *perm, int *pos, int *status) {
+// One wavefront counts its chunk's keys into cnt[E] (zeroed by the caller).
+__device__ __forceinline__ void disp_count_chunk(const int (&key)[DSTEP], int *cnt) {
+#pragma unroll
+    for (int s = 0; s < DSTEP; s++)
+        if (key[s] >= 0) atomicAdd(&cnt[key[s]], 1);
+}
+
+// One wavefront places chunk ch (its keys) in order; bs[E] holds each
+// expert's next position and is advanced.
+__device__ __forceinline__ void disp_scatter_chunk(const int (&key)[DSTEP], int ch, int bits,
+                                                   int *bs, int *perm, int *pos) {
     const int lane = threadIdx.x & 63;
     const uint64_t below = (1ull << lane) - 1;
-    for (int s = 0; s < DCH / 64; s++) {
+#pragma unroll
+    for (int s = 0; s < DSTEP; s++) {
         const int a = ch * DCH + s * 64 + lane;
-        const int k = disp_key(idx, a, A, E, status);
+        const int k = key[s];
         const uint64_t m = same_key_lanes(k, bits);
         if (k >= 0) {
             const int p = bs[k] + __popcll(m & below);
@@ -1012,7 +1029,11 @@ __global__ __launch_bounds__(64 * DWG) void k_disp_count(const int *__restrict__
     int *c = cnt + w * E;
     for (int e = lane; e < E; e += 64) c[e] = 0;
     __syncthreads();
-    if (ch < nch) disp_count_chunk(idx, A, E, ch, c, status);
+    if (ch < nch) {
+        int key[DSTEP];
+        disp_chunk_keys(idx, A, E, ch, status, key);
+        disp_count_chunk(key, c);
+    }
     __syncthreads();
     if (ch < nch)
         for (int e = lane; e < E; e += 64) hist[(size_t)e * nch + ch] = c[e];
@@ -1148,10 +1169,12 @@ __global__ __launch_bounds__(64 * DWG) void k_disp_scatter(const int *__restrict
     disp_tables(E, tot, off, sc, blockIdx.x == 0, counts, offsets, groups, gtile, glight, tm);
     const int ch = blockIdx.x * DWG + w;
     if (ch >= nch) return;  // a whole wavefront: no workgroup barrier follows
+    int key[DSTEP];
+    disp_chunk_keys(idx, A, E, ch, status, key);
     int *bs = base + w * E;
     for (int e = lane; e < E; e += 64) bs[e] = off[e] + hist[(size_t)e * nch + ch];
     wave_order();
-    disp_scatter_chunk(idx, A, E, ch, bits, bs, perm, pos, status);
+    disp_scatter_chunk(key, ch, bits, bs, perm, pos);
 }
 
 // All three steps in one workgroup, one wavefront per chunk, for up to
@@ -1173,9 +1196,13 @@ __global__ __launch_bounds__(64 * DSMALL) void k_disp_small(const int *__restric
     int *off = tot + E;                // [E]
     int *sc = off + E;                 // [16]
     const int w = threadIdx.x >> 6;
+    // the chunk's keys are requested before the histogram is cleared, and
+    // kept for the scatter
+    int key[DSTEP];
+    if (w < nch) disp_chunk_keys(idx, A, E, w, status, key);
     for (int i = threadIdx.x; i < DSMALL * E; i += blockDim.x) hist[i] = 0;
     __syncthreads();
-    if (w < nch) disp_count_chunk(idx, A, E, w, hist + w * E, status);
+    if (w < nch) disp_count_chunk(key, hist + w * E);
     __syncthreads();
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
         int run = 0;
@@ -1192,7 +1219,7 @@ __global__ __launch_bounds__(64 * DSMALL) void k_disp_small(const int *__restric
         int *bs = hist + w * E;
         for (int e = threadIdx.x & 63; e < E; e += 64) bs[e] += off[e];
         wave_order();
-        disp_scatter_chunk(idx, A, E, w, bits, bs, perm, pos, status);
+        disp_scatter_chunk(key, w, bits, bs, perm, pos);
     }
 }
 
